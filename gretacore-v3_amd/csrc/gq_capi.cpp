@@ -1,0 +1,172 @@
+// gq_capi.cpp -- host side of the C ABI: status reporting, sizes, the host
+// (CPU) repack used by the loader, the library-owned workspace and the
+// GretaCompute::gemm-style routing entry.
+#include <mutex>
+#include <string.h>
+#include <vector>
+
+#include "gq_internal.h"
+
+namespace {
+thread_local char g_last_error[256] = {0};
+
+struct DeviceWorkspace {
+  void *ptr = nullptr;
+  size_t bytes = 0;
+};
+std::mutex g_ws_mutex;
+std::vector<DeviceWorkspace> g_ws;
+}  // namespace
+
+int gq_hip_status(hipError_t e) {
+  if (e == hipSuccess) return GQ_OK;
+  strncpy(g_last_error, hipGetErrorString(e), sizeof(g_last_error) - 1);
+  g_last_error[sizeof(g_last_error) - 1] = 0;
+  return GQ_ERR_HIP;
+}
+
+int gq_last_launch(void) { return gq_hip_status(hipGetLastError()); }
+
+int gq_default_workspace(size_t bytes, void **ptr) {
+  int dev = 0;
+  GQ_TRY(gq_hip_status(hipGetDevice(&dev)));
+  std::lock_guard<std::mutex> lock(g_ws_mutex);
+  if ((size_t)dev >= g_ws.size()) g_ws.resize(dev + 1);
+  DeviceWorkspace &w = g_ws[dev];
+  if (w.bytes < bytes) {
+    // the old buffer may still be in use by queued work on any stream
+    GQ_TRY(gq_hip_status(hipDeviceSynchronize()));
+    if (w.ptr) (void)hipFree(w.ptr);
+    w.ptr = nullptr;
+    w.bytes = 0;
+    size_t want = bytes < ((size_t)1 << 20) ? ((size_t)1 << 20) : bytes;
+    GQ_TRY(gq_hip_status(hipMalloc(&w.ptr, want)));
+    w.bytes = want;
+  }
+  *ptr = w.ptr;
+  return GQ_OK;
+}
+
+extern "C" {
+
+int gq_abi_version(void) { return GQ_ABI_VERSION; }
+
+const char *gq_status_string(int status) {
+  switch (status) {
+  case GQ_OK: return "ok";
+  case GQ_ERR_INVALID_ARGS: return "invalid arguments";
+  case GQ_ERR_UNSUPPORTED: return "unsupported format, dtype or batch";
+  case GQ_ERR_HIP: return "HIP error";
+  case GQ_ERR_WORKSPACE: return "workspace missing or too small";
+  case GQ_ERR_NO_DEVICE: return "no usable GPU";
+  default: return "unknown status";
+  }
+}
+
+const char *gq_last_error(void) { return g_last_error; }
+
+size_t gq_gguf_bytes(int fmt, size_t N, size_t K) {
+  if (!gq_fmt_valid(fmt)) return 0;
+  return gq_layout_gguf_bytes(fmt, N, K);
+}
+
+int gq_packed_size(int fmt, size_t N, size_t K, size_t *bytes) {
+  GQ_TRY(gq_check_shape(fmt, N, K));
+  GQ_CHECK(bytes, GQ_ERR_INVALID_ARGS);
+  *bytes = (N == 0 || K == 0) ? 0 : gq_packed_bytes(fmt, N, K);
+  return GQ_OK;
+}
+
+// Host repack: the same per-block functions the device kernel uses.
+int gq_repack_host(int fmt, const void *gguf, size_t N, size_t K, void *packed) {
+  GQ_TRY(gq_check_shape(fmt, N, K));
+  GQ_CHECK(gguf && packed, GQ_ERR_INVALID_ARGS);
+  if (N == 0 || K == 0) return GQ_OK;
+  const uint8_t *src = (const uint8_t *)gguf;
+  uint8_t *dst = (uint8_t *)packed;
+  const size_t Np = gq_tiles(N) * 16, C = gq_chunks(fmt, K), sc = gq_sc_plane_offset(fmt, N, K);
+  memset(dst, 0, gq_packed_bytes(fmt, N, K));
+  if (fmt == GQ_FMT_Q4_0) {
+    const size_t nb = K / 32;
+    for (size_t n = 0; n < N; ++n)
+      for (size_t b = 0; b < nb; ++b) {
+        uint32_t words[4], d16;
+        gq_q4_0_canon(src + (n * nb + b) * 18, words, &d16);
+        for (int w8 = 0; w8 < 4; ++w8) memcpy(dst + gq_q4_0_word_off(n, b, w8, C), &words[w8], 4);
+        uint16_t d = (uint16_t)d16;
+        memcpy(dst + sc + gq_q4_0_d_off(n, b, C), &d, 2);
+      }
+  } else if (fmt == GQ_FMT_Q8_0) {
+    const size_t nb = K / 32;
+    for (size_t n = 0; n < N; ++n)
+      for (size_t b = 0; b < nb; ++b) {
+        const uint8_t *blk = src + (n * nb + b) * 34;
+        for (int g = 0; g < 4; ++g) memcpy(dst + gq_q8_0_byte_off(n, b, 8 * g, C), blk + 2 + 8 * g, 8);
+        memcpy(dst + sc + gq_q4_0_d_off(n, b, C), blk, 2);
+      }
+  } else {
+    const int ggml = fmt == GQ_FMT_Q4_K_GGML;
+    const size_t S = C;
+    for (size_t n = 0; n < N; ++n)
+      for (size_t s = 0; s < S; ++s) {
+        uint32_t words[8][4], meta[4];
+        gq_q4k_canon(ggml, src + (n * S + s) * 144, words, meta);
+        for (int j = 0; j < 8; ++j)
+          for (int w8 = 0; w8 < 4; ++w8) memcpy(dst + gq_q4k_word_off(n, s, j, w8, S), &words[j][w8], 4);
+        memcpy(dst + sc + gq_q4k_meta_off(n, s, S), meta, 16);
+      }
+  }
+  (void)Np;
+  return GQ_OK;
+}
+
+int gq_unpack_host(int fmt, const void *packed, size_t N, size_t K, void *gguf) {
+  GQ_TRY(gq_check_shape(fmt, N, K));
+  GQ_CHECK(gguf && packed, GQ_ERR_INVALID_ARGS);
+  if (N == 0 || K == 0) return GQ_OK;
+  const uint8_t *src = (const uint8_t *)packed;
+  uint8_t *dst = (uint8_t *)gguf;
+  const size_t C = gq_chunks(fmt, K), sc = gq_sc_plane_offset(fmt, N, K);
+  if (fmt == GQ_FMT_Q4_0) {
+    const size_t nb = K / 32;
+    for (size_t n = 0; n < N; ++n)
+      for (size_t b = 0; b < nb; ++b) {
+        uint32_t words[4];
+        uint16_t d = 0;
+        for (int w8 = 0; w8 < 4; ++w8) memcpy(&words[w8], src + gq_q4_0_word_off(n, b, w8, C), 4);
+        memcpy(&d, src + sc + gq_q4_0_d_off(n, b, C), 2);
+        gq_q4_0_uncanon(words, d, dst + (n * nb + b) * 18);
+      }
+  } else if (fmt == GQ_FMT_Q8_0) {
+    const size_t nb = K / 32;
+    for (size_t n = 0; n < N; ++n)
+      for (size_t b = 0; b < nb; ++b) {
+        uint8_t *blk = dst + (n * nb + b) * 34;
+        for (int g = 0; g < 4; ++g) memcpy(blk + 2 + 8 * g, src + gq_q8_0_byte_off(n, b, 8 * g, C), 8);
+        memcpy(blk, src + sc + gq_q4_0_d_off(n, b, C), 2);
+      }
+  } else {
+    const int ggml = fmt == GQ_FMT_Q4_K_GGML;
+    const size_t S = C;
+    for (size_t n = 0; n < N; ++n)
+      for (size_t s = 0; s < S; ++s) {
+        uint32_t words[8][4], meta[4];
+        for (int j = 0; j < 8; ++j)
+          for (int w8 = 0; w8 < 4; ++w8) memcpy(&words[j][w8], src + gq_q4k_word_off(n, s, j, w8, S), 4);
+        memcpy(meta, src + sc + gq_q4k_meta_off(n, s, S), 16);
+        gq_q4k_uncanon(ggml, words, meta, dst + (n * S + s) * 144);
+      }
+  }
+  return GQ_OK;
+}
+
+// GretaCompute::gemm routing for GGUF-native weights
+// (src/compute/src/greta_compute_hip.cpp:148-374): small M goes to the GEMV
+// kernels, larger M to the MFMA GEMM.  A and C are f32, as in the reference.
+int gq_matmul(int fmt, const void *packed, const float *a, float *c, size_t M, size_t N, size_t K, void *stream) {
+  if (M >= 1 && M <= GQ_MAX_BATCH)
+    return gq_gemv(fmt, packed, a, c, N, K, (int)M, nullptr, 0, stream);
+  return gq_gemm(fmt, packed, a, GQ_DT_F32, c, GQ_DT_F32, M, N, K, nullptr, 0, stream);
+}
+
+}  // extern "C"

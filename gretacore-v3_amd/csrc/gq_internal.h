@@ -1,0 +1,50 @@
+// gq_internal.h -- shared declarations of the libgq implementation files.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stddef.h>
+#include <stdint.h>
+
+#include "../../include/gq.h"
+#include "gq_device.h"
+#include "gq_layout.h"
+#include "gq_repack_impl.h"
+
+#define GQ_CHECK(cond, code) \
+  do {                       \
+    if (!(cond)) return (code); \
+  } while (0)
+#define GQ_TRY(expr)          \
+  do {                        \
+    int _st = (expr);         \
+    if (_st != GQ_OK) return _st; \
+  } while (0)
+
+// Records the HIP error (if any) of the last launch and maps it to a status.
+int gq_last_launch(void);
+int gq_hip_status(hipError_t e);
+
+// Validates (fmt, N, K): known format, K a multiple of the block size, sizes
+// within GQ_MAX_DIM.
+static inline int gq_check_shape(int fmt, size_t N, size_t K) {
+  if (!gq_fmt_valid(fmt)) return GQ_ERR_UNSUPPORTED;
+  if (N > GQ_MAX_DIM || K > GQ_MAX_DIM) return GQ_ERR_INVALID_ARGS;
+  if (K % gq_block_elems(fmt)) return GQ_ERR_INVALID_ARGS;
+  return GQ_OK;
+}
+
+static inline size_t gq_align256(size_t v) { return (v + 255) & ~(size_t)255; }
+// padded K of the T16 layout
+static inline size_t gq_kpad(int fmt, size_t K) { return gq_chunks(fmt, K) * gq_chunk_k(fmt); }
+// GEMV workspace: xq fp16 [2B][Kp] then (Q4_K) sq uint32 [B][Kp/32]
+static inline size_t gq_xq_bytes(int fmt, size_t K, int B) {
+  return gq_align256((size_t)2 * B * gq_kpad(fmt, K) * 2);
+}
+static inline size_t gq_sq_bytes(int fmt, size_t K, int B) {
+  return gq_fmt_is_q4k(fmt) ? gq_align256((size_t)B * (gq_kpad(fmt, K) / 32) * 4) : 0;
+}
+
+int gq_launch_prep_x(int fmt, const float *x, void *ws, int B, int K, hipStream_t s);
+int gq_launch_prep_a(const void *a, int a_dtype, _Float16 *out, int M, int K, int Kp, hipStream_t s);
+
+// Library-owned per-device workspace (grown on demand, never shrunk).
+int gq_default_workspace(size_t bytes, void **ptr);

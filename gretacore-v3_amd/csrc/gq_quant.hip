@@ -1,0 +1,412 @@
+// gq_quant.hip -- bit-exact GGUF dequantization, the T16 repack kernel and the
+// activation preparation kernels used by the GEMV/GEMM paths.
+//
+// Dequantized values follow the reference semantics exactly:
+//   Q4_K  src/inference/src/weight_loader.cpp:125-156 (products and the final
+//         difference rounded separately -> contraction is disabled below)
+//   Q8_0  weight_loader.cpp:703-712 + gemm_kernels.hip:612-616: (float)q * d
+//   Q4_0  GGUF spec (no reference implementation): (float)(q - 8) * d
+//   fp16  weight_loader.cpp:91-110 (NaN -> Inf)
+#include "gq_internal.h"
+
+#pragma clang fp contract(off)
+
+namespace {
+
+// ---------------------------------------------------------------------------
+// Dequantization of raw GGUF blocks: one thread per 32 output elements.
+// ---------------------------------------------------------------------------
+__global__ void __launch_bounds__(256)
+k_dequant_q4_0(const uint8_t *__restrict__ src, float *__restrict__ out, size_t nblk) {
+  size_t i = (size_t)blockIdx.x * 256 + threadIdx.x;
+  if (i >= nblk) return;
+  const uint8_t *b = src + i * 18;
+  float d = gq_h2f(gq_rd16(b));
+  float y[32];
+#pragma unroll
+  for (int j = 0; j < 16; ++j) {
+    uint32_t q = b[2 + j];
+    y[j] = (float)((int)(q & 15u) - 8) * d;
+    y[j + 16] = (float)((int)(q >> 4) - 8) * d;
+  }
+  float4 *o = reinterpret_cast<float4 *>(out + i * 32);
+#pragma unroll
+  for (int v = 0; v < 8; ++v) o[v] = make_float4(y[4 * v], y[4 * v + 1], y[4 * v + 2], y[4 * v + 3]);
+}
+
+__global__ void __launch_bounds__(256)
+k_dequant_q8_0(const uint8_t *__restrict__ src, float *__restrict__ out, size_t nblk) {
+  size_t i = (size_t)blockIdx.x * 256 + threadIdx.x;
+  if (i >= nblk) return;
+  const uint8_t *b = src + i * 34;
+  float d = gq_h2f(gq_rd16(b));
+  float4 *o = reinterpret_cast<float4 *>(out + i * 32);
+#pragma unroll
+  for (int v = 0; v < 8; ++v) {
+    float y0 = (float)(int8_t)b[2 + 4 * v] * d, y1 = (float)(int8_t)b[3 + 4 * v] * d;
+    float y2 = (float)(int8_t)b[4 + 4 * v] * d, y3 = (float)(int8_t)b[5 + 4 * v] * d;
+    o[v] = make_float4(y0, y1, y2, y3);
+  }
+}
+
+// one thread per 32-element sub-block of a Q4_K super-block
+__global__ void __launch_bounds__(256)
+k_dequant_q4_k(const uint8_t *__restrict__ src, float *__restrict__ out, size_t nsub, int ggml) {
+  size_t i = (size_t)blockIdx.x * 256 + threadIdx.x;
+  if (i >= nsub) return;
+  size_t sb = i >> 3;
+  int j = (int)(i & 7);
+  const uint8_t *b = src + sb * 144;
+  float d = gq_h2f(gq_rd16(b)), dmin = gq_h2f(gq_rd16(b + 2));
+  uint8_t sc[8], m[8];
+  if (ggml) gq_q4k_ggml_codes(b + 4, sc, m);
+  else gq_q4k_ref_codes(b + 4, sc, m);
+  float scale = d * (float)sc[j];
+  float minv = dmin * (float)m[j];
+  float y[32];
+#pragma unroll
+  for (int e = 0; e < 32; ++e) {
+    float p = scale * (float)gq_q4k_nib(ggml, b + 16, j, e);
+    y[e] = p - minv;
+  }
+  float4 *o = reinterpret_cast<float4 *>(out + i * 32);
+#pragma unroll
+  for (int v = 0; v < 8; ++v) o[v] = make_float4(y[4 * v], y[4 * v + 1], y[4 * v + 2], y[4 * v + 3]);
+}
+
+// ---------------------------------------------------------------------------
+// Dequantization straight from the T16 layout (proves the repack is lossless
+// and gives the GEMM paths' weight values).  One thread per (row, 32-block).
+// ---------------------------------------------------------------------------
+__global__ void __launch_bounds__(256)
+k_dequant_t16(int fmt, const uint8_t *__restrict__ w, float *__restrict__ out, int N, int K) {
+  size_t i = (size_t)blockIdx.x * 256 + threadIdx.x;
+  int nb = K / 32;
+  if (i >= (size_t)N * nb) return;
+  size_t n = i / nb, blk = i % nb;
+  float y[32];
+  if (fmt == GQ_FMT_Q4_0) {
+    size_t C = gq_chunks(fmt, K);
+    const uint8_t *sc = w + gq_sc_plane_offset(fmt, N, K);
+    float d = gq_h2f(gq_rd16(sc + gq_q4_0_d_off(n, blk, C)));
+#pragma unroll
+    for (int w8 = 0; w8 < 4; ++w8) {
+      uint32_t word = *reinterpret_cast<const uint32_t *>(w + gq_q4_0_word_off(n, blk, w8, C));
+#pragma unroll
+      for (int e = 0; e < 8; ++e)
+        y[8 * w8 + e] = (float)((int)((word >> (4 * gq_canon_pos(e))) & 15u) - 8) * d;
+    }
+  } else if (fmt == GQ_FMT_Q8_0) {
+    size_t C = gq_chunks(fmt, K);
+    const uint8_t *sc = w + gq_sc_plane_offset(fmt, N, K);
+    float d = gq_h2f(gq_rd16(sc + gq_q4_0_d_off(n, blk, C)));
+#pragma unroll
+    for (int b = 0; b < 32; ++b) y[b] = (float)(int8_t)w[gq_q8_0_byte_off(n, blk, b, C)] * d;
+  } else {
+    size_t S = gq_chunks(fmt, K);
+    size_t s = blk >> 3;
+    int j = (int)(blk & 7);
+    const uint32_t *meta = reinterpret_cast<const uint32_t *>(
+        w + gq_sc_plane_offset(fmt, N, K) + gq_q4k_meta_off(n, s, S));
+    float d = gq_h2f(meta[0] & 0xFFFFu), dmin = gq_h2f(meta[0] >> 16);
+    uint32_t sc0, m0, sc1, m1;
+    gq_q4k_codes(meta[1], meta[2], meta[3], j >> 1, sc0, m0, sc1, m1);
+    uint32_t scj = (j & 1) ? sc1 : sc0, mj = (j & 1) ? m1 : m0;
+    float scale = d * (float)scj;
+    float minv = dmin * (float)mj;
+#pragma unroll
+    for (int w8 = 0; w8 < 4; ++w8) {
+      uint32_t word = *reinterpret_cast<const uint32_t *>(w + gq_q4k_word_off(n, s, j, w8, S));
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        float p = scale * (float)((word >> (4 * gq_canon_pos(e))) & 15u);
+        y[8 * w8 + e] = p - minv;
+      }
+    }
+  }
+  float4 *o = reinterpret_cast<float4 *>(out + n * (size_t)K + blk * 32);
+#pragma unroll
+  for (int v = 0; v < 8; ++v) o[v] = make_float4(y[4 * v], y[4 * v + 1], y[4 * v + 2], y[4 * v + 3]);
+}
+
+// ---------------------------------------------------------------------------
+// Repack GGUF -> T16.  One thread per (padded row, padded block); positions
+// outside the tensor are written as zeros, so no memset is needed.
+// ---------------------------------------------------------------------------
+__global__ void __launch_bounds__(256)
+k_repack_q4_0(const uint8_t *__restrict__ src, uint8_t *__restrict__ dst, int N, int K) {
+  size_t C = gq_chunks(GQ_FMT_Q4_0, K), nbp = C * 4, Np = gq_tiles(N) * 16;
+  size_t i = (size_t)blockIdx.x * 256 + threadIdx.x;
+  if (i >= Np * nbp) return;
+  size_t n = i / nbp, blk = i % nbp;
+  size_t nb = (size_t)K / 32;
+  uint32_t words[4] = {0, 0, 0, 0}, d16 = 0;
+  if (n < (size_t)N && blk < nb) gq_q4_0_canon(src + (n * nb + blk) * 18, words, &d16);
+  for (int w8 = 0; w8 < 4; ++w8)
+    *reinterpret_cast<uint32_t *>(dst + gq_q4_0_word_off(n, blk, w8, C)) = words[w8];
+  *reinterpret_cast<uint16_t *>(dst + gq_sc_plane_offset(GQ_FMT_Q4_0, N, K) +
+                                gq_q4_0_d_off(n, blk, C)) = (uint16_t)d16;
+}
+
+__global__ void __launch_bounds__(256)
+k_repack_q8_0(const uint8_t *__restrict__ src, uint8_t *__restrict__ dst, int N, int K) {
+  size_t C = gq_chunks(GQ_FMT_Q8_0, K), nbp = C * 4, Np = gq_tiles(N) * 16;
+  size_t i = (size_t)blockIdx.x * 256 + threadIdx.x;
+  if (i >= Np * nbp) return;
+  size_t n = i / nbp, blk = i % nbp;
+  size_t nb = (size_t)K / 32;
+  bool in = n < (size_t)N && blk < nb;
+  const uint8_t *b = src + (n * nb + blk) * 34;
+  for (int g = 0; g < 4; ++g) {
+    uint32_t lo = 0, hi = 0;
+    if (in) {
+      lo = (uint32_t)b[2 + 8 * g] | ((uint32_t)b[3 + 8 * g] << 8) | ((uint32_t)b[4 + 8 * g] << 16) |
+           ((uint32_t)b[5 + 8 * g] << 24);
+      hi = (uint32_t)b[6 + 8 * g] | ((uint32_t)b[7 + 8 * g] << 8) | ((uint32_t)b[8 + 8 * g] << 16) |
+           ((uint32_t)b[9 + 8 * g] << 24);
+    }
+    uint32_t *o = reinterpret_cast<uint32_t *>(dst + gq_q8_0_byte_off(n, blk, 8 * g, C));
+    o[0] = lo;
+    o[1] = hi;
+  }
+  *reinterpret_cast<uint16_t *>(dst + gq_sc_plane_offset(GQ_FMT_Q8_0, N, K) +
+                                gq_q4_0_d_off(n, blk, C)) = (uint16_t)(in ? gq_rd16(b) : 0u);
+}
+
+__global__ void __launch_bounds__(256)
+k_repack_q4_k(const uint8_t *__restrict__ src, uint8_t *__restrict__ dst, int N, int K, int ggml) {
+  size_t S = gq_chunks(GQ_FMT_Q4_K, K), Np = gq_tiles(N) * 16;
+  size_t i = (size_t)blockIdx.x * 256 + threadIdx.x;
+  if (i >= Np * S) return;
+  size_t n = i / S, s = i % S;
+  uint32_t words[8][4], meta[4];
+  if (n < (size_t)N) {
+    gq_q4k_canon(ggml, src + (n * S + s) * 144, words, meta);
+  } else {
+    for (int j = 0; j < 8; ++j)
+      for (int w8 = 0; w8 < 4; ++w8) words[j][w8] = 0;
+    meta[0] = meta[1] = meta[2] = meta[3] = 0;
+  }
+  for (int j = 0; j < 8; ++j)
+    for (int w8 = 0; w8 < 4; ++w8)
+      *reinterpret_cast<uint32_t *>(dst + gq_q4k_word_off(n, s, j, w8, S)) = words[j][w8];
+  uint32_t *mo = reinterpret_cast<uint32_t *>(dst + gq_sc_plane_offset(GQ_FMT_Q4_K, N, K) +
+                                              gq_q4k_meta_off(n, s, S));
+  mo[0] = meta[0];
+  mo[1] = meta[1];
+  mo[2] = meta[2];
+  mo[3] = meta[3];
+}
+
+// ---------------------------------------------------------------------------
+// Activation preparation for the GEMV (decode) path.  x f32 [B][K] ->
+//   xq  fp16 [2B][Kp]: row 2b = hi = fp16(x), row 2b+1 = lo = fp16(x - hi)
+//   sq  (Q4_K only) uint32 [B][Kp/32]: fp16 pair (hi, lo) of the fp32 sum of
+//       each 32-element sub-block of x.
+// Elements k >= K are written as zeros.  One thread per 32 elements.
+// ---------------------------------------------------------------------------
+__global__ void __launch_bounds__(256)
+k_prep_x(const float *__restrict__ x, _Float16 *__restrict__ xq, uint32_t *__restrict__ sq,
+         int B, int K, int Kp) {
+  int nsub = Kp / 32;
+  int i = blockIdx.x * 256 + threadIdx.x;
+  if (i >= B * nsub) return;
+  int b = i / nsub, j = i % nsub;
+  const float *xr = x + (size_t)b * K + 32 * j;
+  bool full = 32 * j + 32 <= K;
+  float v[32];
+  if (full) {
+    const float4 *p = reinterpret_cast<const float4 *>(xr);
+#pragma unroll
+    for (int q = 0; q < 8; ++q) {
+      float4 t = p[q];
+      v[4 * q] = t.x; v[4 * q + 1] = t.y; v[4 * q + 2] = t.z; v[4 * q + 3] = t.w;
+    }
+  } else {
+#pragma unroll
+    for (int e = 0; e < 32; ++e) v[e] = (32 * j + e < K) ? xr[e] : 0.0f;
+  }
+  gq_half8 hi[4], lo[4];
+  float s = 0.0f;
+#pragma unroll
+  for (int e = 0; e < 32; ++e) {
+    _Float16 h = (_Float16)v[e];
+    hi[e >> 3][e & 7] = h;
+    lo[e >> 3][e & 7] = (_Float16)(v[e] - (float)h);
+    s += v[e];
+  }
+  gq_half8 *ph = reinterpret_cast<gq_half8 *>(xq + (size_t)(2 * b) * Kp + 32 * j);
+  gq_half8 *pl = reinterpret_cast<gq_half8 *>(xq + (size_t)(2 * b + 1) * Kp + 32 * j);
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    ph[q] = hi[q];
+    pl[q] = lo[q];
+  }
+  if (sq) {
+    _Float16 sh = (_Float16)s;
+    _Float16 sl = (_Float16)(s - (float)sh);
+    gq_half2 pr = {sh, sl};
+    sq[(size_t)b * nsub + j] = gq_h2_bits(pr);
+  }
+}
+
+// Activation conversion for the GEMM (prefill) path: bf16 / f32 / f16 [M][K]
+// -> f16 [M][Kp], zero padded.  Eight elements per thread.
+__global__ void __launch_bounds__(256)
+k_prep_a_f16(const void *__restrict__ a, int a_dtype, _Float16 *__restrict__ out, int M, int K, int Kp) {
+  size_t i = (size_t)blockIdx.x * 256 + threadIdx.x;
+  size_t per_row = (size_t)Kp / 8;
+  if (i >= (size_t)M * per_row) return;
+  size_t m = i / per_row, k0 = (i % per_row) * 8;
+  gq_half8 h;
+  if (k0 + 8 <= (size_t)K && (K % 8) == 0) {
+    if (a_dtype == GQ_DT_BF16) {
+      gq_u4 u = gq_ld16(reinterpret_cast<const uint16_t *>(a) + m * K + k0);
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        h[2 * q] = (_Float16)__uint_as_float(u[q] << 16);
+        h[2 * q + 1] = (_Float16)__uint_as_float(u[q] & 0xFFFF0000u);
+      }
+    } else if (a_dtype == GQ_DT_F16) {
+      h = *reinterpret_cast<const gq_half8 *>(reinterpret_cast<const _Float16 *>(a) + m * K + k0);
+    } else {
+      const float *f = reinterpret_cast<const float *>(a) + m * K + k0;
+#pragma unroll
+      for (int q = 0; q < 8; ++q) h[q] = (_Float16)f[q];
+    }
+  } else {
+#pragma unroll
+    for (int q = 0; q < 8; ++q) {
+      size_t k = k0 + q;
+      float v = 0.0f;
+      if (k < (size_t)K) {
+        if (a_dtype == GQ_DT_BF16)
+          v = __uint_as_float((uint32_t)reinterpret_cast<const uint16_t *>(a)[m * K + k] << 16);
+        else if (a_dtype == GQ_DT_F16)
+          v = (float)reinterpret_cast<const _Float16 *>(a)[m * K + k];
+        else
+          v = reinterpret_cast<const float *>(a)[m * K + k];
+      }
+      h[q] = (_Float16)v;
+    }
+  }
+  *reinterpret_cast<gq_half8 *>(out + m * Kp + k0) = h;
+}
+
+// Per-32 int8 activation quantization (Q8_0 int8-MFMA path): the reference's
+// INT8 requant rule applied to activations (weight_loader.cpp:780-802):
+// d = amax/127, inv = d > 1e-9 ? 1/d : 0, q = round(a * inv), half away.
+__global__ void __launch_bounds__(256)
+k_quantize_act_q8(const void *__restrict__ a, int a_dtype, int8_t *__restrict__ q,
+                  float *__restrict__ dq, int M, int K) {
+  int nb = K / 32;
+  size_t i = (size_t)blockIdx.x * 256 + threadIdx.x;
+  if (i >= (size_t)M * nb) return;
+  size_t m = i / nb, blk = i % nb;
+  float v[32];
+#pragma unroll
+  for (int e = 0; e < 32; ++e) {
+    size_t idx = m * K + blk * 32 + e;
+    if (a_dtype == GQ_DT_BF16)
+      v[e] = __uint_as_float((uint32_t)reinterpret_cast<const uint16_t *>(a)[idx] << 16);
+    else if (a_dtype == GQ_DT_F16)
+      v[e] = (float)reinterpret_cast<const _Float16 *>(a)[idx];
+    else
+      v[e] = reinterpret_cast<const float *>(a)[idx];
+  }
+  float mx = 0.0f;
+#pragma unroll
+  for (int e = 0; e < 32; ++e) mx = fmaxf(mx, fabsf(v[e]));
+  float d = mx / 127.0f;
+  float inv = d > 1e-9f ? 1.0f / d : 0.0f;
+  uint32_t words[8];
+#pragma unroll
+  for (int w = 0; w < 8; ++w) {
+    uint32_t u = 0;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      float t = v[4 * w + e] * inv;
+      int qi = (int)roundf(t);
+      u |= ((uint32_t)qi & 0xFFu) << (8 * e);
+    }
+    words[w] = u;
+  }
+  gq_u4 *o = reinterpret_cast<gq_u4 *>(q + m * K + blk * 32);
+  o[0] = gq_u4{words[0], words[1], words[2], words[3]};
+  o[1] = gq_u4{words[4], words[5], words[6], words[7]};
+  dq[m * nb + blk] = d;
+}
+
+}  // namespace
+
+static unsigned blocks_for(size_t n) { return (unsigned)((n + 255) / 256); }
+
+extern "C" int gq_dequant_gguf(int fmt, const void *blocks, size_t n_blocks, float *out, void *stream) {
+  GQ_CHECK(gq_fmt_valid(fmt), GQ_ERR_UNSUPPORTED);
+  GQ_CHECK(blocks && out, GQ_ERR_INVALID_ARGS);
+  if (n_blocks == 0) return GQ_OK;
+  hipStream_t s = (hipStream_t)stream;
+  const uint8_t *src = (const uint8_t *)blocks;
+  if (fmt == GQ_FMT_Q4_0)
+    hipLaunchKernelGGL(k_dequant_q4_0, dim3(blocks_for(n_blocks)), dim3(256), 0, s, src, out, n_blocks);
+  else if (fmt == GQ_FMT_Q8_0)
+    hipLaunchKernelGGL(k_dequant_q8_0, dim3(blocks_for(n_blocks)), dim3(256), 0, s, src, out, n_blocks);
+  else
+    hipLaunchKernelGGL(k_dequant_q4_k, dim3(blocks_for(n_blocks * 8)), dim3(256), 0, s, src, out,
+                       n_blocks * 8, (int)(fmt == GQ_FMT_Q4_K_GGML));
+  return gq_last_launch();
+}
+
+extern "C" int gq_dequant_packed(int fmt, const void *packed, size_t N, size_t K, float *out, void *stream) {
+  GQ_TRY(gq_check_shape(fmt, N, K));
+  GQ_CHECK(packed && out, GQ_ERR_INVALID_ARGS);
+  if (N == 0 || K == 0) return GQ_OK;
+  int f = gq_fmt_is_q4k(fmt) ? GQ_FMT_Q4_K : fmt;
+  hipLaunchKernelGGL(k_dequant_t16, dim3(blocks_for(N * (K / 32))), dim3(256), 0, (hipStream_t)stream, f,
+                     (const uint8_t *)packed, out, (int)N, (int)K);
+  return gq_last_launch();
+}
+
+extern "C" int gq_repack(int fmt, const void *gguf, size_t N, size_t K, void *packed, void *stream) {
+  GQ_TRY(gq_check_shape(fmt, N, K));
+  GQ_CHECK(gguf && packed, GQ_ERR_INVALID_ARGS);
+  if (N == 0 || K == 0) return GQ_OK;
+  hipStream_t s = (hipStream_t)stream;
+  size_t Np = gq_tiles(N) * 16, C = gq_chunks(fmt, K);
+  const uint8_t *src = (const uint8_t *)gguf;
+  uint8_t *dst = (uint8_t *)packed;
+  if (fmt == GQ_FMT_Q4_0)
+    hipLaunchKernelGGL(k_repack_q4_0, dim3(blocks_for(Np * C * 4)), dim3(256), 0, s, src, dst, (int)N, (int)K);
+  else if (fmt == GQ_FMT_Q8_0)
+    hipLaunchKernelGGL(k_repack_q8_0, dim3(blocks_for(Np * C * 4)), dim3(256), 0, s, src, dst, (int)N, (int)K);
+  else
+    hipLaunchKernelGGL(k_repack_q4_k, dim3(blocks_for(Np * C)), dim3(256), 0, s, src, dst, (int)N, (int)K,
+                       (int)(fmt == GQ_FMT_Q4_K_GGML));
+  return gq_last_launch();
+}
+
+int gq_launch_prep_x(int fmt, const float *x, void *ws, int B, int K, hipStream_t s) {
+  int Kp = (int)(gq_chunks(fmt, K) * gq_chunk_k(fmt));
+  _Float16 *xq = (_Float16 *)ws;
+  uint32_t *sq = gq_fmt_is_q4k(fmt) ? (uint32_t *)((uint8_t *)ws + gq_xq_bytes(fmt, K, B)) : nullptr;
+  int n = B * (Kp / 32);
+  hipLaunchKernelGGL(k_prep_x, dim3(blocks_for(n)), dim3(256), 0, s, x, xq, sq, B, K, Kp);
+  return gq_last_launch();
+}
+
+int gq_launch_prep_a(const void *a, int a_dtype, _Float16 *out, int M, int K, int Kp, hipStream_t s) {
+  size_t n = (size_t)M * (Kp / 8);
+  hipLaunchKernelGGL(k_prep_a_f16, dim3(blocks_for(n)), dim3(256), 0, s, a, a_dtype, out, M, K, Kp);
+  return gq_last_launch();
+}
+
+extern "C" int gq_quantize_act_q8(const void *a, int a_dtype, size_t M, size_t K, int8_t *q, float *d,
+                                  void *stream) {
+  GQ_CHECK(a && q && d, GQ_ERR_INVALID_ARGS);
+  GQ_CHECK(a_dtype == GQ_DT_F32 || a_dtype == GQ_DT_F16 || a_dtype == GQ_DT_BF16, GQ_ERR_UNSUPPORTED);
+  GQ_CHECK(K % 32 == 0 && K <= GQ_MAX_DIM && M <= GQ_MAX_DIM, GQ_ERR_INVALID_ARGS);
+  if (M == 0 || K == 0) return GQ_OK;
+  hipLaunchKernelGGL(k_quantize_act_q8, dim3(blocks_for(M * (K / 32))), dim3(256), 0, (hipStream_t)stream,
+                     a, a_dtype, q, d, (int)M, (int)K);
+  return gq_last_launch();
+}

@@ -1,0 +1,132 @@
+/*
+ * gq.h -- C ABI of the MI355X-native GGUF quantized-weight matrix path
+ * (libgq.so).  Plain pointers and sizes only; device pointers are HIP device
+ * memory, `stream` is a hipStream_t passed as void* (NULL = default stream).
+ * Every entry point returns a gq status (0 = GQ_OK) and launches
+ * asynchronously on `stream` unless stated otherwise.
+ *
+ * Reference interfaces replaced (paths relative to leaatimberini/gretacore-v3):
+ *   - src/rt/backend/hip/include/gcore/rt/hip/kernels/gemm_kernels.hpp:43-57
+ *       launch_gemm_mfma_int8_wt_fp32_acc32 / launch_gemm_mfma_int4_wt_fp32_acc32
+ *       -> gq_launch_gemm_mfma_int8_wt_fp32_acc32 / ..._int4_... (same args)
+ *       and, for GGUF-native weights, gq_gemv / gq_gemm.
+ *   - src/compute/src/greta_compute_hip.cpp:148-374 GretaCompute::gemm routing
+ *       (M <= 32 -> GEMV kernel, else MFMA GEMM) -> gq_matmul.
+ *   - src/inference/src/weight_loader.cpp:91-156, 703-712 (CPU dequant at load)
+ *       -> gq_dequant_gguf (device, bit-exact) and gq_repack (GGUF -> T16).
+ *   - src/inference/src/weight_loader.cpp:825-1008 load_tensor_int4 upload
+ *       (requant to INT4 + hipMemcpy) -> gq_repack_host / gq_repack + upload of
+ *       the GGUF blocks themselves (see gq_gguf.h for the loader ABI).
+ */
+#ifndef GQ_H
+#define GQ_H
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define GQ_ABI_VERSION 1
+
+/* status codes */
+#define GQ_OK 0
+#define GQ_ERR_INVALID_ARGS 1 /* null pointer, bad shape, size out of range */
+#define GQ_ERR_UNSUPPORTED 2  /* unknown format / dtype / batch */
+#define GQ_ERR_HIP 3          /* a HIP call or kernel launch failed */
+#define GQ_ERR_WORKSPACE 4    /* workspace missing or too small */
+#define GQ_ERR_NO_DEVICE 5    /* no usable GPU */
+
+/* weight formats: GGML type ids (weight_loader.cpp:15-33) + a Q4_K variant */
+#define GQ_FMT_Q4_0 2
+#define GQ_FMT_Q8_0 8
+#define GQ_FMT_Q4_K 12       /* reference (GRETA) Q4_K layout, weight_loader.cpp:125-156 */
+#define GQ_FMT_Q4_K_GGML 112 /* llama.cpp canonical Q4_K layout */
+
+/* activation / output dtypes */
+#define GQ_DT_F32 0
+#define GQ_DT_F16 1
+#define GQ_DT_BF16 2
+
+/* limits checked by every entry point */
+#define GQ_MAX_DIM (1u << 24) /* N, K, M */
+#define GQ_MAX_BATCH 16       /* gq_gemv batch (decode) */
+
+int gq_abi_version(void);
+const char *gq_status_string(int status);
+/* Last HIP error text seen by this thread (empty if none). */
+const char *gq_last_error(void);
+
+/* ---- sizes ---------------------------------------------------------------- */
+/* GGUF bytes of an N x K tensor (weight_loader.cpp:457-463 sizing). */
+size_t gq_gguf_bytes(int fmt, size_t N, size_t K);
+/* Bytes of the repacked (T16) tensor.  Equal to the GGUF size whenever N is a
+ * multiple of 16 and K a multiple of 128 (Q4_0/Q8_0) or 256 (Q4_K). */
+int gq_packed_size(int fmt, size_t N, size_t K, size_t *bytes);
+
+/* ---- load-time repack ----------------------------------------------------- */
+/* Host: GGUF rows (N x K, row-major blocks) -> T16 layout; no GPU needed. */
+int gq_repack_host(int fmt, const void *gguf, size_t N, size_t K, void *packed);
+/* Host: inverse of gq_repack_host (T16 -> GGUF bytes of the same format). */
+int gq_unpack_host(int fmt, const void *packed, size_t N, size_t K, void *gguf);
+/* Device: same as gq_repack_host on device buffers. */
+int gq_repack(int fmt, const void *d_gguf, size_t N, size_t K, void *d_packed, void *stream);
+
+/* ---- dequantization (bit-exact with the reference semantics) -------------- */
+/* n_blocks raw GGUF blocks -> fp32 (n_blocks * 32 or * 256 values). */
+int gq_dequant_gguf(int fmt, const void *d_blocks, size_t n_blocks, float *d_out, void *stream);
+/* T16 tensor -> fp32 [N][K]. */
+int gq_dequant_packed(int fmt, const void *d_packed, size_t N, size_t K, float *d_out, void *stream);
+
+/* ---- decode GEMV: y[b][n] = sum_k x[b][k] * W[n][k], 1 <= batch <= 16 ------- */
+/* Workspace bytes needed by gq_gemv for (fmt, K, batch). */
+size_t gq_gemv_workspace_bytes(int fmt, size_t K, int batch);
+/* x f32 [batch][K], y f32 [batch][N].  workspace may be NULL: the library then
+ * uses a per-device buffer it owns (allocated on first use; not for use under
+ * stream capture).  Concurrent calls that share a workspace race. */
+int gq_gemv(int fmt, const void *d_packed, const float *d_x, float *d_y, size_t N, size_t K, int batch,
+            void *d_workspace, size_t workspace_bytes, void *stream);
+/* Split form: prepare x once (gq_gemv_prep) and run several GEMVs that share
+ * it (q/k/v, gate/up) with gq_gemv_prepped. */
+int gq_gemv_prep(int fmt, const float *d_x, size_t K, int batch, void *d_workspace, size_t workspace_bytes,
+                 void *stream);
+int gq_gemv_prepped(int fmt, const void *d_packed, const void *d_workspace, float *d_y, size_t N, size_t K,
+                    int batch, void *stream);
+
+/* ---- prefill GEMM: C[m][n] = sum_k A[m][k] * W[n][k] ------------------------ */
+/* A is [M][K] of a_dtype (GQ_DT_BF16 / F16 / F32), C is [M][N] of c_dtype
+ * (GQ_DT_F32 or GQ_DT_BF16).  Computes on f16 MFMA (v_mfma_f32_32x32x16_f16)
+ * with fp32 accumulation; weights are dequantized into LDS as fp16. */
+size_t gq_gemm_workspace_bytes(int fmt, size_t M, size_t K);
+int gq_gemm(int fmt, const void *d_packed, const void *d_a, int a_dtype, void *d_c, int c_dtype, size_t M,
+            size_t N, size_t K, void *d_workspace, size_t workspace_bytes, void *stream);
+
+/* Q8_0 x int8 activations (int8 MFMA): activations quantized per 32-block with
+ * the reference's INT8 rule (d = amax/127, q = round(a / d)). */
+int gq_quantize_act_q8(const void *d_a, int a_dtype, size_t M, size_t K, int8_t *d_q, float *d_d,
+                       void *stream);
+int gq_gemm_q8_i8(const void *d_packed_q8, const int8_t *d_qa, const float *d_da, float *d_c, size_t M,
+                  size_t N, size_t K, void *stream);
+
+/* ---- GretaCompute::gemm routing for GGUF-native B (greta_compute_hip.cpp:148)
+ * M <= 16 -> GEMV kernels, otherwise the MFMA GEMM.  A f32 [M][K], C f32. */
+int gq_matmul(int fmt, const void *d_packed, const float *d_a, float *d_c, size_t M, size_t N, size_t K,
+              void *stream);
+
+/* ---- reference-format launchers (drop-in for gemm_kernels.hpp:43-57) ------- */
+/* INT8 weight-only: b int8 [N][K], scales f32 [N*K/group_size]. */
+int gq_launch_gemm_mfma_int8_wt_fp32_acc32(void *stream, const float *a, const int8_t *b, float *c,
+                                            const float *scales, uint32_t M, uint32_t N, uint32_t K,
+                                            uint32_t lda, uint32_t ldb, uint32_t ldc, uint32_t group_size);
+/* INT4 weight-only: b packed nibbles [N][K/2] (even k low, two's complement),
+ * optional head_scales [N/head_dim]; a is f32, or f16 when is_fp16_a != 0. */
+int gq_launch_gemm_mfma_int4_wt_fp32_acc32(void *stream, const void *a, const int8_t *b, float *c,
+                                            const float *scales, const float *head_scales, uint32_t M,
+                                            uint32_t N, uint32_t K, uint32_t lda, uint32_t ldb, uint32_t ldc,
+                                            uint32_t group_size, uint32_t head_dim, int is_fp16_a,
+                                            int force_gemv);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

@@ -1,0 +1,190 @@
+"""GPU parity: libgq.so (HIP, gfx950) against the CPU oracle on the same seeded
+inputs.  Dequantization and repack are bit-exact; GEMV/GEMM must be within
+rel-L2 <= 1e-3 of the fp64-accumulated oracle."""
+import numpy as np
+import pytest
+
+import oracle as O
+
+pytestmark = pytest.mark.gpu
+
+TOL = 1e-3  # rel-L2 bound for GEMV / GEMM vs the fp64 oracle
+FMTS = [O.Q4_0, O.Q8_0, O.Q4_K, O.Q4_K_GGML]
+
+
+def bitexact(got, ref):
+    """Bit-identical, except that any NaN equals any NaN (x86 and CDNA produce
+    different default-NaN payloads for inf*0; the reference defines none)."""
+    got = np.asarray(got, dtype=np.float32).ravel()
+    ref = np.asarray(ref, dtype=np.float32).ravel()
+    same = got.view(np.uint32) == ref.view(np.uint32)
+    same |= np.isnan(got) & np.isnan(ref)
+    return bool(same.all())
+
+
+def _to_dev(a, dev):
+    import torch
+    return torch.from_numpy(np.ascontiguousarray(a)).to(dev)
+
+
+def _special_scales(w, fmt):
+    """Put fp16 edge values into the first blocks' scale fields."""
+    w = w.copy()
+    bb = O.BLOCK_BYTES[fmt]
+    specials = [0x0000, 0x8000, 0x0001, 0x03FF, 0x0400, 0x7BFF, 0x7C00, 0xFC00, 0x7E00, 0x7C01, 0x8001, 0x3C00]
+    nblk = w.size // bb
+    for i, h in enumerate(specials[:nblk]):
+        w[i * bb: i * bb + 2] = np.frombuffer(np.uint16(h).tobytes(), dtype=np.uint8)
+        if fmt in (O.Q4_K, O.Q4_K_GGML):
+            w[i * bb + 2: i * bb + 4] = np.frombuffer(np.uint16(specials[-1 - i]).tobytes(), dtype=np.uint8)
+    return w
+
+
+@pytest.mark.parametrize("fmt", FMTS)
+def test_dequant_gguf_bitexact(dev, fmt):
+    import gq
+    n, k = 48, 1024
+    w = _special_scales(O.gen_weights(fmt, n, k, seed=11 + fmt), fmt)
+    ref = O.dequant(fmt, w)
+    nb = w.size // O.BLOCK_BYTES[fmt]
+    got = gq.dequant_gguf(fmt, _to_dev(w, dev), nb).cpu().numpy()
+    assert bitexact(got, ref)
+
+
+@pytest.mark.parametrize("fmt", FMTS)
+@pytest.mark.parametrize("shape", [(64, 1024), (40, 512), (7, 256), (1, 4096)])
+def test_repack_device_matches_host_and_dequant(dev, fmt, shape):
+    import gq
+    n, k = shape
+    w = _special_scales(O.gen_weights(fmt, n, k, seed=3 + n), fmt)
+    host = gq.repack_host(fmt, w, n, k)
+    d = gq.repack(fmt, _to_dev(w, dev), n, k).cpu().numpy()
+    assert np.array_equal(host, d)
+    back = gq.dequant_packed(fmt, _to_dev(host, dev), n, k).cpu().numpy().ravel()
+    ref = O.dequant(fmt, w)
+    assert bitexact(back, ref)
+
+
+def _gemv_case(dev, fmt, n, k, batch, seed):
+    import gq
+    w = O.gen_weights(fmt, n, k, seed=seed)
+    x = O.gen_x(batch, k, seed=seed + 1)
+    ref = O.gemv(fmt, w, x, n, k)
+    packed = _to_dev(gq.repack_host(fmt, w, n, k), dev)
+    y = gq.gemv(fmt, packed, _to_dev(x, dev), n, k).cpu().numpy()
+    return O.rel_l2(y, ref)
+
+
+@pytest.mark.parametrize("fmt", FMTS)
+@pytest.mark.parametrize("batch", [1, 2, 3, 4, 8, 9, 16])
+def test_gemv_batches(dev, fmt, batch):
+    err = _gemv_case(dev, fmt, 256, 2048, batch, seed=100 + batch)
+    assert err <= TOL, err
+
+
+@pytest.mark.parametrize("fmt", [O.Q4_0, O.Q8_0])
+@pytest.mark.parametrize("shape", [(100, 288), (1, 32), (17, 96), (33, 160)])
+def test_gemv_ragged_q32(dev, fmt, shape):
+    n, k = shape
+    err = _gemv_case(dev, fmt, n, k, 1, seed=7 + n)
+    assert err <= TOL, err
+
+
+@pytest.mark.parametrize("fmt", [O.Q4_K, O.Q4_K_GGML])
+@pytest.mark.parametrize("shape", [(100, 256), (1, 768), (17, 512)])
+def test_gemv_ragged_q4k(dev, fmt, shape):
+    n, k = shape
+    err = _gemv_case(dev, fmt, n, k, 2, seed=9 + n)
+    assert err <= TOL, err
+
+
+@pytest.mark.parametrize("fmt,n,k", [(O.Q4_0, 14336, 4096), (O.Q4_0, 4096, 14336), (O.Q8_0, 4096, 4096),
+                                     (O.Q4_K, 14336, 4096)])
+def test_gemv_baseline_shapes(dev, fmt, n, k):
+    err = _gemv_case(dev, fmt, n, k, 1, seed=1000 + fmt)
+    assert err <= TOL, err
+
+
+def test_gemv_special_inputs(dev):
+    """All-8 nibbles -> zero weights; one-hot x selects a column."""
+    import gq
+    import torch
+    n, k = 64, 512
+    w = O.gen_weights(O.Q4_0, n, k, seed=5).reshape(-1, 18).copy()
+    w[:, 2:] = 0x88
+    packed = _to_dev(gq.repack_host(O.Q4_0, w.ravel(), n, k), dev)
+    x = torch.randn(1, k, device=dev)
+    assert torch.count_nonzero(gq.gemv(O.Q4_0, packed, x, n, k)).item() == 0
+    w2 = O.gen_weights(O.Q8_0, n, k, seed=6)
+    p2 = _to_dev(gq.repack_host(O.Q8_0, w2, n, k), dev)
+    W = O.dequant(O.Q8_0, w2).reshape(n, k)
+    for col in (0, 37, k - 1):
+        x = torch.zeros(1, k, device=dev)
+        x[0, col] = 1.0
+        y = gq.gemv(O.Q8_0, p2, x, n, k).cpu().numpy()[0]
+        assert np.array_equal(y, W[:, col])
+
+
+@pytest.mark.parametrize("fmt", [O.Q4_0, O.Q8_0, O.Q4_K])
+@pytest.mark.parametrize("m,n,k", [(64, 256, 1024), (130, 200, 512), (512, 512, 4096)])
+def test_gemm_parity(dev, fmt, m, n, k):
+    import gq
+    import torch
+    w = O.gen_weights(fmt, n, k, seed=50 + m)
+    a = torch.randn(m, k, generator=torch.Generator().manual_seed(m)).to(torch.bfloat16)
+    ref = O.gemv(fmt, w, a.float().numpy(), n, k)
+    packed = _to_dev(gq.repack_host(fmt, w, n, k), dev)
+    c = gq.gemm(fmt, packed, a.to(dev), n, k).cpu().numpy()
+    assert O.rel_l2(c, ref) <= TOL
+    cb = gq.gemm(fmt, packed, a.to(dev), n, k, out_dtype=torch.bfloat16).float().cpu().numpy()
+    assert O.rel_l2(cb, ref) <= 5e-3  # bf16 output rounding (2^-9) dominates
+
+
+def test_gemm_f32_activations_and_matmul_routing(dev):
+    import gq
+    import torch
+    fmt, n, k = O.Q4_0, 96, 512
+    w = O.gen_weights(fmt, n, k, seed=77)
+    packed = _to_dev(gq.repack_host(fmt, w, n, k), dev)
+    for m in (1, 5, 16, 17, 48):
+        a = O.gen_x(m, k, seed=m)
+        ref = O.gemv(fmt, w, a, n, k)
+        c = gq.matmul(fmt, packed, _to_dev(a, dev), n, k).cpu().numpy()
+        assert O.rel_l2(c, ref) <= TOL, m
+
+
+def test_q8_i8_path(dev):
+    import gq
+    import torch
+    m, n, k = 96, 160, 1024
+    w = O.gen_weights(O.Q8_0, n, k, seed=21)
+    a = O.gen_x(m, k, seed=22)
+    qa, da = gq.quantize_act_q8(_to_dev(a, dev))
+    rq, rd = O.quantize_act_q8(a)
+    assert np.array_equal(qa.cpu().numpy(), rq)
+    assert np.array_equal(da.cpu().numpy().view(np.uint32), rd.view(np.uint32))
+    packed = _to_dev(gq.repack_host(O.Q8_0, w, n, k), dev)
+    c = gq.gemm_q8_i8(packed, qa, da, n).cpu().numpy()
+    ref = O.gemm_q8_i8(w, rq, rd, n)
+    assert O.rel_l2(c, ref) <= 1e-5
+    # error of activation quantization itself, vs the fp32-activation oracle
+    assert O.rel_l2(c, O.gemv(O.Q8_0, w, a, n, k)) <= 2e-2
+
+
+@pytest.mark.parametrize("m", [1, 4, 40])
+def test_compat_int8_int4_launchers(dev, m):
+    import gq
+    n, k = 64, 256
+    rng = np.random.default_rng(m)
+    wf = rng.standard_normal((n, k)).astype(np.float32) * 0.05
+    x = O.gen_x(m, k, seed=m + 1)
+    q8, s8 = O.requant_int8(wf)
+    ref8 = O.gemm_int8_wt(x, q8, s8, m, n, k)
+    y8 = gq.launch_int8_wt(_to_dev(x, dev), _to_dev(q8, dev), _to_dev(s8, dev), m, n, k).cpu().numpy()
+    assert O.rel_l2(y8, ref8) <= 1e-5
+    p4, s4 = O.requant_int4(wf)
+    hs = O.head_scales(wf, 4, 16, k)
+    ref4 = O.gemm_int4_wt(x, p4, s4, hs, m, n, k, 32, 16)
+    y4 = gq.launch_int4_wt(_to_dev(x, dev), _to_dev(p4, dev), _to_dev(s4, dev), _to_dev(hs, dev), m, n, k,
+                           head_dim=16).cpu().numpy()
+    assert O.rel_l2(y4, ref4) <= 1e-5
