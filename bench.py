@@ -1,0 +1,308 @@
+"""Benchmark of the GGUF quantized-weight matrix path on one MI355X.
+
+Headline (BASELINE.json metric, configs[1]): Q4_0 decode GEMV, batch 1,
+14336 x 4096, HBM GB/s of whole-job throughput (activation prep + GEMV kernel)
+with the weights already resident in HBM.  A "step" is one GEMV call over one
+weight copy; >= 8 distinct copies (>= 264 MB) are rotated so the 256 MB
+Infinity Cache cannot serve them.
+
+Also reported (field "extra"): the other BASELINE configs -- Q4_0 / Q8_0 GEMV
+shapes, Q4_K batch 1/4/8/16, the prefill GEMM TFLOPS at M = 512 / 2048, and one
+full 32-layer Llama-3-8B-shaped decode step (225 GEMVs).
+
+  python bench.py [--steps K] [--warmup W] [--gpus 1] [--headline-only]
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path[:0] = [os.path.join(ROOT, "gretacore-v3_amd"), os.path.join(ROOT, "oracle")]
+
+HBM_PEAK_GBS = 8000.0          # MI355X HBM3E, GB/s
+MFMA_F16_PEAK_TFLOPS = 2500.0  # dense fp16/bf16
+MFMA_I8_PEAK_TOPS = 5000.0     # dense int8
+CACHE_DEFEAT_BYTES = 512 << 20  # > 256 MB Infinity Cache
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def gemv_bytes(fmt, n, k, batch):
+    import gq
+    return gq.gguf_bytes(fmt, n, k) + 4 * batch * (n + k)
+
+
+class GemvCase:
+    """Repacked weight copies + activations for one GEMV shape."""
+
+    def __init__(self, fmt, n, k, batch, wseed, xseed, dev, min_copies=8):
+        import torch
+
+        import gq
+        import oracle as O
+        self.fmt, self.n, self.k, self.batch = fmt, n, k, batch
+        self.w = O.gen_weights(fmt, n, k, seed=wseed)
+        self.x_host = O.gen_x(batch, k, seed=xseed)
+        packed = gq.repack(fmt, torch.from_numpy(self.w).to(dev), n, k)
+        nbytes = packed.numel()
+        ncopies = max(min_copies, -(-CACHE_DEFEAT_BYTES // nbytes))
+        self.copies = [packed] + [packed.clone() for _ in range(ncopies - 1)]
+        self.x = torch.from_numpy(self.x_host).to(dev)
+        self.y = torch.empty((batch, n), dtype=torch.float32, device=dev)
+        self.ws = gq.Workspace(dev, gq.gemv_workspace_bytes(fmt, k, batch))
+        self.bytes = gemv_bytes(fmt, n, k, batch)
+
+    def step(self, i):
+        import gq
+        gq.gemv(self.fmt, self.copies[i % len(self.copies)], self.x, self.n, self.k, y=self.y, workspace=self.ws)
+
+    def check(self):
+        import oracle as O
+        self.step(0)
+        ref = O.gemv(self.fmt, self.w, self.x_host, self.n, self.k)
+        return O.rel_l2(self.y.cpu().numpy(), ref)
+
+
+def time_steps(fn, steps, warmup):
+    import torch
+    for i in range(warmup):
+        fn(i)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for i in range(steps):
+        fn(i)
+    torch.cuda.synchronize()
+    return (time.perf_counter() - t0) / steps
+
+
+def kernel_time(launch, steps, warmup):
+    """Mean duration of one launch, from HIP events recorded around each launch
+    on the stream the kernel runs on (torch's current stream)."""
+    import torch
+    for i in range(warmup):
+        launch(i)
+    starts = [torch.cuda.Event(enable_timing=True) for _ in range(steps)]
+    ends = [torch.cuda.Event(enable_timing=True) for _ in range(steps)]
+    torch.cuda.synchronize()
+    for i in range(steps):
+        starts[i].record()
+        launch(i)
+        ends[i].record()
+    torch.cuda.synchronize()
+    ts = sorted(s.elapsed_time(e) for s, e in zip(starts, ends))
+    return sum(ts) / len(ts) / 1e3, ts[len(ts) // 2] / 1e3
+
+
+def bench_gemv(case, steps, warmup):
+    import gq
+    err = case.check()
+    t_job = time_steps(case.step, steps, warmup)
+    gq.gemv_prep(case.fmt, case.x, case.k, case.ws)
+    t_k, t_k_med = kernel_time(
+        lambda i: gq.gemv_prepped(case.fmt, case.copies[i % len(case.copies)], case.ws, case.y, case.n, case.k,
+                                  case.batch), steps, warmup)
+    wbytes = gq.gguf_bytes(case.fmt, case.n, case.k)
+    return {
+        "job_us": t_job * 1e6, "job_GBps": case.bytes / t_job / 1e9,
+        "kernel_us": t_k * 1e6, "kernel_median_us": t_k_med * 1e6,
+        "kernel_GBps": case.bytes / t_k / 1e9, "pct_peak_kernel": 100.0 * case.bytes / t_k / 1e9 / HBM_PEAK_GBS,
+        "weight_bytes": wbytes, "alg_bytes": case.bytes, "copies": len(case.copies), "rel_l2": err,
+    }
+
+
+def bench_gemm(fmt, m, n, k, steps, warmup, dev, out_dtype="f32"):
+    import torch
+
+    import gq
+    import oracle as O
+    w = O.gen_weights(fmt, n, k, seed=1004)
+    packed = gq.repack(fmt, torch.from_numpy(w).to(dev), n, k)
+    a = torch.randn(m, k, generator=torch.Generator().manual_seed(2004)).to(torch.bfloat16).to(dev)
+    odt = torch.float32 if out_dtype == "f32" else torch.bfloat16
+    c = torch.empty((m, n), dtype=odt, device=dev)
+    ws = gq.Workspace(dev, gq.gemm_workspace_bytes(fmt, m, k))
+    # parity on a row sample (fp64 oracle)
+    gq.gemm(fmt, packed, a, n, k, out_dtype=odt, c=c, workspace=ws)
+    rows = list(range(0, m, max(1, m // 32)))
+    ref = O.gemv(fmt, w, a[rows].float().cpu().numpy(), n, k)
+    err = O.rel_l2(c[rows].float().cpu().numpy(), ref)
+    flops = 2.0 * m * n * k
+    t_job = time_steps(lambda i: gq.gemm(fmt, packed, a, n, k, out_dtype=odt, c=c, workspace=ws),
+                       max(3, steps // 4), max(1, warmup // 4))
+    t_k, _ = kernel_time(lambda i: gq.gemm(fmt, packed, a, n, k, out_dtype=odt, c=c, workspace=ws),
+                         max(3, steps // 4), 1)
+    return {"job_us": t_job * 1e6, "job_TFLOPS": flops / t_job / 1e12, "call_us": t_k * 1e6,
+            "call_TFLOPS": flops / t_k / 1e12, "pct_peak_f16": 100.0 * flops / t_k / 1e12 / MFMA_F16_PEAK_TFLOPS,
+            "rel_l2": err}
+
+
+def bench_decode_step(dev, steps, warmup):
+    """Config 5: 32-layer Llama-3-8B-shaped decode step, Q4_K projections and a
+    Q8_0 lm_head, 7 GEMVs per layer + lm_head = 225 GEMVs (x prepared once per
+    distinct input: qkv share one, gate/up share one)."""
+    import torch
+
+    import gq
+    import oracle as O
+    Q4K, Q80 = O.Q4_K, O.Q8_0
+    shapes = {"q": (4096, 4096), "k": (1024, 4096), "v": (1024, 4096), "o": (4096, 4096),
+              "gate": (14336, 4096), "up": (14336, 4096), "down": (4096, 14336)}
+    base = {}
+    for i, (name, (n, k)) in enumerate(shapes.items()):
+        w = O.gen_weights(Q4K, n, k, seed=1005 + i)
+        base[name] = gq.repack(Q4K, torch.from_numpy(w).to(dev), n, k)
+    layers = [{name: base[name].clone() for name in shapes} for _ in range(32)]
+    del base
+    lm = O.gen_weights(Q80, 128256, 4096, seed=1015)
+    lm_packed = gq.repack(Q80, torch.from_numpy(lm).to(dev), 128256, 4096)
+    del lm
+    torch.cuda.synchronize()
+    wbytes = 32 * sum(gq.gguf_bytes(Q4K, n, k) for n, k in shapes.values()) + gq.gguf_bytes(Q80, 128256, 4096)
+    xs = {k: torch.from_numpy(O.gen_x(1, k, seed=2005 + k)).to(dev) for k in (4096, 14336)}
+    ys = {n: torch.empty((1, n), dtype=torch.float32, device=dev) for n in (1024, 4096, 14336, 128256)}
+    ws = gq.Workspace(dev, gq.gemv_workspace_bytes(Q4K, 14336, 1) + gq.gemv_workspace_bytes(Q80, 4096, 1))
+
+    def one_step(_i):
+        for L in layers:
+            gq.gemv_prep(Q4K, xs[4096], 4096, ws)
+            for name in ("q", "k", "v"):
+                n, k = shapes[name]
+                gq.gemv_prepped(Q4K, L[name], ws, ys[n], n, k, 1)
+            gq.gemv_prep(Q4K, xs[4096], 4096, ws)
+            gq.gemv_prepped(Q4K, L["o"], ws, ys[4096], 4096, 4096, 1)
+            gq.gemv_prep(Q4K, xs[4096], 4096, ws)
+            for name in ("gate", "up"):
+                gq.gemv_prepped(Q4K, L[name], ws, ys[14336], 14336, 4096, 1)
+            gq.gemv_prep(Q4K, xs[14336], 14336, ws)
+            gq.gemv_prepped(Q4K, L["down"], ws, ys[4096], 4096, 14336, 1)
+        gq.gemv_prep(Q80, xs[4096], 4096, ws)
+        gq.gemv_prepped(Q80, lm_packed, ws, ys[128256], 128256, 4096, 1)
+
+    t_eager = time_steps(one_step, max(3, steps // 10), 2)
+    # the same step captured once into a HIP graph and replayed
+    g = torch.cuda.CUDAGraph()
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        one_step(0)
+        torch.cuda.synchronize()
+        with torch.cuda.graph(g, stream=s):
+            one_step(0)
+    torch.cuda.current_stream().wait_stream(s)
+    t_graph = time_steps(lambda i: g.replay(), max(5, steps // 5), 2)
+    out = {"weight_bytes": wbytes, "eager_ms": t_eager * 1e3, "graph_ms": t_graph * 1e3,
+           "graph_GBps": wbytes / t_graph / 1e9, "graph_pct_peak": 100.0 * wbytes / t_graph / 1e9 / HBM_PEAK_GBS,
+           "tokens_per_s_projections_only": 1.0 / t_graph}
+    del layers, lm_packed, g
+    torch.cuda.empty_cache()
+    return out
+
+
+def cpu_baseline(target_s=12.0):
+    """The oracle (C restatement of the reference CPU semantics: dequant then
+    fp64-accumulated dot, OpenMP over rows) on the host cores, on the headline
+    workload, repeated for ~target_s seconds."""
+    import oracle as O
+    threads = int(os.environ.get("OMP_NUM_THREADS", "0") or 0) or (os.cpu_count() or 1)
+    n, k = 14336, 4096
+    w = O.gen_weights(O.Q4_0, n, k, seed=1002)
+    x = O.gen_x(1, k, seed=2002)
+    O.gemv(O.Q4_0, w, x, n, k, threads=threads)  # warm
+    reps, t0 = 0, time.perf_counter()
+    while True:
+        O.gemv(O.Q4_0, w, x, n, k, threads=threads)
+        reps += 1
+        el = time.perf_counter() - t0
+        if el >= target_s:
+            break
+    per = el / reps
+    return {"value": gemv_bytes(O.Q4_0, n, k, 1) / per / 1e9, "unit": "GB/s", "cores": threads, "kind": "port",
+            "sample": f"oracle gqo_gemv Q4_0 {n}x{k} batch 1, {reps} reps in {el:.1f} s ({per * 1e3:.2f} ms/GEMV)"}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--headline-only", action="store_true", help="only the headline GEMV (for profiling)")
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-decode-step", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
+        print("bench.py measures one GPU only: this build has no multi-GPU path (each GPU box has one GPU); "
+              "run with --gpus 1", file=sys.stderr)
+        sys.exit(2)
+    import torch
+
+    import gq
+    import oracle as O
+    gq.load()
+    dev = torch.device("cuda:0")
+    steps, warmup = args.steps, args.warmup
+
+    log("[bench] headline: Q4_0 GEMV 14336x4096 batch 1")
+    head = GemvCase(O.Q4_0, 14336, 4096, 1, wseed=1002, xseed=2002, dev=dev)
+    h = bench_gemv(head, steps, warmup)
+    log(f"[bench] headline {h}")
+    extra = {}
+    if not args.headline_only:
+        gemv_cfgs = [("q8_0_4096x4096_b1", O.Q8_0, 4096, 4096, 1, 1001),
+                     ("q4_0_4096x4096_b1", O.Q4_0, 4096, 4096, 1, 1002),
+                     ("q4_0_4096x14336_b1", O.Q4_0, 4096, 14336, 1, 1002)]
+        gemv_cfgs += [(f"q4_k_14336x4096_b{b}", O.Q4_K, 14336, 4096, b, 1003) for b in (1, 4, 8, 16)]
+        for name, fmt, n, k, b, seed in gemv_cfgs:
+            log(f"[bench] {name}")
+            c = GemvCase(fmt, n, k, b, wseed=seed, xseed=seed + 1000, dev=dev)
+            extra[name] = bench_gemv(c, max(20, steps // 2), warmup)
+            del c
+            torch.cuda.empty_cache()
+        for fmt, fname in ((O.Q4_0, "q4_0"), (O.Q8_0, "q8_0"), (O.Q4_K, "q4_k")):
+            for m in (512, 2048):
+                for n in (4096, 14336):
+                    name = f"gemm_{fname}_m{m}_{n}x4096"
+                    log(f"[bench] {name}")
+                    extra[name] = bench_gemm(fmt, m, n, 4096, steps, warmup, dev)
+                    torch.cuda.empty_cache()
+        if not args.no_decode_step:
+            log("[bench] decode step (config 5)")
+            extra["decode_step_llama3_8b_q4k"] = bench_decode_step(dev, steps, warmup)
+    cpu = None
+    if not args.no_cpu:
+        log("[bench] cpu baseline")
+        cpu = cpu_baseline()
+    line = {
+        "metric": "Q4 decode GEMV HBM GB/s (% peak) @14336x4096; prefill quant-GEMM TFLOPS",
+        "value": round(h["job_GBps"], 1),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": steps,
+        "warmup": warmup,
+        "ms_per_step": round(h["job_us"] / 1e3, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "q4_0 weights, f16 MFMA on exact operands, f32 accumulate",
+        "data": "synthetic (seeded GGUF Q4_0 blocks, x ~ N(0,1))",
+        "config": {"workload": "Q4_0 decode GEMV 14336x4096 batch 1 (BASELINE configs[1]), prep + GEMV kernel",
+                   "N": 14336, "K": 4096, "batch": 1, "weight_copies_rotated": h["copies"],
+                   "alg_bytes_per_step": h["alg_bytes"]},
+        "pct_peak": round(100.0 * h["job_GBps"] / HBM_PEAK_GBS, 2),
+        "rel_l2_vs_oracle": h["rel_l2"],
+        "roofline": {"bound": "hbm", "achieved": round(h["kernel_GBps"], 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(h["kernel_GBps"] / HBM_PEAK_GBS, 4), "traffic": None,
+                     "kernel": "k_gemv_t16<Q4_0,1,4>", "kernel_us": round(h["kernel_us"], 3)},
+        "cpu_baseline": cpu,
+        "extra": extra,
+    }
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

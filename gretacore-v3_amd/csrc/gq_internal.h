@@ -35,14 +35,20 @@ static inline int gq_check_shape(int fmt, size_t N, size_t K) {
 static inline size_t gq_align256(size_t v) { return (v + 255) & ~(size_t)255; }
 // padded K of the T16 layout
 static inline size_t gq_kpad(int fmt, size_t K) { return gq_chunks(fmt, K) * gq_chunk_k(fmt); }
-// GEMV workspace: xq fp16 [2B][Kp] then (Q4_K) sq uint32 [B][Kp/32]
+// GEMV workspace: xq fp16 [2B][Kp], sf fp32 [B][Kp/32] (block sums of x),
+// then (Q4_K) sq fp16 (hi, lo) pairs of the same sums [B][Kp/32]
 static inline size_t gq_xq_bytes(int fmt, size_t K, int B) {
   return gq_align256((size_t)2 * B * gq_kpad(fmt, K) * 2);
+}
+static inline size_t gq_sf_bytes(int fmt, size_t K, int B) {
+  return gq_align256((size_t)B * (gq_kpad(fmt, K) / 32) * 4);
 }
 static inline size_t gq_sq_bytes(int fmt, size_t K, int B) {
   return gq_fmt_is_q4k(fmt) ? gq_align256((size_t)B * (gq_kpad(fmt, K) / 32) * 4) : 0;
 }
 
+// Zero-fills n floats with a kernel (no memset node, so it is safe to capture).
+int gq_fill_zero(float *p, size_t n, hipStream_t s);
 int gq_launch_prep_x(int fmt, const float *x, void *ws, int B, int K, hipStream_t s);
 int gq_launch_prep_a(const void *a, int a_dtype, _Float16 *out, int M, int K, int Kp, hipStream_t s);
 

@@ -201,13 +201,13 @@ k_repack_q4_k(const uint8_t *__restrict__ src, uint8_t *__restrict__ dst, int N,
 // ---------------------------------------------------------------------------
 // Activation preparation for the GEMV (decode) path.  x f32 [B][K] ->
 //   xq  fp16 [2B][Kp]: row 2b = hi = fp16(x), row 2b+1 = lo = fp16(x - hi)
-//   sq  (Q4_K only) uint32 [B][Kp/32]: fp16 pair (hi, lo) of the fp32 sum of
-//       each 32-element sub-block of x.
+//   sf  f32 [B][Kp/32]: the fp32 sum of each 32-element block of x
+//   sq  (Q4_K only) uint32 [B][Kp/32]: fp16 pair (hi, lo) of the same sums.
 // Elements k >= K are written as zeros.  One thread per 32 elements.
 // ---------------------------------------------------------------------------
 __global__ void __launch_bounds__(256)
-k_prep_x(const float *__restrict__ x, _Float16 *__restrict__ xq, uint32_t *__restrict__ sq,
-         int B, int K, int Kp) {
+k_prep_x(const float *__restrict__ x, _Float16 *__restrict__ xq, float *__restrict__ sf,
+         uint32_t *__restrict__ sq, int B, int K, int Kp) {
   int nsub = Kp / 32;
   int i = blockIdx.x * 256 + threadIdx.x;
   if (i >= B * nsub) return;
@@ -242,6 +242,7 @@ k_prep_x(const float *__restrict__ x, _Float16 *__restrict__ xq, uint32_t *__res
     ph[q] = hi[q];
     pl[q] = lo[q];
   }
+  sf[(size_t)b * nsub + j] = s;
   if (sq) {
     _Float16 sh = (_Float16)s;
     _Float16 sl = (_Float16)(s - (float)sh);
@@ -388,9 +389,24 @@ extern "C" int gq_repack(int fmt, const void *gguf, size_t N, size_t K, void *pa
 int gq_launch_prep_x(int fmt, const float *x, void *ws, int B, int K, hipStream_t s) {
   int Kp = (int)(gq_chunks(fmt, K) * gq_chunk_k(fmt));
   _Float16 *xq = (_Float16 *)ws;
-  uint32_t *sq = gq_fmt_is_q4k(fmt) ? (uint32_t *)((uint8_t *)ws + gq_xq_bytes(fmt, K, B)) : nullptr;
+  float *sf = (float *)((uint8_t *)ws + gq_xq_bytes(fmt, K, B));
+  uint32_t *sq = gq_fmt_is_q4k(fmt) ? (uint32_t *)((uint8_t *)ws + gq_xq_bytes(fmt, K, B) + gq_sf_bytes(fmt, K, B))
+                                    : nullptr;
   int n = B * (Kp / 32);
-  hipLaunchKernelGGL(k_prep_x, dim3(blocks_for(n)), dim3(256), 0, s, x, xq, sq, B, K, Kp);
+  hipLaunchKernelGGL(k_prep_x, dim3(blocks_for(n)), dim3(256), 0, s, x, xq, sf, sq, B, K, Kp);
+  return gq_last_launch();
+}
+
+namespace {
+__global__ void __launch_bounds__(256) k_fill_zero(float *p, size_t n) {
+  size_t i = (size_t)blockIdx.x * 256 + threadIdx.x;
+  if (i < n) p[i] = 0.0f;
+}
+}  // namespace
+
+int gq_fill_zero(float *p, size_t n, hipStream_t s) {
+  if (n == 0) return GQ_OK;
+  hipLaunchKernelGGL(k_fill_zero, dim3(blocks_for(n)), dim3(256), 0, s, p, n);
   return gq_last_launch();
 }
 

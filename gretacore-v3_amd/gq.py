@@ -272,3 +272,19 @@ def launch_int4_wt(a, b, scales, head_scales, m, n, k, group_size=32, head_dim=0
         _stream(stream), _ptr(a), _ptr(b), _ptr(c), _ptr(scales), _ptr(head_scales), m, n, k, k, n, n, group_size,
         head_dim, int(a.dtype == torch.float16), int(force_gemv)), "gq_launch_gemm_mfma_int4_wt_fp32_acc32")
     return c
+
+
+def gemv_prep(fmt: int, x, k: int, workspace: Workspace, stream=None):
+    """Prepare x [batch][k] once into `workspace` for several gemv_prepped calls."""
+    _require_device(x)
+    batch = 1 if x.dim() == 1 else x.shape[0]
+    buf = workspace.ensure(gemv_workspace_bytes(fmt, k, batch))
+    check(load().gq_gemv_prep(fmt, _ptr(x), k, batch, _ptr(buf), buf.numel(), _stream(stream)), "gq_gemv_prep")
+    return batch
+
+
+def gemv_prepped(fmt: int, d_packed, workspace: Workspace, y, n: int, k: int, batch: int, stream=None):
+    _require_device(d_packed, y)
+    check(load().gq_gemv_prepped(fmt, _ptr(d_packed), _ptr(workspace.buf), _ptr(y), n, k, batch, _stream(stream)),
+          "gq_gemv_prepped")
+    return y
