@@ -70,6 +70,7 @@ class GemvCase:
 
 
 def time_steps(fn, steps, warmup):
+    """Per-step seconds of `fn` launched eagerly (host-side launch loop)."""
     import torch
     for i in range(warmup):
         fn(i)
@@ -81,38 +82,46 @@ def time_steps(fn, steps, warmup):
     return (time.perf_counter() - t0) / steps
 
 
-def kernel_time(launch, steps, warmup):
-    """Mean duration of one launch, from HIP events recorded around each launch
-    on the stream the kernel runs on (torch's current stream)."""
+def graph_steps(fn, steps, warmup):
+    """Per-step seconds of `steps` consecutive calls of `fn` captured into one
+    HIP graph and replayed: device time with no per-launch host overhead.
+    HIP events bracket the replay on the stream the kernels run on."""
     import torch
     for i in range(warmup):
-        launch(i)
-    starts = [torch.cuda.Event(enable_timing=True) for _ in range(steps)]
-    ends = [torch.cuda.Event(enable_timing=True) for _ in range(steps)]
+        fn(i)
     torch.cuda.synchronize()
-    for i in range(steps):
-        starts[i].record()
-        launch(i)
-        ends[i].record()
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(s):
+        with torch.cuda.graph(g, stream=s):
+            for i in range(steps):
+                fn(i)
+        g.replay()  # first replay uploads the graph (untimed)
+        s.synchronize()
+        e0 = torch.cuda.Event(enable_timing=True)
+        e1 = torch.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize()
+        e0.record(s)
+        g.replay()
+        e1.record(s)
+        e1.synchronize()
     torch.cuda.synchronize()
-    ts = sorted(s.elapsed_time(e) for s, e in zip(starts, ends))
-    return sum(ts) / len(ts) / 1e3, ts[len(ts) // 2] / 1e3
+    per = e0.elapsed_time(e1) / 1e3 / steps
+    del g
+    return per
 
 
 def bench_gemv(case, steps, warmup):
-    import gq
     err = case.check()
-    t_job = time_steps(case.step, steps, warmup)
-    gq.gemv_prep(case.fmt, case.x, case.k, case.ws)
-    t_k, t_k_med = kernel_time(
-        lambda i: gq.gemv_prepped(case.fmt, case.copies[i % len(case.copies)], case.ws, case.y, case.n, case.k,
-                                  case.batch), steps, warmup)
-    wbytes = gq.gguf_bytes(case.fmt, case.n, case.k)
+    t_graph = graph_steps(case.step, steps, warmup)
+    t_eager = time_steps(case.step, steps, warmup)
     return {
-        "job_us": t_job * 1e6, "job_GBps": case.bytes / t_job / 1e9,
-        "kernel_us": t_k * 1e6, "kernel_median_us": t_k_med * 1e6,
-        "kernel_GBps": case.bytes / t_k / 1e9, "pct_peak_kernel": 100.0 * case.bytes / t_k / 1e9 / HBM_PEAK_GBS,
-        "weight_bytes": wbytes, "alg_bytes": case.bytes, "copies": len(case.copies), "rel_l2": err,
+        "step_us": t_graph * 1e6, "GBps": case.bytes / t_graph / 1e9,
+        "pct_peak": 100.0 * case.bytes / t_graph / 1e9 / HBM_PEAK_GBS,
+        "eager_step_us": t_eager * 1e6,
+        "weight_bytes": case.bytes - 4 * case.batch * (case.n + case.k), "alg_bytes": case.bytes,
+        "copies": len(case.copies), "rel_l2": err,
     }
 
 
@@ -133,19 +142,15 @@ def bench_gemm(fmt, m, n, k, steps, warmup, dev, out_dtype="f32"):
     ref = O.gemv(fmt, w, a[rows].float().cpu().numpy(), n, k)
     err = O.rel_l2(c[rows].float().cpu().numpy(), ref)
     flops = 2.0 * m * n * k
-    t_job = time_steps(lambda i: gq.gemm(fmt, packed, a, n, k, out_dtype=odt, c=c, workspace=ws),
-                       max(3, steps // 4), max(1, warmup // 4))
-    t_k, _ = kernel_time(lambda i: gq.gemm(fmt, packed, a, n, k, out_dtype=odt, c=c, workspace=ws),
-                         max(3, steps // 4), 1)
-    return {"job_us": t_job * 1e6, "job_TFLOPS": flops / t_job / 1e12, "call_us": t_k * 1e6,
-            "call_TFLOPS": flops / t_k / 1e12, "pct_peak_f16": 100.0 * flops / t_k / 1e12 / MFMA_F16_PEAK_TFLOPS,
+    run = lambda i: gq.gemm(fmt, packed, a, n, k, out_dtype=odt, c=c, workspace=ws)
+    t = graph_steps(run, max(4, steps // 8), 2)
+    return {"step_us": t * 1e6, "TFLOPS": flops / t / 1e12, "pct_peak_f16": 100.0 * flops / t / 1e12 / MFMA_F16_PEAK_TFLOPS,
             "rel_l2": err}
 
 
 def bench_decode_step(dev, steps, warmup):
     """Config 5: 32-layer Llama-3-8B-shaped decode step, Q4_K projections and a
-    Q8_0 lm_head, 7 GEMVs per layer + lm_head = 225 GEMVs (x prepared once per
-    distinct input: qkv share one, gate/up share one)."""
+    Q8_0 lm_head: 7 GEMVs per layer + lm_head = 225 single-kernel GEMVs."""
     import torch
 
     import gq
@@ -166,40 +171,19 @@ def bench_decode_step(dev, steps, warmup):
     wbytes = 32 * sum(gq.gguf_bytes(Q4K, n, k) for n, k in shapes.values()) + gq.gguf_bytes(Q80, 128256, 4096)
     xs = {k: torch.from_numpy(O.gen_x(1, k, seed=2005 + k)).to(dev) for k in (4096, 14336)}
     ys = {n: torch.empty((1, n), dtype=torch.float32, device=dev) for n in (1024, 4096, 14336, 128256)}
-    ws = gq.Workspace(dev, gq.gemv_workspace_bytes(Q4K, 14336, 1) + gq.gemv_workspace_bytes(Q80, 4096, 1))
 
     def one_step(_i):
         for L in layers:
-            gq.gemv_prep(Q4K, xs[4096], 4096, ws)
-            for name in ("q", "k", "v"):
-                n, k = shapes[name]
-                gq.gemv_prepped(Q4K, L[name], ws, ys[n], n, k, 1)
-            gq.gemv_prep(Q4K, xs[4096], 4096, ws)
-            gq.gemv_prepped(Q4K, L["o"], ws, ys[4096], 4096, 4096, 1)
-            gq.gemv_prep(Q4K, xs[4096], 4096, ws)
-            for name in ("gate", "up"):
-                gq.gemv_prepped(Q4K, L[name], ws, ys[14336], 14336, 4096, 1)
-            gq.gemv_prep(Q4K, xs[14336], 14336, ws)
-            gq.gemv_prepped(Q4K, L["down"], ws, ys[4096], 4096, 14336, 1)
-        gq.gemv_prep(Q80, xs[4096], 4096, ws)
-        gq.gemv_prepped(Q80, lm_packed, ws, ys[128256], 128256, 4096, 1)
+            for name, (n, k) in shapes.items():
+                gq.gemv(Q4K, L[name], xs[k], n, k, y=ys[n])
+        gq.gemv(Q80, lm_packed, xs[4096], 128256, 4096, y=ys[128256])
 
-    t_eager = time_steps(one_step, max(3, steps // 10), 2)
-    # the same step captured once into a HIP graph and replayed
-    g = torch.cuda.CUDAGraph()
-    s = torch.cuda.Stream()
-    s.wait_stream(torch.cuda.current_stream())
-    with torch.cuda.stream(s):
-        one_step(0)
-        torch.cuda.synchronize()
-        with torch.cuda.graph(g, stream=s):
-            one_step(0)
-    torch.cuda.current_stream().wait_stream(s)
-    t_graph = time_steps(lambda i: g.replay(), max(5, steps // 5), 2)
-    out = {"weight_bytes": wbytes, "eager_ms": t_eager * 1e3, "graph_ms": t_graph * 1e3,
+    t_eager = time_steps(one_step, 3, 1)
+    t_graph = graph_steps(one_step, 4, 1)
+    out = {"weight_bytes": wbytes, "gemv_launches": 225, "eager_ms": t_eager * 1e3, "graph_ms": t_graph * 1e3,
            "graph_GBps": wbytes / t_graph / 1e9, "graph_pct_peak": 100.0 * wbytes / t_graph / 1e9 / HBM_PEAK_GBS,
-           "tokens_per_s_projections_only": 1.0 / t_graph}
-    del layers, lm_packed, g
+           "projection_steps_per_s": 1.0 / t_graph}
+    del layers, lm_packed
     torch.cuda.empty_cache()
     return out
 
@@ -254,6 +238,7 @@ def main():
     extra = {}
     if not args.headline_only:
         gemv_cfgs = [("q8_0_4096x4096_b1", O.Q8_0, 4096, 4096, 1, 1001),
+                     ("q8_0_lm_head_128256x4096_b1", O.Q8_0, 128256, 4096, 1, 1005),
                      ("q4_0_4096x4096_b1", O.Q4_0, 4096, 4096, 1, 1002),
                      ("q4_0_4096x14336_b1", O.Q4_0, 4096, 14336, 1, 1002)]
         gemv_cfgs += [(f"q4_k_14336x4096_b{b}", O.Q4_K, 14336, 4096, b, 1003) for b in (1, 4, 8, 16)]
@@ -277,27 +262,32 @@ def main():
     if not args.no_cpu:
         log("[bench] cpu baseline")
         cpu = cpu_baseline()
+    R, ks, cpw = gq.gemv_plan(O.Q4_0, 14336, 4096, 1)
     line = {
         "metric": "Q4 decode GEMV HBM GB/s (% peak) @14336x4096; prefill quant-GEMM TFLOPS",
-        "value": round(h["job_GBps"], 1),
+        "value": round(h["GBps"], 1),
         "unit": "GB/s",
         "n_gpus": 1,
         "steps": steps,
         "warmup": warmup,
-        "ms_per_step": round(h["job_us"] / 1e3, 5),
+        "ms_per_step": round(h["step_us"] / 1e3, 6),
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "q4_0 weights, f16 MFMA on exact operands, f32 accumulate",
+        "dtype": "q4_0 weights x int8 2-limb activations, i8 MFMA, f32 accumulate",
         "data": "synthetic (seeded GGUF Q4_0 blocks, x ~ N(0,1))",
-        "config": {"workload": "Q4_0 decode GEMV 14336x4096 batch 1 (BASELINE configs[1]), prep + GEMV kernel",
+        "config": {"workload": "Q4_0 decode GEMV 14336x4096 batch 1 (BASELINE configs[1]); one step = one "
+                               "gq_gemv call (a single kernel) on one of the rotated weight copies; K steps "
+                               "replayed from one HIP graph",
                    "N": 14336, "K": 4096, "batch": 1, "weight_copies_rotated": h["copies"],
                    "alg_bytes_per_step": h["alg_bytes"]},
-        "pct_peak": round(100.0 * h["job_GBps"] / HBM_PEAK_GBS, 2),
+        "pct_peak": round(h["pct_peak"], 2),
         "rel_l2_vs_oracle": h["rel_l2"],
-        "roofline": {"bound": "hbm", "achieved": round(h["kernel_GBps"], 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(h["kernel_GBps"] / HBM_PEAK_GBS, 4), "traffic": None,
-                     "kernel": "k_gemv_t16<Q4_0,1,4>", "kernel_us": round(h["kernel_us"], 3)},
+        "roofline": {"bound": "hbm", "achieved": round(h["GBps"], 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(h["GBps"] / HBM_PEAK_GBS, 4), "traffic": None,
+                     "kernel": f"k_gemv_q<Q4_0, NB=1, R={R}, KSPLIT={ks}>",
+                     "kernel_us": round(h["step_us"], 3),
+                     "timing": "HIP events around the replay of K back-to-back launches; includes dispatch gaps"},
         "cpu_baseline": cpu,
         "extra": extra,
     }

@@ -84,15 +84,16 @@ int gq_repack_host(int fmt, const void *gguf, size_t N, size_t K, void *packed) 
   if (N == 0 || K == 0) return GQ_OK;
   const uint8_t *src = (const uint8_t *)gguf;
   uint8_t *dst = (uint8_t *)packed;
-  const size_t Np = gq_tiles(N) * 16, C = gq_chunks(fmt, K), sc = gq_sc_plane_offset(fmt, N, K);
+  const size_t C = gq_chunks(fmt, K), sc = gq_sc_plane_offset(fmt, N, K);
   memset(dst, 0, gq_packed_bytes(fmt, N, K));
   if (fmt == GQ_FMT_Q4_0) {
     const size_t nb = K / 32;
     for (size_t n = 0; n < N; ++n)
       for (size_t b = 0; b < nb; ++b) {
-        uint32_t words[4], d16;
-        gq_q4_0_canon(src + (n * nb + b) * 18, words, &d16);
-        for (int w8 = 0; w8 < 4; ++w8) memcpy(dst + gq_q4_0_word_off(n, b, w8, C), &words[w8], 4);
+        uint64_t grp[2];
+        uint32_t d16;
+        gq_q4_0_groups(src + (n * nb + b) * 18, grp, &d16);
+        for (int eh = 0; eh < 2; ++eh) memcpy(dst + gq_q4_0_grp_off(n, b, eh, C), &grp[eh], 8);
         uint16_t d = (uint16_t)d16;
         memcpy(dst + sc + gq_q4_0_d_off(n, b, C), &d, 2);
       }
@@ -101,7 +102,7 @@ int gq_repack_host(int fmt, const void *gguf, size_t N, size_t K, void *packed) 
     for (size_t n = 0; n < N; ++n)
       for (size_t b = 0; b < nb; ++b) {
         const uint8_t *blk = src + (n * nb + b) * 34;
-        for (int g = 0; g < 4; ++g) memcpy(dst + gq_q8_0_byte_off(n, b, 8 * g, C), blk + 2 + 8 * g, 8);
+        for (int eh = 0; eh < 2; ++eh) memcpy(dst + gq_q8_0_half_off(n, b, eh, C), blk + 2 + 16 * eh, 16);
         memcpy(dst + sc + gq_q4_0_d_off(n, b, C), blk, 2);
       }
   } else {
@@ -109,14 +110,14 @@ int gq_repack_host(int fmt, const void *gguf, size_t N, size_t K, void *packed) 
     const size_t S = C;
     for (size_t n = 0; n < N; ++n)
       for (size_t s = 0; s < S; ++s) {
-        uint32_t words[8][4], meta[4];
-        gq_q4k_canon(ggml, src + (n * S + s) * 144, words, meta);
+        uint64_t grp[16];
+        uint32_t meta[4];
+        gq_q4k_groups(ggml, src + (n * S + s) * 144, grp, meta);
         for (int j = 0; j < 8; ++j)
-          for (int w8 = 0; w8 < 4; ++w8) memcpy(dst + gq_q4k_word_off(n, s, j, w8, S), &words[j][w8], 4);
+          for (int eh = 0; eh < 2; ++eh) memcpy(dst + gq_q4k_grp_off(n, s, j, eh, S), &grp[2 * j + eh], 8);
         memcpy(dst + sc + gq_q4k_meta_off(n, s, S), meta, 16);
       }
   }
-  (void)Np;
   return GQ_OK;
 }
 
@@ -131,18 +132,18 @@ int gq_unpack_host(int fmt, const void *packed, size_t N, size_t K, void *gguf) 
     const size_t nb = K / 32;
     for (size_t n = 0; n < N; ++n)
       for (size_t b = 0; b < nb; ++b) {
-        uint32_t words[4];
+        uint64_t grp[2];
         uint16_t d = 0;
-        for (int w8 = 0; w8 < 4; ++w8) memcpy(&words[w8], src + gq_q4_0_word_off(n, b, w8, C), 4);
+        for (int eh = 0; eh < 2; ++eh) memcpy(&grp[eh], src + gq_q4_0_grp_off(n, b, eh, C), 8);
         memcpy(&d, src + sc + gq_q4_0_d_off(n, b, C), 2);
-        gq_q4_0_uncanon(words, d, dst + (n * nb + b) * 18);
+        gq_q4_0_from_groups(grp, d, dst + (n * nb + b) * 18);
       }
   } else if (fmt == GQ_FMT_Q8_0) {
     const size_t nb = K / 32;
     for (size_t n = 0; n < N; ++n)
       for (size_t b = 0; b < nb; ++b) {
         uint8_t *blk = dst + (n * nb + b) * 34;
-        for (int g = 0; g < 4; ++g) memcpy(blk + 2 + 8 * g, src + gq_q8_0_byte_off(n, b, 8 * g, C), 8);
+        for (int eh = 0; eh < 2; ++eh) memcpy(blk + 2 + 16 * eh, src + gq_q8_0_half_off(n, b, eh, C), 16);
         memcpy(blk, src + sc + gq_q4_0_d_off(n, b, C), 2);
       }
   } else {
@@ -150,11 +151,12 @@ int gq_unpack_host(int fmt, const void *packed, size_t N, size_t K, void *gguf) 
     const size_t S = C;
     for (size_t n = 0; n < N; ++n)
       for (size_t s = 0; s < S; ++s) {
-        uint32_t words[8][4], meta[4];
+        uint64_t grp[16];
+        uint32_t meta[4];
         for (int j = 0; j < 8; ++j)
-          for (int w8 = 0; w8 < 4; ++w8) memcpy(&words[j][w8], src + gq_q4k_word_off(n, s, j, w8, S), 4);
+          for (int eh = 0; eh < 2; ++eh) memcpy(&grp[2 * j + eh], src + gq_q4k_grp_off(n, s, j, eh, S), 8);
         memcpy(meta, src + sc + gq_q4k_meta_off(n, s, S), 16);
-        gq_q4k_uncanon(ggml, words, meta, dst + (n * S + s) * 144);
+        gq_q4k_from_groups(ggml, grp, meta, dst + (n * S + s) * 144);
       }
   }
   return GQ_OK;

@@ -92,95 +92,128 @@ GQ_DEV gq_half2 h2_of_bits16(uint32_t b16) {
   return gq_bits_h2(v);
 }
 
+// 4 byte values u (0..255) -> 2 fp16 pairs holding (1024 + u)
+GQ_DEV void bytes_to_magic(uint32_t u, gq_half2 &lo, gq_half2 &hi) {
+  lo = gq_bits_h2(__builtin_amdgcn_perm(0x64646464u, u, 0x04010400u));
+  hi = gq_bits_h2(__builtin_amdgcn_perm(0x64646464u, u, 0x04030402u));
+}
+
+// T16 code group (8 bytes) -> 16 fp16 values (c - bias) * scale, slot order,
+// computed as one rounding of the exact product.
+GQ_DEV void group_to_h16(uint32_t w0, uint32_t w1, gq_half2 off, gq_half2 scale, gq_half8 &o0, gq_half8 &o1) {
+  const uint32_t regs[4] = {w0 & 0x0F0F0F0Fu, (w0 >> 4) & 0x0F0F0F0Fu, w1 & 0x0F0F0F0Fu, (w1 >> 4) & 0x0F0F0F0Fu};
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    gq_half2 lo, hi;
+    bytes_to_magic(regs[q], lo, hi);
+    lo = (lo + off) * scale;
+    hi = (hi + off) * scale;
+    gq_half8 &o = (q < 2) ? o0 : o1;
+    const int b = 4 * (q & 1);
+    o[b] = lo[0];
+    o[b + 1] = lo[1];
+    o[b + 2] = hi[0];
+    o[b + 3] = hi[1];
+  }
+}
+
 // ---- weight tile: registers -> dequantized fp16 in LDS ---------------------
+// Thread slot (rt, lane = 16g + r): row 16rt + r, and for MFMA step m the
+// elements 16(g&1)..+15 of block 2m + (g>>1) of the 128-k step.
 template <int FMT>
 GQ_DEV void store_b(const BRegs<FMT> &br, int step, int tid, _Float16 *Bs) {
+  (void)step;
   if constexpr (FMT == GQ_FMT_Q4_0) {
     const gq_half2 off = {(_Float16)-1032.0f, (_Float16)-1032.0f};
 #pragma unroll
     for (int i = 0; i < 2; ++i) {
       int slot = tid + 256 * i, rt = slot >> 6, lane = slot & 63, g = lane >> 4, r = lane & 15;
-      _Float16 *dst = Bs + (16 * rt + r) * LDS_STRIDE + 8 * g;
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        uint32_t dbits = (j & 1) ? (br.d[i][j >> 1] >> 16) : br.d[i][j >> 1];
-        gq_half2 d2 = h2_of_bits16(dbits);
-        gq_half8 o;
-#pragma unroll
-        for (int s = 0; s < 4; ++s) {
-          uint32_t tq = ((br.q[i][j] >> (4 * s)) & 0x000F000Fu) | 0x64006400u;
-          gq_half2 hq = (gq_bits_h2(tq) + off) * d2;
-          o[2 * s] = hq[0];
-          o[2 * s + 1] = hq[1];
-        }
-        *reinterpret_cast<gq_half8 *>(dst + 32 * j) = o;
+      for (int m = 0; m < 2; ++m) {
+        const int j = 2 * m + (g >> 1);
+        uint32_t dbits = (j >> 1) ? (br.d[i][j & 1] >> 16) : br.d[i][j & 1];
+        gq_half8 o0, o1;
+        group_to_h16(br.q[i][2 * m], br.q[i][2 * m + 1], off, h2_of_bits16(dbits), o0, o1);
+        _Float16 *dst = Bs + (16 * rt + r) * LDS_STRIDE + 32 * j + 16 * (g & 1);
+        *reinterpret_cast<gq_half8 *>(dst) = o0;
+        *reinterpret_cast<gq_half8 *>(dst + 8) = o1;
       }
     }
   } else if constexpr (FMT == GQ_FMT_Q8_0) {
+    const gq_half2 off = {(_Float16)-1152.0f, (_Float16)-1152.0f};
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      int slot = tid + 256 * i, rt = slot >> 7, part = (slot >> 6) & 1, lane = slot & 63;
+      int slot = tid + 256 * i, rt = slot >> 7, m = (slot >> 6) & 1, lane = slot & 63;
       int g = lane >> 4, r = lane & 15;
-      _Float16 *dst = Bs + (16 * rt + r) * LDS_STRIDE + 8 * g;
+      const int j = 2 * m + (g >> 1);
+      uint32_t dbits = (j >> 1) ? (br.d[i][j & 1] >> 16) : br.d[i][j & 1];
+      const gq_half2 d2 = h2_of_bits16(dbits);
+      _Float16 *dst = Bs + (16 * rt + r) * LDS_STRIDE + 32 * j + 16 * (g & 1);
 #pragma unroll
-      for (int hh = 0; hh < 2; ++hh) {
-        int j = 2 * part + hh;
-        uint32_t dbits = (j & 1) ? (br.d[i][j >> 1] >> 16) : br.d[i][j >> 1];
-        gq_half2 d2 = h2_of_bits16(dbits);
+      for (int q2 = 0; q2 < 2; ++q2) {
         gq_half8 o;
-        gq_i8x8_to_h8(br.q[i][2 * hh], br.q[i][2 * hh + 1], o);
 #pragma unroll
-        for (int s = 0; s < 4; ++s) {
-          gq_half2 p = {o[2 * s], o[2 * s + 1]};
-          p = p * d2;
-          o[2 * s] = p[0];
-          o[2 * s + 1] = p[1];
+        for (int q = 0; q < 2; ++q) {
+          gq_half2 lo, hi;
+          bytes_to_magic(br.q[i][2 * q2 + q] ^ 0x80808080u, lo, hi);
+          lo = (lo + off) * d2;
+          hi = (hi + off) * d2;
+          o[4 * q] = lo[0];
+          o[4 * q + 1] = lo[1];
+          o[4 * q + 2] = hi[0];
+          o[4 * q + 3] = hi[1];
         }
-        *reinterpret_cast<gq_half8 *>(dst + 32 * j) = o;
+        *reinterpret_cast<gq_half8 *>(dst + 8 * q2) = o;
       }
     }
   } else {
-    const int h = step & 1;
+    const int hh = step & 1;
 #pragma unroll
     for (int i = 0; i < 2; ++i) {
       int slot = tid + 256 * i, rt = slot >> 6, lane = slot & 63, g = lane >> 4, r = lane & 15;
       const gq_u4 &mt = br.meta[i];
-      uint32_t sc0, m0, sc1, m1;
-      gq_q4k_codes(mt[1], mt[2], mt[3], g, sc0, m0, sc1, m1);
-      uint32_t sc = h ? sc1 : sc0, mm = h ? m1 : m0;
-      float d = gq_h2f(mt[0] & 0xFFFFu), dmin = gq_h2f(mt[0] >> 16);
-      _Float16 hsc = (_Float16)(float)sc, hnsc = (_Float16)(-1024.0f * (float)sc);
-      _Float16 hd = (_Float16)d;  // exact: d came from fp16 (NaN aside)
-      _Float16 hmin = (_Float16)(-(dmin * (float)mm));
-      gq_half2 sc2 = {hsc, hsc}, nsc2 = {hnsc, hnsc}, d2 = {hd, hd}, mn2 = {hmin, hmin};
-      _Float16 *dst = Bs + (16 * rt + r) * LDS_STRIDE + 32 * g;
+      const uint32_t mv[4] = {mt[0], mt[1], mt[2], mt[3]};
+      const float d = gq_h2f(mv[0] & 0xFFFFu), dmin = gq_h2f(mv[0] >> 16);
+      const _Float16 hd = (_Float16)d;  // exact: d came from fp16 (NaN aside)
 #pragma unroll
-      for (int w8 = 0; w8 < 4; ++w8) {
-        gq_half8 o;
-        gq_q4word_scaled_h8(br.q[i][w8], sc2, nsc2, o);
+      for (int m2 = 0; m2 < 2; ++m2) {
+        const int m = 2 * hh + m2, j = 2 * m + (g >> 1);
+        uint32_t sc, mn;
+        gq_q4k_meta_codes(mv, j, &sc, &mn);
+        const _Float16 hsc = (_Float16)(float)sc, hnsc = (_Float16)(-1024.0f * (float)sc);
+        const _Float16 hmin = (_Float16)(-(dmin * (float)mn));
+        const gq_half2 sc2 = {hsc, hsc}, nsc2 = {hnsc, hnsc}, d2 = {hd, hd}, mn2 = {hmin, hmin};
+        const uint32_t w0 = br.q[i][2 * m2], w1 = br.q[i][2 * m2 + 1];
+        const uint32_t regs[4] = {w0 & 0x0F0F0F0Fu, (w0 >> 4) & 0x0F0F0F0Fu, w1 & 0x0F0F0F0Fu,
+                                  (w1 >> 4) & 0x0F0F0F0Fu};
+        gq_half8 o[2];
 #pragma unroll
-        for (int s = 0; s < 4; ++s) {
-          gq_half2 p = {o[2 * s], o[2 * s + 1]};
-          p = __builtin_elementwise_fma(p, d2, mn2);
-          o[2 * s] = p[0];
-          o[2 * s + 1] = p[1];
+        for (int q = 0; q < 4; ++q) {
+          gq_half2 lo, hi;
+          bytes_to_magic(regs[q], lo, hi);
+          lo = __builtin_elementwise_fma(__builtin_elementwise_fma(lo, sc2, nsc2), d2, mn2);
+          hi = __builtin_elementwise_fma(__builtin_elementwise_fma(hi, sc2, nsc2), d2, mn2);
+          const int b = 4 * (q & 1);
+          o[q >> 1][b] = lo[0];
+          o[q >> 1][b + 1] = lo[1];
+          o[q >> 1][b + 2] = hi[0];
+          o[q >> 1][b + 3] = hi[1];
         }
-        *reinterpret_cast<gq_half8 *>(dst + 8 * w8) = o;
+        // local k of sub-block j within this 128-k step: 32 * (j - 4hh)
+        _Float16 *dst = Bs + (16 * rt + r) * LDS_STRIDE + 32 * (j - 4 * hh) + 16 * (g & 1);
+        *reinterpret_cast<gq_half8 *>(dst) = o[0];
+        *reinterpret_cast<gq_half8 *>(dst + 8) = o[1];
       }
     }
   }
 }
 
 // ---- activation tile -------------------------------------------------------
-// LDS column kk of step `step` holds activation column kcol(step, kk).
+// LDS column kk of step `step` holds activation column step * BK + kk (a Q4_K
+// super-block is two consecutive 128-k steps).
 template <int FMT>
 GQ_DEV int a_col(int step, int kk) {
-  if constexpr (FMT == GQ_FMT_Q4_K) {
-    int s = step >> 1, h = step & 1;
-    return s * 256 + 32 * (2 * (kk >> 5) + h) + (kk & 31);
-  } else {
-    return step * BK + kk;
-  }
+  return step * BK + kk;
 }
 
 template <int FMT>

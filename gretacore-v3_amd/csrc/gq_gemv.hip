@@ -4,522 +4,446 @@
 // (src/rt/backend/hip/kernels/gemm_kernels.hip:594-634, 763-817) for
 // GGUF-native weights: y[b][n] = sum_k x[b][k] * W[n][k].
 //
-// Design (CDNA4, wave64):
-//  * One workgroup per 16-row tile; its KSPLIT waves split the K axis and meet
-//    in LDS at the end.  Each wave first issues the loads of ALL its chunks
-//    (one dwordx4 per lane per chunk: 1 KiB per wave, fully coalesced), so the
-//    whole weight stream is in flight at once, then consumes them in order.
-//  * Weights become fp16 MFMA operands without any float math: a 4-bit (or
-//    offset 8-bit) code placed in the low bits of an fp16 is the subnormal
-//    value code * 2^-24, which the matrix cores multiply exactly.  So a
-//    canonical Q4 word turns into four operand pairs with one shift and one AND
-//    each.  The 2^-24 is folded into the final store; the GGUF offsets (q - 8,
-//    q - 128) are applied per block as d * 8 * S with S = sum of x over the
-//    block.  Q4_K folds its 6-bit sub-block scale into the code
-//    (sc * q <= 945 still fits the subnormal mantissa) and gets
-//    sum_j m_j * S_j from one extra MFMA per super-block.
-//  * Dot products run on v_mfma_f32_16x16x32_f16 with A = activations (rows =
-//    batch rows) and B = the weight tile (cols = 16 weight rows).  The fp32
-//    activation is split into fp16 hi + lo rows (x = hi + lo to ~2^-22), so no
-//    precision is lost to fp16; hi and lo ride in spare MFMA rows.
-//  * Batch <= 2 (decode): each wave converts its own K slice of the fp32
-//    activations into LDS (hi/lo rows + block sums) -- no separate kernel.
-//    Batch 3..16: a small prep kernel writes the same data to a workspace once
-//    and the GEMV reads its operands from there (L2-resident).
+// Design (CDNA4, wave64), built so that the VALU work per weight stays far
+// below what HBM delivers:
+//  * Workgroup = R row tiles (16 rows each) x KSPLIT waves; each wave owns one K
+//    slice and first issues the loads of ALL its chunks (one dwordx4 per lane
+//    per chunk: 1 KiB per wave, fully coalesced), so the weight stream is in
+//    flight at once; the chunks are then consumed in arrival order.
+//  * Dot products run on the int8 matrix cores (v_mfma_i32_16x16x64_i8).  The
+//    B operand is the weights themselves: Q4 codes come out of the T16 code
+//    groups with one AND (plus one shift) per four weights, Q8_0 bytes are used
+//    as they are.  Integer accumulation is exact.
+//  * The activation is split per 32-block into two int8 limbs,
+//    x ~ s * (a + b / 254) with s = amax / 127 (error <= s / 508), staged by
+//    each wave for its K slice in LDS.  A rows are (block-of-pair h, limb l,
+//    batch b) so each MFMA yields, per weight row, the exact integer dot
+//    products of two blocks and both limbs at once; lane group g of the D
+//    fragment holds combination (h, l) = (g >> 1, g & 1).
+//  * Scales are applied in fp32 once per (row, block): acc += d * s' * D with
+//    s' = s or s / 254.  The GGUF offsets are applied through block sums S of
+//    the represented activation: Q4_0 y -= 8 d S, Q4_K y -= dmin m_j S_j;
+//    Q8_0 is signed.
+//  * Batch <= 4 stages the activations in-kernel (no workspace, one launch);
+//    batch 5..16 uses a prep kernel that writes the same limbs to a workspace.
 #include <stdlib.h>
 
 #include "gq_internal.h"
 
 namespace {
 
-constexpr float kTwo24 = 16777216.0f;
-
 template <int FMT>
 struct Fmt;
 template <>
 struct Fmt<GQ_FMT_Q4_0> {
-  static constexpr int CK = 128, QB = 1024, SB = 128, MAXC = 8;
+  static constexpr int CK = 128, QB = 1024, SB = 128, MAXC = 8, STEPS = 2;
 };
 template <>
 struct Fmt<GQ_FMT_Q8_0> {
-  static constexpr int CK = 128, QB = 2048, SB = 128, MAXC = 8;
+  static constexpr int CK = 128, QB = 2048, SB = 128, MAXC = 8, STEPS = 2;
 };
 template <>
 struct Fmt<GQ_FMT_Q4_K> {
-  static constexpr int CK = 256, QB = 2048, SB = 256, MAXC = 4;
+  static constexpr int CK = 256, QB = 2048, SB = 256, MAXC = 4, STEPS = 4;
 };
 
-// weight registers of one chunk
+// weight registers of one chunk (one row tile)
 template <int FMT>
 struct Chunk;
 template <>
 struct Chunk<GQ_FMT_Q4_0> {
-  gq_u4 q;
-  gq_u2 d;
+  gq_u4 q;      // steps 0, 1: 8-byte code groups
+  uint32_t d;   // (d of block h', d of block 2 + h') for this lane
 };
 template <>
 struct Chunk<GQ_FMT_Q8_0> {
-  gq_u4 q0, q1;
-  gq_u2 d;
+  gq_u4 q0, q1;  // steps 0, 1: 16 int8
+  uint32_t d;
 };
 template <>
 struct Chunk<GQ_FMT_Q4_K> {
-  gq_u4 qa, qb, meta;
+  gq_u4 qa, qb;  // steps 0,1 and 2,3
+  gq_u4 meta;    // d, dmin, W1, W2, W3 of this lane's row
 };
 
+// qp / sp: wave-uniform chunk bases; qo / so: this lane's 32-bit offsets
 template <int FMT>
-GQ_DEV void load_chunk(const uint8_t *qp, const uint8_t *sp, int r, Chunk<FMT> &ch) {
+GQ_DEV void load_chunk(const uint8_t *qp, const uint8_t *sp, uint32_t qo, uint32_t so, Chunk<FMT> &ch) {
   if constexpr (FMT == GQ_FMT_Q4_0) {
-    ch.q = gq_ld16(qp);
-    ch.d = gq_ld8(sp + 8 * r);
+    ch.q = gq_ld16_nt(qp + qo);
+    ch.d = gq_ld4_nt(sp + so);
   } else if constexpr (FMT == GQ_FMT_Q8_0) {
-    ch.q0 = gq_ld16(qp);
-    ch.q1 = gq_ld16(qp + 1024);
-    ch.d = gq_ld8(sp + 8 * r);
+    ch.q0 = gq_ld16_nt(qp + qo);
+    ch.q1 = gq_ld16_nt(qp + 1024 + qo);
+    ch.d = gq_ld4_nt(sp + so);
   } else {
-    ch.qa = gq_ld16(qp);
-    ch.qb = gq_ld16(qp + 1024);
-    ch.meta = gq_ld16(sp + 16 * r);
+    ch.qa = gq_ld16_nt(qp + qo);
+    ch.qb = gq_ld16_nt(qp + 1024 + qo);
+    ch.meta = gq_ld16_nt(sp + so);
   }
 }
 
-// canonical Q4 word -> 4 subnormal-code operand pairs (value q * 2^-24)
-GQ_DEV gq_half8 q4_codes(uint32_t w) {
-  gq_u4 t;
-#pragma unroll
-  for (int s = 0; s < 4; ++s) t[s] = (w >> (4 * s)) & 0x000F000Fu;
-  return __builtin_bit_cast(gq_half8, t);
+// code group (2 words) -> 16 codes as bytes, slot order
+GQ_DEV gq_i4 codes16(uint32_t w0, uint32_t w1) {
+  gq_i4 v;
+  v[0] = (int)(w0 & 0x0F0F0F0Fu);
+  v[1] = (int)((w0 >> 4) & 0x0F0F0F0Fu);
+  v[2] = (int)(w1 & 0x0F0F0F0Fu);
+  v[3] = (int)((w1 >> 4) & 0x0F0F0F0Fu);
+  return v;
 }
-// canonical Q4 word -> codes sc * q (value sc * q * 2^-24, exact)
-GQ_DEV gq_half8 q4_scaled_codes(uint32_t w, uint32_t sc) {
-  gq_u4 t;
-#pragma unroll
-  for (int s = 0; s < 4; ++s) t[s] = __umul24((w >> (4 * s)) & 0x000F000Fu, sc);
-  return __builtin_bit_cast(gq_half8, t);
-}
-// 8 int8 -> codes q + 128 (value (q + 128) * 2^-24)
-GQ_DEV gq_half8 q8_codes(uint32_t w0, uint32_t w1) {
-  uint32_t u0 = w0 ^ 0x80808080u, u1 = w1 ^ 0x80808080u;
-  gq_u4 t;
-  t[0] = __builtin_amdgcn_perm(0u, u0, 0x04010400u);
-  t[1] = __builtin_amdgcn_perm(0u, u0, 0x04030402u);
-  t[2] = __builtin_amdgcn_perm(0u, u1, 0x04010400u);
-  t[3] = __builtin_amdgcn_perm(0u, u1, 0x04030402u);
-  return __builtin_bit_cast(gq_half8, t);
+
+GQ_DEV gq_i4 mfma_i8(const gq_i4 &a, const gq_i4 &b) {
+  const gq_i4 z = {0, 0, 0, 0};
+  return __builtin_amdgcn_mfma_i32_16x16x64_i8(a, b, z, 0, 0, 0);
 }
 
 GQ_DEV float h16lo(uint32_t v) { return (float)__builtin_bit_cast(gq_half2, v)[0]; }
 GQ_DEV float h16hi(uint32_t v) { return (float)__builtin_bit_cast(gq_half2, v)[1]; }
 
+// low byte of each of four floats, packed into one word
+GQ_DEV uint32_t pack_lo_bytes(float f0, float f1, float f2, float f3) {
+  const uint32_t p01 = __builtin_amdgcn_perm(__float_as_uint(f1), __float_as_uint(f0), 0x00000400u);
+  const uint32_t p23 = __builtin_amdgcn_perm(__float_as_uint(f3), __float_as_uint(f2), 0x00000400u);
+  return __builtin_amdgcn_perm(p23, p01, 0x05040100u);
+}
 
 // ---------------------------------------------------------------------------
-// Fused path (batch NB <= 2): each wave stages its own K slice of the fp32
-// activations in LDS: rows 2b (hi) and 2b+1 (lo), row stride `stride` halves,
-// then the per-32-block sums (fp32; Q4_K: fp16 (hi, lo) pairs).
+// Activation limbs.  Per batch row b and limb l (0: a, 1: b) an int8 array of
+// the slice, a zero region of the slice length, and per (b, 32-block) the
+// float4 (s, S, s / 254, 0): the (scale, sum) pair of limb a then of limb b.
 // ---------------------------------------------------------------------------
 struct XlLayout {
-  int lk, stride, sf_off, wave_bytes;
+  int lk, zero_off, scl_off, wave_bytes;
 };
 __host__ __device__ inline XlLayout xl_layout(int lk, int nb) {
   XlLayout L;
   L.lk = lk;
-  L.stride = lk + 8;
-  L.sf_off = 2 * nb * L.stride * 2;
-  L.wave_bytes = (L.sf_off + nb * (lk / 32) * 4 + 15) & ~15;
+  L.zero_off = 2 * nb * lk;
+  L.scl_off = L.zero_off + lk;
+  L.wave_bytes = (L.scl_off + nb * (lk / 32) * 16 + 15) & ~15;
   return L;
 }
 
-template <int FMT, int NB, int KSPLIT>
-__global__ void __launch_bounds__(64 * KSPLIT)
-k_gemv_xl(const uint8_t *__restrict__ w, size_t sc_off, const float *__restrict__ x, float *__restrict__ y, int N,
-          int K, int C) {
-  using F = Fmt<FMT>;
-  constexpr int LKMAX = F::CK * F::MAXC;
-  constexpr int TPR = LKMAX / 8 / 64;  // 8-element tasks per batch row per lane
-  extern __shared__ __attribute__((aligned(16))) unsigned char gq_dyn_lds[];
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const int g = lane >> 4, r = lane & 15;
-  const size_t t = blockIdx.x;
-  const int c0 = (C * wave) / KSPLIT, c1 = (C * (wave + 1)) / KSPLIT;
-  const int nck = c1 - c0;  // <= F::MAXC (host-checked)
-  const int k0 = c0 * F::CK, LK = nck * F::CK;
-  const XlLayout L = xl_layout(F::CK * ((C + KSPLIT - 1) / KSPLIT), NB);
-  unsigned char *lds = gq_dyn_lds + (size_t)wave * L.wave_bytes;
-  _Float16 *xs = reinterpret_cast<_Float16 *>(lds);
-  float *sf = reinterpret_cast<float *>(lds + L.sf_off);
-  const int nblk = L.lk / 32;
+constexpr float kMagic = 12582912.0f;  // 1.5 * 2^23: adding it rounds to an integer in the low mantissa bits
 
-  // 1. activation loads first (so waiting for them never waits for weights)
-  // Loads are unconditional (out-of-range ones read a clamped valid address
-  // and are discarded) so the compiler can count outstanding loads exactly and
-  // start on chunk 0 as soon as it lands.
-  float4 xv[NB * TPR][2];
-  bool xin[NB * TPR];
+// Splits 8 consecutive elements into the two limbs (4 int8 per word) and
+// returns sum(a) * 254 + sum(b) (an exact integer in fp32), so the block sum of
+// the represented values is s / 254 times it.
+GQ_DEV float split8(const float (&v)[8], float inv, uint32_t (&la)[2], uint32_t (&lb)[2]) {
+  float fa[8], fb[8];
+  float sum = 0.f;
 #pragma unroll
-  for (int i = 0; i < NB * TPR; ++i) {
-    const int b = i / TPR, e8 = lane + 64 * (i % TPR), k = k0 + 8 * e8;
-    xin[i] = 8 * e8 < LK && k < K;
-    const float4 *p = reinterpret_cast<const float4 *>(x + (size_t)b * K + (xin[i] ? k : 0));
-    xv[i][0] = p[0];
-    xv[i][1] = p[1];
+  for (int e = 0; e < 8; ++e) {
+    const float t = v[e] * inv;
+    fa[e] = t + kMagic;                    // bits: integer a in the low byte
+    const float ai = fa[e] - kMagic;
+    const float r = t - ai;                // in [-0.5, 0.5]
+    fb[e] = __builtin_fmaf(r, 254.0f, kMagic);
+    sum += __builtin_fmaf(ai, 254.0f, fb[e] - kMagic);
   }
-  __builtin_amdgcn_sched_barrier(0);  // keep the activation loads ahead of the weights
-  // 2. weight loads for every chunk of this wave
-  Chunk<FMT> ch[F::MAXC];
-  const uint8_t *qp = w + (t * (size_t)C + c0) * F::QB + 16 * lane;
-  const uint8_t *sp = w + sc_off + (t * (size_t)C + c0) * F::SB;
+  la[0] = pack_lo_bytes(fa[0], fa[1], fa[2], fa[3]);
+  la[1] = pack_lo_bytes(fa[4], fa[5], fa[6], fa[7]);
+  lb[0] = pack_lo_bytes(fb[0], fb[1], fb[2], fb[3]);
+  lb[1] = pack_lo_bytes(fb[4], fb[5], fb[6], fb[7]);
+  return sum;
+}
+
+template <int FMT, int NBC, int MT, int R, int KSPLIT, bool PREP>
+__global__ void __launch_bounds__(64 * KSPLIT)
+k_gemv_q(const uint8_t *__restrict__ w, size_t sc_off, const float *__restrict__ x,
+         const int8_t *__restrict__ xl_g, const float *__restrict__ scl_g, float *__restrict__ y, int N, int K,
+         int C, int Kp, int nb) {
+  using F = Fmt<FMT>;
+  constexpr int NCK = F::MAXC / R;           // chunks per wave (upper bound)
+  constexpr int LKMAX = F::CK * NCK;         // slice elements per wave
+  constexpr int TPR = LKMAX / 8 / 64;        // 8-element staging tasks per batch row per lane
+  constexpr int BPC = F::CK / 32;            // 32-blocks per chunk
+  extern __shared__ __attribute__((aligned(16))) unsigned char gq_dyn_lds[];
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform (SGPR)
+  const int g = lane >> 4, r = lane & 15;
+  const size_t tile0 = (size_t)blockIdx.x * R;
+  const int ntiles = (int)gq_tiles(N);
+  const int c0 = (C * wave) / KSPLIT, c1 = (C * (wave + 1)) / KSPLIT;
+  const int nck = c1 - c0;  // <= NCK (host-checked)
+  const int k0 = c0 * F::CK, LK = nck * F::CK;
+
+  // ---- 1. activation loads (fused path), issued before the weights ----------
+  float4 xv[PREP ? 1 : NBC * TPR][2];
+  bool xin[PREP ? 1 : NBC * TPR];
+  if constexpr (!PREP) {
 #pragma unroll
-  for (int i = 0; i < F::MAXC; ++i) {
-    const int ii = i < nck ? i : nck - 1;
-    load_chunk<FMT>(qp + (size_t)ii * F::QB, sp + (size_t)ii * F::SB, r, ch[i]);
+    for (int i = 0; i < NBC * TPR; ++i) {
+      const int b = i / TPR, e8 = lane + 64 * (i % TPR), k = k0 + 8 * e8;
+      xin[i] = b < nb && 8 * e8 < LK && k < K;
+      const float4 *p = reinterpret_cast<const float4 *>(x + (xin[i] ? (size_t)b * K + k : 0));
+      xv[i][0] = p[0];
+      xv[i][1] = p[1];
+    }
   }
   __builtin_amdgcn_sched_barrier(0);
 
-  // 3. hi/lo split + block sums into LDS
+  // ---- 2. weight loads for every chunk of this wave (clamped, unconditional) -
+  // Issued in consumption order (chunk-major, then tile) with wave-uniform
+  // base addresses, so each load is a scalar base + the lane's fixed offset.
+  Chunk<FMT> ch[R][NCK];
+  const uint32_t qlane = 16u * (uint32_t)lane;
+  const uint32_t slane = (FMT == GQ_FMT_Q4_K) ? 16u * (uint32_t)r : 8u * (uint32_t)r + 4u * (uint32_t)(g >> 1);
+  const uint8_t *qbase[R], *sbase[R];
 #pragma unroll
-  for (int i = 0; i < NB * TPR; ++i) {
-    const int b = i / TPR, e8 = lane + 64 * (i % TPR);
-    float v[8] = {xv[i][0].x, xv[i][0].y, xv[i][0].z, xv[i][0].w,
-                  xv[i][1].x, xv[i][1].y, xv[i][1].z, xv[i][1].w};
-#pragma unroll
-    for (int e = 0; e < 8; ++e) v[e] = xin[i] ? v[e] : 0.f;
-    gq_half8 hi, lo;
-    float s = 0.f;
-#pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      hi[e] = (_Float16)v[e];
-      lo[e] = (_Float16)(v[e] - (float)hi[e]);
-      s += v[e];
-    }
-    s += __shfl_xor(s, 1, 64);
-    s += __shfl_xor(s, 2, 64);
-    if (8 * e8 < LK) {
-      *reinterpret_cast<gq_half8 *>(xs + (2 * b) * L.stride + 8 * e8) = hi;
-      *reinterpret_cast<gq_half8 *>(xs + (2 * b + 1) * L.stride + 8 * e8) = lo;
-      if ((lane & 3) == 0) {
-        const int blk = b * nblk + (e8 >> 2);
-        if constexpr (FMT == GQ_FMT_Q4_K) {
-          const _Float16 shh = (_Float16)s;
-          const gq_half2 pr = {shh, (_Float16)(s - (float)shh)};
-          reinterpret_cast<uint32_t *>(sf)[blk] = gq_h2_bits(pr);
-        } else {
-          sf[blk] = s;
-        }
-      }
-    }
+  for (int rt = 0; rt < R; ++rt) {
+    const size_t t = (tile0 + rt < (size_t)ntiles) ? tile0 + rt : (size_t)ntiles - 1;
+    qbase[rt] = w + (t * (size_t)C + c0) * F::QB;
+    sbase[rt] = w + sc_off + (t * (size_t)C + c0) * F::SB;
   }
-  __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
-  __builtin_amdgcn_wave_barrier();
+#pragma unroll
+  for (int i = 0; i < NCK; ++i) {
+    // surplus loads re-read the wave's last chunk (its first one when the
+    // wave has no chunk: c0 < C always holds), never outside the tensor
+    const int ii = i < nck ? i : (nck > 0 ? nck - 1 : 0);
+#pragma unroll
+    for (int rt = 0; rt < R; ++rt)
+      load_chunk<FMT>(qbase[rt] + (size_t)ii * F::QB, sbase[rt] + (size_t)ii * F::SB, qlane, slane, ch[rt][i]);
+  }
+  __builtin_amdgcn_sched_barrier(0);
 
-  // 4. consume the chunks.  A rows >= 2NB read real (finite) data: they only
-  // feed D rows that are never used, so no masking is needed.
-  const int ar = r & (2 * NB - 1);
-  const gq_f4 zero4 = {0.f, 0.f, 0.f, 0.f};
-  float acc[2 * NB], cor[NB];
+  // ---- 3. activation limbs --------------------------------------------------
+  const int8_t *limbs;
+  const float *scl;
+  const int8_t *zero;
+  int lds_ld, scl_ld, kbase;  // limb row stride, scale row stride (blocks), slice origin
+  if constexpr (!PREP) {
+#if defined(GQ_EXPERIMENT) && GQ_EXPERIMENT == 1
+    constexpr bool kStage = false;  // skip the activation split (wrong results)
+#else
+    constexpr bool kStage = true;
+#endif
+    const XlLayout L = xl_layout(F::CK * ((C + KSPLIT - 1) / KSPLIT), NBC);
+    unsigned char *base = gq_dyn_lds + (size_t)wave * L.wave_bytes;
+    int8_t *lm = reinterpret_cast<int8_t *>(base);
+    float *sc = reinterpret_cast<float *>(base + L.scl_off);
+    const int nblk = L.lk / 32;
+    for (int o = 16 * lane; o < L.lk; o += 1024)
+      *reinterpret_cast<gq_u4 *>(base + L.zero_off + o) = gq_u4{0u, 0u, 0u, 0u};
 #pragma unroll
-  for (int v = 0; v < 2 * NB; ++v) acc[v] = 0.f;
+    for (int i = 0; i < (kStage ? NBC * TPR : 0); ++i) {
+      const int b = i / TPR, e8 = lane + 64 * (i % TPR);
+      float v[8] = {xv[i][0].x, xv[i][0].y, xv[i][0].z, xv[i][0].w, xv[i][1].x, xv[i][1].y, xv[i][1].z, xv[i][1].w};
+      float amax = 0.f;
 #pragma unroll
-  for (int u = 0; u < NB; ++u) cor[u] = 0.f;
-
-  if constexpr (FMT == GQ_FMT_Q4_0 || FMT == GQ_FMT_Q8_0) {
-    const _Float16 *xa = xs + ar * L.stride + 8 * g;
-#pragma unroll
-    for (int i = 0; i < F::MAXC; ++i) {
-      if (i >= nck) break;
-      gq_f4 D[4];
-      float sblk[NB][4];
-#pragma unroll
-      for (int u = 0; u < NB; ++u) {
-        const gq_f4 s4 = *reinterpret_cast<const gq_f4 *>(sf + u * nblk + 4 * i);
-#pragma unroll
-        for (int j = 0; j < 4; ++j) sblk[u][j] = s4[j];
+      for (int e = 0; e < 8; ++e) {
+        v[e] = xin[i] ? v[e] : 0.f;
+        amax = fmaxf(amax, fabsf(v[e]));
       }
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        gq_half8 b;
-        if constexpr (FMT == GQ_FMT_Q4_0) {
-          b = q4_codes(ch[i].q[j]);
-        } else {
-          const gq_u4 &qq = (j < 2) ? ch[i].q0 : ch[i].q1;
-          b = q8_codes(qq[2 * (j & 1)], qq[2 * (j & 1) + 1]);
-        }
-        const gq_half8 a = *reinterpret_cast<const gq_half8 *>(xa + i * 128 + 32 * j);
-        D[j] = gq_mfma16(a, b, zero4);
-      }
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const float d = (j & 1) ? h16hi(ch[i].d[j >> 1]) : h16lo(ch[i].d[j >> 1]);
-#pragma unroll
-        for (int v = 0; v < 2 * NB; ++v) acc[v] += d * D[j][v];
-#pragma unroll
-        for (int u = 0; u < NB; ++u) cor[u] += d * sblk[u][j];
+      amax = fmaxf(amax, __shfl_xor(amax, 1, 64));
+      amax = fmaxf(amax, __shfl_xor(amax, 2, 64));
+      const float inv = amax > 0.f ? 127.0f / amax : 0.f;
+      const float sx = amax * (1.0f / 127.0f);
+      uint32_t la[2], lb[2];
+      // block sum of the represented values: offsets and mins then act on
+      // exactly the activation the integer products see
+      float s = split8(v, inv, la, lb);
+      s += __shfl_xor(s, 1, 64);
+      s += __shfl_xor(s, 2, 64);
+      s *= sx * (1.0f / 254.0f);
+      if (8 * e8 < L.lk) {
+        *reinterpret_cast<gq_u2 *>(lm + (2 * b) * L.lk + 8 * e8) = gq_u2{la[0], la[1]};
+        *reinterpret_cast<gq_u2 *>(lm + (2 * b + 1) * L.lk + 8 * e8) = gq_u2{lb[0], lb[1]};
+        if ((lane & 3) == 0)
+          *reinterpret_cast<gq_f4 *>(sc + 4 * (b * nblk + (e8 >> 2))) = gq_f4{sx, s, sx * (1.0f / 254.0f), 0.f};
       }
     }
+    __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    limbs = lm;
+    scl = sc;
+    zero = reinterpret_cast<const int8_t *>(base + L.zero_off);
+    lds_ld = L.lk;
+    scl_ld = nblk;
+    kbase = k0;
   } else {
-    const _Float16 *xa = xs + ar * L.stride + 64 * g;
-    const uint32_t *sh = reinterpret_cast<const uint32_t *>(sf);
-    const bool hirow = !(ar & 1);
+    limbs = xl_g;
+    scl = scl_g;
+    zero = xl_g + (size_t)2 * nb * Kp;
+    lds_ld = Kp;
+    scl_ld = Kp / 32;
+    kbase = 0;
+  }
+
+  // A operand: lane (row r, group g) is combination c = r >> 2 = (h, l) of
+  // batch row 4 * mt + (r & 3); it carries data only where its lane group
+  // covers block h of the MFMA pair ((g >> 1) == h), zeros otherwise.
+  const int8_t *abase[MT];
+  {
+    const int c = r >> 2, h = c >> 1, l = c & 1;
 #pragma unroll
-    for (int i = 0; i < F::MAXC; ++i) {
-      if (i >= nck) break;
-      const uint32_t m0w = ch[i].meta[0];
-      const float d = h16lo(m0w), dmin = h16hi(m0w);
-      uint32_t sc0, m0, sc1, m1;
-      gq_q4k_codes(ch[i].meta[1], ch[i].meta[2], ch[i].meta[3], g, sc0, m0, sc1, m1);
-      gq_f4 D1 = zero4;
+    for (int mt = 0; mt < MT; ++mt) {
+      const int b = 4 * mt + (r & 3);
+      const bool act = ((g >> 1) == h) && b < nb && (r & 3) < NBC;
+      abase[mt] = act ? limbs + (size_t)(2 * b + l) * lds_ld + (k0 - kbase) + 32 * h + 16 * (g & 1)
+                      : zero + (k0 - kbase);
+    }
+  }
+  // D side: this lane's combination (h', l') = (g >> 1, g & 1)
+  const int hp = g >> 1, lp = g & 1;
+
+  float acc[R][MT][NBC], cor[R][MT][NBC];
 #pragma unroll
-      for (int tt = 0; tt < 8; ++tt) {
-        const int h = tt >> 2;
-        const uint32_t word = h ? ch[i].qb[tt & 3] : ch[i].qa[tt & 3];
-        const gq_half8 b = q4_scaled_codes(word, h ? sc1 : sc0);
-        const gq_half8 a = *reinterpret_cast<const gq_half8 *>(xa + i * 256 + 32 * h + 8 * (tt & 3));
-        D1 = gq_mfma16(a, b, D1);
+  for (int rt = 0; rt < R; ++rt)
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+      for (int v = 0; v < NBC; ++v) acc[rt][mt][v] = cor[rt][mt][v] = 0.f;
+
+#if defined(GQ_EXPERIMENT) && GQ_EXPERIMENT == 2
+  {  // memory only: fold the loaded words, skip all compute
+    uint32_t acc2 = 0;
+#pragma unroll
+    for (int i = 0; i < NCK; ++i)
+#pragma unroll
+      for (int rt = 0; rt < R; ++rt) {
+        const uint32_t *pw = reinterpret_cast<const uint32_t *>(&ch[rt][i]);
+#pragma unroll
+        for (int q = 0; q < (int)(sizeof(Chunk<FMT>) / 4); ++q) acc2 ^= pw[q];
       }
-      // min term: A = (S_hi, S_lo) of sub-blocks 2g, 2g+1 on hi rows
-      const gq_u2 sp2 = *reinterpret_cast<const gq_u2 *>(sh + (ar >> 1) * nblk + 8 * i + 2 * g);
-      gq_u4 at = {0u, 0u, 0u, 0u};
-      at[0] = hirow ? ((sp2[0] & 0xFFFFu) | (sp2[1] << 16)) : 0u;
-      at[1] = hirow ? ((sp2[0] >> 16) | (sp2[1] & 0xFFFF0000u)) : 0u;
-      const gq_u4 bmt = {m0 | (m1 << 16), m0 | (m1 << 16), 0u, 0u};
-      const gq_f4 D2 =
-          gq_mfma16(__builtin_bit_cast(gq_half8, at), __builtin_bit_cast(gq_half8, bmt), zero4);
+    if (acc2 == 0x9E3779B9u && r == 0) y[0] = 1.0f;
+    return;
+  }
+#endif
+  // ---- 4. consume the chunks -------------------------------------------------
 #pragma unroll
-      for (int v = 0; v < 2 * NB; ++v) acc[v] += d * D1[v] - dmin * D2[v];
+  for (int i = 0; i < NCK; ++i) {
+    if (i < nck)
+#pragma unroll
+    for (int m = 0; m < F::STEPS; ++m) {
+      const int koff = i * F::CK + 64 * m;
+      const int blk = (k0 - kbase) / 32 + i * BPC + 2 * m + hp;  // this lane's block, in scale rows
+      gq_i4 a[MT];
+      float2 sv[MT][NBC];
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt) {
+        a[mt] = *reinterpret_cast<const gq_i4 *>(abase[mt] + koff);
+#pragma unroll
+        for (int v = 0; v < NBC; ++v) {
+          const int b = 4 * mt + v;
+          sv[mt][v] = *reinterpret_cast<const float2 *>(scl + 4 * ((size_t)(b < nb ? b : 0) * scl_ld + blk) + 2 * lp);
+        }
+      }
+#pragma unroll
+      for (int rt = 0; rt < R; ++rt) {
+        const Chunk<FMT> &cc = ch[rt][i];
+        gq_i4 bop;
+        float ws, wm = 0.f;  // weight scale and offset/min factor of block (2m + h')
+        if constexpr (FMT == GQ_FMT_Q4_0) {
+          bop = codes16(cc.q[2 * m], cc.q[2 * m + 1]);
+          ws = m ? h16hi(cc.d) : h16lo(cc.d);
+          wm = ws;
+        } else if constexpr (FMT == GQ_FMT_Q8_0) {
+          const gq_u4 &qq = m ? cc.q1 : cc.q0;
+          bop = gq_i4{(int)qq[0], (int)qq[1], (int)qq[2], (int)qq[3]};
+          ws = m ? h16hi(cc.d) : h16lo(cc.d);
+        } else {
+          const uint32_t w0 = (m < 2) ? cc.qa[2 * (m & 1)] : cc.qb[2 * (m & 1)];
+          const uint32_t w1 = (m < 2) ? cc.qa[2 * (m & 1) + 1] : cc.qb[2 * (m & 1) + 1];
+          bop = codes16(w0, w1);
+          const uint32_t wsc = hp ? cc.meta[2] : cc.meta[1];
+          const uint32_t byte = (wsc >> (8 * m)) & 0xFFu;
+          const uint32_t b3 = (cc.meta[3] >> (8 * m + 4 * hp)) & 15u;
+          ws = h16lo(cc.meta[0]) * (float)(byte & 63u);
+          wm = h16hi(cc.meta[0]) * (float)((byte >> 6) | (b3 << 2));
+        }
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt) {
+          const gq_i4 D = mfma_i8(a[mt], bop);
+#pragma unroll
+          for (int v = 0; v < NBC; ++v) {
+            acc[rt][mt][v] += (ws * sv[mt][v].x) * (float)D[v];
+            if constexpr (FMT != GQ_FMT_Q8_0) cor[rt][mt][v] += wm * sv[mt][v].y;
+          }
+        }
+      }
     }
   }
 
-  constexpr float OFF = (FMT == GQ_FMT_Q4_0) ? 8.f : (FMT == GQ_FMT_Q8_0) ? 128.f : 0.f;
-  float part[NB];
+  // ---- 5. reduce: lane groups (4 combinations), then the KSPLIT waves --------
+  constexpr float OFF = (FMT == GQ_FMT_Q4_0) ? 8.f : (FMT == GQ_FMT_Q4_K) ? 1.f : 0.f;
+  float part[R][MT][NBC];
 #pragma unroll
-  for (int u = 0; u < NB; ++u) part[u] = kTwo24 * (acc[2 * u] + acc[2 * u + 1]) - OFF * cor[u];
+  for (int rt = 0; rt < R; ++rt)
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+      for (int v = 0; v < NBC; ++v) {
+        float p = acc[rt][mt][v] - OFF * cor[rt][mt][v];
+        p += __shfl_xor(p, 16, 64);
+        p += __shfl_xor(p, 32, 64);
+        part[rt][mt][v] = p;
+      }
   if constexpr (KSPLIT > 1) {
-    __shared__ float red[KSPLIT][NB][16];
+    __shared__ float red[KSPLIT][R * MT * NBC][16];
     if (g == 0) {
 #pragma unroll
-      for (int u = 0; u < NB; ++u) red[wave][u][r] = part[u];
+      for (int rt = 0; rt < R; ++rt)
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+          for (int v = 0; v < NBC; ++v) red[wave][(rt * MT + mt) * NBC + v][r] = part[rt][mt][v];
     }
     __syncthreads();
     if (wave != 0 || g != 0) return;
 #pragma unroll
-    for (int u = 0; u < NB; ++u) {
-      float s = 0.f;
+    for (int rt = 0; rt < R; ++rt)
 #pragma unroll
-      for (int q = 0; q < KSPLIT; ++q) s += red[q][u][r];
-      part[u] = s;
-    }
+      for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+        for (int v = 0; v < NBC; ++v) {
+          float s = 0.f;
+#pragma unroll
+          for (int q = 0; q < KSPLIT; ++q) s += red[q][(rt * MT + mt) * NBC + v][r];
+          part[rt][mt][v] = s;
+        }
   } else if (g != 0) {
     return;
   }
-  const size_t row = t * 16 + r;
-  if (row < (size_t)N) {
 #pragma unroll
-    for (int u = 0; u < NB; ++u) y[(size_t)u * N + row] = part[u];
-  }
-}
-
-// ---------------------------------------------------------------------------
-// Workspace path (batch 3..16): operands from the prepared buffers
-//   xq [2B][Kp] fp16 (rows 2b hi, 2b+1 lo), sf [B][Kp/32] f32,
-//   sh [B][Kp/32] fp16 (hi, lo) sums (Q4_K).
-// D rows: lane (g, r) holds rows 16mt + 4g + v, i.e. batch 8mt + 2g + v/2.
-// ---------------------------------------------------------------------------
-template <int FMT, int MT, int KSPLIT>
-__global__ void __launch_bounds__(64 * KSPLIT)
-k_gemv_xg(const uint8_t *__restrict__ w, size_t sc_off, const _Float16 *__restrict__ xq,
-          const float *__restrict__ sfq, const uint32_t *__restrict__ shq, float *__restrict__ y, int N, int C,
-          int Kp, int nb) {
-  using F = Fmt<FMT>;
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const int g = lane >> 4, r = lane & 15;
-  const size_t t = blockIdx.x;
-  const int c0 = (C * wave) / KSPLIT, c1 = (C * (wave + 1)) / KSPLIT;
-  const int nck = c1 - c0;
-  const int nsub = Kp / 32;
-
-  Chunk<FMT> ch[F::MAXC];
-  const uint8_t *qp = w + (t * (size_t)C + c0) * F::QB + 16 * lane;
-  const uint8_t *sp = w + sc_off + (t * (size_t)C + c0) * F::SB;
-#pragma unroll
-  for (int i = 0; i < F::MAXC; ++i) {
-    const int ii = i < nck ? i : nck - 1;
-    load_chunk<FMT>(qp + (size_t)ii * F::QB, sp + (size_t)ii * F::SB, r, ch[i]);
-  }
-
-  // per-lane operand rows (rows >= 2nb read a valid row; their D rows are unused)
-  const _Float16 *xa[MT];
-  int ar[MT], bs[MT][2];
-#pragma unroll
-  for (int mt = 0; mt < MT; ++mt) {
-    const int row = 16 * mt + r;
-    ar[mt] = row < 2 * nb ? row : row % (2 * nb);
-    xa[mt] = xq + (size_t)ar[mt] * Kp + (FMT == GQ_FMT_Q4_K ? 64 : 8) * g;
-#pragma unroll
-    for (int u = 0; u < 2; ++u) {
-      const int b = 8 * mt + 2 * g + u;
-      bs[mt][u] = b < nb ? b : 0;
-    }
-  }
-  const gq_f4 zero4 = {0.f, 0.f, 0.f, 0.f};
-  gq_f4 acc[MT];
-  float cor[MT][2];
-#pragma unroll
-  for (int mt = 0; mt < MT; ++mt) {
-    acc[mt] = zero4;
-    cor[mt][0] = cor[mt][1] = 0.f;
-  }
-
-#pragma unroll
-  for (int i = 0; i < F::MAXC; ++i) {
-    if (i >= nck) break;
-    const int c = c0 + i;
-    if constexpr (FMT == GQ_FMT_Q4_0 || FMT == GQ_FMT_Q8_0) {
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        gq_half8 b;
-        if constexpr (FMT == GQ_FMT_Q4_0) {
-          b = q4_codes(ch[i].q[j]);
-        } else {
-          const gq_u4 &qq = (j < 2) ? ch[i].q0 : ch[i].q1;
-          b = q8_codes(qq[2 * (j & 1)], qq[2 * (j & 1) + 1]);
-        }
-        const float d = (j & 1) ? h16hi(ch[i].d[j >> 1]) : h16lo(ch[i].d[j >> 1]);
-        const int blk = 4 * c + j;
-#pragma unroll
-        for (int mt = 0; mt < MT; ++mt) {
-          const gq_half8 a = *reinterpret_cast<const gq_half8 *>(xa[mt] + blk * 32);
-          acc[mt] += d * gq_mfma16(a, b, zero4);
-#pragma unroll
-          for (int u = 0; u < 2; ++u) cor[mt][u] += d * sfq[(size_t)bs[mt][u] * nsub + blk];
-        }
-      }
-    } else {
-      const uint32_t m0w = ch[i].meta[0];
-      const float d = h16lo(m0w), dmin = h16hi(m0w);
-      uint32_t sc0, m0, sc1, m1;
-      gq_q4k_codes(ch[i].meta[1], ch[i].meta[2], ch[i].meta[3], g, sc0, m0, sc1, m1);
-      gq_f4 D1[MT];
-#pragma unroll
-      for (int mt = 0; mt < MT; ++mt) D1[mt] = zero4;
-#pragma unroll
-      for (int tt = 0; tt < 8; ++tt) {
-        const int h = tt >> 2;
-        const uint32_t word = h ? ch[i].qb[tt & 3] : ch[i].qa[tt & 3];
-        const gq_half8 b = q4_scaled_codes(word, h ? sc1 : sc0);
-#pragma unroll
-        for (int mt = 0; mt < MT; ++mt) {
-          const gq_half8 a = *reinterpret_cast<const gq_half8 *>(xa[mt] + c * 256 + 32 * h + 8 * (tt & 3));
-          D1[mt] = gq_mfma16(a, b, D1[mt]);
-        }
-      }
-      const gq_u4 bmt = {m0 | (m1 << 16), m0 | (m1 << 16), 0u, 0u};
-#pragma unroll
-      for (int mt = 0; mt < MT; ++mt) {
-        const bool hirow = !(ar[mt] & 1);
-        const gq_u2 sp2 = *reinterpret_cast<const gq_u2 *>(shq + (size_t)(ar[mt] >> 1) * nsub + 8 * c + 2 * g);
-        gq_u4 at = {0u, 0u, 0u, 0u};
-        at[0] = hirow ? ((sp2[0] & 0xFFFFu) | (sp2[1] << 16)) : 0u;
-        at[1] = hirow ? ((sp2[0] >> 16) | (sp2[1] & 0xFFFF0000u)) : 0u;
-        const gq_f4 D2 =
-            gq_mfma16(__builtin_bit_cast(gq_half8, at), __builtin_bit_cast(gq_half8, bmt), zero4);
-        acc[mt] += d * D1[mt] - dmin * D2;
-      }
-    }
-  }
-
-  constexpr float OFF = (FMT == GQ_FMT_Q4_0) ? 8.f : (FMT == GQ_FMT_Q8_0) ? 128.f : 0.f;
-  float part[MT][2];
-#pragma unroll
-  for (int mt = 0; mt < MT; ++mt)
-#pragma unroll
-    for (int u = 0; u < 2; ++u)
-      part[mt][u] = kTwo24 * (acc[mt][2 * u] + acc[mt][2 * u + 1]) - OFF * cor[mt][u];
-  if constexpr (KSPLIT > 1) {
-    __shared__ float red[KSPLIT][MT * 2][64];
+  for (int rt = 0; rt < R; ++rt) {
+    const size_t row = (tile0 + rt) * 16 + r;
+    if (row >= (size_t)N) continue;
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
-      for (int u = 0; u < 2; ++u) red[wave][mt * 2 + u][lane] = part[mt][u];
-    __syncthreads();
-    if (wave != 0) return;
-#pragma unroll
-    for (int mt = 0; mt < MT; ++mt)
-#pragma unroll
-      for (int u = 0; u < 2; ++u) {
-        float s = 0.f;
-#pragma unroll
-        for (int q = 0; q < KSPLIT; ++q) s += red[q][mt * 2 + u][lane];
-        part[mt][u] = s;
+      for (int v = 0; v < NBC; ++v) {
+        const int b = 4 * mt + v;
+        if (b < nb) y[(size_t)b * N + row] = part[rt][mt][v];
       }
   }
-  const size_t row = t * 16 + r;
-  if (row >= (size_t)N) return;
-#pragma unroll
-  for (int mt = 0; mt < MT; ++mt)
-#pragma unroll
-    for (int u = 0; u < 2; ++u) {
-      const int b = 8 * mt + 2 * g + u;
-      if (b < nb) y[(size_t)b * N + row] = part[mt][u];
-    }
 }
 
-// GQ_GEMV_KSPLIT=1|2|4|8|16 overrides the K-split heuristic (for tuning).
-int env_ksplit() {
-  const char *e = getenv("GQ_GEMV_KSPLIT");
+// GQ_GEMV_KSPLIT=2|4|8|16 and GQ_GEMV_R=1|2 override the launch heuristic
+// (for tuning).
+int env_int(const char *name) {
+  const char *e = getenv(name);
   return e ? atoi(e) : 0;
 }
 
-// K-split: enough waves to cover the chip (~4 per SIMD), each wave holding at
-// most MAXC chunks in registers.
-template <int FMT>
-int pick_ksplit(size_t tiles, int C) {
+template <int FMT, int NBC, int MT, int R, bool PREP>
+int launch_r(const void *packed, const float *x, const void *ws, float *y, int N, int K, int nb, int ks,
+             hipStream_t s) {
   using F = Fmt<FMT>;
-  int ks = 1;
-  while (ks < 16 && (C + ks - 1) / ks > F::MAXC) ks *= 2;
-  while (ks < 16 && tiles * ks < 4096 && 2 * ks <= C) ks *= 2;
-  int e = env_ksplit();
-  if (e == 1 || e == 2 || e == 4 || e == 8 || e == 16)
-    if ((C + e - 1) / e <= F::MAXC) ks = e;
-  return ks;
-}
-
-template <int FMT, int NB>
-int launch_xl(const void *packed, const float *x, float *y, int N, int K, hipStream_t s) {
-  const int C = (int)gq_chunks(FMT, K);
-  const size_t tiles = gq_tiles(N);
-  const size_t sc_off = gq_sc_plane_offset(FMT, N, K);
-  const int ks = pick_ksplit<FMT>(tiles, C);
-  const size_t lds = (size_t)ks * xl_layout(Fmt<FMT>::CK * ((C + ks - 1) / ks), NB).wave_bytes;
-  const uint8_t *w = (const uint8_t *)packed;
-#define GQ_LAUNCH_KS(KS)                                                                                  \
-  hipLaunchKernelGGL((k_gemv_xl<FMT, NB, KS>), dim3((unsigned)tiles), dim3(64 * KS), lds, s, w, sc_off, x, y, \
-                     N, K, C)
-  switch (ks) {
-  case 1: GQ_LAUNCH_KS(1); break;
-  case 2: GQ_LAUNCH_KS(2); break;
-  case 4: GQ_LAUNCH_KS(4); break;
-  case 8: GQ_LAUNCH_KS(8); break;
-  default: GQ_LAUNCH_KS(16); break;
-  }
-#undef GQ_LAUNCH_KS
-  return gq_last_launch();
-}
-
-template <int FMT, int MT>
-int launch_xg(const void *packed, const void *ws, float *y, int N, int K, int nb, hipStream_t s) {
   const int C = (int)gq_chunks(FMT, K);
   const int Kp = (int)gq_kpad(FMT, K);
   const size_t tiles = gq_tiles(N);
+  const size_t wgs = (tiles + R - 1) / R;
   const size_t sc_off = gq_sc_plane_offset(FMT, N, K);
-  const _Float16 *xq = (const _Float16 *)ws;
-  const float *sf = (const float *)((const uint8_t *)ws + gq_xq_bytes(FMT, K, nb));
-  const uint32_t *sh = (const uint32_t *)((const uint8_t *)ws + gq_xq_bytes(FMT, K, nb) + gq_sf_bytes(FMT, K, nb));
-  const int ks = pick_ksplit<FMT>(tiles, C);
+  const int8_t *xl = PREP ? (const int8_t *)ws : nullptr;
+  const float *scl = PREP ? (const float *)((const uint8_t *)ws + gq_xl_bytes(FMT, K, nb)) : nullptr;
+  const size_t lds = PREP ? 0 : (size_t)ks * xl_layout(F::CK * ((C + ks - 1) / ks), NBC).wave_bytes;
   const uint8_t *w = (const uint8_t *)packed;
-#define GQ_LAUNCH_KS(KS)                                                                                     \
-  hipLaunchKernelGGL((k_gemv_xg<FMT, MT, KS>), dim3((unsigned)tiles), dim3(64 * KS), 0, s, w, sc_off, xq, sf, sh, \
-                     y, N, C, Kp, nb)
+#define GQ_LAUNCH_KS(KS)                                                                                          \
+  hipLaunchKernelGGL((k_gemv_q<FMT, NBC, MT, R, KS, PREP>), dim3((unsigned)wgs), dim3(64 * KS), lds, s, w, sc_off, \
+                     x, xl, scl, y, N, K, C, Kp, nb)
   switch (ks) {
-  case 1: GQ_LAUNCH_KS(1); break;
   case 2: GQ_LAUNCH_KS(2); break;
   case 4: GQ_LAUNCH_KS(4); break;
   case 8: GQ_LAUNCH_KS(8); break;
@@ -527,13 +451,67 @@ int launch_xg(const void *packed, const void *ws, float *y, int N, int K, int nb
   }
 #undef GQ_LAUNCH_KS
   return gq_last_launch();
+}
+
+}  // namespace
+
+// Launch plan: R row tiles per workgroup (2 when there are many tiles: halves
+// the activation staging per weight) and KSPLIT waves, so that every wave holds
+// at most MAXC / R chunks and the grid has enough waves to keep HBM busy.
+// Every wave's chunk range [C*w/KSPLIT, C*(w+1)/KSPLIT) lies inside [0, C).
+extern "C" int gq_gemv_plan(int fmt, size_t N, size_t K, int batch, int *R_out, int *ksplit_out,
+                            int *chunks_per_wave_out) {
+  GQ_TRY(gq_check_shape(fmt, N, K));
+  GQ_CHECK(batch >= 1 && batch <= GQ_MAX_BATCH, GQ_ERR_UNSUPPORTED);
+  const int f = gq_fmt_is_q4k(fmt) ? GQ_FMT_Q4_K : fmt;
+  const int maxc = f == GQ_FMT_Q4_K ? Fmt<GQ_FMT_Q4_K>::MAXC : f == GQ_FMT_Q8_0 ? Fmt<GQ_FMT_Q8_0>::MAXC
+                                                                                  : Fmt<GQ_FMT_Q4_0>::MAXC;
+  const int C = (int)gq_chunks(f, K);
+  const size_t tiles = gq_tiles(N);
+  const int mt = batch <= 4 ? 1 : (batch + 3) / 4;
+  int R = (tiles >= 512 && C >= 4) ? 2 : 1;
+  const int er = env_int("GQ_GEMV_R");
+  if (er == 1 || er == 2) R = er;
+  if ((C + 15) / 16 > maxc / 2) R = 1;  // very long K: keep every register for chunks
+  // 1024-thread workgroups cap a wave at 128 VGPRs: keep wide batches at <= 8 waves
+  const int cap = mt >= 2 ? 8 : 16;
+  if (R == 2 && (C + cap - 1) / cap > maxc / 2) R = 1;
+  // fewest waves per workgroup that fit the register budget (measured best:
+  // long per-wave chunk lists, every workgroup resident in the first round),
+  // more only when the grid would otherwise have too few waves
+  int ks = 2;
+  while (ks < 16 && (C + ks - 1) / ks > maxc / R) ks *= 2;
+  while (ks < cap && ((tiles + R - 1) / R) * ks < 1024 && 2 * ks <= C) ks *= 2;
+  const int e = env_int("GQ_GEMV_KSPLIT");
+  if ((e == 2 || e == 4 || e == 8 || e == 16) && (C + e - 1) / e <= maxc / R) ks = e;
+  if (R_out) *R_out = R;
+  if (ksplit_out) *ksplit_out = ks;
+  if (chunks_per_wave_out) *chunks_per_wave_out = (C + ks - 1) / ks;
+  return GQ_OK;
+}
+
+namespace {
+
+template <int FMT, int NBC, int MT, bool PREP>
+int launch_shape(const void *packed, const float *x, const void *ws, float *y, int N, int K, int nb, hipStream_t s) {
+  int R = 1, ks = 2, cpw = 0;
+  GQ_TRY(gq_gemv_plan(FMT, N, K, nb, &R, &ks, &cpw));
+  if (cpw > Fmt<FMT>::MAXC / R) return GQ_ERR_INVALID_ARGS;  // the kernel's register budget
+  if (R == 2) return launch_r<FMT, NBC, MT, 2, PREP>(packed, x, ws, y, N, K, nb, ks, s);
+  return launch_r<FMT, NBC, MT, 1, PREP>(packed, x, ws, y, N, K, nb, ks, s);
 }
 
 template <int FMT>
 int launch_gemv(const void *packed, const float *x, const void *ws, float *y, int N, int K, int nb, hipStream_t s) {
-  if (x) return nb == 1 ? launch_xl<FMT, 1>(packed, x, y, N, K, s) : launch_xl<FMT, 2>(packed, x, y, N, K, s);
-  if (nb <= 8) return launch_xg<FMT, 1>(packed, ws, y, N, K, nb, s);
-  return launch_xg<FMT, 2>(packed, ws, y, N, K, nb, s);
+  if (x) {  // fused staging, batch <= 4
+    if (nb == 1) return launch_shape<FMT, 1, 1, false>(packed, x, nullptr, y, N, K, nb, s);
+    if (nb == 2) return launch_shape<FMT, 2, 1, false>(packed, x, nullptr, y, N, K, nb, s);
+    return launch_shape<FMT, 4, 1, false>(packed, x, nullptr, y, N, K, nb, s);
+  }
+  if (nb <= 4) return launch_shape<FMT, 4, 1, true>(packed, nullptr, ws, y, N, K, nb, s);
+  if (nb <= 8) return launch_shape<FMT, 4, 2, true>(packed, nullptr, ws, y, N, K, nb, s);
+  if (nb <= 12) return launch_shape<FMT, 4, 3, true>(packed, nullptr, ws, y, N, K, nb, s);
+  return launch_shape<FMT, 4, 4, true>(packed, nullptr, ws, y, N, K, nb, s);
 }
 
 int dispatch(int fmt, const void *packed, const float *x, const void *ws, float *y, int N, int K, int nb,
@@ -548,11 +526,11 @@ int dispatch(int fmt, const void *packed, const float *x, const void *ws, float 
 }  // namespace
 
 // batch sizes whose activations are staged in-kernel (no workspace)
-static inline bool gq_gemv_fused(int batch) { return batch <= 2; }
+static inline bool gq_gemv_fused(int batch) { return batch <= 4; }
 
 extern "C" size_t gq_gemv_workspace_bytes(int fmt, size_t K, int batch) {
   if (!gq_fmt_valid(fmt) || batch < 1 || batch > GQ_MAX_BATCH || K > GQ_MAX_DIM) return 0;
-  return gq_xq_bytes(fmt, K, batch) + gq_sf_bytes(fmt, K, batch) + gq_sq_bytes(fmt, K, batch);
+  return gq_xl_bytes(fmt, K, batch) + gq_scl_bytes(fmt, K, batch);
 }
 
 extern "C" int gq_gemv_prep(int fmt, const float *x, size_t K, int batch, void *ws, size_t ws_bytes,

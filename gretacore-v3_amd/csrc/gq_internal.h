@@ -35,16 +35,13 @@ static inline int gq_check_shape(int fmt, size_t N, size_t K) {
 static inline size_t gq_align256(size_t v) { return (v + 255) & ~(size_t)255; }
 // padded K of the T16 layout
 static inline size_t gq_kpad(int fmt, size_t K) { return gq_chunks(fmt, K) * gq_chunk_k(fmt); }
-// GEMV workspace: xq fp16 [2B][Kp], sf fp32 [B][Kp/32] (block sums of x),
-// then (Q4_K) sq fp16 (hi, lo) pairs of the same sums [B][Kp/32]
-static inline size_t gq_xq_bytes(int fmt, size_t K, int B) {
-  return gq_align256((size_t)2 * B * gq_kpad(fmt, K) * 2);
+// GEMV workspace (batch > 4): int8 limbs [B][2][Kp] then a zero region of Kp
+// bytes, then per (batch row, 32-block) float4 (s, S, s / 254, 0).
+static inline size_t gq_xl_bytes(int fmt, size_t K, int B) {
+  return gq_align256(((size_t)2 * B + 1) * gq_kpad(fmt, K));
 }
-static inline size_t gq_sf_bytes(int fmt, size_t K, int B) {
-  return gq_align256((size_t)B * (gq_kpad(fmt, K) / 32) * 4);
-}
-static inline size_t gq_sq_bytes(int fmt, size_t K, int B) {
-  return gq_fmt_is_q4k(fmt) ? gq_align256((size_t)B * (gq_kpad(fmt, K) / 32) * 4) : 0;
+static inline size_t gq_scl_bytes(int fmt, size_t K, int B) {
+  return gq_align256((size_t)B * (gq_kpad(fmt, K) / 32) * 16);
 }
 
 // Zero-fills n floats with a kernel (no memset node, so it is safe to capture).

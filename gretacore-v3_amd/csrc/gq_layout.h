@@ -9,34 +9,31 @@
 //   Q4_K 256 weights / 144 B: fp16 d | fp16 dmin | 12 B 6-bit codes | 128 B nibbles
 //
 // T16 layout.  Rows are grouped into row tiles of 16 (N is padded up to a
-// multiple of 16 with all-zero rows).  Within a tile, lane l = 16*g + r of a
-// wavefront owns row r and "word slot" g (g = 0..3).  The K axis is cut into
-// chunks; every chunk of a row tile is one contiguous 1 KiB (or 2 KiB) record so
-// that one dwordx4 load per lane streams it with perfect coalescing.
+// multiple of 16 with all-zero rows).  The K axis is cut into chunks; every
+// chunk of a row tile is one contiguous 1 KiB (or 2 KiB) record, so one
+// dwordx4 load per lane streams it with perfect coalescing.  Within a chunk,
+// lane l = 16*g + r of a wavefront owns row r; for each int8-MFMA step m
+// (64 k) it holds the 16 elements 16*(g&1) .. +15 of 32-element (sub-)block
+// 2m + (g>>1) -- the lane's share of a v_mfma_i32_16x16x64_i8 B operand.
 //
-//  canonical word: a 32-bit word that holds 8 consecutive elements e0..e7 of a
-//  32-element (sub-)block, element i at nibble position (i>>1) | ((i&1)<<2).
-//  Then ((w >> 4s) & 0x000F000F) holds elements (2s, 2s+1) in its two 16-bit
-//  halves, which turns into an fp16 pair with one OR and one packed subtract.
+//  code group: 16 four-bit codes in 8 bytes, byte b = slot 8(b>>2)+(b&3) in the
+//  low nibble and slot 8(b>>2)+(b&3)+4 in the high nibble, so that one AND
+//  (and one shift) per word yields 4 codes as bytes in slot order.
 //
-//  Q4_0: chunk = 4 blocks (128 k).  C = ceil(K/128) chunks per row.
-//    qs plane   [tile][C][64 lanes][4 words] : lane l word j = canonical word g of
-//               block 4c+j of row r                                 1024 B/chunk
-//    d plane    [tile][C][16 rows][4] fp16                           128 B/chunk
+//  Q4_0: chunk = 4 blocks (128 k, two MFMA steps).  C = ceil(K/128).
+//    qs plane  [tile][C][64 lanes][2 steps][8 B code group]      1024 B/chunk
+//    d plane   [tile][C][16 rows][d0 d2 d1 d3] fp16               128 B/chunk
 //  Q8_0: chunk = 4 blocks (128 k).
-//    qs plane   [tile][C][2 parts][64 lanes][16 B] : part p lane l = bytes
-//               8g..8g+7 of block 4c+2p then of block 4c+2p+1 of row r
-//                                                                   2048 B/chunk
-//    d plane    as Q4_0                                              128 B/chunk
-//  Q4_K: chunk = 1 super-block (256 k).  S = K/256 chunks per row.
-//    qs plane   [tile][S][2 halves][64 lanes][16 B] : half h lane l = the 4
-//               canonical words of sub-block 2g+h of row r           2048 B/chunk
-//    meta plane [tile][S][16 rows][16 B] : d, dmin (fp16) | W1 | W2 | W3 with
-//               byte g of W1 = sc[2g]   | (m[2g]   & 3) << 6
-//               byte g of W2 = sc[2g+1] | (m[2g+1] & 3) << 6
-//               byte g of W3 = (m[2g] >> 2) | (m[2g+1] >> 2) << 4    256 B/chunk
+//    qs plane  [tile][C][2 steps][64 lanes][16 x int8]            2048 B/chunk
+//    d plane   as Q4_0                                            128 B/chunk
+//  Q4_K: chunk = 1 super-block (256 k, four MFMA steps).  S = K/256.
+//    qs plane  [tile][S][2 step pairs][64 lanes][2 steps][8 B]    2048 B/chunk
+//    meta plane [tile][S][16 rows][16 B]: d, dmin (fp16) | W1 | W2 | W3 with
+//              byte i of W1 = sc[2i]   | (m[2i]   & 3) << 6
+//              byte i of W2 = sc[2i+1] | (m[2i+1] & 3) << 6
+//              byte i of W3 = (m[2i] >> 2) | (m[2i+1] >> 2) << 4   256 B/chunk
 // Padding blocks (K not a multiple of 128 for Q4_0/Q8_0) carry d = 0 and zero
-// weights, so they add exact zeros.  Bytes per weight are unchanged by the
+// codes, so they add exact zeros.  Bytes per weight are unchanged by the
 // repack: 0.5625 (Q4_0, Q4_K) and 1.0625 (Q8_0).
 #ifndef GQ_LAYOUT_H
 #define GQ_LAYOUT_H
@@ -91,7 +88,5 @@ GQ_LHD size_t gq_packed_bytes(int fmt, size_t N, size_t K) {
 GQ_LHD size_t gq_layout_gguf_bytes(int fmt, size_t N, size_t K) {
   return N * (K / gq_block_elems(fmt)) * gq_block_bytes(fmt);
 }
-// nibble position of element i (0..7) inside a canonical word
-GQ_LHD int gq_canon_pos(int i) { return (i >> 1) | ((i & 1) << 2); }
 
 #endif

@@ -27,9 +27,7 @@ k_gemm_q8_i8(const uint8_t *__restrict__ w, size_t sc_off, const int8_t *__restr
   const gq_i16v zero = {};
   for (int blk = 0; blk < nb; ++blk) {
     gq_i4 af = *reinterpret_cast<const gq_i4 *>(qa + (size_t)am * K + blk * 32 + 16 * hl);
-    gq_u2 b0 = gq_ld8(w + gq_q8_0_byte_off(bn, blk, 16 * hl, C));
-    gq_u2 b1 = gq_ld8(w + gq_q8_0_byte_off(bn, blk, 16 * hl + 8, C));
-    gq_i4 bf = {(int)b0[0], (int)b0[1], (int)b1[0], (int)b1[1]};
+    gq_i4 bf = *reinterpret_cast<const gq_i4 *>(w + gq_q8_0_half_off(bn, blk, hl, C));
     float dw = gq_h2f(*reinterpret_cast<const uint16_t *>(w + sc_off + gq_q4_0_d_off(bn, blk, C)));
     gq_i16v D = __builtin_amdgcn_mfma_i32_32x32x32_i8(af, bf, zero, 0, 0, 0);
 #pragma unroll

@@ -85,42 +85,43 @@ k_dequant_t16(int fmt, const uint8_t *__restrict__ w, float *__restrict__ out, i
   if (i >= (size_t)N * nb) return;
   size_t n = i / nb, blk = i % nb;
   float y[32];
+  const size_t C = gq_chunks(fmt, K);
+  const uint8_t *scp = w + gq_sc_plane_offset(fmt, N, K);
   if (fmt == GQ_FMT_Q4_0) {
-    size_t C = gq_chunks(fmt, K);
-    const uint8_t *sc = w + gq_sc_plane_offset(fmt, N, K);
-    float d = gq_h2f(gq_rd16(sc + gq_q4_0_d_off(n, blk, C)));
+    float d = gq_h2f(gq_rd16(scp + gq_q4_0_d_off(n, blk, C)));
 #pragma unroll
-    for (int w8 = 0; w8 < 4; ++w8) {
-      uint32_t word = *reinterpret_cast<const uint32_t *>(w + gq_q4_0_word_off(n, blk, w8, C));
+    for (int eh = 0; eh < 2; ++eh) {
+      uint8_t c[16];
+      gq_unpack_codes16(*reinterpret_cast<const uint64_t *>(w + gq_q4_0_grp_off(n, blk, eh, C)), c);
 #pragma unroll
-      for (int e = 0; e < 8; ++e)
-        y[8 * w8 + e] = (float)((int)((word >> (4 * gq_canon_pos(e))) & 15u) - 8) * d;
+      for (int s = 0; s < 16; ++s) y[16 * eh + s] = (float)((int)c[s] - 8) * d;
     }
   } else if (fmt == GQ_FMT_Q8_0) {
-    size_t C = gq_chunks(fmt, K);
-    const uint8_t *sc = w + gq_sc_plane_offset(fmt, N, K);
-    float d = gq_h2f(gq_rd16(sc + gq_q4_0_d_off(n, blk, C)));
+    float d = gq_h2f(gq_rd16(scp + gq_q4_0_d_off(n, blk, C)));
 #pragma unroll
-    for (int b = 0; b < 32; ++b) y[b] = (float)(int8_t)w[gq_q8_0_byte_off(n, blk, b, C)] * d;
+    for (int eh = 0; eh < 2; ++eh) {
+      const int8_t *q = reinterpret_cast<const int8_t *>(w + gq_q8_0_half_off(n, blk, eh, C));
+#pragma unroll
+      for (int s = 0; s < 16; ++s) y[16 * eh + s] = (float)q[s] * d;
+    }
   } else {
-    size_t S = gq_chunks(fmt, K);
     size_t s = blk >> 3;
     int j = (int)(blk & 7);
-    const uint32_t *meta = reinterpret_cast<const uint32_t *>(
-        w + gq_sc_plane_offset(fmt, N, K) + gq_q4k_meta_off(n, s, S));
-    float d = gq_h2f(meta[0] & 0xFFFFu), dmin = gq_h2f(meta[0] >> 16);
-    uint32_t sc0, m0, sc1, m1;
-    gq_q4k_codes(meta[1], meta[2], meta[3], j >> 1, sc0, m0, sc1, m1);
-    uint32_t scj = (j & 1) ? sc1 : sc0, mj = (j & 1) ? m1 : m0;
+    const uint32_t *meta = reinterpret_cast<const uint32_t *>(scp + gq_q4k_meta_off(n, s, C));
+    uint32_t mv[4] = {meta[0], meta[1], meta[2], meta[3]};
+    float d = gq_h2f(mv[0] & 0xFFFFu), dmin = gq_h2f(mv[0] >> 16);
+    uint32_t scj, mj;
+    gq_q4k_meta_codes(mv, j, &scj, &mj);
     float scale = d * (float)scj;
     float minv = dmin * (float)mj;
 #pragma unroll
-    for (int w8 = 0; w8 < 4; ++w8) {
-      uint32_t word = *reinterpret_cast<const uint32_t *>(w + gq_q4k_word_off(n, s, j, w8, S));
+    for (int eh = 0; eh < 2; ++eh) {
+      uint8_t c[16];
+      gq_unpack_codes16(*reinterpret_cast<const uint64_t *>(w + gq_q4k_grp_off(n, s, j, eh, C)), c);
 #pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        float p = scale * (float)((word >> (4 * gq_canon_pos(e))) & 15u);
-        y[8 * w8 + e] = p - minv;
+      for (int e = 0; e < 16; ++e) {
+        float p = scale * (float)c[e];
+        y[16 * eh + e] = p - minv;
       }
     }
   }
@@ -140,12 +141,12 @@ k_repack_q4_0(const uint8_t *__restrict__ src, uint8_t *__restrict__ dst, int N,
   if (i >= Np * nbp) return;
   size_t n = i / nbp, blk = i % nbp;
   size_t nb = (size_t)K / 32;
-  uint32_t words[4] = {0, 0, 0, 0}, d16 = 0;
-  if (n < (size_t)N && blk < nb) gq_q4_0_canon(src + (n * nb + blk) * 18, words, &d16);
-  for (int w8 = 0; w8 < 4; ++w8)
-    *reinterpret_cast<uint32_t *>(dst + gq_q4_0_word_off(n, blk, w8, C)) = words[w8];
-  *reinterpret_cast<uint16_t *>(dst + gq_sc_plane_offset(GQ_FMT_Q4_0, N, K) +
-                                gq_q4_0_d_off(n, blk, C)) = (uint16_t)d16;
+  uint64_t grp[2] = {0, 0};
+  uint32_t d16 = 0;
+  if (n < (size_t)N && blk < nb) gq_q4_0_groups(src + (n * nb + blk) * 18, grp, &d16);
+  for (int eh = 0; eh < 2; ++eh) *reinterpret_cast<uint64_t *>(dst + gq_q4_0_grp_off(n, blk, eh, C)) = grp[eh];
+  *reinterpret_cast<uint16_t *>(dst + gq_sc_plane_offset(GQ_FMT_Q4_0, N, K) + gq_q4_0_d_off(n, blk, C)) =
+      (uint16_t)d16;
 }
 
 __global__ void __launch_bounds__(256)
@@ -157,20 +158,16 @@ k_repack_q8_0(const uint8_t *__restrict__ src, uint8_t *__restrict__ dst, int N,
   size_t nb = (size_t)K / 32;
   bool in = n < (size_t)N && blk < nb;
   const uint8_t *b = src + (n * nb + blk) * 34;
-  for (int g = 0; g < 4; ++g) {
-    uint32_t lo = 0, hi = 0;
-    if (in) {
-      lo = (uint32_t)b[2 + 8 * g] | ((uint32_t)b[3 + 8 * g] << 8) | ((uint32_t)b[4 + 8 * g] << 16) |
-           ((uint32_t)b[5 + 8 * g] << 24);
-      hi = (uint32_t)b[6 + 8 * g] | ((uint32_t)b[7 + 8 * g] << 8) | ((uint32_t)b[8 + 8 * g] << 16) |
-           ((uint32_t)b[9 + 8 * g] << 24);
-    }
-    uint32_t *o = reinterpret_cast<uint32_t *>(dst + gq_q8_0_byte_off(n, blk, 8 * g, C));
-    o[0] = lo;
-    o[1] = hi;
+  for (int eh = 0; eh < 2; ++eh) {
+    uint32_t wv[4] = {0, 0, 0, 0};
+    if (in)
+      for (int q = 0; q < 4; ++q)
+        wv[q] = (uint32_t)b[2 + 16 * eh + 4 * q] | ((uint32_t)b[3 + 16 * eh + 4 * q] << 8) |
+                ((uint32_t)b[4 + 16 * eh + 4 * q] << 16) | ((uint32_t)b[5 + 16 * eh + 4 * q] << 24);
+    *reinterpret_cast<gq_u4 *>(dst + gq_q8_0_half_off(n, blk, eh, C)) = gq_u4{wv[0], wv[1], wv[2], wv[3]};
   }
-  *reinterpret_cast<uint16_t *>(dst + gq_sc_plane_offset(GQ_FMT_Q8_0, N, K) +
-                                gq_q4_0_d_off(n, blk, C)) = (uint16_t)(in ? gq_rd16(b) : 0u);
+  *reinterpret_cast<uint16_t *>(dst + gq_sc_plane_offset(GQ_FMT_Q8_0, N, K) + gq_q4_0_d_off(n, blk, C)) =
+      (uint16_t)(in ? gq_rd16(b) : 0u);
 }
 
 __global__ void __launch_bounds__(256)
@@ -179,76 +176,80 @@ k_repack_q4_k(const uint8_t *__restrict__ src, uint8_t *__restrict__ dst, int N,
   size_t i = (size_t)blockIdx.x * 256 + threadIdx.x;
   if (i >= Np * S) return;
   size_t n = i / S, s = i % S;
-  uint32_t words[8][4], meta[4];
+  uint64_t grp[16];
+  uint32_t meta[4] = {0, 0, 0, 0};
   if (n < (size_t)N) {
-    gq_q4k_canon(ggml, src + (n * S + s) * 144, words, meta);
+    gq_q4k_groups(ggml, src + (n * S + s) * 144, grp, meta);
   } else {
-    for (int j = 0; j < 8; ++j)
-      for (int w8 = 0; w8 < 4; ++w8) words[j][w8] = 0;
-    meta[0] = meta[1] = meta[2] = meta[3] = 0;
+    for (int q = 0; q < 16; ++q) grp[q] = 0;
   }
   for (int j = 0; j < 8; ++j)
-    for (int w8 = 0; w8 < 4; ++w8)
-      *reinterpret_cast<uint32_t *>(dst + gq_q4k_word_off(n, s, j, w8, S)) = words[j][w8];
-  uint32_t *mo = reinterpret_cast<uint32_t *>(dst + gq_sc_plane_offset(GQ_FMT_Q4_K, N, K) +
-                                              gq_q4k_meta_off(n, s, S));
-  mo[0] = meta[0];
-  mo[1] = meta[1];
-  mo[2] = meta[2];
-  mo[3] = meta[3];
+    for (int eh = 0; eh < 2; ++eh)
+      *reinterpret_cast<uint64_t *>(dst + gq_q4k_grp_off(n, s, j, eh, S)) = grp[2 * j + eh];
+  *reinterpret_cast<gq_u4 *>(dst + gq_sc_plane_offset(GQ_FMT_Q4_K, N, K) + gq_q4k_meta_off(n, s, S)) =
+      gq_u4{meta[0], meta[1], meta[2], meta[3]};
 }
 
 // ---------------------------------------------------------------------------
-// Activation preparation for the GEMV (decode) path.  x f32 [B][K] ->
-//   xq  fp16 [2B][Kp]: row 2b = hi = fp16(x), row 2b+1 = lo = fp16(x - hi)
-//   sf  f32 [B][Kp/32]: the fp32 sum of each 32-element block of x
-//   sq  (Q4_K only) uint32 [B][Kp/32]: fp16 pair (hi, lo) of the same sums.
-// Elements k >= K are written as zeros.  One thread per 32 elements.
+// Activation preparation for the GEMV with batch > 4.  x f32 [B][K] ->
+//   limbs int8 [B][2][Kp]: x ~ s * (a + b / 254) per 32-block, s = amax / 127
+//   zero  int8 [Kp]
+//   scl   float4 [B][Kp/32]: (s, S, s / 254, 0), S = sum of the represented block
+// Elements k >= K are zeros.  One thread per 32-block.
 // ---------------------------------------------------------------------------
 __global__ void __launch_bounds__(256)
-k_prep_x(const float *__restrict__ x, _Float16 *__restrict__ xq, float *__restrict__ sf,
-         uint32_t *__restrict__ sq, int B, int K, int Kp) {
-  int nsub = Kp / 32;
-  int i = blockIdx.x * 256 + threadIdx.x;
-  if (i >= B * nsub) return;
-  int b = i / nsub, j = i % nsub;
+k_prep_x(const float *__restrict__ x, int8_t *__restrict__ xl, float *__restrict__ scl, int B, int K, int Kp) {
+  const int nblk = Kp / 32;
+  const int i = blockIdx.x * 256 + threadIdx.x;
+  if (i >= B * nblk) return;
+  const int b = i / nblk, j = i % nblk;
   const float *xr = x + (size_t)b * K + 32 * j;
-  bool full = 32 * j + 32 <= K;
   float v[32];
-  if (full) {
+  if (32 * j + 32 <= K) {
     const float4 *p = reinterpret_cast<const float4 *>(xr);
 #pragma unroll
     for (int q = 0; q < 8; ++q) {
-      float4 t = p[q];
+      const float4 t = p[q];
       v[4 * q] = t.x; v[4 * q + 1] = t.y; v[4 * q + 2] = t.z; v[4 * q + 3] = t.w;
     }
   } else {
 #pragma unroll
-    for (int e = 0; e < 32; ++e) v[e] = (32 * j + e < K) ? xr[e] : 0.0f;
+    for (int e = 0; e < 32; ++e) v[e] = 0.0f;
   }
-  gq_half8 hi[4], lo[4];
-  float s = 0.0f;
+  float amax = 0.f, s = 0.f;
 #pragma unroll
-  for (int e = 0; e < 32; ++e) {
-    _Float16 h = (_Float16)v[e];
-    hi[e >> 3][e & 7] = h;
-    lo[e >> 3][e & 7] = (_Float16)(v[e] - (float)h);
-    s += v[e];
-  }
-  gq_half8 *ph = reinterpret_cast<gq_half8 *>(xq + (size_t)(2 * b) * Kp + 32 * j);
-  gq_half8 *pl = reinterpret_cast<gq_half8 *>(xq + (size_t)(2 * b + 1) * Kp + 32 * j);
+  for (int e = 0; e < 32; ++e) amax = fmaxf(amax, fabsf(v[e]));
+  const float inv = amax > 0.f ? 127.0f / amax : 0.f;
+  const float sx = amax * (1.0f / 127.0f);
+  uint32_t la[8], lb[8];
 #pragma unroll
-  for (int q = 0; q < 4; ++q) {
-    ph[q] = hi[q];
-    pl[q] = lo[q];
+  for (int q = 0; q < 8; ++q) {
+    uint32_t wa = 0, wb = 0;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const float t = v[4 * q + e] * inv;
+      const float a = rintf(t);
+      const float bb = rintf((t - a) * 254.0f);
+      s += a * 254.0f + bb;  // exact integer
+      wa |= ((uint32_t)(int)a & 0xFFu) << (8 * e);
+      wb |= ((uint32_t)(int)bb & 0xFFu) << (8 * e);
+    }
+    la[q] = wa;
+    lb[q] = wb;
   }
-  sf[(size_t)b * nsub + j] = s;
-  if (sq) {
-    _Float16 sh = (_Float16)s;
-    _Float16 sl = (_Float16)(s - (float)sh);
-    gq_half2 pr = {sh, sl};
-    sq[(size_t)b * nsub + j] = gq_h2_bits(pr);
+  gq_u4 *pa = reinterpret_cast<gq_u4 *>(xl + (size_t)(2 * b) * Kp + 32 * j);
+  gq_u4 *pb = reinterpret_cast<gq_u4 *>(xl + (size_t)(2 * b + 1) * Kp + 32 * j);
+  pa[0] = gq_u4{la[0], la[1], la[2], la[3]};
+  pa[1] = gq_u4{la[4], la[5], la[6], la[7]};
+  pb[0] = gq_u4{lb[0], lb[1], lb[2], lb[3]};
+  pb[1] = gq_u4{lb[4], lb[5], lb[6], lb[7]};
+  if (b == 0) {
+    gq_u4 *pz = reinterpret_cast<gq_u4 *>(xl + (size_t)2 * B * Kp + 32 * j);
+    pz[0] = gq_u4{0u, 0u, 0u, 0u};
+    pz[1] = gq_u4{0u, 0u, 0u, 0u};
   }
+  s *= sx * (1.0f / 254.0f);  // block sum of the represented values
+  *reinterpret_cast<gq_f4 *>(scl + 4 * ((size_t)b * nblk + j)) = gq_f4{sx, s, sx * (1.0f / 254.0f), 0.f};
 }
 
 // Activation conversion for the GEMM (prefill) path: bf16 / f32 / f16 [M][K]
@@ -387,13 +388,11 @@ extern "C" int gq_repack(int fmt, const void *gguf, size_t N, size_t K, void *pa
 }
 
 int gq_launch_prep_x(int fmt, const float *x, void *ws, int B, int K, hipStream_t s) {
-  int Kp = (int)(gq_chunks(fmt, K) * gq_chunk_k(fmt));
-  _Float16 *xq = (_Float16 *)ws;
-  float *sf = (float *)((uint8_t *)ws + gq_xq_bytes(fmt, K, B));
-  uint32_t *sq = gq_fmt_is_q4k(fmt) ? (uint32_t *)((uint8_t *)ws + gq_xq_bytes(fmt, K, B) + gq_sf_bytes(fmt, K, B))
-                                    : nullptr;
-  int n = B * (Kp / 32);
-  hipLaunchKernelGGL(k_prep_x, dim3(blocks_for(n)), dim3(256), 0, s, x, xq, sf, sq, B, K, Kp);
+  const int Kp = (int)gq_kpad(fmt, K);
+  int8_t *xl = (int8_t *)ws;
+  float *scl = (float *)((uint8_t *)ws + gq_xl_bytes(fmt, K, B));
+  const int n = B * (Kp / 32);
+  hipLaunchKernelGGL(k_prep_x, dim3(blocks_for(n)), dim3(256), 0, s, x, xl, scl, B, K, Kp);
   return gq_last_launch();
 }
 

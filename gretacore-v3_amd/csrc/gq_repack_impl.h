@@ -14,32 +14,50 @@
 
 GQ_HD uint32_t gq_rd16(const uint8_t *p) { return (uint32_t)p[0] | ((uint32_t)p[1] << 8); }
 
-// Build the canonical word for elements 8*w8 .. 8*w8+7 of a 32-element block
-// whose element e has 4-bit value nib(e).
-template <typename NibFn>
-GQ_HD uint32_t gq_canon_word(int w8, NibFn nib) {
-  uint32_t w = 0;
-  for (int i = 0; i < 8; ++i)
-    w |= (uint32_t)(nib(8 * w8 + i) & 15u) << (4 * gq_canon_pos(i));
-  return w;
+// A T16 "code group": the 16 codes of 16 consecutive elements of a block packed
+// into 8 bytes.  Byte b holds slot 8*(b>>2) + (b&3) in its low nibble and
+// slot 8*(b>>2) + (b&3) + 4 in its high nibble, so that with the two words w0,
+// w1 of the group
+//   w0 & 0x0F0F0F0F, (w0 >> 4) & 0x0F0F0F0F, w1 & 0x0F0F0F0F, (w1 >> 4) & 0x0F0F0F0F
+// are the 16 codes as bytes in slot order (an int8 MFMA operand).
+GQ_HD uint64_t gq_pack_codes16(const uint8_t codes[16]) {
+  uint64_t v = 0;
+  for (int b = 0; b < 8; ++b) {
+    int s = 8 * (b >> 2) + (b & 3);
+    v |= (uint64_t)((codes[s] & 15u) | ((codes[s + 4] & 15u) << 4)) << (8 * b);
+  }
+  return v;
+}
+GQ_HD void gq_unpack_codes16(uint64_t v, uint8_t codes[16]) {
+  for (int b = 0; b < 8; ++b) {
+    int s = 8 * (b >> 2) + (b & 3);
+    uint32_t byte = (uint32_t)(v >> (8 * b)) & 0xFFu;
+    codes[s] = (uint8_t)(byte & 15u);
+    codes[s + 4] = (uint8_t)(byte >> 4);
+  }
 }
 
 // ---- Q4_0 ----------------------------------------------------------------
 // GGUF Q4_0: byte j holds element j (low nibble) and element j+16 (high).
-GQ_HD void gq_q4_0_canon(const uint8_t *blk, uint32_t words[4], uint32_t *d16) {
+GQ_HD uint32_t gq_q4_0_code(const uint8_t *blk, int e) {
   const uint8_t *qs = blk + 2;
-  *d16 = gq_rd16(blk);
-  for (int w8 = 0; w8 < 4; ++w8)
-    words[w8] = gq_canon_word(w8, [&](int e) -> uint32_t {
-      return e < 16 ? (qs[e] & 15u) : (qs[e - 16] >> 4);
-    });
+  return e < 16 ? (qs[e] & 15u) : (qs[e - 16] >> 4);
 }
-GQ_HD void gq_q4_0_uncanon(const uint32_t words[4], uint32_t d16, uint8_t *blk) {
+// GGUF Q4_0 block -> the two code groups (elements 0..15, 16..31) and d.
+GQ_HD void gq_q4_0_groups(const uint8_t *blk, uint64_t grp[2], uint32_t *d16) {
+  *d16 = gq_rd16(blk);
+  for (int eh = 0; eh < 2; ++eh) {
+    uint8_t c[16];
+    for (int s = 0; s < 16; ++s) c[s] = (uint8_t)gq_q4_0_code(blk, 16 * eh + s);
+    grp[eh] = gq_pack_codes16(c);
+  }
+}
+GQ_HD void gq_q4_0_from_groups(const uint64_t grp[2], uint32_t d16, uint8_t *blk) {
   blk[0] = (uint8_t)(d16 & 0xFF);
   blk[1] = (uint8_t)(d16 >> 8);
   uint8_t q[32];
-  for (int w8 = 0; w8 < 4; ++w8)
-    for (int i = 0; i < 8; ++i) q[8 * w8 + i] = (words[w8] >> (4 * gq_canon_pos(i))) & 15u;
+  gq_unpack_codes16(grp[0], q);
+  gq_unpack_codes16(grp[1], q + 16);
   for (int j = 0; j < 16; ++j) blk[2 + j] = (uint8_t)(q[j] | (q[j + 16] << 4));
 }
 
@@ -107,37 +125,49 @@ GQ_HD void gq_q4k_set_nib(int ggml, uint8_t *qs, int j, int e, uint32_t v) {
     *b = (j & 1) ? (uint8_t)((*b & 0x0F) | (v << 4)) : (uint8_t)((*b & 0xF0) | v);
   }
 }
-// GGUF Q4_K super-block -> canonical: words[8][4] (sub-block j, word w8) and
-// the 16-byte meta record (d | dmin | W1 | W2 | W3).
-GQ_HD void gq_q4k_canon(int ggml, const uint8_t *blk, uint32_t words[8][4], uint32_t meta[4]) {
+// GGUF Q4_K super-block -> 16 code groups (sub-block j, half eh -> grp[2j+eh])
+// and the 16-byte meta record (d | dmin | W1 | W2 | W3):
+//   byte i of W1 = sc[2i]   | (m[2i]   & 3) << 6
+//   byte i of W2 = sc[2i+1] | (m[2i+1] & 3) << 6
+//   byte i of W3 = (m[2i] >> 2) | (m[2i+1] >> 2) << 4
+GQ_HD void gq_q4k_groups(int ggml, const uint8_t *blk, uint64_t grp[16], uint32_t meta[4]) {
   uint8_t sc[8], m[8];
   if (ggml) gq_q4k_ggml_codes(blk + 4, sc, m);
   else gq_q4k_ref_codes(blk + 4, sc, m);
   const uint8_t *qs = blk + 16;
   for (int j = 0; j < 8; ++j)
-    for (int w8 = 0; w8 < 4; ++w8)
-      words[j][w8] = gq_canon_word(w8, [&](int e) -> uint32_t { return gq_q4k_nib(ggml, qs, j, e); });
+    for (int eh = 0; eh < 2; ++eh) {
+      uint8_t c[16];
+      for (int s2 = 0; s2 < 16; ++s2) c[s2] = (uint8_t)gq_q4k_nib(ggml, qs, j, 16 * eh + s2);
+      grp[2 * j + eh] = gq_pack_codes16(c);
+    }
   meta[0] = gq_rd16(blk) | (gq_rd16(blk + 2) << 16);
   uint32_t W1 = 0, W2 = 0, W3 = 0;
-  for (int g = 0; g < 4; ++g) {
-    uint32_t s0 = sc[2 * g], s1 = sc[2 * g + 1], m0 = m[2 * g], m1 = m[2 * g + 1];
-    W1 |= (s0 | ((m0 & 3u) << 6)) << (8 * g);
-    W2 |= (s1 | ((m1 & 3u) << 6)) << (8 * g);
-    W3 |= ((m0 >> 2) | ((m1 >> 2) << 4)) << (8 * g);
+  for (int i = 0; i < 4; ++i) {
+    uint32_t s0 = sc[2 * i], s1 = sc[2 * i + 1], m0 = m[2 * i], m1 = m[2 * i + 1];
+    W1 |= (s0 | ((m0 & 3u) << 6)) << (8 * i);
+    W2 |= (s1 | ((m1 & 3u) << 6)) << (8 * i);
+    W3 |= ((m0 >> 2) | ((m1 >> 2) << 4)) << (8 * i);
   }
   meta[1] = W1;
   meta[2] = W2;
   meta[3] = W3;
 }
-GQ_HD void gq_q4k_uncanon(int ggml, const uint32_t words[8][4], const uint32_t meta[4], uint8_t *blk) {
+// codes of sub-block j from the meta words
+GQ_HD void gq_q4k_meta_codes(const uint32_t meta[4], int j, uint32_t *sc, uint32_t *mn) {
+  int i = j >> 1;
+  uint32_t b = ((j & 1) ? meta[2] : meta[1]) >> (8 * i) & 0xFFu;
+  uint32_t b3 = (meta[3] >> (8 * i)) & 0xFFu;
+  *sc = b & 63u;
+  *mn = (b >> 6) | ((((j & 1) ? (b3 >> 4) : b3) & 15u) << 2);
+}
+GQ_HD void gq_q4k_from_groups(int ggml, const uint64_t grp[16], const uint32_t meta[4], uint8_t *blk) {
   uint8_t sc[8], m[8];
-  for (int g = 0; g < 4; ++g) {
-    uint32_t b1 = (meta[1] >> (8 * g)) & 0xFF, b2 = (meta[2] >> (8 * g)) & 0xFF,
-             b3 = (meta[3] >> (8 * g)) & 0xFF;
-    sc[2 * g] = (uint8_t)(b1 & 63);
-    sc[2 * g + 1] = (uint8_t)(b2 & 63);
-    m[2 * g] = (uint8_t)((b1 >> 6) | ((b3 & 15) << 2));
-    m[2 * g + 1] = (uint8_t)((b2 >> 6) | ((b3 >> 4) << 2));
+  for (int j = 0; j < 8; ++j) {
+    uint32_t a, b;
+    gq_q4k_meta_codes(meta, j, &a, &b);
+    sc[j] = (uint8_t)a;
+    m[j] = (uint8_t)b;
   }
   blk[0] = (uint8_t)(meta[0] & 0xFF);
   blk[1] = (uint8_t)((meta[0] >> 8) & 0xFF);
@@ -148,34 +178,42 @@ GQ_HD void gq_q4k_uncanon(int ggml, const uint32_t words[8][4], const uint32_t m
   uint8_t *qs = blk + 16;
   for (int i = 0; i < 128; ++i) qs[i] = 0;
   for (int j = 0; j < 8; ++j)
-    for (int w8 = 0; w8 < 4; ++w8)
-      for (int i = 0; i < 8; ++i)
-        gq_q4k_set_nib(ggml, qs, j, 8 * w8 + i, (words[j][w8] >> (4 * gq_canon_pos(i))) & 15u);
+    for (int eh = 0; eh < 2; ++eh) {
+      uint8_t c[16];
+      gq_unpack_codes16(grp[2 * j + eh], c);
+      for (int s2 = 0; s2 < 16; ++s2) gq_q4k_set_nib(ggml, qs, j, 16 * eh + s2, c[s2]);
+    }
 }
 
 // ---- addressing in the T16 layout ---------------------------------------
-// Byte offset, within the qs plane, of the 4-byte word holding canonical word
-// `w8` of block `blk` (Q4_0: 32-block index; Q4_K: sub-block index) of row n.
-GQ_HD size_t gq_q4_0_word_off(size_t n, size_t blk, int w8, size_t C) {
+// Within a chunk of a 16-row tile, lane l = 16*g + r (row r) holds, for the
+// int8 MFMA pair m, the 16 elements 16*(g&1) .. +15 of (sub-)block 2m + (g>>1).
+//
+// Q4_0: byte offset (qs plane) of the code group (element half eh) of 32-block
+// `blk` of row n; 8 bytes.
+GQ_HD size_t gq_q4_0_grp_off(size_t n, size_t blk, int eh, size_t C) {
   size_t t = n >> 4, r = n & 15, c = blk >> 2, j = blk & 3;
-  return ((t * C + c) << 10) + 16 * (16 * (size_t)w8 + r) + 4 * j;
+  size_t m = j >> 1, g = 2 * (j & 1) + (size_t)eh;
+  return ((t * C + c) << 10) + 16 * (16 * g + r) + 8 * m;
 }
+// d of 32-block blk of row n (Q4_0 and Q8_0).  Per row and chunk the four d
+// are stored in the order (d0, d2, d1, d3): lane (g, r) reads the 4 bytes at
+// 4*(g>>1), the d of its blocks (g>>1) and 2 + (g>>1).
 GQ_HD size_t gq_q4_0_d_off(size_t n, size_t blk, size_t C) {
   size_t t = n >> 4, r = n & 15, c = blk >> 2, j = blk & 3;
-  return (t * C + c) * 128 + (r * 4 + j) * 2;
+  return (t * C + c) * 128 + r * 8 + 4 * (j & 1) + 2 * (j >> 1);
 }
-// Q8_0: byte `b` (0..31) of 32-block `blk` of row n.
-GQ_HD size_t gq_q8_0_byte_off(size_t n, size_t blk, int b, size_t C) {
+// Q8_0: byte offset of the 16 int8 elements 16*eh .. +15 of 32-block blk.
+GQ_HD size_t gq_q8_0_half_off(size_t n, size_t blk, int eh, size_t C) {
   size_t t = n >> 4, r = n & 15, c = blk >> 2, j = blk & 3;
-  size_t p = j >> 1, half = j & 1;
-  size_t g = (size_t)b >> 3, within = (size_t)b & 7;
-  return ((t * C + c) << 11) + (p << 10) + 16 * (16 * g + r) + 8 * half + within;
+  size_t m = j >> 1, g = 2 * (j & 1) + (size_t)eh;
+  return ((t * C + c) << 11) + (m << 10) + 16 * (16 * g + r);
 }
-// Q4_K: canonical word w8 of sub-block j of super-block s of row n.
-GQ_HD size_t gq_q4k_word_off(size_t n, size_t s, int j, int w8, size_t S) {
+// Q4_K: code group (sub-block j, half eh) of super-block s of row n; 8 bytes.
+GQ_HD size_t gq_q4k_grp_off(size_t n, size_t s, int j, int eh, size_t S) {
   size_t t = n >> 4, r = n & 15;
-  size_t g = (size_t)j >> 1, h = (size_t)j & 1;
-  return ((t * S + s) << 11) + (h << 10) + 16 * (16 * g + r) + 4 * (size_t)w8;
+  size_t m = (size_t)j >> 1, g = 2 * ((size_t)j & 1) + (size_t)eh;
+  return ((t * S + s) << 11) + ((m >> 1) << 10) + 16 * (16 * g + r) + 8 * (m & 1);
 }
 GQ_HD size_t gq_q4k_meta_off(size_t n, size_t s, size_t S) {
   size_t t = n >> 4, r = n & 15;

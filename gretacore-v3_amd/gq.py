@@ -39,6 +39,8 @@ _SIGS = {
     "gq_dequant_packed": (ctypes.c_int, [ctypes.c_int, _vp, _c_size, _c_size, _vp, _vp]),
     "gq_gemv_workspace_bytes": (_c_size, [ctypes.c_int, _c_size, ctypes.c_int]),
     "gq_gemv": (ctypes.c_int, [ctypes.c_int, _vp, _vp, _vp, _c_size, _c_size, ctypes.c_int, _vp, _c_size, _vp]),
+    "gq_gemv_plan": (ctypes.c_int, [ctypes.c_int, _c_size, _c_size, ctypes.c_int, ctypes.POINTER(ctypes.c_int),
+                                     ctypes.POINTER(ctypes.c_int), ctypes.POINTER(ctypes.c_int)]),
     "gq_gemv_prep": (ctypes.c_int, [ctypes.c_int, _vp, _c_size, ctypes.c_int, _vp, _c_size, _vp]),
     "gq_gemv_prepped": (ctypes.c_int, [ctypes.c_int, _vp, _vp, _vp, _c_size, _c_size, ctypes.c_int, _vp]),
     "gq_gemm_workspace_bytes": (_c_size, [ctypes.c_int, _c_size, _c_size]),
@@ -172,6 +174,13 @@ class Workspace:
         if self.buf is None or self.buf.numel() < nbytes:
             self.buf = torch.empty(max(nbytes, 1 << 20), dtype=torch.uint8, device=self.device)
         return self.buf
+
+
+def gemv_plan(fmt: int, n: int, k: int, batch: int):
+    """(row tiles per workgroup, waves per workgroup, max chunks per wave)."""
+    r, ks, cpw = ctypes.c_int(), ctypes.c_int(), ctypes.c_int()
+    check(load().gq_gemv_plan(fmt, n, k, batch, ctypes.byref(r), ctypes.byref(ks), ctypes.byref(cpw)), "gq_gemv_plan")
+    return r.value, ks.value, cpw.value
 
 
 def gemv_workspace_bytes(fmt: int, k: int, batch: int) -> int:

@@ -86,6 +86,11 @@ size_t gq_gemv_workspace_bytes(int fmt, size_t K, int batch);
  * stream capture).  Concurrent calls that share a workspace race. */
 int gq_gemv(int fmt, const void *d_packed, const float *d_x, float *d_y, size_t N, size_t K, int batch,
             void *d_workspace, size_t workspace_bytes, void *stream);
+/* Launch plan of gq_gemv for a shape (no GPU needed): row tiles per
+ * workgroup, waves per workgroup (K split) and the most K chunks one wave
+ * streams.  Environment overrides for tuning: GQ_GEMV_R, GQ_GEMV_KSPLIT. */
+int gq_gemv_plan(int fmt, size_t N, size_t K, int batch, int *row_tiles_per_wg, int *ksplit,
+                 int *chunks_per_wave);
 /* Split form: prepare x once (gq_gemv_prep) and run several GEMVs that share
  * it (q/k/v, gate/up) with gq_gemv_prepped. */
 int gq_gemv_prep(int fmt, const float *d_x, size_t K, int batch, void *d_workspace, size_t workspace_bytes,
