@@ -27,6 +27,11 @@ HBM_PEAK_GBS = 8000.0          # MI355X HBM3E, GB/s
 MFMA_F16_PEAK_TFLOPS = 2500.0  # dense fp16/bf16
 MFMA_I8_PEAK_TOPS = 5000.0     # dense int8
 CACHE_DEFEAT_BYTES = 512 << 20  # > 256 MB Infinity Cache
+# HBM bytes per launch of the headline kernel, measured with rocprofv3 PMC
+# FETCH_SIZE + WRITE_SIZE and calibrated against a 64 MiB bitwise_not in the
+# same runs (profiles/k_gemv_q_q4_0_14336x4096.md); valid for the launch plan
+# it was measured with.
+PROFILED_TRAFFIC = {("q4_0", 14336, 4096, 1, 2, 8): 33_280_000}
 
 
 def log(*a):
@@ -231,6 +236,15 @@ def main():
     dev = torch.device("cuda:0")
     steps, warmup = args.steps, args.warmup
 
+    if args.headline_only:
+        # a plain copy of known size, so profiler byte counters can be
+        # calibrated against the GEMV dispatches of the same run
+        src = torch.empty(64 << 20, dtype=torch.uint8, device=dev).fill_(1)
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            torch.bitwise_not(src, out=dst)  # reads 64 MiB, writes 64 MiB
+        torch.cuda.synchronize()
+        del src, dst
     log("[bench] headline: Q4_0 GEMV 14336x4096 batch 1")
     head = GemvCase(O.Q4_0, 14336, 4096, 1, wseed=1002, xseed=2002, dev=dev)
     h = bench_gemv(head, steps, warmup)
@@ -284,7 +298,8 @@ def main():
         "pct_peak": round(h["pct_peak"], 2),
         "rel_l2_vs_oracle": h["rel_l2"],
         "roofline": {"bound": "hbm", "achieved": round(h["GBps"], 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(h["GBps"] / HBM_PEAK_GBS, 4), "traffic": None,
+                     "frac": round(h["GBps"] / HBM_PEAK_GBS, 4),
+                     "traffic": PROFILED_TRAFFIC.get(("q4_0", 14336, 4096, 1, R, ks)),
                      "kernel": f"k_gemv_q<Q4_0, NB=1, R={R}, KSPLIT={ks}>",
                      "kernel_us": round(h["step_us"], 3),
                      "timing": "HIP events around the replay of K back-to-back launches; includes dispatch gaps"},
