@@ -49,5 +49,9 @@ int gq_fill_zero(float *p, size_t n, hipStream_t s);
 int gq_launch_prep_x(int fmt, const float *x, void *ws, int B, int K, hipStream_t s);
 int gq_launch_prep_a(const void *a, int a_dtype, _Float16 *out, int M, int K, int Kp, hipStream_t s);
 
+// load-time conversions (gq_loadconv.hip)
+int gq_launch_dequant_q6_k(const void *blocks, size_t n_blocks, float *out, hipStream_t s);
+int gq_launch_f16_to_f32(const void *in, size_t n, float *out, hipStream_t s);
+
 // Library-owned per-device workspace (grown on demand, never shrunk).
 int gq_default_workspace(size_t bytes, void **ptr);

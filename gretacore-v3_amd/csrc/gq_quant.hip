@@ -344,10 +344,12 @@ k_quantize_act_q8(const void *__restrict__ a, int a_dtype, int8_t *__restrict__ 
 static unsigned blocks_for(size_t n) { return (unsigned)((n + 255) / 256); }
 
 extern "C" int gq_dequant_gguf(int fmt, const void *blocks, size_t n_blocks, float *out, void *stream) {
-  GQ_CHECK(gq_fmt_valid(fmt), GQ_ERR_UNSUPPORTED);
+  GQ_CHECK(gq_fmt_valid(fmt) || fmt == GQ_FMT_F16 || fmt == GQ_FMT_Q6_K, GQ_ERR_UNSUPPORTED);
   GQ_CHECK(blocks && out, GQ_ERR_INVALID_ARGS);
   if (n_blocks == 0) return GQ_OK;
   hipStream_t s = (hipStream_t)stream;
+  if (fmt == GQ_FMT_F16) return gq_launch_f16_to_f32(blocks, n_blocks, out, s);
+  if (fmt == GQ_FMT_Q6_K) return gq_launch_dequant_q6_k(blocks, n_blocks, out, s);
   const uint8_t *src = (const uint8_t *)blocks;
   if (fmt == GQ_FMT_Q4_0)
     hipLaunchKernelGGL(k_dequant_q4_0, dim3(blocks_for(n_blocks)), dim3(256), 0, s, src, out, n_blocks);

@@ -17,6 +17,8 @@ FMT_Q4_0 = 2
 FMT_Q8_0 = 8
 FMT_Q4_K = 12
 FMT_Q4_K_GGML = 112
+FMT_F16 = 1    # gq_dequant_gguf only
+FMT_Q6_K = 14  # gq_dequant_gguf only
 FORMATS = {"q4_0": FMT_Q4_0, "q8_0": FMT_Q8_0, "q4_k": FMT_Q4_K, "q4_k_ggml": FMT_Q4_K_GGML}
 
 DT_F32, DT_F16, DT_BF16 = 0, 1, 2
@@ -49,11 +51,35 @@ _SIGS = {
     "gq_quantize_act_q8": (ctypes.c_int, [_vp, ctypes.c_int, _c_size, _c_size, _vp, _vp, _vp]),
     "gq_gemm_q8_i8": (ctypes.c_int, [_vp, _vp, _vp, _vp, _c_size, _c_size, _c_size, _vp]),
     "gq_matmul": (ctypes.c_int, [ctypes.c_int, _vp, _vp, _vp, _c_size, _c_size, _c_size, _vp]),
+    "gq_convert_f32_to_f16": (ctypes.c_int, [_vp, _c_size, _vp, _vp]),
+    "gq_transpose_kv": (ctypes.c_int, [ctypes.c_int, _vp, _c_size, _c_size, _vp, _vp]),
+    "gq_requant_int8": (ctypes.c_int, [_vp, _c_size, _vp, _vp, _vp]),
+    "gq_requant_int4": (ctypes.c_int, [_vp, _c_size, _vp, _vp, _vp]),
+    "gq_head_scales": (ctypes.c_int, [_vp, _c_size, ctypes.c_uint32, ctypes.c_uint32, ctypes.c_uint32, _vp, _vp]),
+    "gq_split_q8_0": (ctypes.c_int, [_vp, _c_size, _vp, _vp, _vp]),
     "gq_launch_gemm_mfma_int8_wt_fp32_acc32": (
         ctypes.c_int, [_vp, _vp, _vp, _vp, _vp] + [ctypes.c_uint32] * 7),
     "gq_launch_gemm_mfma_int4_wt_fp32_acc32": (
         ctypes.c_int, [_vp, _vp, _vp, _vp, _vp, _vp] + [ctypes.c_uint32] * 8 + [ctypes.c_int, ctypes.c_int]),
 }
+
+# include/gq_gguf.h
+_SIGS_GGUF = {
+    "gq_gguf_open": (ctypes.c_int, [ctypes.c_char_p, ctypes.POINTER(_vp)]),
+    "gq_gguf_open_error": (ctypes.c_char_p, []),
+    "gq_gguf_close": (None, [_vp]),
+    "gq_gguf_error": (ctypes.c_char_p, [_vp]),
+    "gq_gguf_tensor_count": (_c_size, [_vp]),
+    "gq_gguf_tensor_info": (ctypes.c_int, [_vp, _c_size, _vp]),
+    "gq_gguf_find": (ctypes.c_int, [_vp, ctypes.c_char_p, ctypes.POINTER(_c_size)]),
+    "gq_gguf_get_config": (ctypes.c_int, [_vp, _vp]),
+    "gq_gguf_vocab_token": (ctypes.c_int, [_vp, _c_size, ctypes.POINTER(ctypes.c_char_p), ctypes.POINTER(_c_size)]),
+    "gq_gguf_set_q4k_layout": (ctypes.c_int, [_vp, ctypes.c_int]),
+    "gq_gguf_read_raw": (ctypes.c_int, [_vp, ctypes.c_char_p, _vp, _c_size]),
+    "gq_gguf_plan_load": (ctypes.c_int, [_vp, ctypes.c_char_p, ctypes.c_int, _vp]),
+    "gq_gguf_load": (ctypes.c_int, [_vp, ctypes.c_char_p, ctypes.c_int, _vp, _c_size, _vp, _c_size, _vp, _c_size]),
+}
+_SIGS.update(_SIGS_GGUF)
 
 _lib = None
 
@@ -147,7 +173,7 @@ def repack(fmt: int, d_gguf, n: int, k: int, stream=None):
 def dequant_gguf(fmt: int, d_blocks, n_blocks: int, stream=None):
     import torch
     _require_device(d_blocks)
-    per = 256 if fmt in (FMT_Q4_K, FMT_Q4_K_GGML) else 32
+    per = 256 if fmt in (FMT_Q4_K, FMT_Q4_K_GGML, FMT_Q6_K) else (1 if fmt == FMT_F16 else 32)
     out = torch.empty(n_blocks * per, dtype=torch.float32, device=d_blocks.device)
     check(load().gq_dequant_gguf(fmt, _ptr(d_blocks), n_blocks, _ptr(out), _stream(stream)), "gq_dequant_gguf")
     return out
@@ -297,3 +323,183 @@ def gemv_prepped(fmt: int, d_packed, workspace: Workspace, y, n: int, k: int, ba
     check(load().gq_gemv_prepped(fmt, _ptr(d_packed), _ptr(workspace.buf), _ptr(y), n, k, batch, _stream(stream)),
           "gq_gemv_prepped")
     return y
+
+
+# ---- load-time conversions (bit-exact with the reference loader) ------------
+def convert_f32_to_f16(w, stream=None):
+    """Reference truncating fp32 -> fp16 (weight_loader.cpp:112-123); returns int16 bits."""
+    import torch
+    _require_device(w)
+    out = torch.empty(w.numel(), dtype=torch.int16, device=w.device)
+    check(load().gq_convert_f32_to_f16(_ptr(w), w.numel(), _ptr(out), _stream(stream)), "gq_convert_f32_to_f16")
+    return out
+
+
+def transpose_kv(t, model_dim: int, kv_dim: int, stream=None):
+    import torch
+    _require_device(t)
+    out = torch.empty(t.numel(), dtype=t.dtype, device=t.device)
+    check(load().gq_transpose_kv(t.element_size(), _ptr(t), model_dim, kv_dim, _ptr(out), _stream(stream)),
+          "gq_transpose_kv")
+    return out
+
+
+def requant_int8(w, stream=None):
+    import torch
+    _require_device(w)
+    n = w.numel()
+    q = torch.empty(n, dtype=torch.int8, device=w.device)
+    s = torch.empty((n + 31) // 32, dtype=torch.float32, device=w.device)
+    check(load().gq_requant_int8(_ptr(w), n, _ptr(q), _ptr(s), _stream(stream)), "gq_requant_int8")
+    return q, s
+
+
+def requant_int4(w, stream=None):
+    import torch
+    _require_device(w)
+    n = w.numel()
+    q = torch.empty((n + 1) // 2, dtype=torch.uint8, device=w.device)
+    s = torch.empty((n + 31) // 32, dtype=torch.float32, device=w.device)
+    check(load().gq_requant_int4(_ptr(w), n, _ptr(q), _ptr(s), _stream(stream)), "gq_requant_int4")
+    return q, s
+
+
+def head_scales(w, num_heads: int, head_dim: int, dim: int, stream=None):
+    import torch
+    _require_device(w)
+    out = torch.empty(num_heads, dtype=torch.float32, device=w.device)
+    check(load().gq_head_scales(_ptr(w), w.numel(), num_heads, head_dim, dim, _ptr(out), _stream(stream)),
+          "gq_head_scales")
+    return out
+
+
+def split_q8_0(d_blocks, n_blocks: int, stream=None):
+    import torch
+    _require_device(d_blocks)
+    q = torch.empty(n_blocks * 32, dtype=torch.int8, device=d_blocks.device)
+    s = torch.empty(n_blocks, dtype=torch.float32, device=d_blocks.device)
+    check(load().gq_split_q8_0(_ptr(d_blocks), n_blocks, _ptr(q), _ptr(s), _stream(stream)), "gq_split_q8_0")
+    return q, s
+
+
+# ---- GGUF loader (include/gq_gguf.h) ----------------------------------------
+LOAD_F32, LOAD_F16, LOAD_INT8, LOAD_INT4, LOAD_QUANT = range(5)
+
+
+class _Tensor(ctypes.Structure):
+    _fields_ = [("name", ctypes.c_char * 256), ("dtype", ctypes.c_char * 16), ("ggml_type", ctypes.c_uint32),
+                ("n_dims", ctypes.c_uint32), ("shape", ctypes.c_uint64 * 8), ("offset", ctypes.c_uint64),
+                ("size_bytes", ctypes.c_uint64)]
+
+
+class _Config(ctypes.Structure):
+    _fields_ = [(f, ctypes.c_uint32) for f in ("dim", "num_heads", "num_heads_kv", "num_layers", "vocab_size",
+                                                "hidden_dim", "head_dim", "max_seq_len")] + \
+               [("rope_base", ctypes.c_float), ("rms_eps", ctypes.c_float)]
+
+
+class _Plan(ctypes.Structure):
+    _fields_ = [("n_elem", ctypes.c_uint64), ("bytes", ctypes.c_uint64), ("scale_bytes", ctypes.c_uint64),
+                ("num_heads", ctypes.c_uint32), ("has_head_scales", ctypes.c_int32), ("is_qkv", ctypes.c_int32),
+                ("transpose", ctypes.c_int32), ("fmt", ctypes.c_int32), ("N", ctypes.c_uint64),
+                ("K", ctypes.c_uint64)]
+
+
+class GGUF:
+    """GGUF file opened through libgq's loader (GGUFLoader, weight_loader.cpp:467-1008).
+
+    Parsing needs no GPU; load() converts on the GPU into torch device tensors.
+    """
+
+    def __init__(self, path: str):
+        lib = load()
+        h = _vp()
+        st = lib.gq_gguf_open(os.fsencode(path), ctypes.byref(h))
+        if st != 0:
+            raise GQError(f"gq_gguf_open({path}) failed: {lib.gq_gguf_open_error().decode()}")
+        self._h = h
+        self.path = path
+
+    def close(self):
+        if self._h:
+            load().gq_gguf_close(self._h)
+            self._h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *a):
+        self.close()
+
+    def _check(self, st, what):
+        if st != 0:
+            raise GQError(f"{what} failed ({st}): {load().gq_gguf_error(self._h).decode()}")
+
+    def tensors(self):
+        lib = load()
+        out = []
+        for i in range(lib.gq_gguf_tensor_count(self._h)):
+            t = _Tensor()
+            self._check(lib.gq_gguf_tensor_info(self._h, i, ctypes.byref(t)), "gq_gguf_tensor_info")
+            out.append({"name": t.name.decode(), "dtype": t.dtype.decode(), "ggml_type": t.ggml_type,
+                        "shape": [int(t.shape[d]) for d in range(t.n_dims)], "offset": int(t.offset),
+                        "size_bytes": int(t.size_bytes)})
+        return out
+
+    def config(self):
+        c = _Config()
+        self._check(load().gq_gguf_get_config(self._h, ctypes.byref(c)), "gq_gguf_get_config")
+        return {f: getattr(c, f) for f, _ in _Config._fields_}
+
+    def vocab(self):
+        lib = load()
+        n = self.config()["vocab_size"]
+        out = []
+        for i in range(n):
+            s, ln = ctypes.c_char_p(), _c_size()
+            if lib.gq_gguf_vocab_token(self._h, i, ctypes.byref(s), ctypes.byref(ln)) != 0:
+                break
+            out.append(ctypes.string_at(s, ln.value))
+        return out
+
+    def set_q4k_layout(self, ggml: bool):
+        self._check(load().gq_gguf_set_q4k_layout(self._h, int(ggml)), "gq_gguf_set_q4k_layout")
+
+    def read_raw(self, name: str):
+        import numpy as np
+        t = next(t for t in self.tensors() if t["name"] == name)
+        out = np.empty(t["size_bytes"], dtype=np.uint8)
+        self._check(load().gq_gguf_read_raw(self._h, name.encode(), out.ctypes.data, out.size), "gq_gguf_read_raw")
+        return out
+
+    def plan(self, name: str, kind: int):
+        p = _Plan()
+        self._check(load().gq_gguf_plan_load(self._h, name.encode(), kind, ctypes.byref(p)), "gq_gguf_plan_load")
+        return {f: getattr(p, f) for f, _ in _Plan._fields_}
+
+    def load(self, name: str, kind: int, device="cuda"):
+        """Returns (data, scales, head_scales, plan) as device tensors (None where absent)."""
+        import torch
+        p = self.plan(name, kind)
+        out = torch.empty(max(p["bytes"], 1), dtype=torch.uint8, device=device)
+        sc = torch.empty(max(p["scale_bytes"], 1), dtype=torch.uint8, device=device) if p["scale_bytes"] else None
+        hs = torch.empty(p["num_heads"], dtype=torch.float32, device=device) if p["has_head_scales"] else None
+        self._check(load().gq_gguf_load(self._h, name.encode(), kind, _ptr(out), out.numel(), _ptr(sc),
+                                        sc.numel() if sc is not None else 0, _ptr(hs),
+                                        hs.numel() * 4 if hs is not None else 0), "gq_gguf_load")
+        out = out[:p["bytes"]]
+        if kind == LOAD_F32:
+            out = out.view(torch.float32)
+        elif kind == LOAD_F16:
+            out = out.view(torch.int16)
+        elif kind == LOAD_INT8:
+            out = out.view(torch.int8)
+        if sc is not None:
+            sc = sc[:p["scale_bytes"]].view(torch.float32)
+        return out, sc, hs, p

@@ -42,6 +42,9 @@ extern "C" {
 #define GQ_FMT_Q8_0 8
 #define GQ_FMT_Q4_K 12       /* reference (GRETA) Q4_K layout, weight_loader.cpp:125-156 */
 #define GQ_FMT_Q4_K_GGML 112 /* llama.cpp canonical Q4_K layout */
+/* accepted by gq_dequant_gguf only (loader conversions) */
+#define GQ_FMT_F16 1         /* one "block" = one fp16 value (weight_loader.cpp:91-110) */
+#define GQ_FMT_Q6_K 14       /* reference Q6_K layout, weight_loader.cpp:158-177 */
 
 /* activation / output dtypes */
 #define GQ_DT_F32 0
@@ -73,10 +76,33 @@ int gq_unpack_host(int fmt, const void *packed, size_t N, size_t K, void *gguf);
 int gq_repack(int fmt, const void *d_gguf, size_t N, size_t K, void *d_packed, void *stream);
 
 /* ---- dequantization (bit-exact with the reference semantics) -------------- */
-/* n_blocks raw GGUF blocks -> fp32 (n_blocks * 32 or * 256 values). */
+/* n_blocks raw GGUF blocks -> fp32 (n_blocks * 32 or * 256 values; F16:
+ * n_blocks values).  Formats: Q4_0, Q8_0, Q4_K, Q4_K_GGML, Q6_K, F16. */
 int gq_dequant_gguf(int fmt, const void *d_blocks, size_t n_blocks, float *d_out, void *stream);
 /* T16 tensor -> fp32 [N][K]. */
 int gq_dequant_packed(int fmt, const void *d_packed, size_t N, size_t K, float *d_out, void *stream);
+
+/* ---- load-time conversions of the reference loader (all bit-exact) -------- */
+/* fp32 -> fp16 with the reference's truncating rule (weight_loader.cpp:112-123):
+ * mantissa truncated, below the normal range -> signed zero, above -> Inf. */
+int gq_convert_f32_to_f16(const float *d_in, size_t n, uint16_t *d_out, void *stream);
+/* GQA K/V transpose (weight_loader.cpp:634-658, 739-781, 877-918): in is
+ * [model_dim][kv_dim] (kv contiguous), out [kv_dim][model_dim]; elem_bytes 2 or
+ * 4; out must not alias in. */
+int gq_transpose_kv(int elem_bytes, const void *d_in, size_t model_dim, size_t kv_dim, void *d_out,
+                    void *stream);
+/* INT8 requant per 32 of the flat tensor (weight_loader.cpp:780-802):
+ * scales[ceil(n/32)], q[n]. */
+int gq_requant_int8(const float *d_w, size_t n, int8_t *d_q, float *d_scales, void *stream);
+/* INT4 requant + pack (weight_loader.cpp:920-957): packed[ceil(n/2)], scales[ceil(n/32)]. */
+int gq_requant_int4(const float *d_w, size_t n, uint8_t *d_packed, float *d_scales, void *stream);
+/* Per-head max |w| (weight_loader.cpp:972-998): out[h] over the head_dim rows of
+ * dim values of head h, 1.0 if <= 1e-9.  Requires num_heads*head_dim*dim <= n. */
+int gq_head_scales(const float *d_w, size_t n, uint32_t num_heads, uint32_t head_dim, uint32_t dim,
+                   float *d_out, void *stream);
+/* Q8_0 blocks -> int8 q[32 * n_blocks] + fp32 scales[n_blocks]
+ * (weight_loader.cpp:703-712). */
+int gq_split_q8_0(const void *d_blocks, size_t n_blocks, int8_t *d_q, float *d_scales, void *stream);
 
 /* ---- decode GEMV: y[b][n] = sum_k x[b][k] * W[n][k], 1 <= batch <= 16 ------- */
 /* Workspace bytes needed by gq_gemv for (fmt, K, batch). */

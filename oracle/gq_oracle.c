@@ -87,6 +87,13 @@ uint16_t gqo_fp32_to_fp16_trunc(float f) {
   return (uint16_t)(sign | ((uint32_t)e << 10) | (m >> 13));
 }
 
+void gqo_fp16_to_fp32_n(const uint16_t *h, size_t n, float *out) {
+  for (size_t i = 0; i < n; ++i) out[i] = gqo_fp16_to_fp32(h[i]);
+}
+void gqo_fp32_to_fp16_trunc_n(const float *f, size_t n, uint16_t *out) {
+  for (size_t i = 0; i < n; ++i) out[i] = gqo_fp32_to_fp16_trunc(f[i]);
+}
+
 /* Block geometry, weight_loader.cpp:38-82. */
 size_t gqo_block_elems(int fmt) {
   switch (fmt) {

@@ -46,6 +46,9 @@ enum {
 float gqo_fp16_to_fp32(uint16_t h);
 uint16_t gqo_float_to_half(float f);
 uint16_t gqo_fp32_to_fp16_trunc(float f);
+/* Array forms of the two conversions above. */
+void gqo_fp16_to_fp32_n(const uint16_t *h, size_t n, float *out);
+void gqo_fp32_to_fp16_trunc_n(const float *f, size_t n, uint16_t *out);
 
 size_t gqo_block_elems(int fmt);
 size_t gqo_block_bytes(int fmt);

@@ -46,6 +46,8 @@ def lib():
             build()
         L = ctypes.CDLL(ORACLE_SO)
         vp, sz, i = ctypes.c_void_p, ctypes.c_size_t, ctypes.c_int
+        L.gqo_fp16_to_fp32_n.argtypes = [vp, sz, vp]
+        L.gqo_fp32_to_fp16_trunc_n.argtypes = [vp, sz, vp]
         L.gqo_fp16_to_fp32.restype = ctypes.c_float
         L.gqo_fp16_to_fp32.argtypes = [ctypes.c_uint16]
         L.gqo_float_to_half.restype = ctypes.c_uint16
@@ -87,6 +89,12 @@ def ref():
         R.gqref_dequant_q4_k.argtypes = [vp, sz, vp]
         R.gqref_dequant_q6_k.argtypes = [vp, sz, vp]
         R.gqref_gemm.argtypes = [vp, vp, vp, i, i, i]
+        R.gqref_gguf_parse.argtypes = [ctypes.c_char_p, vp, i, vp, ctypes.c_char_p, i]
+        R.gqref_gguf_parse.restype = i
+        u64p = ctypes.POINTER(ctypes.c_uint64)
+        R.gqref_gguf_load.argtypes = [ctypes.c_char_p, ctypes.c_char_p, i, vp, ctypes.c_uint64, u64p, vp,
+                                      ctypes.c_uint64, u64p, vp, ctypes.c_uint64, u64p, ctypes.c_char_p, i]
+        R.gqref_gguf_load.restype = i
         _ref = R
     return _ref
 
@@ -96,6 +104,22 @@ def _p(a):
 
 
 # ---- oracle functions ------------------------------------------------------
+def fp16_to_fp32(h) -> np.ndarray:
+    """Reference fp16 -> fp32 (NaN -> Inf) of a uint16 array."""
+    h = np.ascontiguousarray(h, dtype=np.uint16).ravel()
+    out = np.empty(h.size, dtype=np.float32)
+    lib().gqo_fp16_to_fp32_n(_p(h), h.size, _p(out))
+    return out
+
+
+def fp32_to_fp16_trunc(f) -> np.ndarray:
+    """Reference truncating fp32 -> fp16 bits of a float32 array."""
+    f = np.ascontiguousarray(f, dtype=np.float32).ravel()
+    out = np.empty(f.size, dtype=np.uint16)
+    lib().gqo_fp32_to_fp16_trunc_n(_p(f), f.size, _p(out))
+    return out
+
+
 def dequant(fmt: int, blocks: np.ndarray) -> np.ndarray:
     blocks = np.ascontiguousarray(blocks, dtype=np.uint8).ravel()
     nb = blocks.size // BLOCK_BYTES[fmt]
@@ -232,3 +256,46 @@ def rel_l2(a, b) -> float:
     b = np.asarray(b, dtype=np.float64)
     den = np.linalg.norm(b)
     return float(np.linalg.norm(a - b) / (den if den > 0 else 1.0))
+
+
+# ---- the reference's own GGUF loader (oracle/_ref) ---------------------------
+class _RefTensor(ctypes.Structure):
+    _fields_ = [("name", ctypes.c_char * 128), ("dtype", ctypes.c_char * 16), ("shape", ctypes.c_uint64 * 4),
+                ("n_dims", ctypes.c_uint32), ("offset", ctypes.c_uint64), ("size_bytes", ctypes.c_uint64)]
+
+
+class _RefConfig(ctypes.Structure):
+    _fields_ = [(f, ctypes.c_uint32) for f in ("dim", "num_heads", "num_heads_kv", "num_layers", "vocab_size",
+                                                "hidden_dim", "head_dim", "max_seq_len")] + \
+               [("rope_base", ctypes.c_float), ("rms_eps", ctypes.c_float)]
+
+
+def ref_gguf_parse(path: str, cap: int = 4096):
+    """GGUFLoader::open + list_tensors + get_config of the reference, or
+    (None, None, message) when it refuses the file."""
+    R = ref()
+    arr = (_RefTensor * cap)()
+    cfg = _RefConfig()
+    err = ctypes.create_string_buffer(512)
+    n = R.gqref_gguf_parse(os.fsencode(path), ctypes.cast(arr, ctypes.c_void_p), cap, ctypes.byref(cfg), err, 512)
+    if n < 0:
+        return None, None, err.value.decode(errors="replace")
+    ts = [{"name": t.name.decode(), "dtype": t.dtype.decode(), "shape": [int(t.shape[d]) for d in range(t.n_dims)],
+           "offset": int(t.offset), "size_bytes": int(t.size_bytes)} for t in arr[:n]]
+    return ts, {f: getattr(cfg, f) for f, _ in _RefConfig._fields_}, ""
+
+
+def ref_gguf_load(path: str, name: str, kind: int, max_bytes: int):
+    """The reference loader's load_tensor / _fp16 / _int8 / _int4 (kind 0..3),
+    run on the GPU; returns (data bytes, scales f32, head scales f32)."""
+    R = ref()
+    out = np.empty(max_bytes, dtype=np.uint8)
+    sc = np.empty(max_bytes // 8 + 64, dtype=np.float32)
+    hs = np.empty(4096, dtype=np.float32)
+    ob, sb, hc = ctypes.c_uint64(), ctypes.c_uint64(), ctypes.c_uint64()
+    err = ctypes.create_string_buffer(512)
+    st = R.gqref_gguf_load(os.fsencode(path), name.encode(), kind, _p(out), out.nbytes, ctypes.byref(ob), _p(sc),
+                           sc.nbytes, ctypes.byref(sb), _p(hs), hs.nbytes, ctypes.byref(hc), err, 512)
+    if st != 0:
+        raise RuntimeError(f"reference load failed: {err.value.decode(errors='replace')}")
+    return out[:ob.value].copy(), sc[:sb.value // 4].copy(), hs[:hc.value].copy()

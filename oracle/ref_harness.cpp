@@ -83,4 +83,44 @@ int gqref_gguf_parse(const char *path, gqref_tensor *out, int cap,
   }
   return (int)ts.size();
 }
+
+// GGUFLoader::load_tensor / _fp16 / _int8 / _int4 (weight_loader.cpp:517-1008),
+// the reference's own loader run end to end (it allocates device Buffers, so
+// this needs a GPU).  kind: 0 fp32, 1 fp16, 2 int8, 3 int4.  Device results
+// are copied back into the host arrays (capacities in bytes); the sizes are
+// returned.  Returns 0 on success, -1 on failure.
+int gqref_gguf_load(const char *path, const char *name, int kind, void *out, uint64_t out_cap,
+                    uint64_t *out_bytes, float *scales, uint64_t scales_cap, uint64_t *scales_bytes,
+                    float *head_scales, uint64_t head_cap, uint64_t *head_count, char *err, int err_cap) {
+  gcore::inference::GGUFLoader l;
+  std::string e;
+  auto fail = [&]() {
+    if (err && err_cap > 0) {
+      std::strncpy(err, e.c_str(), err_cap - 1);
+      err[err_cap - 1] = 0;
+    }
+    return -1;
+  };
+  if (!l.open(path, &e)) return fail();
+  gcore::rt::hip::Buffer b, s, h;
+  bool ok = false;
+  if (kind == 0) ok = l.load_tensor(name, b, &e);
+  else if (kind == 1) ok = l.load_tensor_fp16(name, b, &e);
+  else if (kind == 2) ok = l.load_tensor_int8(name, b, s, &e);
+  else if (kind == 3) ok = l.load_tensor_int4(name, b, s, h, &e);
+  if (!ok) return fail();
+  *out_bytes = b.size();
+  if (b.size() > out_cap || !b.copy_to_host(out, b.size(), &e)) return fail();
+  *scales_bytes = 0;
+  *head_count = 0;
+  if (kind >= 2) {
+    *scales_bytes = s.size();
+    if (s.size() > scales_cap || !s.copy_to_host(scales, s.size(), &e)) return fail();
+  }
+  if (kind == 3 && h.size() > 0) {
+    *head_count = h.size() / 4;
+    if (h.size() > head_cap || !h.copy_to_host(head_scales, h.size(), &e)) return fail();
+  }
+  return 0;
+}
 }

@@ -1,0 +1,307 @@
+"""GGUF loader: the build's parser and device loads (libgq.so, include/gq_gguf.h)
+against the reference's own GGUFLoader (compiled into oracle/_ref from the
+reference sources) and the oracle.
+
+Files are written by tests/gguf_writer.py.  Parsing needs no GPU; the load
+tests are marked gpu.  Reference quirks kept (weight_loader.cpp): data section
+at the next 32-byte boundary; llama.* defaults from ModelConfig::llama2_7b;
+GQA K/V tensors of shape [D, KV] transposed as if stored [D][KV].
+Deliberate differences: Q8_0 is named "Q8_0" (the reference says "UNKNOWN"),
+and 64-bit integer llama.* values are accepted."""
+import os
+
+import numpy as np
+import pytest
+
+import gguf_writer as W
+import oracle as O
+
+DIM, HEADS, HEADS_KV, HD = 256, 4, 2, 64
+KV = HEADS_KV * HD
+VOCAB = ["<unk>", "<s>", "</s>", "hello", "world", "x" * 2000, "end"]
+
+# (name, shape (ne0 first), ggml type, oracle format)
+TENSORS = [
+    ("token_embd.weight", [DIM, 64], W.GGML_Q4_K, O.Q4_K),
+    ("blk.0.attn_norm.weight", [DIM], W.GGML_F32, None),
+    ("blk.0.attn_q.weight", [DIM, DIM], W.GGML_Q4_K, O.Q4_K),
+    ("blk.0.attn_k.weight", [DIM, KV], W.GGML_Q4_K, O.Q4_K),
+    ("blk.0.attn_v.weight", [DIM, KV], W.GGML_Q6_K, O.Q6_K),
+    ("blk.0.attn_output.weight", [DIM, DIM], W.GGML_F16, None),
+    ("blk.0.ffn_gate.weight", [DIM, 512], W.GGML_Q4_0, O.Q4_0),
+    ("blk.0.ffn_down.weight", [512, DIM], W.GGML_Q8_0, O.Q8_0),
+    ("blk.1.attn_k.weight", [KV, DIM], W.GGML_F16, None),
+    ("blk.1.attn_v.weight", [DIM, KV], W.GGML_F32, None),
+    ("output.weight", [DIM, 48], W.GGML_Q6_K, O.Q6_K),
+]
+
+
+def _tensor_data(name, shape, gt, fmt, seed):
+    n = int(np.prod(shape))
+    rng = np.random.default_rng(seed)
+    if gt == W.GGML_F32:
+        return (rng.standard_normal(n) * 0.05).astype(np.float32).tobytes()
+    if gt == W.GGML_F16:
+        return (rng.standard_normal(n) * 0.05).astype(np.float16).tobytes()
+    rows = n // shape[0]
+    return O.gen_weights(fmt, rows, shape[0], seed).tobytes()
+
+
+@pytest.fixture(scope="module")
+def model_file(tmp_path_factory):
+    path = str(tmp_path_factory.mktemp("gguf") / "tiny-llama.gguf")
+    tensors = [(nm, sh, gt, _tensor_data(nm, sh, gt, f, 100 + i)) for i, (nm, sh, gt, f) in enumerate(TENSORS)]
+    W.write_gguf(path, W.llama_kv(dim=DIM, heads=HEADS, heads_kv=HEADS_KV, layers=2, ff=512, ctx=2048,
+                                  vocab=VOCAB, rope=500000.0, eps=1e-6), tensors)
+    return path, {nm: (sh, gt, f, data) for nm, sh, gt, f, data in
+                  [(t[0], t[1], t[2], TENSORS[i][3], t[3]) for i, t in enumerate(tensors)]}
+
+
+def _ours(path):
+    import gq
+    return gq.GGUF(path)
+
+
+# ---- parsing (CPU) -----------------------------------------------------------
+def test_parse_matches_written_file(model_file):
+    path, spec = model_file
+    with _ours(path) as g:
+        ts = g.tensors()
+        assert [t["name"] for t in ts] == [t[0] for t in TENSORS]
+        raw = open(path, "rb").read()
+        for t in ts:
+            sh, gt, fmt, data = spec[t["name"]]
+            assert t["shape"] == sh and t["ggml_type"] == gt
+            assert t["size_bytes"] == W.tensor_bytes(gt, sh) == len(data)
+            assert t["offset"] % 32 == 0
+            assert raw[t["offset"]:t["offset"] + t["size_bytes"]] == data
+            assert g.read_raw(t["name"]).tobytes() == data
+        c = g.config()
+        assert (c["dim"], c["num_heads"], c["num_heads_kv"], c["head_dim"]) == (DIM, HEADS, HEADS_KV, HD)
+        assert (c["num_layers"], c["hidden_dim"], c["max_seq_len"]) == (2, 512, 2048)
+        assert c["rope_base"] == 500000.0 and c["rms_eps"] == np.float32(1e-6)
+        assert c["vocab_size"] == len(VOCAB)
+        voc = g.vocab()
+        assert voc[:5] == [v.encode() for v in VOCAB[:5]]
+        assert voc[5] == b"<too_long>" and voc[6] == b"end"
+
+
+@pytest.mark.skipif(not O.ref_available(), reason="oracle/_ref not built")
+def test_parse_matches_reference_loader(model_file):
+    path, _ = model_file
+    rts, rcfg, err = O.ref_gguf_parse(path)
+    assert rts is not None, err
+    with _ours(path) as g:
+        ts = g.tensors()
+        assert len(ts) == len(rts)
+        for a, b in zip(ts, rts):
+            assert a["name"] == b["name"] and a["shape"] == b["shape"]
+            assert a["offset"] == b["offset"] and a["size_bytes"] == b["size_bytes"]
+            want = "UNKNOWN" if a["dtype"] == "Q8_0" else a["dtype"]
+            assert want == b["dtype"]
+        c = g.config()
+        for k, v in rcfg.items():
+            assert c[k] == v, k
+
+
+def _write(tmp_path, name, kv, tensors, **kw):
+    p = str(tmp_path / name)
+    W.write_gguf(p, kv, tensors, **kw)
+    return p
+
+
+@pytest.mark.skipif(not O.ref_available(), reason="oracle/_ref not built")
+def test_defaults_and_key_order_match_reference(tmp_path):
+    """No head_count_kv -> the 7B default (32) is kept; head_dim follows the
+    last of embedding_length / head_count; other llama.* defaults stay."""
+    kv = [("llama.attention.head_count", W.U32, 8), ("llama.embedding_length", W.I32, 512),
+          ("llama.rope.freq_base", W.F32, 1234.5), ("some.other", W.ARR, (W.ARR, [(W.U8, [1, 2]), (W.U8, [3])])),
+          ("llama.context_length", W.U16, 77)]
+    data = O.gen_weights(O.Q4_0, 4, 64, 1).tobytes()
+    p = _write(tmp_path, "d.gguf", kv[:3] + kv[4:], [("w", [64, 4], W.GGML_Q4_0, data)])
+    rts, rcfg, err = O.ref_gguf_parse(p)
+    assert rts is not None, err
+    with _ours(p) as g:
+        c = g.config()
+        for k, v in rcfg.items():
+            assert c[k] == v, k
+        assert c["num_heads_kv"] == 32 and c["head_dim"] == 64 and c["max_seq_len"] == 77
+        assert c["vocab_size"] == 32000 and c["num_layers"] == 32
+    # nested arrays are skipped by the spec-following parser
+    p2 = _write(tmp_path, "n.gguf", kv, [("w", [64, 4], W.GGML_Q4_0, data)])
+    with _ours(p2) as g:
+        assert g.tensors()[0]["name"] == "w"
+
+
+def test_rejects_malformed_files(tmp_path):
+    import gq
+    data = O.gen_weights(O.Q4_0, 4, 64, 1).tobytes()
+    good = _write(tmp_path, "ok.gguf", W.llama_kv(), [("w", [64, 4], W.GGML_Q4_0, data)])
+    raw = open(good, "rb").read()
+    cases = {
+        "magic": b"GGUX" + raw[4:],
+        "version": raw[:4] + (1).to_bytes(4, "little") + raw[8:],
+        "truncated_header": raw[:40],
+        "empty": b"",
+    }
+    for name, blob in cases.items():
+        p = str(tmp_path / f"bad_{name}.gguf")
+        open(p, "wb").write(blob)
+        with pytest.raises(gq.GQError):
+            gq.GGUF(p)
+    # too many key/value pairs (the reference stops at 2000)
+    p = _write(tmp_path, "kv.gguf", W.llama_kv(), [("w", [64, 4], W.GGML_Q4_0, data)], kv_count=2001)
+    with pytest.raises(gq.GQError):
+        gq.GGUF(p)
+    with pytest.raises(gq.GQError, match="Not GGUF"):
+        gq.GGUF(str(tmp_path / "bad_magic.gguf"))
+    with pytest.raises(gq.GQError, match="Old GGUF"):
+        gq.GGUF(str(tmp_path / "bad_version.gguf"))
+
+
+def test_tensor_data_outside_file_is_an_error(tmp_path):
+    import gq
+    data = O.gen_weights(O.Q4_0, 4, 64, 1).tobytes()
+    p = _write(tmp_path, "cut.gguf", W.llama_kv(), [("w", [64, 4], W.GGML_Q4_0, data)])
+    blob = open(p, "rb").read()
+    open(p, "wb").write(blob[:-10])
+    with gq.GGUF(p) as g:
+        assert g.tensors()[0]["size_bytes"] == len(data)
+        with pytest.raises(gq.GQError, match="outside the file"):
+            g.read_raw("w")
+        with pytest.raises(gq.GQError, match="outside the file"):
+            g.plan("w", gq.LOAD_QUANT)
+
+
+def test_plans(model_file):
+    import gq
+    path, spec = model_file
+    with _ours(path) as g:
+        p = g.plan("blk.0.attn_k.weight", gq.LOAD_INT4)
+        assert p["transpose"] and p["is_qkv"] and p["has_head_scales"] and p["num_heads"] == HEADS_KV
+        assert p["bytes"] == DIM * KV // 2 and p["scale_bytes"] == DIM * KV // 32 * 4
+        p = g.plan("blk.1.attn_k.weight", gq.LOAD_F16)
+        assert not p["transpose"] and p["bytes"] == DIM * KV * 2
+        p = g.plan("blk.0.ffn_down.weight", gq.LOAD_INT8)
+        assert not p["transpose"] and p["bytes"] == 512 * DIM
+        p = g.plan("blk.0.ffn_gate.weight", gq.LOAD_QUANT)
+        assert (p["fmt"], p["N"], p["K"], p["bytes"]) == (gq.FMT_Q4_0, 512, DIM, gq.packed_size(gq.FMT_Q4_0, 512, DIM))
+        with pytest.raises(gq.GQError, match="Q4_0, Q8_0 or Q4_K"):
+            g.plan("output.weight", gq.LOAD_QUANT)
+        with pytest.raises(gq.GQError, match="not found"):
+            g.plan("nope", gq.LOAD_F32)
+
+
+# ---- device loads (GPU) ------------------------------------------------------
+def _f32_of(spec_entry):
+    sh, gt, fmt, data = spec_entry
+    if gt == W.GGML_F32:
+        return np.frombuffer(data, dtype=np.float32).copy()
+    if gt == W.GGML_F16:
+        return O.fp16_to_fp32(np.frombuffer(data, dtype=np.uint16))
+    return O.dequant(fmt, np.frombuffer(data, dtype=np.uint8))
+
+
+def _is_kv_transposed(name, shape):
+    return ("attn_k.weight" in name or "attn_v.weight" in name) and shape == [DIM, KV]
+
+
+def _oracle_load(name, spec_entry, kind):
+    sh = spec_entry[0]
+    w = _f32_of(spec_entry)
+    if kind == 0:
+        return w.view(np.uint8), None, None
+    if kind == 2 and spec_entry[1] == W.GGML_Q8_0:
+        blk = np.frombuffer(spec_entry[3], dtype=np.uint8).reshape(-1, 34)
+        q = blk[:, 2:].copy().reshape(-1)
+        s = O.fp16_to_fp32(blk[:, :2].copy().view(np.uint16).ravel())
+        return q, s, None
+    if _is_kv_transposed(name, sh):
+        w = O.gqa_transpose(w, DIM, KV)
+    if kind == 1:
+        if spec_entry[1] == W.GGML_F16:  # stored fp16 is kept as is (subnormals included)
+            h = np.frombuffer(spec_entry[3], dtype=np.uint16)
+            if _is_kv_transposed(name, sh):
+                h = h.reshape(DIM, KV).T.copy()
+            return h.view(np.uint8), None, None
+        return O.fp32_to_fp16_trunc(w).view(np.uint8), None, None
+    if kind == 2:
+        q, s = O.requant_int8(w)
+        return q.view(np.uint8), s, None
+    q, s = O.requant_int4(w)
+    hs = None
+    if any(t in name for t in ("attn_q", "attn_k", "attn_v")):
+        nh = HEADS_KV if ("attn_k.weight" in name or "attn_v.weight" in name) else HEADS
+        hs = O.head_scales(w, nh, HD, DIM)
+    return q, s, hs
+
+
+def _bits_equal(a, b):
+    a = np.asarray(a).view(np.uint8).ravel()
+    b = np.asarray(b).view(np.uint8).ravel()
+    return a.size == b.size and bool((a == b).all())
+
+
+REF_TYPES = (W.GGML_F32, W.GGML_F16, W.GGML_Q4_K, W.GGML_Q6_K)  # types the reference loader converts
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("kind", [0, 1, 2, 3])
+@pytest.mark.parametrize("name", [t[0] for t in TENSORS])
+def test_load_matches_oracle(dev, model_file, name, kind):
+    import gq
+    path, spec = model_file
+    with _ours(path) as g:
+        data, sc, hs, plan = g.load(name, kind, device=dev)
+    q, s, h = _oracle_load(name, spec[name], kind)
+    assert _bits_equal(data.cpu().numpy(), q), name
+    if s is not None:
+        assert _bits_equal(sc.cpu().numpy(), s)
+    if h is not None:
+        assert _bits_equal(hs.cpu().numpy(), h)
+    else:
+        assert hs is None
+
+
+@pytest.mark.gpu
+@pytest.mark.skipif(not O.ref_available(), reason="oracle/_ref not built")
+@pytest.mark.parametrize("kind", [0, 1, 2, 3])
+@pytest.mark.parametrize("name", [t[0] for t in TENSORS if t[2] in REF_TYPES])
+def test_load_matches_reference_loader(dev, model_file, name, kind):
+    """Bit-identical to the reference GGUFLoader run on the same file."""
+    import gq
+    path, spec = model_file
+    rq, rs, rh = O.ref_gguf_load(path, name, kind, max_bytes=4 << 20)
+    with _ours(path) as g:
+        data, sc, hs, plan = g.load(name, kind, device=dev)
+    assert _bits_equal(data.cpu().numpy(), rq), name
+    if kind >= 2:
+        assert _bits_equal(sc.cpu().numpy(), rs)
+    if kind == 3 and rh.size:
+        assert _bits_equal(hs.cpu().numpy(), rh)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("ggml", [False, True])
+def test_load_quant_is_the_t16_repack(dev, model_file, ggml):
+    import gq
+    path, spec = model_file
+    with _ours(path) as g:
+        g.set_q4k_layout(ggml)
+        for name, (sh, gt, fmt, data) in spec.items():
+            if gt not in (W.GGML_Q4_0, W.GGML_Q8_0, W.GGML_Q4_K):
+                continue
+            packed, _, _, plan = g.load(name, gq.LOAD_QUANT, device=dev)
+            f = plan["fmt"]
+            if gt == W.GGML_Q4_K:
+                assert f == (gq.FMT_Q4_K_GGML if ggml else gq.FMT_Q4_K)
+            k = sh[0]
+            n = int(np.prod(sh)) // k
+            host = gq.repack_host(f, np.frombuffer(data, dtype=np.uint8), n, k)
+            assert _bits_equal(packed.cpu().numpy(), host), name
+            # and the packed weights feed the GEMV directly
+            x = O.gen_x(1, k, 5)
+            import torch
+            y = gq.gemv(f, packed, torch.from_numpy(x).to(dev), n, k).cpu().numpy()
+            ref = O.gemv(f, np.frombuffer(data, dtype=np.uint8), x, n, k)
+            assert O.rel_l2(y, ref) <= 1e-3

@@ -1,0 +1,107 @@
+"""The C++ host mirror (GGUFLoader + GretaCompute::gemm, the reference's
+interfaces) driven end to end by tests/cpp/greta_compute_driver.cpp on the GPU,
+checked against the oracle within rel-L2 1e-3 (fp64-accumulated reference)."""
+import os
+import subprocess
+
+import numpy as np
+import pytest
+
+import gguf_writer as W
+import oracle as O
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+DRIVER = os.path.join(ROOT, "gretacore-v3_amd", "lib", "greta_compute_driver")
+TOL = 1e-3
+DIM, HEADS, HEADS_KV, HD = 256, 4, 2, 64
+KV = HEADS_KV * HD
+
+TENSORS = [  # name, shape (ne0 first), ggml type, oracle fmt
+    ("blk.0.ffn_gate.weight", [DIM, 512], W.GGML_Q4_0, O.Q4_0),
+    ("blk.0.ffn_down.weight", [512, DIM], W.GGML_Q8_0, O.Q8_0),
+    ("blk.0.attn_q.weight", [DIM, DIM], W.GGML_Q4_K, O.Q4_K),
+    ("blk.0.attn_k.weight", [DIM, KV], W.GGML_Q4_K, O.Q4_K),
+    ("output.weight", [DIM, 96], W.GGML_Q6_K, O.Q6_K),
+]
+
+
+@pytest.fixture(scope="module")
+def model(tmp_path_factory):
+    d = tmp_path_factory.mktemp("mirror")
+    path = str(d / "m.gguf")
+    tensors, spec = [], {}
+    for i, (nm, sh, gt, fmt) in enumerate(TENSORS):
+        data = O.gen_weights(fmt, int(np.prod(sh)) // sh[0], sh[0], 300 + i).tobytes()
+        tensors.append((nm, sh, gt, data))
+        spec[nm] = (sh, fmt, np.frombuffer(data, dtype=np.uint8))
+    W.write_gguf(path, W.llama_kv(dim=DIM, heads=HEADS, heads_kv=HEADS_KV), tensors)
+    return path, spec, d
+
+
+def _run(model, name, kind, M, label="", adt="f32", seed=0):
+    path, spec, d = model
+    sh = spec[name][0]
+    K = sh[0]
+    N = int(np.prod(sh)) // K
+    a = O.gen_x(M, K, seed)
+    ap, cp = str(d / f"a_{name}_{M}.f32"), str(d / f"c_{name}_{M}.f32")
+    a.tofile(ap)
+    r = subprocess.run([DRIVER, path, name, kind, str(M), ap, cp, label, adt], capture_output=True, text=True,
+                       timeout=120)
+    assert r.returncode == 0, r.stderr + r.stdout
+    c = np.fromfile(cp, dtype=np.float32).reshape(M, N)
+    route = r.stdout.split("route=")[1].split()[0]
+    return a, c, route, N, K
+
+
+def _round_a(a, adt):
+    import torch
+    if adt == "f16":
+        return a.astype(np.float16).astype(np.float32)
+    if adt == "bf16":
+        return torch.from_numpy(a).to(torch.bfloat16).float().numpy()
+    return a
+
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.mark.parametrize("M,adt", [(1, "f32"), (4, "f32"), (16, "f32"), (64, "f32"), (96, "bf16"), (80, "f16")])
+@pytest.mark.parametrize("name", ["blk.0.ffn_gate.weight", "blk.0.ffn_down.weight", "blk.0.attn_q.weight"])
+def test_gemm_gguf_native(dev, model, name, M, adt):
+    a, c, route, N, K = _run(model, name, "quant", M, adt=adt, seed=M)
+    assert route == ("GEMV" if M <= 16 else "GEMM")
+    sh, fmt, raw = model[1][name]
+    ref = O.gemv(fmt, raw, _round_a(a, adt), N, K)
+    assert O.rel_l2(c, ref) <= TOL
+
+
+@pytest.mark.parametrize("M", [1, 8, 33, 64])
+@pytest.mark.parametrize("name", ["blk.0.attn_q.weight", "blk.0.attn_k.weight", "output.weight"])
+@pytest.mark.parametrize("kind", ["int8", "int4"])
+def test_gemm_reference_formats(dev, model, name, kind, M):
+    """load_tensor_int8 / load_tensor_int4 (with GQA transpose and per-head
+    scales) then GretaCompute::gemm -> the reference launchers' math."""
+    a, c, route, N, K = _run(model, name, kind, M, seed=7 + M)
+    assert route == ("GEMV" if M <= 32 else "GEMM")
+    sh, fmt, raw = model[1][name]
+    w = O.dequant(fmt, raw)
+    if "attn_k" in name:
+        w = O.gqa_transpose(w, DIM, KV)
+    if kind == "int8":
+        q, s = O.requant_int8(w)
+        ref = O.gemm_int8_wt(a, q, s, M, N, K)
+    else:
+        q, s = O.requant_int4(w)
+        hs = None
+        if "attn_q" in name or "attn_k" in name:
+            nh = HEADS_KV if "attn_k" in name else HEADS
+            hs = O.head_scales(w, nh, HD, DIM)
+        ref = O.gemm_int4_wt(a, q, s, hs, M, N, K, head_dim=(N // nh) if hs is not None else 0)
+    assert O.rel_l2(c, ref) <= TOL
+
+
+def test_int4_force_gemv_label(dev, model, monkeypatch):
+    monkeypatch.setenv("GRETA_WO_LAYOUT_FORCE", "row")
+    a, c, route, N, K = _run(model, "blk.0.attn_q.weight", "int4", 64, label="attn_o_prefill", seed=3)
+    assert route == "GEMV"

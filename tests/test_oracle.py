@@ -267,3 +267,48 @@ def test_act_q8_quant_and_int_gemm():
     qa = q.reshape(4, 2, 32).astype(np.int64)
     want = np.einsum("mbk,nbk,mb,nb->mn", qa, qw, d.astype(np.float64), dw)
     assert np.allclose(c, want, rtol=1e-6)
+
+
+def _f32_samples(seed=7, n=200000):
+    rng = np.random.default_rng(seed)
+    bits = rng.integers(0, 2**32, size=n, dtype=np.uint64).astype(np.uint32)
+    special = np.array([0, 0x80000000, 0x7F800000, 0xFF800000, 0x7FC00000, 0x33800000, 0x387FC000, 0x38800000,
+                        0x477FE000, 0x477FF000, 0x47800000, 0x3F800000, 0x3F801000, 0xBF801FFF, 0x00000001],
+                       dtype=np.uint32)
+    normal = (rng.standard_normal(n) * 0.05).astype(np.float32).view(np.uint32)
+    return np.concatenate([special, bits, normal]).view(np.float32)
+
+
+def test_fp32_to_fp16_trunc_closed_form():
+    """Truncating conversion (weight_loader.cpp:112-123): exact fp16 values
+    round-trip; mantissa bits below fp16 precision are dropped (toward zero);
+    below the fp16 normal range -> signed zero; at/above 2^16 -> signed Inf."""
+    h = np.arange(0, 1 << 16, dtype=np.uint32).astype(np.uint16)
+    exp = (h >> 10) & 0x1F
+    normal = (exp > 0) & (exp < 31)
+    f = h[normal].view(np.float16).astype(np.float32)
+    assert (O.fp32_to_fp16_trunc(f) == h[normal]).all()
+    # an fp32 value strictly between two fp16 neighbours truncates to the lower magnitude
+    nxt = np.nextafter(f, np.float32(np.inf) * np.sign(f)).astype(np.float32)
+    assert (O.fp32_to_fp16_trunc(nxt) == h[normal]).all()
+    t = O.fp32_to_fp16_trunc(np.array([1e-5, -1e-5, 6.1035156e-05, 65536.0, -1e9, np.inf, np.nan], np.float32))
+    assert list(t) == [0x0000, 0x8000, 0x0400, 0x7C00, 0xFC00, 0x7C00, 0x7C00]
+
+
+@pytest.mark.skipif(not O.ref_available(), reason="oracle/_ref not built")
+def test_fp32_to_fp16_trunc_matches_reference():
+    R = O.ref()
+    f = _f32_samples()
+    ours = O.fp32_to_fp16_trunc(f)
+    idx = np.random.default_rng(1).choice(f.size, 20000, replace=False)
+    idx = np.concatenate([np.arange(15), idx])
+    ref = np.array([R.gqref_fp32_to_fp16(float(v)) for v in f[idx]], dtype=np.uint16)
+    assert (ours[idx] == ref).all()
+
+
+def test_fp16_array_form_matches_scalar():
+    h = np.arange(0, 1 << 16, dtype=np.uint32).astype(np.uint16)
+    a = O.fp16_to_fp32(h)
+    L = O.lib()
+    for v in range(0, 1 << 16, 97):
+        assert a[v].tobytes() == np.float32(L.gqo_fp16_to_fp32(v)).tobytes()
