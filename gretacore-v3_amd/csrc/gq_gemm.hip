@@ -6,86 +6,36 @@
 // the reference kernels' transposed 16x16 tile store is a bug, not a contract.
 //
 // Design:
-//  * A (activations) is first converted to fp16 [M][Kp] (bf16 values are exact
-//    in fp16 inside fp16's range) so the main loop stages it with plain copies.
-//  * Workgroup tile BM x BN = 128 x 128, K step 128 (one T16 chunk; for Q4_K one
-//    half super-block).  The weight tile is dequantized in registers with the
-//    per-block scale folded in (one fp16 rounding per weight, as the reference's
-//    __float2half(w * s) does) and written to LDS; A and W tiles are read back
-//    as v_mfma_f32_32x32x16_f16 operands.  Global loads of step k+1 are issued
-//    before the MFMAs of step k.
-//  * 4 waves in a 2 x 2 arrangement, each owning a 64 x 64 block of C (2 x 2
-//    MFMA tiles, fp32 accumulators).
+//  * Workgroup tile BM x BN (256 x 256, 256 x 128 or 128 x 128), K step 64,
+//    8 waves (two per SIMD, so one wave's dequantization overlaps the other's
+//    MFMAs) in a 2 x 4 arrangement; each wave owns a (BM/2) x (BN/4) block of
+//    C as v_mfma_f32_32x32x16_f16 tiles with fp32 accumulators.
+//  * Activations are fp16 [M][lda] in HBM (bf16 / fp32 callers get one
+//    conversion pass first; bf16 -> fp16 is exact inside fp16's range, and
+//    the reference rounds A to fp16 before its MFMAs too).  They go straight
+//    from global memory into LDS (global_load_lds_dwordx4, no registers, no
+//    VALU) with the 16-byte chunks of each row XOR-swizzled by the row index,
+//    so the MFMA fragment reads are free of bank conflicts.
+//  * Weights are loaded two K steps ahead into registers (wave-uniform base +
+//    32-bit lane offset addressing), dequantized with the per-block scale
+//    folded in (one fp16 rounding of the exact product, as the reference's
+//    __float2half(w * s) does) and stored to LDS one step ahead.  Both LDS
+//    operand tiles are double-buffered: one barrier per K step.
+//  * Tiles are assigned so that the 8 XCDs (workgroup id mod 8) each work on a
+//    contiguous range of weight column tiles, all M tiles of one column tile
+//    in a row: a weight tile is fetched from HBM once per XCD and then served
+//    from that XCD's L2.
+#include <stdlib.h>
+
+#include <type_traits>
+
 #include "gq_internal.h"
 
 namespace {
 
-constexpr int BM = 128, BN = 128, BK = 128;
-constexpr int LDS_STRIDE = BK + 8;  // halves; pads rows apart in the LDS banks
-
-// Global-load staging registers for one K step.
-template <int FMT>
-struct BRegs;
-template <>
-struct BRegs<GQ_FMT_Q4_0> {
-  gq_u4 q[2];
-  gq_u2 d[2];
-};
-template <>
-struct BRegs<GQ_FMT_Q8_0> {
-  gq_u4 q[4];
-  gq_u2 d[4];
-};
-template <>
-struct BRegs<GQ_FMT_Q4_K> {
-  gq_u4 q[2];
-  gq_u4 meta[2];
-};
-
-struct Tile {
-  const uint8_t *w;
-  size_t sc_off;
-  int C;        // T16 chunks per row
-  int tile0;    // first 16-row tile of this workgroup
-  int ntiles;   // tiles in the tensor
-};
-
-// ---- weight tile: global -> registers --------------------------------------
-template <int FMT>
-GQ_DEV void load_b(const Tile &tl, int step, int tid, BRegs<FMT> &br) {
-  if constexpr (FMT == GQ_FMT_Q4_0) {
-#pragma unroll
-    for (int i = 0; i < 2; ++i) {
-      int slot = tid + 256 * i, rt = slot >> 6, lane = slot & 63;
-      int tile = tl.tile0 + rt;
-      if (tile >= tl.ntiles) tile = tl.ntiles - 1;  // clamped; results discarded
-      size_t ch = (size_t)tile * tl.C + step;
-      br.q[i] = gq_ld16(tl.w + (ch << 10) + 16 * lane);
-      br.d[i] = gq_ld8(tl.w + tl.sc_off + ch * 128 + 8 * (lane & 15));
-    }
-  } else if constexpr (FMT == GQ_FMT_Q8_0) {
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      int slot = tid + 256 * i, rt = slot >> 7, part = (slot >> 6) & 1, lane = slot & 63;
-      int tile = tl.tile0 + rt;
-      if (tile >= tl.ntiles) tile = tl.ntiles - 1;
-      size_t ch = (size_t)tile * tl.C + step;
-      br.q[i] = gq_ld16(tl.w + (ch << 11) + (part << 10) + 16 * lane);
-      br.d[i] = gq_ld8(tl.w + tl.sc_off + ch * 128 + 8 * (lane & 15));
-    }
-  } else {
-    const int s = step >> 1, h = step & 1;
-#pragma unroll
-    for (int i = 0; i < 2; ++i) {
-      int slot = tid + 256 * i, rt = slot >> 6, lane = slot & 63;
-      int tile = tl.tile0 + rt;
-      if (tile >= tl.ntiles) tile = tl.ntiles - 1;
-      size_t ch = (size_t)tile * tl.C + s;
-      br.q[i] = gq_ld16(tl.w + (ch << 11) + (h << 10) + 16 * lane);
-      br.meta[i] = gq_ld16(tl.w + tl.sc_off + ch * 256 + 16 * (lane & 15));
-    }
-  }
-}
+constexpr int BK = 64;
+constexpr int BSTRIDE = BK + 8;  // weight tile row stride (halves): padding keeps ds_read_b128 conflict-free
+constexpr int NTHR = 512;
 
 GQ_DEV gq_half2 h2_of_bits16(uint32_t b16) {
   uint32_t v = (b16 & 0xFFFFu) * 0x10001u;
@@ -117,121 +67,149 @@ GQ_DEV void group_to_h16(uint32_t w0, uint32_t w1, gq_half2 off, gq_half2 scale,
   }
 }
 
-// ---- weight tile: registers -> dequantized fp16 in LDS ---------------------
-// Thread slot (rt, lane = 16g + r): row 16rt + r, and for MFMA step m the
-// elements 16(g&1)..+15 of block 2m + (g>>1) of the 128-k step.
+
+// ---- weight records ---------------------------------------------------------
+// A record is (row tile tl of the workgroup, lane = 16 g + r): row 16 tl + r
+// and, for K step s (64 k), the 16 elements 16 (g & 1) .. + 15 of the step's
+// 32-block (g >> 1).
 template <int FMT>
-GQ_DEV void store_b(const BRegs<FMT> &br, int step, int tid, _Float16 *Bs) {
-  (void)step;
+struct WRec;
+template <>
+struct WRec<GQ_FMT_Q4_0> {
+  gq_u2 q;     // 16 codes
+  uint32_t d;  // d of the record's block for step m = 0 (low half) and m = 1 (high half)
+};
+template <>
+struct WRec<GQ_FMT_Q8_0> {
+  gq_u4 q;     // 16 int8
+  uint32_t d;
+};
+template <>
+struct WRec<GQ_FMT_Q4_K> {
+  gq_u2 q;
+  gq_u4 meta;  // d, dmin, W1, W2, W3 of the row's super-block
+};
+
+// Per-record byte offsets that do not change with the K step (32-bit: the
+// host checks that the packed tensor is smaller than 4 GiB).
+struct WOff {
+  uint32_t q, s;
+};
+
+template <int FMT>
+GQ_DEV WOff rec_offsets(int tile, int lane, int C, uint32_t sc_off) {
+  const int g = lane >> 4, r = lane & 15;
+  const uint32_t tc = (uint32_t)tile * (uint32_t)C;
+  WOff o;
+  if constexpr (FMT == GQ_FMT_Q4_0) {
+    o.q = (tc << 10) + 16u * lane;
+    o.s = sc_off + tc * 128u + 8u * r + 4u * (g >> 1);
+  } else if constexpr (FMT == GQ_FMT_Q8_0) {
+    o.q = (tc << 11) + 16u * lane;
+    o.s = sc_off + tc * 128u + 8u * r + 4u * (g >> 1);
+  } else {
+    o.q = (tc << 11) + 16u * lane;
+    o.s = sc_off + tc * 256u + 16u * r;
+  }
+  return o;
+}
+
+// K step `step` of a record: 16 codes (8 bytes, Q8_0 16 bytes) and the scales.
+template <int FMT>
+GQ_DEV void load_w(const uint8_t *w, const WOff &o, int step, WRec<FMT> &rec) {
+  if constexpr (FMT == GQ_FMT_Q4_0) {
+    const uint8_t *wq = w + (((size_t)(step >> 1)) << 10) + 8 * (step & 1);
+    const uint8_t *ws = w + ((size_t)(step >> 1)) * 128;
+    rec.q = gq_ld8(wq + o.q);
+    rec.d = *reinterpret_cast<const uint32_t *>(ws + o.s);
+  } else if constexpr (FMT == GQ_FMT_Q8_0) {
+    const uint8_t *wq = w + (((size_t)(step >> 1)) << 11) + ((step & 1) << 10);
+    const uint8_t *ws = w + ((size_t)(step >> 1)) * 128;
+    rec.q = gq_ld16(wq + o.q);
+    rec.d = *reinterpret_cast<const uint32_t *>(ws + o.s);
+  } else {
+    const int m = step & 3;
+    const uint8_t *wq = w + (((size_t)(step >> 2)) << 11) + ((m >> 1) << 10) + 8 * (m & 1);
+    const uint8_t *ws = w + ((size_t)(step >> 2)) * 256;
+    rec.q = gq_ld8(wq + o.q);
+    rec.meta = gq_ld16(ws + o.s);
+  }
+}
+
+// dequantized fp16 values of a record -> its 16 LDS slots
+template <int FMT>
+GQ_DEV void store_w(const WRec<FMT> &rec, int tl, int lane, int step, _Float16 *Bs) {
+  const int g = lane >> 4, r = lane & 15;
+  _Float16 *dst = Bs + (16 * tl + r) * BSTRIDE + 32 * (g >> 1) + 16 * (g & 1);
+  gq_half8 o0, o1;
   if constexpr (FMT == GQ_FMT_Q4_0) {
     const gq_half2 off = {(_Float16)-1032.0f, (_Float16)-1032.0f};
-#pragma unroll
-    for (int i = 0; i < 2; ++i) {
-      int slot = tid + 256 * i, rt = slot >> 6, lane = slot & 63, g = lane >> 4, r = lane & 15;
-#pragma unroll
-      for (int m = 0; m < 2; ++m) {
-        const int j = 2 * m + (g >> 1);
-        uint32_t dbits = (j >> 1) ? (br.d[i][j & 1] >> 16) : br.d[i][j & 1];
-        gq_half8 o0, o1;
-        group_to_h16(br.q[i][2 * m], br.q[i][2 * m + 1], off, h2_of_bits16(dbits), o0, o1);
-        _Float16 *dst = Bs + (16 * rt + r) * LDS_STRIDE + 32 * j + 16 * (g & 1);
-        *reinterpret_cast<gq_half8 *>(dst) = o0;
-        *reinterpret_cast<gq_half8 *>(dst + 8) = o1;
-      }
-    }
+    const uint32_t dbits = (step & 1) ? (rec.d >> 16) : rec.d;
+    group_to_h16(rec.q[0], rec.q[1], off, h2_of_bits16(dbits), o0, o1);
   } else if constexpr (FMT == GQ_FMT_Q8_0) {
     const gq_half2 off = {(_Float16)-1152.0f, (_Float16)-1152.0f};
+    const uint32_t dbits = (step & 1) ? (rec.d >> 16) : rec.d;
+    const gq_half2 d2 = h2_of_bits16(dbits);
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      int slot = tid + 256 * i, rt = slot >> 7, m = (slot >> 6) & 1, lane = slot & 63;
-      int g = lane >> 4, r = lane & 15;
-      const int j = 2 * m + (g >> 1);
-      uint32_t dbits = (j >> 1) ? (br.d[i][j & 1] >> 16) : br.d[i][j & 1];
-      const gq_half2 d2 = h2_of_bits16(dbits);
-      _Float16 *dst = Bs + (16 * rt + r) * LDS_STRIDE + 32 * j + 16 * (g & 1);
-#pragma unroll
-      for (int q2 = 0; q2 < 2; ++q2) {
-        gq_half8 o;
-#pragma unroll
-        for (int q = 0; q < 2; ++q) {
-          gq_half2 lo, hi;
-          bytes_to_magic(br.q[i][2 * q2 + q] ^ 0x80808080u, lo, hi);
-          lo = (lo + off) * d2;
-          hi = (hi + off) * d2;
-          o[4 * q] = lo[0];
-          o[4 * q + 1] = lo[1];
-          o[4 * q + 2] = hi[0];
-          o[4 * q + 3] = hi[1];
-        }
-        *reinterpret_cast<gq_half8 *>(dst + 8 * q2) = o;
-      }
+    for (int q = 0; q < 4; ++q) {
+      gq_half2 lo, hi;
+      bytes_to_magic(rec.q[q] ^ 0x80808080u, lo, hi);
+      lo = (lo + off) * d2;
+      hi = (hi + off) * d2;
+      gq_half8 &o = (q < 2) ? o0 : o1;
+      const int b = 4 * (q & 1);
+      o[b] = lo[0];
+      o[b + 1] = lo[1];
+      o[b + 2] = hi[0];
+      o[b + 3] = hi[1];
     }
   } else {
-    const int hh = step & 1;
+    const uint32_t mv[4] = {rec.meta[0], rec.meta[1], rec.meta[2], rec.meta[3]};
+    const float d = gq_h2f(mv[0] & 0xFFFFu), dmin = gq_h2f(mv[0] >> 16);
+    const _Float16 hd = (_Float16)d;  // exact: d came from fp16 (NaN aside)
+    const int j = 2 * (step & 3) + (g >> 1);
+    uint32_t sc, mn;
+    gq_q4k_meta_codes(mv, j, &sc, &mn);
+    const _Float16 hsc = (_Float16)(float)sc, hnsc = (_Float16)(-1024.0f * (float)sc);
+    const _Float16 hmin = (_Float16)(-(dmin * (float)mn));
+    const gq_half2 sc2 = {hsc, hsc}, nsc2 = {hnsc, hnsc}, d2 = {hd, hd}, mn2 = {hmin, hmin};
+    const uint32_t w0 = rec.q[0], w1 = rec.q[1];
+    const uint32_t regs[4] = {w0 & 0x0F0F0F0Fu, (w0 >> 4) & 0x0F0F0F0Fu, w1 & 0x0F0F0F0Fu, (w1 >> 4) & 0x0F0F0F0Fu};
 #pragma unroll
-    for (int i = 0; i < 2; ++i) {
-      int slot = tid + 256 * i, rt = slot >> 6, lane = slot & 63, g = lane >> 4, r = lane & 15;
-      const gq_u4 &mt = br.meta[i];
-      const uint32_t mv[4] = {mt[0], mt[1], mt[2], mt[3]};
-      const float d = gq_h2f(mv[0] & 0xFFFFu), dmin = gq_h2f(mv[0] >> 16);
-      const _Float16 hd = (_Float16)d;  // exact: d came from fp16 (NaN aside)
-#pragma unroll
-      for (int m2 = 0; m2 < 2; ++m2) {
-        const int m = 2 * hh + m2, j = 2 * m + (g >> 1);
-        uint32_t sc, mn;
-        gq_q4k_meta_codes(mv, j, &sc, &mn);
-        const _Float16 hsc = (_Float16)(float)sc, hnsc = (_Float16)(-1024.0f * (float)sc);
-        const _Float16 hmin = (_Float16)(-(dmin * (float)mn));
-        const gq_half2 sc2 = {hsc, hsc}, nsc2 = {hnsc, hnsc}, d2 = {hd, hd}, mn2 = {hmin, hmin};
-        const uint32_t w0 = br.q[i][2 * m2], w1 = br.q[i][2 * m2 + 1];
-        const uint32_t regs[4] = {w0 & 0x0F0F0F0Fu, (w0 >> 4) & 0x0F0F0F0Fu, w1 & 0x0F0F0F0Fu,
-                                  (w1 >> 4) & 0x0F0F0F0Fu};
-        gq_half8 o[2];
-#pragma unroll
-        for (int q = 0; q < 4; ++q) {
-          gq_half2 lo, hi;
-          bytes_to_magic(regs[q], lo, hi);
-          lo = __builtin_elementwise_fma(__builtin_elementwise_fma(lo, sc2, nsc2), d2, mn2);
-          hi = __builtin_elementwise_fma(__builtin_elementwise_fma(hi, sc2, nsc2), d2, mn2);
-          const int b = 4 * (q & 1);
-          o[q >> 1][b] = lo[0];
-          o[q >> 1][b + 1] = lo[1];
-          o[q >> 1][b + 2] = hi[0];
-          o[q >> 1][b + 3] = hi[1];
-        }
-        // local k of sub-block j within this 128-k step: 32 * (j - 4hh)
-        _Float16 *dst = Bs + (16 * rt + r) * LDS_STRIDE + 32 * (j - 4 * hh) + 16 * (g & 1);
-        *reinterpret_cast<gq_half8 *>(dst) = o[0];
-        *reinterpret_cast<gq_half8 *>(dst + 8) = o[1];
-      }
+    for (int q = 0; q < 4; ++q) {
+      gq_half2 lo, hi;
+      bytes_to_magic(regs[q], lo, hi);
+      lo = __builtin_elementwise_fma(__builtin_elementwise_fma(lo, sc2, nsc2), d2, mn2);
+      hi = __builtin_elementwise_fma(__builtin_elementwise_fma(hi, sc2, nsc2), d2, mn2);
+      gq_half8 &o = (q < 2) ? o0 : o1;
+      const int b = 4 * (q & 1);
+      o[b] = lo[0];
+      o[b + 1] = lo[1];
+      o[b + 2] = hi[0];
+      o[b + 3] = hi[1];
     }
   }
+  *reinterpret_cast<gq_half8 *>(dst) = o0;
+  *reinterpret_cast<gq_half8 *>(dst + 8) = o1;
 }
 
-// ---- activation tile -------------------------------------------------------
-// LDS column kk of step `step` holds activation column step * BK + kk (a Q4_K
-// super-block is two consecutive 128-k steps).
-template <int FMT>
-GQ_DEV int a_col(int step, int kk) {
-  return step * BK + kk;
-}
-
-template <int FMT>
-GQ_DEV void load_a(const _Float16 *__restrict__ a, int M, int Kp, int m0, int step, int tid, gq_u4 (&ar)[8]) {
+// ---- activation tile: global fp16 -> LDS directly ----------------------------
+// A K step of the tile is BM rows x 8 chunks of 16 B.  One wave instruction
+// fills 8 consecutive rows (1 KiB of LDS, lane l at byte 16 l); lane l loads
+// logical chunk (l & 7) ^ (l >> 3) of row l >> 3 -- the chunk index is XORed
+// with the row index mod 8.
+template <int BM>
+GQ_DEV void load_a_lds(const _Float16 *a16, int lda, int M, int m0, int step, int wave, int lane, _Float16 *As) {
+  constexpr int PER_WAVE = BM / 64;  // instructions per wave per K step
 #pragma unroll
-  for (int i = 0; i < 8; ++i) {
-    int idx = tid + 256 * i, row = idx >> 4, c8 = (idx & 15) * 8;
-    int m = m0 + row;
+  for (int i = 0; i < PER_WAVE; ++i) {
+    const int row0 = 8 * (wave * PER_WAVE + i);
+    const int c = (lane & 7) ^ (lane >> 3);
+    int m = m0 + row0 + (lane >> 3);
     if (m >= M) m = M - 1;  // clamped; rows >= M are never stored
-    ar[i] = gq_ld16(a + (size_t)m * Kp + a_col<FMT>(step, c8));
-  }
-}
-
-GQ_DEV void store_a(const gq_u4 (&ar)[8], int tid, _Float16 *As) {
-#pragma unroll
-  for (int i = 0; i < 8; ++i) {
-    int idx = tid + 256 * i, row = idx >> 4, c8 = (idx & 15) * 8;
-    *reinterpret_cast<gq_u4 *>(As + row * LDS_STRIDE + c8) = ar[i];
+    const _Float16 *src = a16 + (size_t)m * lda + step * BK + 8 * c;
+    __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void *)src,
+                                     (__attribute__((address_space(3))) void *)(As + row0 * BK), 16, 0, 0);
   }
 }
 
@@ -242,67 +220,156 @@ GQ_DEV uint16_t f32_to_bf16_rne(float f) {
   return (uint16_t)(u >> 16);
 }
 
-template <int FMT, int CBF16>
-__global__ void __launch_bounds__(256)
-k_gemm_t16(const uint8_t *__restrict__ w, size_t sc_off, const _Float16 *__restrict__ a, void *__restrict__ c,
-           int M, int N, int C, int Kp) {
-  __shared__ __attribute__((aligned(16))) _Float16 As[BM * LDS_STRIDE];
-  __shared__ __attribute__((aligned(16))) _Float16 Bs[BN * LDS_STRIDE];
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int wm = wave >> 1, wn = wave & 1;
-  const int m0 = blockIdx.y * BM, n0 = blockIdx.x * BN;
-  Tile tl{w, sc_off, C, n0 / 16, (int)gq_tiles(N)};
-  const int nsteps = (FMT == GQ_FMT_Q4_K) ? 2 * C : C;
 
-  gq_f16v acc[2][2];
+// Workgroup tile -> (m tile, n tile): ids are spread over the 8 XCDs
+// round-robin, so id -> (id mod 8) * (G / 8) + id / 8 gives each XCD a
+// contiguous range of tile indices; consecutive indices walk the M tiles of one
+// weight column tile.
+GQ_DEV void tile_of(int id, int G, int tiles_m, int &mt, int &nt) {
+  const int t = (G % 8 == 0) ? (id % 8) * (G / 8) + id / 8 : id;
+  nt = t / tiles_m;
+  mt = t % tiles_m;
+}
+
+template <int FMT, int CBF16, int BM, int BN>
+__global__ void __launch_bounds__(NTHR) __attribute__((amdgpu_waves_per_eu(2, 2)))
+k_gemm_t16(const uint8_t *__restrict__ w, uint32_t sc_off, const _Float16 *__restrict__ a16, int lda,
+           void *__restrict__ c, int M, int N, int C, int nsteps, int tiles_m) {
+  constexpr int TM = BM / 64, TN = BN / 128;  // 32 x 32 MFMA tiles per wave along M and N
+  static_assert(TN >= 1, "BN >= 128");
+  static_assert(2 * (BN * 4 / NTHR) <= 15, "vmcnt immediate");
+  constexpr int WR = BN * 4 / NTHR;          // weight records per thread per step
+  constexpr int KS = BK / 16;                // MFMA k-steps per K step
+  // separate arrays, so the compiler can tell the A tile's LDS DMA from the
+  // weight tile's LDS stores
+  // (one array per buffer: the buffer index is a compile-time constant
+  // everywhere, so no wait for an in-flight DMA into the other buffer is needed)
+  __shared__ __attribute__((aligned(16))) _Float16 As_0[BM * BK];  // [BM][BK], swizzled
+  __shared__ __attribute__((aligned(16))) _Float16 As_1[BM * BK];
+  __shared__ __attribute__((aligned(16))) _Float16 Bs_0[BN * BSTRIDE];  // [BN][BSTRIDE]
+  __shared__ __attribute__((aligned(16))) _Float16 Bs_1[BN * BSTRIDE];
+  auto As_of = [&](auto b) -> _Float16 * { return decltype(b)::value ? As_1 : As_0; };
+  auto Bs_of = [&](auto b) -> _Float16 * { return decltype(b)::value ? Bs_1 : Bs_0; };
+  using B0 = std::integral_constant<int, 0>;
+  using B1 = std::integral_constant<int, 1>;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wm = wave >> 2, wn = wave & 3;
+  int mt, nt;
+  tile_of(blockIdx.x, gridDim.x, tiles_m, mt, nt);
+  const int m0 = mt * BM, n0 = nt * BN;
+  const int ntiles = (int)gq_tiles(N);
+
+  WOff wo[WR];
 #pragma unroll
-  for (int i = 0; i < 2; ++i)
+  for (int i = 0; i < WR; ++i) {
+    const int rec = tid + NTHR * i;
+    int tile = n0 / 16 + (rec >> 6);
+    if (tile >= ntiles) tile = ntiles - 1;  // clamped; those columns are never stored
+    wo[i] = rec_offsets<FMT>(tile, rec & 63, C, sc_off);
+  }
+
+  gq_f16v acc[TM][TN];
 #pragma unroll
-    for (int j = 0; j < 2; ++j)
+  for (int i = 0; i < TM; ++i)
+#pragma unroll
+    for (int j = 0; j < TN; ++j)
 #pragma unroll
       for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.f;
 
-  gq_u4 ar[8];
-  BRegs<FMT> br;
-  load_a<FMT>(a, M, Kp, m0, 0, tid, ar);
-  load_b<FMT>(tl, 0, tid, br);
+  // two register stages of raw weight records: stage s & 1 holds step s
+  WRec<FMT> wr[2][WR];
+  auto load_w_step = [&](int step, int st) {
+#pragma unroll
+    for (int i = 0; i < WR; ++i) load_w<FMT>(w, wo[i], step, wr[st][i]);
+  };
+  auto store_w_part = [&](int q, int step, int st, auto buf_c) {
+    _Float16 *Bs = Bs_of(buf_c);
+#pragma unroll
+    for (int i = 0; i < WR; ++i)
+      if (i % KS == q) {
+        const int rec = tid + NTHR * i;
+        store_w<FMT>(wr[st][i], rec >> 6, rec & 63, step, Bs);
+      }
+  };
 
-  for (int step = 0; step < nsteps; ++step) {
-    __syncthreads();  // previous step's MFMAs are done with the LDS tiles
-    store_a(ar, tid, As);
-    store_b<FMT>(br, step, tid, Bs);
+  // fragment addressing: A rows (BM/2) wm + 32 i + (lane & 31), swizzled chunk;
+  // B rows (BN/4) wn + 32 j + (lane & 31), padded rows
+  const int arow = (BM / 2) * wm + (lane & 31);
+  const int brow = (BN / 4) * wn + (lane & 31);
+  const int sw = lane & 7;  // == arow & 7
+
+  // One K step on LDS buffer BUF: first the weight records of step + 1
+  // (register stage BUF ^ 1, loaded one step ago) are dequantized into weight
+  // buffer BUF ^ 1; then the A tile of step + 1 is requested (LDS DMA into A
+  // buffer BUF ^ 1) and the records of step + 2 (into register stage BUF,
+  // consumed one step ago); then the MFMAs.  The two waves of a SIMD overlap
+  // one's dequantization with the other's MFMAs.
+  auto run_step = [&](int step, auto buf_c) {
+    constexpr int BUF = decltype(buf_c)::value;
+    using NB = std::integral_constant<int, BUF ^ 1>;
+    // the last steps' loads are clamped: loaded, never read
+    const int s1 = step + 1 < nsteps ? step + 1 : nsteps - 1;
+    const int s2 = step + 2 < nsteps ? step + 2 : nsteps - 1;
+#pragma unroll
+    for (int q = 0; q < KS; ++q) store_w_part(q, s1, BUF ^ 1, NB{});
+    // (the stores only wait for loads issued a step ago)
+    __builtin_amdgcn_sched_barrier(0);
+    load_a_lds<BM>(a16, lda, M, m0, s1, wave, lane, As_of(NB{}));
+    load_w_step(s2, BUF);
+    // keep the requests ahead of the MFMAs: they have the whole step to land
+    __builtin_amdgcn_sched_barrier(0);
+    const _Float16 *As = As_of(buf_c) + arow * BK;
+    const _Float16 *Bs = Bs_of(buf_c) + brow * BSTRIDE + 8 * (lane >> 5);
+    gq_half8 af[2][TM], bf[2][TN];
+    auto read_frags = [&](int ks, int fb) {
+      const int ch = (2 * ks + (lane >> 5)) ^ sw;
+#pragma unroll
+      for (int i = 0; i < TM; ++i)
+        af[fb][i] = *reinterpret_cast<const gq_half8 *>(As + 32 * i * BK + 8 * ch);
+#pragma unroll
+      for (int j = 0; j < TN; ++j)
+        bf[fb][j] = *reinterpret_cast<const gq_half8 *>(Bs + 32 * j * BSTRIDE + 16 * ks);
+    };
+    read_frags(0, 0);
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) {
+      if (ks + 1 < KS) read_frags(ks + 1, (ks + 1) & 1);
+#pragma unroll
+      for (int i = 0; i < TM; ++i)
+#pragma unroll
+        for (int j = 0; j < TN; ++j) acc[i][j] = gq_mfma32(af[ks & 1][i], bf[ks & 1][j], acc[i][j]);
+    }
+    // the A tile of step + 1 (LDS DMA, issued before the 2 * WR record
+    // loads) must land before any wave reads buffer BUF ^ 1
+    __builtin_amdgcn_s_waitcnt(0x0F70 | (2 * WR));  // vmcnt(2 * WR)
     __syncthreads();
-    if (step + 1 < nsteps) {
-      load_a<FMT>(a, M, Kp, m0, step + 1, tid, ar);
-      load_b<FMT>(tl, step + 1, tid, br);
-    }
+  };
+
+  // prologue: step 0 in buffer 0, step 1 in register stage 1
+  load_a_lds<BM>(a16, lda, M, m0, 0, wave, lane, As_0);
+  load_w_step(0, 0);
+  load_w_step(nsteps > 1 ? 1 : 0, 1);
 #pragma unroll
-    for (int ks = 0; ks < BK / 16; ++ks) {
-      const int kk = ks * 16 + 8 * (lane >> 5);
-      gq_half8 af[2], bf[2];
-#pragma unroll
-      for (int i = 0; i < 2; ++i)
-        af[i] = *reinterpret_cast<const gq_half8 *>(As + (64 * wm + 32 * i + (lane & 31)) * LDS_STRIDE + kk);
-#pragma unroll
-      for (int j = 0; j < 2; ++j)
-        bf[j] = *reinterpret_cast<const gq_half8 *>(Bs + (64 * wn + 32 * j + (lane & 31)) * LDS_STRIDE + kk);
-#pragma unroll
-      for (int i = 0; i < 2; ++i)
-#pragma unroll
-        for (int j = 0; j < 2; ++j) acc[i][j] = gq_mfma32(af[i], bf[j], acc[i][j]);
-    }
+  for (int q = 0; q < KS; ++q) store_w_part(q, 0, 0, B0{});
+  __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
+  __syncthreads();
+  // nsteps is even (K is padded to whole 128-k chunks)
+  for (int step = 0; step < nsteps; step += 2) {
+    run_step(step, B0{});
+    run_step(step + 1, B1{});
   }
 
   // D layout (32x32): lane l holds column l%32, rows 8*(v/4) + 4*(l/32) + v%4.
 #pragma unroll
-  for (int i = 0; i < 2; ++i)
+  for (int i = 0; i < TM; ++i)
 #pragma unroll
-    for (int j = 0; j < 2; ++j) {
-      const int n = n0 + 64 * wn + 32 * j + (lane & 31);
+    for (int j = 0; j < TN; ++j) {
+      const int n = n0 + (BN / 4) * wn + 32 * j + (lane & 31);
       if (n >= N) continue;
 #pragma unroll
       for (int v = 0; v < 16; ++v) {
-        const int m = m0 + 64 * wm + 32 * i + 8 * (v >> 2) + 4 * (lane >> 5) + (v & 3);
+        const int m = m0 + (BM / 2) * wm + 32 * i + 8 * (v >> 2) + 4 * (lane >> 5) + (v & 3);
         if (m < M) {
           if constexpr (CBF16)
             reinterpret_cast<uint16_t *>(c)[(size_t)m * N + n] = f32_to_bf16_rne(acc[i][j][v]);
@@ -313,23 +380,81 @@ k_gemm_t16(const uint8_t *__restrict__ w, size_t sc_off, const _Float16 *__restr
     }
 }
 
-template <int FMT>
-int launch_gemm(const void *packed, const _Float16 *a16, void *c, int c_dtype, int M, int N, int K, hipStream_t s) {
-  const int C = (int)gq_chunks(FMT, K), Kp = (int)gq_kpad(FMT, K);
-  const size_t sc_off = gq_sc_plane_offset(FMT, N, K);
-  dim3 grid((unsigned)((N + BN - 1) / BN), (unsigned)((M + BM - 1) / BM));
-  if (c_dtype == GQ_DT_BF16)
-    hipLaunchKernelGGL((k_gemm_t16<FMT, 1>), grid, dim3(256), 0, s, (const uint8_t *)packed, sc_off, a16, c, M, N,
-                       C, Kp);
-  else
-    hipLaunchKernelGGL((k_gemm_t16<FMT, 0>), grid, dim3(256), 0, s, (const uint8_t *)packed, sc_off, a16, c, M, N,
-                       C, Kp);
+// Activations -> fp16 [M][ldo] (ldo >= K, columns K..ldo-1 zero), 8 per thread.
+// bf16 -> fp16 is exact inside fp16's range; fp32 rounds to nearest even.
+__global__ void __launch_bounds__(256) k_a_to_f16(const void *__restrict__ a, int a_dtype, _Float16 *__restrict__ o,
+                                                  int M, int K, int ldo) {
+  const size_t i = (size_t)blockIdx.x * 256 + threadIdx.x;
+  const int per_row = ldo / 8;
+  if (i >= (size_t)M * per_row) return;
+  const size_t m = i / per_row;
+  const int k0 = (int)(i % per_row) * 8;
+  gq_half8 h;
+  if (k0 >= K) {
+#pragma unroll
+    for (int q = 0; q < 8; ++q) h[q] = (_Float16)0.0f;
+  } else if (a_dtype == GQ_DT_BF16) {
+    const gq_u4 u = gq_ld16(reinterpret_cast<const uint16_t *>(a) + m * K + k0);
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      h[2 * q] = (_Float16)__uint_as_float(u[q] << 16);
+      h[2 * q + 1] = (_Float16)__uint_as_float(u[q] & 0xFFFF0000u);
+    }
+  } else if (a_dtype == GQ_DT_F16) {
+    h = *reinterpret_cast<const gq_half8 *>(reinterpret_cast<const _Float16 *>(a) + m * K + k0);
+  } else {
+    const float *f = reinterpret_cast<const float *>(a) + m * K + k0;
+    const gq_f4 v0 = *reinterpret_cast<const gq_f4 *>(f), v1 = *reinterpret_cast<const gq_f4 *>(f + 4);
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      h[q] = (_Float16)v0[q];
+      h[4 + q] = (_Float16)v1[q];
+    }
+  }
+  *reinterpret_cast<gq_half8 *>(o + m * ldo + k0) = h;
+}
+
+template <int FMT, int CBF16, int BM, int BN>
+int launch_cfg(const void *packed, const _Float16 *a16, int lda, void *c, int M, int N, int K, hipStream_t s) {
+  auto kern = k_gemm_t16<FMT, CBF16, BM, BN>;
+  const int C = (int)gq_chunks(FMT, K);
+  const int nsteps = (int)(gq_kpad(FMT, K) / BK);
+  const int tiles_m = (M + BM - 1) / BM, tiles_n = (N + BN - 1) / BN;
+  hipLaunchKernelGGL(kern, dim3((unsigned)(tiles_m * tiles_n)), dim3(NTHR), 0, s, (const uint8_t *)packed,
+                     (uint32_t)gq_sc_plane_offset(FMT, N, K), a16, lda, c, M, N, C, nsteps, tiles_m);
   return gq_last_launch();
+}
+
+// Tile shape: the largest tile that still gives every CU a workgroup.
+int pick_tile(int M, int N) {
+  auto wgs = [&](int bm, int bn) { return (long)((M + bm - 1) / bm) * ((N + bn - 1) / bn); };
+  if (const char *e = getenv("GQ_GEMM_TILE")) return atoi(e);
+  if (wgs(256, 256) >= 256) return 0;
+  if (wgs(256, 128) >= 256) return 1;
+  return 2;
+}
+
+template <int FMT, int CBF16>
+int launch_fmt(const void *packed, const _Float16 *a16, int lda, void *c, int M, int N, int K, hipStream_t s) {
+  switch (pick_tile(M, N)) {
+  case 0: return launch_cfg<FMT, CBF16, 256, 256>(packed, a16, lda, c, M, N, K, s);
+  case 1: return launch_cfg<FMT, CBF16, 256, 128>(packed, a16, lda, c, M, N, K, s);
+  default: return launch_cfg<FMT, CBF16, 128, 128>(packed, a16, lda, c, M, N, K, s);
+  }
+}
+
+template <int FMT>
+int launch_gemm(const void *packed, const _Float16 *a16, int lda, void *c, int c_dtype, int M, int N, int K,
+                hipStream_t s) {
+  return c_dtype == GQ_DT_BF16 ? launch_fmt<FMT, 1>(packed, a16, lda, c, M, N, K, s)
+                               : launch_fmt<FMT, 0>(packed, a16, lda, c, M, N, K, s);
 }
 
 }  // namespace
 
 extern "C" size_t gq_gemm_workspace_bytes(int fmt, size_t M, size_t K) {
+  // activations other than fp16 with K == padded K are first written as fp16
+  // [M][padded K]
   if (!gq_fmt_valid(fmt) || M > GQ_MAX_DIM || K > GQ_MAX_DIM) return 0;
   return gq_align256(M * gq_kpad(fmt, K) * 2);
 }
@@ -343,19 +468,28 @@ extern "C" int gq_gemm(int fmt, const void *packed, const void *a, int a_dtype, 
   GQ_CHECK(packed && a && c, GQ_ERR_INVALID_ARGS);
   if (M == 0 || N == 0) return GQ_OK;
   GQ_CHECK(K > 0, GQ_ERR_INVALID_ARGS);
-  size_t need = gq_gemm_workspace_bytes(fmt, M, K);
-  if (!ws) {
-    GQ_TRY(gq_default_workspace(need, &ws));
-    ws_bytes = need;
-  }
-  GQ_CHECK(ws_bytes >= need, GQ_ERR_WORKSPACE);
+  // the kernel addresses the packed tensor with 32-bit offsets
+  GQ_CHECK(gq_packed_bytes(fmt, N, K) < ((size_t)1 << 32), GQ_ERR_INVALID_ARGS);
   hipStream_t s = (hipStream_t)stream;
-  const int Kp = (int)gq_kpad(fmt, K);
-  _Float16 *a16 = (_Float16 *)ws;
-  GQ_TRY(gq_launch_prep_a(a, a_dtype, a16, (int)M, (int)K, Kp, s));
+  const size_t Kp = gq_kpad(fmt, K);
+  const _Float16 *a16 = (const _Float16 *)a;
+  if (a_dtype != GQ_DT_F16 || Kp != K) {
+    const size_t need = gq_gemm_workspace_bytes(fmt, M, K);
+    if (!ws) {
+      GQ_TRY(gq_default_workspace(need, &ws));
+      ws_bytes = need;
+    }
+    GQ_CHECK(ws_bytes >= need, GQ_ERR_WORKSPACE);
+    const size_t n8 = M * (Kp / 8);
+    hipLaunchKernelGGL(k_a_to_f16, dim3((unsigned)((n8 + 255) / 256)), dim3(256), 0, s, a, a_dtype, (_Float16 *)ws,
+                       (int)M, (int)K, (int)Kp);
+    GQ_TRY(gq_last_launch());
+    a16 = (const _Float16 *)ws;
+  }
+  const int lda = (int)Kp;
   switch (fmt) {
-  case GQ_FMT_Q4_0: return launch_gemm<GQ_FMT_Q4_0>(packed, a16, c, c_dtype, (int)M, (int)N, (int)K, s);
-  case GQ_FMT_Q8_0: return launch_gemm<GQ_FMT_Q8_0>(packed, a16, c, c_dtype, (int)M, (int)N, (int)K, s);
-  default: return launch_gemm<GQ_FMT_Q4_K>(packed, a16, c, c_dtype, (int)M, (int)N, (int)K, s);
+  case GQ_FMT_Q4_0: return launch_gemm<GQ_FMT_Q4_0>(packed, a16, lda, c, c_dtype, (int)M, (int)N, (int)K, s);
+  case GQ_FMT_Q8_0: return launch_gemm<GQ_FMT_Q8_0>(packed, a16, lda, c, c_dtype, (int)M, (int)N, (int)K, s);
+  default: return launch_gemm<GQ_FMT_Q4_K>(packed, a16, lda, c, c_dtype, (int)M, (int)N, (int)K, s);
   }
 }

@@ -197,15 +197,23 @@ k_gemv_q(const uint8_t *__restrict__ w, size_t sc_off, const float *__restrict__
     qbase[rt] = w + (t * (size_t)C + c0) * F::QB;
     sbase[rt] = w + sc_off + (t * (size_t)C + c0) * F::SB;
   }
-#pragma unroll
-  for (int i = 0; i < NCK; ++i) {
-    // surplus loads re-read the wave's last chunk (its first one when the
-    // wave has no chunk: c0 < C always holds), never outside the tensor
+  // surplus loads re-read the wave's last chunk (its first one when the wave
+  // has no chunk: c0 < C always holds), never outside the tensor
+  auto issue = [&](int i) {
     const int ii = i < nck ? i : (nck > 0 ? nck - 1 : 0);
 #pragma unroll
     for (int rt = 0; rt < R; ++rt)
       load_chunk<FMT>(qbase[rt] + (size_t)ii * F::QB, sbase[rt] + (size_t)ii * F::SB, qlane, slane, ch[rt][i]);
-  }
+  };
+  // PF chunks are requested up front; chunk i + PF is requested once chunk i
+  // has been consumed
+#ifdef GQ_GEMV_PF
+  constexpr int PF = GQ_GEMV_PF < NCK ? GQ_GEMV_PF : NCK;
+#else
+  constexpr int PF = NCK;
+#endif
+#pragma unroll
+  for (int i = 0; i < PF; ++i) issue(i);
   __builtin_amdgcn_sched_barrier(0);
 
   // ---- 3. activation limbs --------------------------------------------------
@@ -303,15 +311,25 @@ k_gemv_q(const uint8_t *__restrict__ w, size_t sc_off, const float *__restrict__
     for (int i = 0; i < NCK; ++i)
 #pragma unroll
       for (int rt = 0; rt < R; ++rt) {
-        const uint32_t *pw = reinterpret_cast<const uint32_t *>(&ch[rt][i]);
-#pragma unroll
-        for (int q = 0; q < (int)(sizeof(Chunk<FMT>) / 4); ++q) acc2 ^= pw[q];
+        if constexpr (FMT == GQ_FMT_Q4_0) {
+          acc2 ^= ch[rt][i].q[0] ^ ch[rt][i].q[1] ^ ch[rt][i].q[2] ^ ch[rt][i].q[3] ^ ch[rt][i].d;
+        } else if constexpr (FMT == GQ_FMT_Q8_0) {
+          acc2 ^= ch[rt][i].q0[0] ^ ch[rt][i].q0[1] ^ ch[rt][i].q0[2] ^ ch[rt][i].q0[3] ^ ch[rt][i].d;
+          acc2 ^= ch[rt][i].q1[0] ^ ch[rt][i].q1[1] ^ ch[rt][i].q1[2] ^ ch[rt][i].q1[3];
+        } else {
+          acc2 ^= ch[rt][i].qa[0] ^ ch[rt][i].qa[1] ^ ch[rt][i].qa[2] ^ ch[rt][i].qa[3] ^ ch[rt][i].meta[0];
+          acc2 ^= ch[rt][i].qb[0] ^ ch[rt][i].qb[1] ^ ch[rt][i].qb[2] ^ ch[rt][i].qb[3] ^ ch[rt][i].meta[1];
+          acc2 ^= ch[rt][i].meta[2] ^ ch[rt][i].meta[3];
+        }
       }
     if (acc2 == 0x9E3779B9u && r == 0) y[0] = 1.0f;
     return;
   }
 #endif
   // ---- 4. consume the chunks -------------------------------------------------
+#if defined(GQ_EXPERIMENT) && GQ_EXPERIMENT == 4
+  for (int rep = 0; rep < 2; ++rep)  // twice the consume work (timing probe)
+#endif
 #pragma unroll
   for (int i = 0; i < NCK; ++i) {
     if (i < nck)
@@ -364,6 +382,7 @@ k_gemv_q(const uint8_t *__restrict__ w, size_t sc_off, const float *__restrict__
         }
       }
     }
+    if (i + PF < NCK) issue(i + PF);
   }
 
   // ---- 5. reduce: lane groups (4 combinations), then the KSPLIT waves --------
@@ -380,7 +399,12 @@ k_gemv_q(const uint8_t *__restrict__ w, size_t sc_off, const float *__restrict__
         p += __shfl_xor(p, 32, 64);
         part[rt][mt][v] = p;
       }
-  if constexpr (KSPLIT > 1) {
+#if defined(GQ_EXPERIMENT) && GQ_EXPERIMENT == 3
+  constexpr bool kReduce = false;  // every wave stores its partial (wrong results)
+#else
+  constexpr bool kReduce = true;
+#endif
+  if constexpr (KSPLIT > 1 && kReduce) {
     __shared__ float red[KSPLIT][R * MT * NBC][16];
     if (g == 0) {
 #pragma unroll

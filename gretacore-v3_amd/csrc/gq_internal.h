@@ -47,7 +47,6 @@ static inline size_t gq_scl_bytes(int fmt, size_t K, int B) {
 // Zero-fills n floats with a kernel (no memset node, so it is safe to capture).
 int gq_fill_zero(float *p, size_t n, hipStream_t s);
 int gq_launch_prep_x(int fmt, const float *x, void *ws, int B, int K, hipStream_t s);
-int gq_launch_prep_a(const void *a, int a_dtype, _Float16 *out, int M, int K, int Kp, hipStream_t s);
 
 // load-time conversions (gq_loadconv.hip)
 int gq_launch_dequant_q6_k(const void *blocks, size_t n_blocks, float *out, hipStream_t s);

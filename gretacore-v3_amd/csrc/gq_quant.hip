@@ -252,49 +252,6 @@ k_prep_x(const float *__restrict__ x, int8_t *__restrict__ xl, float *__restrict
   *reinterpret_cast<gq_f4 *>(scl + 4 * ((size_t)b * nblk + j)) = gq_f4{sx, s, sx * (1.0f / 254.0f), 0.f};
 }
 
-// Activation conversion for the GEMM (prefill) path: bf16 / f32 / f16 [M][K]
-// -> f16 [M][Kp], zero padded.  Eight elements per thread.
-__global__ void __launch_bounds__(256)
-k_prep_a_f16(const void *__restrict__ a, int a_dtype, _Float16 *__restrict__ out, int M, int K, int Kp) {
-  size_t i = (size_t)blockIdx.x * 256 + threadIdx.x;
-  size_t per_row = (size_t)Kp / 8;
-  if (i >= (size_t)M * per_row) return;
-  size_t m = i / per_row, k0 = (i % per_row) * 8;
-  gq_half8 h;
-  if (k0 + 8 <= (size_t)K && (K % 8) == 0) {
-    if (a_dtype == GQ_DT_BF16) {
-      gq_u4 u = gq_ld16(reinterpret_cast<const uint16_t *>(a) + m * K + k0);
-#pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        h[2 * q] = (_Float16)__uint_as_float(u[q] << 16);
-        h[2 * q + 1] = (_Float16)__uint_as_float(u[q] & 0xFFFF0000u);
-      }
-    } else if (a_dtype == GQ_DT_F16) {
-      h = *reinterpret_cast<const gq_half8 *>(reinterpret_cast<const _Float16 *>(a) + m * K + k0);
-    } else {
-      const float *f = reinterpret_cast<const float *>(a) + m * K + k0;
-#pragma unroll
-      for (int q = 0; q < 8; ++q) h[q] = (_Float16)f[q];
-    }
-  } else {
-#pragma unroll
-    for (int q = 0; q < 8; ++q) {
-      size_t k = k0 + q;
-      float v = 0.0f;
-      if (k < (size_t)K) {
-        if (a_dtype == GQ_DT_BF16)
-          v = __uint_as_float((uint32_t)reinterpret_cast<const uint16_t *>(a)[m * K + k] << 16);
-        else if (a_dtype == GQ_DT_F16)
-          v = (float)reinterpret_cast<const _Float16 *>(a)[m * K + k];
-        else
-          v = reinterpret_cast<const float *>(a)[m * K + k];
-      }
-      h[q] = (_Float16)v;
-    }
-  }
-  *reinterpret_cast<gq_half8 *>(out + m * Kp + k0) = h;
-}
-
 // Per-32 int8 activation quantization (Q8_0 int8-MFMA path): the reference's
 // INT8 requant rule applied to activations (weight_loader.cpp:780-802):
 // d = amax/127, inv = d > 1e-9 ? 1/d : 0, q = round(a * inv), half away.
@@ -411,11 +368,6 @@ int gq_fill_zero(float *p, size_t n, hipStream_t s) {
   return gq_last_launch();
 }
 
-int gq_launch_prep_a(const void *a, int a_dtype, _Float16 *out, int M, int K, int Kp, hipStream_t s) {
-  size_t n = (size_t)M * (Kp / 8);
-  hipLaunchKernelGGL(k_prep_a_f16, dim3(blocks_for(n)), dim3(256), 0, s, a, a_dtype, out, M, K, Kp);
-  return gq_last_launch();
-}
 
 extern "C" int gq_quantize_act_q8(const void *a, int a_dtype, size_t M, size_t K, int8_t *q, float *d,
                                   void *stream) {
