@@ -483,8 +483,7 @@ int launch_r(const void *packed, const float *x, const void *ws, float *y, int N
 // the activation staging per weight) and KSPLIT waves, so that every wave holds
 // at most MAXC / R chunks and the grid has enough waves to keep HBM busy.
 // Every wave's chunk range [C*w/KSPLIT, C*(w+1)/KSPLIT) lies inside [0, C).
-extern "C" int gq_gemv_plan(int fmt, size_t N, size_t K, int batch, int *R_out, int *ksplit_out,
-                            int *chunks_per_wave_out) {
+static int q_plan(int fmt, size_t N, size_t K, int batch, int *R_out, int *ksplit_out, int *chunks_per_wave_out) {
   GQ_TRY(gq_check_shape(fmt, N, K));
   GQ_CHECK(batch >= 1 && batch <= GQ_MAX_BATCH, GQ_ERR_UNSUPPORTED);
   const int f = gq_fmt_is_q4k(fmt) ? GQ_FMT_Q4_K : fmt;
@@ -514,12 +513,27 @@ extern "C" int gq_gemv_plan(int fmt, size_t N, size_t K, int batch, int *R_out, 
   return GQ_OK;
 }
 
+// The plan of the kernel gq_gemv launches for (fmt, N, K, batch): the int8
+// kernel above, or from batch gq_gemv_h_min() on the fp16 batch kernel.
+extern "C" int gq_gemv_plan(int fmt, size_t N, size_t K, int batch, int *R_out, int *ksplit_out,
+                            int *chunks_per_wave_out) {
+  GQ_TRY(gq_check_shape(fmt, N, K));
+  GQ_CHECK(batch >= 1 && batch <= GQ_MAX_BATCH, GQ_ERR_UNSUPPORTED);
+  if (batch < gq_gemv_h_min()) return q_plan(fmt, N, K, batch, R_out, ksplit_out, chunks_per_wave_out);
+  int R = 1, ks = 1, cpw = 0;
+  GQ_TRY(gq_gemv_h_plan(fmt, N, K, &R, &ks, &cpw));
+  if (R_out) *R_out = R;
+  if (ksplit_out) *ksplit_out = ks;
+  if (chunks_per_wave_out) *chunks_per_wave_out = cpw;
+  return GQ_OK;
+}
+
 namespace {
 
 template <int FMT, int NBC, int MT, bool PREP>
 int launch_shape(const void *packed, const float *x, const void *ws, float *y, int N, int K, int nb, hipStream_t s) {
   int R = 1, ks = 2, cpw = 0;
-  GQ_TRY(gq_gemv_plan(FMT, N, K, nb, &R, &ks, &cpw));
+  GQ_TRY(q_plan(FMT, N, K, nb, &R, &ks, &cpw));
   if (cpw > Fmt<FMT>::MAXC / R) return GQ_ERR_INVALID_ARGS;  // the kernel's register budget
   if (R == 2) return launch_r<FMT, NBC, MT, 2, PREP>(packed, x, ws, y, N, K, nb, ks, s);
   return launch_r<FMT, NBC, MT, 1, PREP>(packed, x, ws, y, N, K, nb, ks, s);
@@ -551,6 +565,14 @@ int dispatch(int fmt, const void *packed, const float *x, const void *ws, float 
 
 // batch sizes whose activations are staged in-kernel (no workspace)
 static inline bool gq_gemv_fused(int batch) { return batch <= 4; }
+
+// smallest batch that gq_gemv runs on the fp16 batch kernel (GQ_GEMV_H_MIN
+// overrides it, for tuning)
+int gq_gemv_h_min(void) {
+  const char *e = getenv("GQ_GEMV_H_MIN");
+  const int v = e ? atoi(e) : 0;
+  return (v >= 1 && v <= GQ_MAX_BATCH + 1) ? v : 5;
+}
 
 extern "C" size_t gq_gemv_workspace_bytes(int fmt, size_t K, int batch) {
   if (!gq_fmt_valid(fmt) || batch < 1 || batch > GQ_MAX_BATCH || K > GQ_MAX_DIM) return 0;
@@ -585,6 +607,8 @@ extern "C" int gq_gemv(int fmt, const void *packed, const float *x, float *y, si
   GQ_CHECK(packed && x && y, GQ_ERR_INVALID_ARGS);
   if (N == 0) return GQ_OK;
   if (K == 0) return gq_fill_zero(y, N * batch, (hipStream_t)stream);
+  if (batch >= gq_gemv_h_min())
+    return gq_launch_gemv_h(fmt, packed, x, y, (int)N, (int)K, batch, (hipStream_t)stream);
   if (gq_gemv_fused(batch))
     return dispatch(gq_fmt_is_q4k(fmt) ? GQ_FMT_Q4_K : fmt, packed, x, nullptr, y, (int)N, (int)K, batch,
                     (hipStream_t)stream);

@@ -48,6 +48,11 @@ static inline size_t gq_scl_bytes(int fmt, size_t K, int B) {
 int gq_fill_zero(float *p, size_t n, hipStream_t s);
 int gq_launch_prep_x(int fmt, const float *x, void *ws, int B, int K, hipStream_t s);
 
+// fp16 batch GEMV (gq_gemv_h.hip)
+int gq_gemv_h_min(void);
+int gq_gemv_h_plan(int fmt, size_t N, size_t K, int *R_out, int *ks_out, int *cpw_out);
+int gq_launch_gemv_h(int fmt, const void *packed, const float *x, float *y, int N, int K, int nb, hipStream_t s);
+
 // load-time conversions (gq_loadconv.hip)
 int gq_launch_dequant_q6_k(const void *blocks, size_t n_blocks, float *out, hipStream_t s);
 int gq_launch_f16_to_f32(const void *in, size_t n, float *out, hipStream_t s);

@@ -1,7 +1,12 @@
-"""CPU checks of the GEMV launch plan: for every shape the kernel is launched
-with, each wave's chunk range and every weight load it issues (including the
-surplus loads that re-read a chunk to keep the load count static) stay inside
-the repacked tensor, and no wave holds more chunks than its registers."""
+"""CPU checks of the GEMV launch plans: for every shape the kernels are
+launched with, each wave's chunk range and every weight and activation load it
+issues (including the surplus loads that re-read a chunk to keep the load count
+static) stay inside the tensors, and no wave holds more chunks than its
+registers.  Covers the int8 kernel (batch 1..4, and every batch through the
+split gq_gemv_prep / gq_gemv_prepped form) and the fp16 batch kernel
+(batch >= 5)."""
+import os
+
 import pytest
 
 import gq
@@ -14,8 +19,47 @@ SHAPES = [(1, 32), (100, 288), (17, 96), (33, 160), (1, 256), (100, 256), (1, 76
           (4096, 4096), (14336, 4096), (4096, 14336), (1024, 4096), (128256, 4096), (7, 256), (40, 512)]
 
 
+NCK_H = {gq.FMT_Q4_0: 4, gq.FMT_Q8_0: 4, gq.FMT_Q4_K: 2, gq.FMT_Q4_K_GGML: 2}
+SB = {gq.FMT_Q4_0: 128, gq.FMT_Q8_0: 128, gq.FMT_Q4_K: 256, gq.FMT_Q4_K_GGML: 256}
+RMAX_H = {gq.FMT_Q4_0: 2, gq.FMT_Q8_0: 2, gq.FMT_Q4_K: 2, gq.FMT_Q4_K_GGML: 2}
+
+
+def emulate_h(fmt, n, k, batch):
+    """Replays k_gemv_h's chunk-group and address arithmetic on the host."""
+    R, ks, cpw = gq.gemv_plan(fmt, n, k, batch)
+    assert R in (1, 2) and R <= RMAX_H[fmt] and ks in (1, 2, 4, 8)
+    C = -(-k // CK[fmt])
+    tiles = -(-n // 16)
+    assert cpw == -(-C // ks)
+    steps = CK[fmt] // 64
+    wgs = -(-tiles // R)
+    nck_g = NCK_H[fmt]
+    for wave in range(ks):
+        c0, c1 = C * wave // ks, C * (wave + 1) // ks
+        nck = c1 - c0
+        assert 0 <= c0 < C and c1 <= C
+        gb = 0
+        while gb == 0 or gb < nck:
+            ng = min(nck_g, nck - gb)
+            for i in range(nck_g):
+                ci = c0 + gb + (i if i < ng else (ng - 1 if ng > 0 else 0))
+                assert 0 <= ci < C
+                for blk in (0, wgs - 1):
+                    for rt in range(R):
+                        t = min(blk * R + rt, tiles - 1)
+                        chunk = t * C + ci
+                        assert chunk * QB[fmt] + QB[fmt] <= tiles * C * QB[fmt]
+                        assert chunk * SB[fmt] + SB[fmt] <= tiles * C * SB[fmt]
+                for m in range(steps):
+                    for g in range(4):
+                        kk = ci * CK[fmt] + 64 * m + 32 * (g >> 1) + 16 * (g & 1)
+                        if kk < k:
+                            assert kk + 16 <= k  # a 16-element run is read only when wholly inside
+            gb += nck_g
+
+
 def emulate(fmt, n, k, batch):
-    """Replays the kernel's chunk/address arithmetic on the host."""
+    """Replays the int8 kernel's chunk/address arithmetic on the host."""
     R, ks, cpw = gq.gemv_plan(fmt, n, k, batch)
     C = -(-k // CK[fmt])
     tiles = -(-n // 16)
@@ -37,9 +81,19 @@ def emulate(fmt, n, k, batch):
                     assert chunk * QB[fmt] + QB[fmt] <= qs_plane
 
 
+SHAPES_H = SHAPES + [(14336, 14336), (4096, 28672), (16, 65536)]
+
+
 @pytest.mark.parametrize("fmt", [gq.FMT_Q4_0, gq.FMT_Q8_0, gq.FMT_Q4_K])
 @pytest.mark.parametrize("batch", [1, 2, 3, 4, 5, 8, 9, 16])
-def test_gemv_plan_in_bounds(fmt, batch):
+def test_gemv_plan_in_bounds(fmt, batch, monkeypatch):
+    for n, k in SHAPES_H:
+        if k % (256 if fmt == gq.FMT_Q4_K else 32):
+            continue
+        if batch >= 5:
+            emulate_h(fmt, n, k, batch)
+    # the int8 kernel at every batch (the split prep / prepped form uses it)
+    monkeypatch.setenv("GQ_GEMV_H_MIN", "17")
     for n, k in SHAPES:
         if k % (256 if fmt == gq.FMT_Q4_K else 32):
             continue
