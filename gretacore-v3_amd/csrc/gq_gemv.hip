@@ -149,11 +149,44 @@ GQ_DEV float split8(const float (&v)[8], float inv, uint32_t (&la)[2], uint32_t 
   return sum;
 }
 
-template <int FMT, int NBC, int MT, int R, int KSPLIT, bool PREP>
+// One weight matrix of a launch: T16 data, its scale-plane offset, output
+// y [batch][N], and the end (exclusive) of its workgroup range.
+struct GemvSeg {
+  const uint8_t *w;
+  size_t sc_off;
+  float *y;
+  int N;
+  int wg_end;
+};
+// FUSE = 0: one matrix.  1: up to 4 matrices sharing x (e.g. q, k, v), each
+// with its own workgroup range.  2: gate and up matrices of one FFN: the
+// workgroup's row tile 0 is read from seg[0], tile 1 from seg[1] (same rows),
+// and y = silu(gate) * up goes to seg[0].y.  With FUSE > 0 and gamma set, x is
+// first RMS-normalised per batch row: x * (1 / sqrt(mean(x^2) + eps)) * gamma.
+struct GemvFuse {
+  GemvSeg seg[4];
+  int nseg;
+  const float *gamma;
+  float eps;
+};
+
+template <int FMT, int NBC, int MT, int R, int KSPLIT, bool PREP, int FUSE>
 __global__ void __launch_bounds__(64 * KSPLIT)
-k_gemv_q(const uint8_t *__restrict__ w, size_t sc_off, const float *__restrict__ x,
-         const int8_t *__restrict__ xl_g, const float *__restrict__ scl_g, float *__restrict__ y, int N, int K,
-         int C, int Kp, int nb) {
+k_gemv_q(const GemvFuse fz, const float *__restrict__ x, const int8_t *__restrict__ xl_g,
+         const float *__restrict__ scl_g, int K, int C, int Kp, int nb) {
+  static_assert(FUSE != 2 || R == 2, "gate/up pairs need two row tiles");
+  // this workgroup's matrix (wave-uniform selects; no dynamic indexing)
+  int si = 0;
+  if constexpr (FUSE == 1) {
+#pragma unroll
+    for (int q = 0; q < 3; ++q) si += (q + 1 < fz.nseg && (int)blockIdx.x >= fz.seg[q].wg_end) ? 1 : 0;
+  }
+  const GemvSeg s0 = fz.seg[0], s1 = fz.seg[1], s2 = fz.seg[2], s3 = fz.seg[3];
+  const uint8_t *const w = si == 0 ? s0.w : si == 1 ? s1.w : si == 2 ? s2.w : s3.w;
+  const size_t sc_off = si == 0 ? s0.sc_off : si == 1 ? s1.sc_off : si == 2 ? s2.sc_off : s3.sc_off;
+  float *const y = si == 0 ? s0.y : si == 1 ? s1.y : si == 2 ? s2.y : s3.y;
+  const int N = si == 0 ? s0.N : si == 1 ? s1.N : si == 2 ? s2.N : s3.N;
+  const int wg0 = si == 0 ? 0 : si == 1 ? s0.wg_end : si == 2 ? s1.wg_end : s2.wg_end;
   using F = Fmt<FMT>;
   constexpr int NCK = F::MAXC / R;           // chunks per wave (upper bound)
   constexpr int LKMAX = F::CK * NCK;         // slice elements per wave
@@ -163,11 +196,12 @@ k_gemv_q(const uint8_t *__restrict__ w, size_t sc_off, const float *__restrict__
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform (SGPR)
   const int g = lane >> 4, r = lane & 15;
-  const size_t tile0 = (size_t)blockIdx.x * R;
+  const size_t tile0 = FUSE == 2 ? (size_t)blockIdx.x : (size_t)((int)blockIdx.x - wg0) * R;
   const int ntiles = (int)gq_tiles(N);
   const int c0 = (C * wave) / KSPLIT, c1 = (C * (wave + 1)) / KSPLIT;
   const int nck = c1 - c0;  // <= NCK (host-checked)
   const int k0 = c0 * F::CK, LK = nck * F::CK;
+  const bool norm = FUSE > 0 && fz.gamma != nullptr;
 
   // ---- 1. activation loads (fused path), issued before the weights ----------
   float4 xv[PREP ? 1 : NBC * TPR][2];
@@ -182,6 +216,19 @@ k_gemv_q(const uint8_t *__restrict__ w, size_t sc_off, const float *__restrict__
       xv[i][1] = p[1];
     }
   }
+  float4 gv[FUSE > 0 && !PREP ? TPR : 1][2];
+  if constexpr (FUSE > 0 && !PREP) {
+    if (norm) {
+#pragma unroll
+      for (int i = 0; i < TPR; ++i) {
+        const int e8 = lane + 64 * i, k = k0 + 8 * e8;
+        const bool in = 8 * e8 < LK && k < K;
+        const float4 *p = reinterpret_cast<const float4 *>(fz.gamma + (in ? k : 0));
+        gv[i][0] = p[0];
+        gv[i][1] = p[1];
+      }
+    }
+  }
   __builtin_amdgcn_sched_barrier(0);
 
   // ---- 2. weight loads for every chunk of this wave (clamped, unconditional) -
@@ -193,9 +240,17 @@ k_gemv_q(const uint8_t *__restrict__ w, size_t sc_off, const float *__restrict__
   const uint8_t *qbase[R], *sbase[R];
 #pragma unroll
   for (int rt = 0; rt < R; ++rt) {
-    const size_t t = (tile0 + rt < (size_t)ntiles) ? tile0 + rt : (size_t)ntiles - 1;
-    qbase[rt] = w + (t * (size_t)C + c0) * F::QB;
-    sbase[rt] = w + sc_off + (t * (size_t)C + c0) * F::SB;
+    if constexpr (FUSE == 2) {
+      const size_t t = tile0 < (size_t)ntiles ? tile0 : (size_t)ntiles - 1;
+      const uint8_t *wr = rt == 0 ? s0.w : s1.w;
+      const size_t so = rt == 0 ? s0.sc_off : s1.sc_off;
+      qbase[rt] = wr + (t * (size_t)C + c0) * F::QB;
+      sbase[rt] = wr + so + (t * (size_t)C + c0) * F::SB;
+    } else {
+      const size_t t = (tile0 + rt < (size_t)ntiles) ? tile0 + rt : (size_t)ntiles - 1;
+      qbase[rt] = w + (t * (size_t)C + c0) * F::QB;
+      sbase[rt] = w + sc_off + (t * (size_t)C + c0) * F::SB;
+    }
   }
   // surplus loads re-read the wave's last chunk (its first one when the wave
   // has no chunk: c0 < C always holds), never outside the tensor
@@ -234,10 +289,53 @@ k_gemv_q(const uint8_t *__restrict__ w, size_t sc_off, const float *__restrict__
     const int nblk = L.lk / 32;
     for (int o = 16 * lane; o < L.lk; o += 1024)
       *reinterpret_cast<gq_u4 *>(base + L.zero_off + o) = gq_u4{0u, 0u, 0u, 0u};
+    // RMS normalisation (fused entry points): sum of squares of the row over
+    // all waves' slices, then x * inv_rms * gamma
+    float inv_rms[NBC];
+#pragma unroll
+    for (int b = 0; b < NBC; ++b) inv_rms[b] = 1.f;
+    if constexpr (FUSE > 0) {
+      if (norm) {
+        __shared__ float ssred[KSPLIT][NBC];
+        float ss[NBC];
+#pragma unroll
+        for (int b = 0; b < NBC; ++b) ss[b] = 0.f;
+#pragma unroll
+        for (int i = 0; i < NBC * TPR; ++i) {
+          const float vv[8] = {xv[i][0].x, xv[i][0].y, xv[i][0].z, xv[i][0].w,
+                               xv[i][1].x, xv[i][1].y, xv[i][1].z, xv[i][1].w};
+#pragma unroll
+          for (int e = 0; e < 8; ++e) ss[i / TPR] += xin[i] ? vv[e] * vv[e] : 0.f;
+        }
+#pragma unroll
+        for (int b = 0; b < NBC; ++b) {
+#pragma unroll
+          for (int o = 1; o < 64; o <<= 1) ss[b] += __shfl_xor(ss[b], o, 64);
+          if (lane == 0) ssred[wave][b] = ss[b];
+        }
+        __syncthreads();
+#pragma unroll
+        for (int b = 0; b < NBC; ++b) {
+          float t = 0.f;
+#pragma unroll
+          for (int q = 0; q < KSPLIT; ++q) t += ssred[q][b];
+          inv_rms[b] = 1.0f / sqrtf(t / (float)K + fz.eps);
+        }
+      }
+    }
 #pragma unroll
     for (int i = 0; i < (kStage ? NBC * TPR : 0); ++i) {
       const int b = i / TPR, e8 = lane + 64 * (i % TPR);
       float v[8] = {xv[i][0].x, xv[i][0].y, xv[i][0].z, xv[i][0].w, xv[i][1].x, xv[i][1].y, xv[i][1].z, xv[i][1].w};
+      if constexpr (FUSE > 0) {
+        if (norm) {
+          const int ti = i % TPR;
+          const float gg[8] = {gv[ti][0].x, gv[ti][0].y, gv[ti][0].z, gv[ti][0].w,
+                               gv[ti][1].x, gv[ti][1].y, gv[ti][1].z, gv[ti][1].w};
+#pragma unroll
+          for (int e = 0; e < 8; ++e) v[e] = (v[e] * inv_rms[b]) * gg[e];
+        }
+      }
       float amax = 0.f;
 #pragma unroll
       for (int e = 0; e < 8; ++e) {
@@ -430,6 +528,19 @@ k_gemv_q(const uint8_t *__restrict__ w, size_t sc_off, const float *__restrict__
   } else if (g != 0) {
     return;
   }
+  if constexpr (FUSE == 2) {
+    const size_t row = tile0 * 16 + r;
+    if (row < (size_t)N) {
+#pragma unroll
+      for (int v = 0; v < NBC; ++v) {
+        if (v < nb) {
+          const float gt = part[0][0][v], up = part[1][0][v];
+          y[(size_t)v * N + row] = gt / (1.0f + expf(-gt)) * up;  // silu(gate) * up
+        }
+      }
+    }
+    return;
+  }
 #pragma unroll
   for (int rt = 0; rt < R; ++rt) {
     const size_t row = (tile0 + rt) * 16 + r;
@@ -463,10 +574,12 @@ int launch_r(const void *packed, const float *x, const void *ws, float *y, int N
   const int8_t *xl = PREP ? (const int8_t *)ws : nullptr;
   const float *scl = PREP ? (const float *)((const uint8_t *)ws + gq_xl_bytes(FMT, K, nb)) : nullptr;
   const size_t lds = PREP ? 0 : (size_t)ks * xl_layout(F::CK * ((C + ks - 1) / ks), NBC).wave_bytes;
-  const uint8_t *w = (const uint8_t *)packed;
-#define GQ_LAUNCH_KS(KS)                                                                                          \
-  hipLaunchKernelGGL((k_gemv_q<FMT, NBC, MT, R, KS, PREP>), dim3((unsigned)wgs), dim3(64 * KS), lds, s, w, sc_off, \
-                     x, xl, scl, y, N, K, C, Kp, nb)
+  GemvFuse fz{};
+  fz.seg[0] = GemvSeg{(const uint8_t *)packed, sc_off, y, N, (int)wgs};
+  fz.nseg = 1;
+#define GQ_LAUNCH_KS(KS)                                                                                         \
+  hipLaunchKernelGGL((k_gemv_q<FMT, NBC, MT, R, KS, PREP, 0>), dim3((unsigned)wgs), dim3(64 * KS), lds, s, fz, x, \
+                     xl, scl, K, C, Kp, nb)
   switch (ks) {
   case 2: GQ_LAUNCH_KS(2); break;
   case 4: GQ_LAUNCH_KS(4); break;
@@ -619,4 +732,127 @@ extern "C" int gq_gemv(int fmt, const void *packed, const float *x, float *y, si
   }
   GQ_TRY(gq_gemv_prep(fmt, x, K, batch, ws, ws_bytes, stream));
   return gq_gemv_prepped(fmt, packed, ws, y, N, K, batch, stream);
+}
+
+// ---- fused entry points: several matrices sharing x, gate/up with SwiGLU ----
+namespace {
+
+// waves per workgroup for a forced R (the q_plan rules for a given R)
+int ks_for(int fmt, size_t wgs, int C, int R) {
+  const int f = gq_fmt_is_q4k(fmt) ? GQ_FMT_Q4_K : fmt;
+  const int maxc = f == GQ_FMT_Q4_K ? Fmt<GQ_FMT_Q4_K>::MAXC : Fmt<GQ_FMT_Q4_0>::MAXC;
+  int ks = 2;
+  while (ks < 16 && (C + ks - 1) / ks > maxc / R) ks *= 2;
+  if ((C + ks - 1) / ks > maxc / R) return 0;  // K too long for one wave's registers
+  while (ks < 8 && wgs * ks < 1024 && 2 * ks <= C) ks *= 2;
+  return ks;
+}
+
+template <int FMT, int NBC, int R, int FUSE>
+int launch_fused_nbc(const GemvFuse &fz, size_t wgs, int ks, const float *x, int K, int nb, hipStream_t s) {
+  using F = Fmt<FMT>;
+  const int C = (int)gq_chunks(FMT, K);
+  const int Kp = (int)gq_kpad(FMT, K);
+  const size_t lds = (size_t)ks * xl_layout(F::CK * ((C + ks - 1) / ks), NBC).wave_bytes;
+#define GQ_LAUNCH_F(KS)                                                                                        \
+  hipLaunchKernelGGL((k_gemv_q<FMT, NBC, 1, R, KS, false, FUSE>), dim3((unsigned)wgs), dim3(64 * KS), lds, s, fz, \
+                     x, nullptr, nullptr, K, C, Kp, nb)
+  switch (ks) {
+  case 2: GQ_LAUNCH_F(2); break;
+  case 4: GQ_LAUNCH_F(4); break;
+  case 8: GQ_LAUNCH_F(8); break;
+  default: GQ_LAUNCH_F(16); break;
+  }
+#undef GQ_LAUNCH_F
+  return gq_last_launch();
+}
+
+template <int FMT, int R, int FUSE>
+int launch_fused(const GemvFuse &fz, size_t wgs, int ks, const float *x, int K, int nb, hipStream_t s) {
+  if (nb == 1) return launch_fused_nbc<FMT, 1, R, FUSE>(fz, wgs, ks, x, K, nb, s);
+  if (nb == 2) return launch_fused_nbc<FMT, 2, R, FUSE>(fz, wgs, ks, x, K, nb, s);
+  return launch_fused_nbc<FMT, 4, R, FUSE>(fz, wgs, ks, x, K, nb, s);
+}
+
+template <int R, int FUSE>
+int launch_fused_fmt(int fmt, const GemvFuse &fz, size_t wgs, int ks, const float *x, int K, int nb,
+                     hipStream_t s) {
+  switch (gq_fmt_is_q4k(fmt) ? GQ_FMT_Q4_K : fmt) {
+  case GQ_FMT_Q4_0: return launch_fused<GQ_FMT_Q4_0, R, FUSE>(fz, wgs, ks, x, K, nb, s);
+  case GQ_FMT_Q8_0: return launch_fused<GQ_FMT_Q8_0, R, FUSE>(fz, wgs, ks, x, K, nb, s);
+  default: return launch_fused<GQ_FMT_Q4_K, R, FUSE>(fz, wgs, ks, x, K, nb, s);
+  }
+}
+
+}  // namespace
+
+extern "C" int gq_gemv_multi_plan(int fmt, int n_mats, const size_t *N, size_t K, int batch, int *R_out,
+                                  int *ksplit_out, int *chunks_per_wave_out) {
+  GQ_CHECK(n_mats >= 1 && n_mats <= 4 && N, GQ_ERR_INVALID_ARGS);
+  GQ_CHECK(batch >= 1 && batch <= 4, GQ_ERR_UNSUPPORTED);
+  size_t tiles = 0;
+  for (int i = 0; i < n_mats; ++i) {
+    GQ_TRY(gq_check_shape(fmt, N[i], K));
+    tiles += gq_tiles(N[i]);
+  }
+  int R = 1, ks = 2, cpw = 0;
+  GQ_TRY(q_plan(fmt, tiles * 16, K, batch, &R, &ks, &cpw));
+  if (R_out) *R_out = R;
+  if (ksplit_out) *ksplit_out = ks;
+  if (chunks_per_wave_out) *chunks_per_wave_out = cpw;
+  return GQ_OK;
+}
+
+extern "C" int gq_gemv_multi(int fmt, int n_mats, const void *const *packed, const size_t *N, size_t K,
+                             const float *x, float *const *y, int batch, const float *gamma, float eps,
+                             void *stream) {
+  GQ_CHECK(packed && y && x && N, GQ_ERR_INVALID_ARGS);
+  int R = 1, ks = 2, cpw = 0;
+  GQ_TRY(gq_gemv_multi_plan(fmt, n_mats, N, K, batch, &R, &ks, &cpw));
+  GemvFuse fz{};
+  size_t wgs = 0;
+  for (int i = 0; i < n_mats; ++i) {
+    GQ_CHECK(packed[i] && y[i], GQ_ERR_INVALID_ARGS);
+    wgs += (gq_tiles(N[i]) + R - 1) / R;
+    fz.seg[i] = GemvSeg{(const uint8_t *)packed[i], gq_sc_plane_offset(fmt, N[i], K), y[i], (int)N[i], (int)wgs};
+  }
+  for (int i = n_mats; i < 4; ++i) fz.seg[i] = fz.seg[n_mats - 1];
+  fz.nseg = n_mats;
+  fz.gamma = gamma;
+  fz.eps = eps;
+  if (K == 0 || wgs == 0) return GQ_ERR_INVALID_ARGS;
+  hipStream_t s = (hipStream_t)stream;
+  return R == 2 ? launch_fused_fmt<2, 1>(fmt, fz, wgs, ks, x, (int)K, batch, s)
+                : launch_fused_fmt<1, 1>(fmt, fz, wgs, ks, x, (int)K, batch, s);
+}
+
+extern "C" int gq_gemv_swiglu_plan(int fmt, size_t N, size_t K, int batch, int *ksplit_out,
+                                   int *chunks_per_wave_out) {
+  GQ_TRY(gq_check_shape(fmt, N, K));
+  GQ_CHECK(batch >= 1 && batch <= 4, GQ_ERR_UNSUPPORTED);
+  const int C = (int)gq_chunks(fmt, K);
+  const int ks = ks_for(fmt, gq_tiles(N), C, 2);
+  GQ_CHECK(ks > 0, GQ_ERR_UNSUPPORTED);
+  if (ksplit_out) *ksplit_out = ks;
+  if (chunks_per_wave_out) *chunks_per_wave_out = (C + ks - 1) / ks;
+  return GQ_OK;
+}
+
+extern "C" int gq_gemv_swiglu(int fmt, const void *gate, const void *up, size_t N, size_t K, const float *x,
+                              float *y, int batch, const float *gamma, float eps, void *stream) {
+  GQ_CHECK(gate && up && x && y, GQ_ERR_INVALID_ARGS);
+  int ks = 2, cpw = 0;
+  GQ_TRY(gq_gemv_swiglu_plan(fmt, N, K, batch, &ks, &cpw));
+  if (N == 0) return GQ_OK;
+  GQ_CHECK(K > 0, GQ_ERR_INVALID_ARGS);
+  GemvFuse fz{};
+  const size_t sc = gq_sc_plane_offset(fmt, N, K);
+  const size_t wgs = gq_tiles(N);
+  fz.seg[0] = GemvSeg{(const uint8_t *)gate, sc, y, (int)N, (int)wgs};
+  fz.seg[1] = GemvSeg{(const uint8_t *)up, sc, y, (int)N, (int)wgs};
+  fz.seg[2] = fz.seg[3] = fz.seg[1];
+  fz.nseg = 2;
+  fz.gamma = gamma;
+  fz.eps = eps;
+  return launch_fused_fmt<2, 2>(fmt, fz, wgs, ks, x, (int)K, batch, (hipStream_t)stream);
 }

@@ -51,6 +51,15 @@ _SIGS = {
     "gq_quantize_act_q8": (ctypes.c_int, [_vp, ctypes.c_int, _c_size, _c_size, _vp, _vp, _vp]),
     "gq_gemm_q8_i8": (ctypes.c_int, [_vp, _vp, _vp, _vp, _c_size, _c_size, _c_size, _vp]),
     "gq_matmul": (ctypes.c_int, [ctypes.c_int, _vp, _vp, _vp, _c_size, _c_size, _c_size, _vp]),
+    "gq_gemv_multi": (ctypes.c_int, [ctypes.c_int, ctypes.c_int, _vp, _vp, _c_size, _vp, _vp, ctypes.c_int, _vp,
+                                     ctypes.c_float, _vp]),
+    "gq_gemv_multi_plan": (ctypes.c_int, [ctypes.c_int, ctypes.c_int, _vp, _c_size, ctypes.c_int,
+                                          ctypes.POINTER(ctypes.c_int), ctypes.POINTER(ctypes.c_int),
+                                          ctypes.POINTER(ctypes.c_int)]),
+    "gq_gemv_swiglu": (ctypes.c_int, [ctypes.c_int, _vp, _vp, _c_size, _c_size, _vp, _vp, ctypes.c_int, _vp,
+                                      ctypes.c_float, _vp]),
+    "gq_gemv_swiglu_plan": (ctypes.c_int, [ctypes.c_int, _c_size, _c_size, ctypes.c_int,
+                                           ctypes.POINTER(ctypes.c_int), ctypes.POINTER(ctypes.c_int)]),
     "gq_convert_f32_to_f16": (ctypes.c_int, [_vp, _c_size, _vp, _vp]),
     "gq_transpose_kv": (ctypes.c_int, [ctypes.c_int, _vp, _c_size, _c_size, _vp, _vp]),
     "gq_requant_int8": (ctypes.c_int, [_vp, _c_size, _vp, _vp, _vp]),
@@ -323,6 +332,47 @@ def gemv_prepped(fmt: int, d_packed, workspace: Workspace, y, n: int, k: int, ba
     check(load().gq_gemv_prepped(fmt, _ptr(d_packed), _ptr(workspace.buf), _ptr(y), n, k, batch, _stream(stream)),
           "gq_gemv_prepped")
     return y
+
+
+# ---- fused decode GEMVs ----------------------------------------------------------
+def gemv_multi(fmt: int, mats, x, k: int, gamma=None, eps: float = 1e-5, ys=None, stream=None):
+    """mats: list of (d_packed, n).  Returns [y_i [batch][n_i]] (one launch)."""
+    import torch
+    _require_device(x)
+    batch = 1 if x.dim() == 1 else x.shape[0]
+    if ys is None:
+        ys = [torch.empty((batch, n), dtype=torch.float32, device=x.device) for _, n in mats]
+    P = (_vp * len(mats))(*[t.data_ptr() for t, _ in mats])
+    Y = (_vp * len(mats))(*[t.data_ptr() for t in ys])
+    N = (_c_size * len(mats))(*[n for _, n in mats])
+    check(load().gq_gemv_multi(fmt, len(mats), ctypes.cast(P, _vp), ctypes.cast(N, _vp), k, _ptr(x),
+                               ctypes.cast(Y, _vp), batch, _ptr(gamma), eps, _stream(stream)), "gq_gemv_multi")
+    return ys
+
+
+def gemv_multi_plan(fmt: int, ns, k: int, batch: int):
+    N = (_c_size * len(ns))(*ns)
+    r, ks, cpw = ctypes.c_int(), ctypes.c_int(), ctypes.c_int()
+    check(load().gq_gemv_multi_plan(fmt, len(ns), ctypes.cast(N, _vp), k, batch, ctypes.byref(r), ctypes.byref(ks),
+                                    ctypes.byref(cpw)), "gq_gemv_multi_plan")
+    return r.value, ks.value, cpw.value
+
+
+def gemv_swiglu(fmt: int, gate, up, x, n: int, k: int, gamma=None, eps: float = 1e-5, y=None, stream=None):
+    import torch
+    _require_device(gate, up, x)
+    batch = 1 if x.dim() == 1 else x.shape[0]
+    if y is None:
+        y = torch.empty((batch, n), dtype=torch.float32, device=x.device)
+    check(load().gq_gemv_swiglu(fmt, _ptr(gate), _ptr(up), n, k, _ptr(x), _ptr(y), batch, _ptr(gamma), eps,
+                                _stream(stream)), "gq_gemv_swiglu")
+    return y
+
+
+def gemv_swiglu_plan(fmt: int, n: int, k: int, batch: int):
+    ks, cpw = ctypes.c_int(), ctypes.c_int()
+    check(load().gq_gemv_swiglu_plan(fmt, n, k, batch, ctypes.byref(ks), ctypes.byref(cpw)), "gq_gemv_swiglu_plan")
+    return ks.value, cpw.value
 
 
 # ---- load-time conversions (bit-exact with the reference loader) ------------

@@ -124,6 +124,26 @@ int gq_gemv_prep(int fmt, const float *d_x, size_t K, int batch, void *d_workspa
 int gq_gemv_prepped(int fmt, const void *d_packed, const void *d_workspace, float *d_y, size_t N, size_t K,
                     int batch, void *stream);
 
+/* ---- fused decode GEMVs (batch 1..4) ----------------------------------------
+ * Quantized counterparts of the reference's fp16 fused kernels
+ * (src/rt/backend/hip/kernels/fused_compute_kernels.hip:22-243,
+ * launch_fused_rmsnorm_qkv_gemv_f16 / launch_fused_ffn_front_f16), in one
+ * launch each.  When gamma is not NULL, x is first RMS-normalised per batch row:
+ * xn = x * (1 / sqrt(sum(x^2) / K + eps)) * gamma (gamma has K values).
+ *
+ * gq_gemv_multi: y[i] [batch][N[i]] = W_i xn for n_mats (1..4) matrices of one
+ * format sharing K and x (e.g. q, k, v with GQA shapes). */
+int gq_gemv_multi(int fmt, int n_mats, const void *const *d_packed, const size_t *N, size_t K, const float *d_x,
+                  float *const *d_y, int batch, const float *d_gamma, float eps, void *stream);
+/* Launch plan of gq_gemv_multi (row tiles per workgroup, waves, chunks per wave). */
+int gq_gemv_multi_plan(int fmt, int n_mats, const size_t *N, size_t K, int batch, int *row_tiles_per_wg,
+                       int *ksplit, int *chunks_per_wave);
+/* gq_gemv_swiglu: y [batch][N] = silu(W_gate xn) * (W_up xn), silu(g) = g / (1 + e^-g)
+ * (the FFN front of launch_fused_ffn_front_f16). */
+int gq_gemv_swiglu(int fmt, const void *d_gate, const void *d_up, size_t N, size_t K, const float *d_x, float *d_y,
+                   int batch, const float *d_gamma, float eps, void *stream);
+int gq_gemv_swiglu_plan(int fmt, size_t N, size_t K, int batch, int *ksplit, int *chunks_per_wave);
+
 /* ---- prefill GEMM: C[m][n] = sum_k A[m][k] * W[n][k] ------------------------ */
 /* A is [M][K] of a_dtype (GQ_DT_BF16 / F16 / F32), C is [M][N] of c_dtype
  * (GQ_DT_F32 or GQ_DT_BF16).  Computes on f16 MFMA (v_mfma_f32_32x32x16_f16)

@@ -478,3 +478,16 @@ int gqo_gemm_q8_i8(const uint8_t *w, const int8_t *qa, const float *da,
   }
   return 0;
 }
+
+void gqo_rmsnorm(const float *x, const float *gamma, int rows, int K, float eps, double *out) {
+  for (int b = 0; b < rows; ++b) {
+    double ss = 0.0;
+    for (int k = 0; k < K; ++k) ss += (double)x[(size_t)b * K + k] * (double)x[(size_t)b * K + k];
+    const double inv = 1.0 / sqrt(ss / (double)K + (double)eps);
+    for (int k = 0; k < K; ++k) out[(size_t)b * K + k] = (double)x[(size_t)b * K + k] * inv * (double)gamma[k];
+  }
+}
+
+void gqo_swiglu(const double *g, const double *u, size_t n, double *out) {
+  for (size_t i = 0; i < n; ++i) out[i] = g[i] / (1.0 + exp(-g[i])) * u[i];
+}

@@ -87,6 +87,14 @@ void gqo_gemm_int4_wt(const float *x, const uint8_t *packed, const float *s,
                       const float *head_scales, float *y, int M, int N, int K,
                       int gs, int head_dim);
 
+/* RMS normalisation of fused_rmsnorm_qkv_gemv_kernel_f16
+ * (src/rt/backend/hip/kernels/fused_compute_kernels.hip:36-87), in fp64:
+ * out[b][k] = x[b][k] / sqrt(sum_k x^2 / K + eps) * gamma[k]. */
+void gqo_rmsnorm(const float *x, const float *gamma, int rows, int K, float eps, double *out);
+/* silu(g) * u of fused_ffn_front_gemv_kernel_f16 (fused_compute_kernels.hip:162-241),
+ * silu(g) = g / (1 + exp(-g)), in fp64. */
+void gqo_swiglu(const double *g, const double *u, size_t n, double *out);
+
 /* Per-32 activation quantization used by the int8-MFMA Q8_0 path:
  * d = amax/127, inv = d>1e-9 ? 1/d : 0, q = round(a*inv) (half away). */
 void gqo_quantize_act_q8(const float *a, int M, int K, int8_t *q, float *d);

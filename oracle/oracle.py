@@ -47,6 +47,8 @@ def lib():
         L = ctypes.CDLL(ORACLE_SO)
         vp, sz, i = ctypes.c_void_p, ctypes.c_size_t, ctypes.c_int
         L.gqo_fp16_to_fp32_n.argtypes = [vp, sz, vp]
+        L.gqo_rmsnorm.argtypes = [vp, vp, i, i, ctypes.c_float, vp]
+        L.gqo_swiglu.argtypes = [vp, vp, sz, vp]
         L.gqo_fp32_to_fp16_trunc_n.argtypes = [vp, sz, vp]
         L.gqo_fp16_to_fp32.restype = ctypes.c_float
         L.gqo_fp16_to_fp32.argtypes = [ctypes.c_uint16]
@@ -109,6 +111,24 @@ def fp16_to_fp32(h) -> np.ndarray:
     h = np.ascontiguousarray(h, dtype=np.uint16).ravel()
     out = np.empty(h.size, dtype=np.float32)
     lib().gqo_fp16_to_fp32_n(_p(h), h.size, _p(out))
+    return out
+
+
+def rmsnorm(x, gamma, eps):
+    """fp64 RMS normalisation of each row of x (rows x K) times gamma."""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    x2 = x.reshape(-1, x.shape[-1])
+    gamma = np.ascontiguousarray(gamma, dtype=np.float32)
+    out = np.empty(x2.shape, dtype=np.float64)
+    lib().gqo_rmsnorm(_p(x2), _p(gamma), x2.shape[0], x2.shape[1], float(eps), _p(out))
+    return out.reshape(x.shape)
+
+
+def swiglu(g, u):
+    g = np.ascontiguousarray(g, dtype=np.float64)
+    u = np.ascontiguousarray(u, dtype=np.float64)
+    out = np.empty(g.shape, dtype=np.float64)
+    lib().gqo_swiglu(_p(g), _p(u), g.size, _p(out))
     return out
 
 

@@ -106,3 +106,41 @@ def test_plan_single_chunk_has_idle_wave():
     R, ks, cpw = gq.gemv_plan(gq.FMT_Q4_0, 1, 32, 1)
     assert ks >= 2 and cpw == 1
     emulate(gq.FMT_Q4_0, 1, 32, 1)
+
+
+def _emulate_int8_segment(fmt, n, k, R, ks):
+    C = -(-k // CK[fmt])
+    tiles = -(-n // 16)
+    nck_max = MAXC[fmt] // R
+    assert -(-C // ks) <= nck_max
+    wgs = -(-tiles // R)
+    for wave in range(ks):
+        c0, c1 = C * wave // ks, C * (wave + 1) // ks
+        nck = c1 - c0
+        assert 0 <= c0 < C and c1 <= C
+        for blk in (0, wgs - 1):
+            for rt in range(R):
+                t = min(blk * R + rt, tiles - 1)
+                for i in range(nck_max):
+                    ii = i if i < nck else (nck - 1 if nck > 0 else 0)
+                    chunk = t * C + c0 + ii
+                    assert 0 <= chunk < tiles * C
+
+
+@pytest.mark.parametrize("fmt", [gq.FMT_Q4_0, gq.FMT_Q8_0, gq.FMT_Q4_K])
+@pytest.mark.parametrize("batch", [1, 2, 4])
+def test_fused_plans_in_bounds(fmt, batch):
+    for ns, k in [((4096, 1024, 1024), 4096), ((14336,), 4096), ((64, 48, 16, 512), 1024), ((16,), 256),
+                  ((4096, 4096, 4096), 4096), ((1024,), 14336)]:
+        if k % (256 if fmt == gq.FMT_Q4_K else 32):
+            continue
+        R, ks, cpw = gq.gemv_multi_plan(fmt, list(ns), k, batch)
+        assert ks in (2, 4, 8, 16) and R in (1, 2)
+        for n in ns:
+            _emulate_int8_segment(fmt, n, k, R, ks)
+    for n, k in [(14336, 4096), (16, 256), (100, 512), (11008, 4096)]:
+        if k % (256 if fmt == gq.FMT_Q4_K else 32):
+            continue
+        ks, cpw = gq.gemv_swiglu_plan(fmt, n, k, batch)
+        assert ks in (2, 4, 8, 16)
+        _emulate_int8_segment(fmt, n, k, 2, ks)  # tile rt of workgroup i is tile i of gate / up

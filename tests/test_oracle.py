@@ -312,3 +312,35 @@ def test_fp16_array_form_matches_scalar():
     L = O.lib()
     for v in range(0, 1 << 16, 97):
         assert a[v].tobytes() == np.float32(L.gqo_fp16_to_fp32(v)).tobytes()
+
+
+def test_rmsnorm_closed_forms():
+    K = 64
+    gamma = np.linspace(0.5, 2.0, K).astype(np.float32)
+    # constant row c: mean square c^2, normalised value c / sqrt(c^2 + eps)
+    for c in (1.0, -3.0, 1e-3):
+        x = np.full((1, K), c, dtype=np.float32)
+        out = O.rmsnorm(x, gamma, 1e-5)
+        ref = np.float64(np.float32(c)) / np.sqrt(np.float64(np.float32(c)) ** 2 + np.float64(np.float32(1e-5)))
+        assert np.allclose(out[0], ref * gamma.astype(np.float64), rtol=1e-12, atol=0)
+    # one-hot row: mean square 1/K
+    x = np.zeros((2, K), dtype=np.float32)
+    x[0, 5] = 2.0
+    x[1, 0] = -1.0
+    out = O.rmsnorm(x, np.ones(K, np.float32), 0.0)
+    assert np.isclose(out[0, 5], np.sqrt(K)) and np.isclose(out[1, 0], -np.sqrt(K))
+    assert np.count_nonzero(out) == 2
+    # scale invariance: rmsnorm(a x) == rmsnorm(x) for eps = 0
+    rng = np.random.default_rng(3)
+    x = rng.standard_normal((3, K)).astype(np.float32)
+    assert np.allclose(O.rmsnorm(x * 4, gamma, 0.0), O.rmsnorm(x, gamma, 0.0), rtol=1e-12)
+
+
+def test_swiglu_closed_forms():
+    g = np.array([0.0, 40.0, -40.0, 1.0, -1.0])
+    u = np.array([3.0, 2.0, 5.0, 1.0, 1.0])
+    out = O.swiglu(g, u)
+    assert out[0] == 0.0
+    assert np.isclose(out[1], 80.0) and abs(out[2]) < 1e-15
+    # silu(1) - silu(-1) = 1 (silu(x) - silu(-x) = x)
+    assert np.isclose(out[3] - out[4], 1.0, rtol=1e-15)
