@@ -170,7 +170,7 @@ struct GemvFuse {
   float eps;
 };
 
-template <int FMT, int NBC, int MT, int R, int KSPLIT, bool PREP, int FUSE>
+template <int FMT, int NBC, int MT, int R, int NCKT, int KSPLIT, bool PREP, int FUSE>
 __global__ void __launch_bounds__(64 * KSPLIT)
 k_gemv_q(const GemvFuse fz, const float *__restrict__ x, const int8_t *__restrict__ xl_g,
          const float *__restrict__ scl_g, int K, int C, int Kp, int nb) {
@@ -188,7 +188,8 @@ k_gemv_q(const GemvFuse fz, const float *__restrict__ x, const int8_t *__restric
   const int N = si == 0 ? s0.N : si == 1 ? s1.N : si == 2 ? s2.N : s3.N;
   const int wg0 = si == 0 ? 0 : si == 1 ? s0.wg_end : si == 2 ? s1.wg_end : s2.wg_end;
   using F = Fmt<FMT>;
-  constexpr int NCK = F::MAXC / R;           // chunks per wave (upper bound)
+  constexpr int NCK = NCKT;                  // chunks per wave (upper bound, <= MAXC / R)
+  static_assert(NCK * R <= F::MAXC, "register budget");
   constexpr int LKMAX = F::CK * NCK;         // slice elements per wave
   constexpr int TPR = LKMAX / 8 / 64;        // 8-element staging tasks per batch row per lane
   constexpr int BPC = F::CK / 32;            // 32-blocks per chunk
@@ -562,10 +563,11 @@ int env_int(const char *name) {
   return e ? atoi(e) : 0;
 }
 
-template <int FMT, int NBC, int MT, int R, bool PREP>
+template <int FMT, int NBC, int MT, int R, bool PREP, bool HALF>
 int launch_r(const void *packed, const float *x, const void *ws, float *y, int N, int K, int nb, int ks,
              hipStream_t s) {
   using F = Fmt<FMT>;
+  constexpr int NCKT = F::MAXC / R / (HALF ? 2 : 1);
   const int C = (int)gq_chunks(FMT, K);
   const int Kp = (int)gq_kpad(FMT, K);
   const size_t tiles = gq_tiles(N);
@@ -578,8 +580,8 @@ int launch_r(const void *packed, const float *x, const void *ws, float *y, int N
   fz.seg[0] = GemvSeg{(const uint8_t *)packed, sc_off, y, N, (int)wgs};
   fz.nseg = 1;
 #define GQ_LAUNCH_KS(KS)                                                                                         \
-  hipLaunchKernelGGL((k_gemv_q<FMT, NBC, MT, R, KS, PREP, 0>), dim3((unsigned)wgs), dim3(64 * KS), lds, s, fz, x, \
-                     xl, scl, K, C, Kp, nb)
+  hipLaunchKernelGGL((k_gemv_q<FMT, NBC, MT, R, NCKT, KS, PREP, 0>), dim3((unsigned)wgs), dim3(64 * KS), lds, s, \
+                     fz, x, xl, scl, K, C, Kp, nb)
   switch (ks) {
   case 2: GQ_LAUNCH_KS(2); break;
   case 4: GQ_LAUNCH_KS(4); break;
@@ -615,8 +617,12 @@ static int q_plan(int fmt, size_t N, size_t K, int batch, int *R_out, int *kspli
   // fewest waves per workgroup that fit the register budget (measured best:
   // long per-wave chunk lists, every workgroup resident in the first round),
   // more only when the grid would otherwise have too few waves
+  // a single-tile workgroup aims at maxc / 2 chunks per wave (half the
+  // activation staging and registers per wave), when 16 waves can cover K so
+  int target = maxc / R;
+  if (R == 1 && (C + 15) / 16 <= maxc / 2) target = maxc / 2;
   int ks = 2;
-  while (ks < 16 && (C + ks - 1) / ks > maxc / R) ks *= 2;
+  while (ks < 16 && (C + ks - 1) / ks > target) ks *= 2;
   while (ks < cap && ((tiles + R - 1) / R) * ks < 1024 && 2 * ks <= C) ks *= 2;
   const int e = env_int("GQ_GEMV_KSPLIT");
   if ((e == 2 || e == 4 || e == 8 || e == 16) && (C + e - 1) / e <= maxc / R) ks = e;
@@ -648,8 +654,9 @@ int launch_shape(const void *packed, const float *x, const void *ws, float *y, i
   int R = 1, ks = 2, cpw = 0;
   GQ_TRY(q_plan(FMT, N, K, nb, &R, &ks, &cpw));
   if (cpw > Fmt<FMT>::MAXC / R) return GQ_ERR_INVALID_ARGS;  // the kernel's register budget
-  if (R == 2) return launch_r<FMT, NBC, MT, 2, PREP>(packed, x, ws, y, N, K, nb, ks, s);
-  return launch_r<FMT, NBC, MT, 1, PREP>(packed, x, ws, y, N, K, nb, ks, s);
+  if (R == 2) return launch_r<FMT, NBC, MT, 2, PREP, false>(packed, x, ws, y, N, K, nb, ks, s);
+  if (!PREP && cpw <= Fmt<FMT>::MAXC / 2) return launch_r<FMT, NBC, MT, 1, PREP, true>(packed, x, ws, y, N, K, nb, ks, s);
+  return launch_r<FMT, NBC, MT, 1, PREP, false>(packed, x, ws, y, N, K, nb, ks, s);
 }
 
 template <int FMT>
@@ -755,8 +762,8 @@ int launch_fused_nbc(const GemvFuse &fz, size_t wgs, int ks, const float *x, int
   const int Kp = (int)gq_kpad(FMT, K);
   const size_t lds = (size_t)ks * xl_layout(F::CK * ((C + ks - 1) / ks), NBC).wave_bytes;
 #define GQ_LAUNCH_F(KS)                                                                                        \
-  hipLaunchKernelGGL((k_gemv_q<FMT, NBC, 1, R, KS, false, FUSE>), dim3((unsigned)wgs), dim3(64 * KS), lds, s, fz, \
-                     x, nullptr, nullptr, K, C, Kp, nb)
+  hipLaunchKernelGGL((k_gemv_q<FMT, NBC, 1, R, F::MAXC / R, KS, false, FUSE>), dim3((unsigned)wgs), dim3(64 * KS), \
+                     lds, s, fz, x, nullptr, nullptr, K, C, Kp, nb)
   switch (ks) {
   case 2: GQ_LAUNCH_F(2); break;
   case 4: GQ_LAUNCH_F(4); break;
