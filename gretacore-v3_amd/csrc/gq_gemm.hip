@@ -195,16 +195,19 @@ GQ_DEV void store_w(const WRec<FMT> &rec, int tl, int lane, int step, _Float16 *
 
 // ---- activation tile: global fp16 -> LDS directly ----------------------------
 // A K step of the tile is BM rows x 8 chunks of 16 B.  One wave instruction
-// fills 8 consecutive rows (1 KiB of LDS, lane l at byte 16 l); lane l loads
-// logical chunk (l & 7) ^ (l >> 3) of row l >> 3 -- the chunk index is XORed
-// with the row index mod 8.
+// fills 8 consecutive rows (1 KiB of LDS, lane l at byte 16 l).  Logical chunk
+// c of row j sits in physical chunk c ^ swz(j), swz(j) = (j ^ (j >> 3)) & 7 on
+// the row index mod 32: any 8 (or 16) consecutive rows then read the same
+// logical chunk from 8 (16) different bank groups, for 32 or 64 LDS banks.
+GQ_DEV int a_swz(int row) { return (row ^ ((row >> 3) & 3)) & 7; }
+
 template <int BM>
 GQ_DEV void load_a_lds(const _Float16 *a16, int lda, int M, int m0, int step, int wave, int lane, _Float16 *As) {
   constexpr int PER_WAVE = BM / 64;  // instructions per wave per K step
 #pragma unroll
   for (int i = 0; i < PER_WAVE; ++i) {
     const int row0 = 8 * (wave * PER_WAVE + i);
-    const int c = (lane & 7) ^ (lane >> 3);
+    const int c = (lane & 7) ^ a_swz(row0 + (lane >> 3));
     int m = m0 + row0 + (lane >> 3);
     if (m >= M) m = M - 1;  // clamped; rows >= M are never stored
     const _Float16 *src = a16 + (size_t)m * lda + step * BK + 8 * c;
@@ -297,7 +300,7 @@ k_gemm_t16(const uint8_t *__restrict__ w, uint32_t sc_off, const _Float16 *__res
   // B rows (BN/4) wn + 32 j + (lane & 31), padded rows
   const int arow = (BM / 2) * wm + (lane & 31);
   const int brow = (BN / 4) * wn + (lane & 31);
-  const int sw = lane & 7;  // == arow & 7
+  const int sw = a_swz(lane & 31);  // == a_swz(arow + 32 i): row bases are multiples of 32
 
   // One K step on LDS buffer BUF: first the weight records of step + 1
   // (register stage BUF ^ 1, loaded one step ago) are dequantized into weight
