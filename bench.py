@@ -244,6 +244,8 @@ def main():
     ap.add_argument("--headline-only", action="store_true", help="only the headline GEMV (for profiling)")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-decode-step", action="store_true")
+    ap.add_argument("--gemm-only", action="store_true",
+                    help="only the Q4_0 M=2048 14336x4096 prefill GEMM, --steps times (for profiling)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one GPU only: this build has no multi-GPU path (each GPU box has one GPU); "
@@ -257,6 +259,10 @@ def main():
     dev = torch.device("cuda:0")
     steps, warmup = args.steps, args.warmup
 
+    if args.gemm_only:
+        r = bench_gemm(O.Q4_0, 2048, 14336, 4096, steps, warmup, dev)
+        print(json.dumps({"gemm_q4_0_m2048_14336x4096": r}), flush=True)
+        return
     if args.headline_only:
         # a plain copy of known size, so profiler byte counters can be
         # calibrated against the GEMV dispatches of the same run
