@@ -128,25 +128,45 @@ __host__ __device__ inline XlLayout xl_layout(int lk, int nb) {
 constexpr float kMagic = 12582912.0f;  // 1.5 * 2^23: adding it rounds to an integer in the low mantissa bits
 
 // Splits 8 consecutive elements into the two limbs (4 int8 per word) and
-// returns sum(a) * 254 + sum(b) (an exact integer in fp32), so the block sum of
-// the represented values is s / 254 times it.
-GQ_DEV float split8(const float (&v)[8], float inv, uint32_t (&la)[2], uint32_t (&lb)[2]) {
+// returns sum(a) * 254 + sum(b) as an exact integer, so the block sum of the
+// represented values is s / 254 times it.  a = round(v * inv) comes out of the
+// low mantissa bits of fma(v, inv, 1.5 * 2^23); the remainder v * inv - a is
+// formed by a second fma (exact), scaled by 254 and rounded the same way.  The
+// limb sums are integer dot products of the packed bytes with ones.
+GQ_DEV int split8(const float (&v)[8], float inv, uint32_t (&la)[2], uint32_t (&lb)[2]) {
   float fa[8], fb[8];
-  float sum = 0.f;
 #pragma unroll
   for (int e = 0; e < 8; ++e) {
-    const float t = v[e] * inv;
-    fa[e] = t + kMagic;                    // bits: integer a in the low byte
+    fa[e] = __builtin_fmaf(v[e], inv, kMagic);  // bits: integer a in the low byte
     const float ai = fa[e] - kMagic;
-    const float r = t - ai;                // in [-0.5, 0.5]
-    fb[e] = __builtin_fmaf(r, 254.0f, kMagic);
-    sum += __builtin_fmaf(ai, 254.0f, fb[e] - kMagic);
+    fb[e] = __builtin_fmaf(__builtin_fmaf(v[e], inv, -ai), 254.0f, kMagic);
   }
   la[0] = pack_lo_bytes(fa[0], fa[1], fa[2], fa[3]);
   la[1] = pack_lo_bytes(fa[4], fa[5], fa[6], fa[7]);
   lb[0] = pack_lo_bytes(fb[0], fb[1], fb[2], fb[3]);
   lb[1] = pack_lo_bytes(fb[4], fb[5], fb[6], fb[7]);
-  return sum;
+  constexpr int kOnes = 0x01010101;
+  const int sa = __builtin_amdgcn_sdot4((int)la[1], kOnes, __builtin_amdgcn_sdot4((int)la[0], kOnes, 0, false), false);
+  const int sb = __builtin_amdgcn_sdot4((int)lb[1], kOnes, __builtin_amdgcn_sdot4((int)lb[0], kOnes, 0, false), false);
+  return 254 * sa + sb;
+}
+
+// Quad-wide (lanes 4j .. 4j+3) max / integer sum through DPP quad permutes.
+GQ_DEV float quad_max(float v) {
+  v = fmaxf(v, __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0xB1, 0xF, 0xF, false)));  // lane ^ 1
+  return fmaxf(v, __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x4E, 0xF, 0xF, false)));  // lane ^ 2
+}
+GQ_DEV int quad_sum(int v) {
+  v += __builtin_amdgcn_mov_dpp(v, 0xB1, 0xF, 0xF, false);
+  return v + __builtin_amdgcn_mov_dpp(v, 0x4E, 0xF, 0xF, false);
+}
+// Sum over the four 16-lane groups (lane, lane ^ 16, lane ^ 32, lane ^ 48):
+// each permlane swap returns the pair (own, partner) in some order.
+GQ_DEV float sum_lane_groups(float p) {
+  const auto s32 = __builtin_amdgcn_permlane32_swap(__float_as_uint(p), __float_as_uint(p), false, false);
+  p = __uint_as_float(s32[0]) + __uint_as_float(s32[1]);
+  const auto s16 = __builtin_amdgcn_permlane16_swap(__float_as_uint(p), __float_as_uint(p), false, false);
+  return __uint_as_float(s16[0]) + __uint_as_float(s16[1]);
 }
 
 // One weight matrix of a launch: T16 data, its scale-plane offset, output
@@ -233,8 +253,8 @@ k_gemv_q(const GemvFuse fz, const float *__restrict__ x, const int8_t *__restric
   __builtin_amdgcn_sched_barrier(0);
 
   // ---- 2. weight loads for every chunk of this wave (clamped, unconditional) -
-  // Issued in consumption order (chunk-major, then tile) with wave-uniform
-  // base addresses, so each load is a scalar base + the lane's fixed offset.
+  // Wave-uniform base addresses, so each load is a scalar base + the lane's
+  // fixed offset.
   Chunk<FMT> ch[R][NCK];
   const uint32_t qlane = 16u * (uint32_t)lane;
   const uint32_t slane = (FMT == GQ_FMT_Q4_K) ? 16u * (uint32_t)r : 8u * (uint32_t)r + 4u * (uint32_t)(g >> 1);
@@ -253,23 +273,17 @@ k_gemv_q(const GemvFuse fz, const float *__restrict__ x, const int8_t *__restric
       sbase[rt] = w + sc_off + (t * (size_t)C + c0) * F::SB;
     }
   }
-  // surplus loads re-read the wave's last chunk (its first one when the wave
-  // has no chunk: c0 < C always holds), never outside the tensor
-  auto issue = [&](int i) {
-    const int ii = i < nck ? i : (nck > 0 ? nck - 1 : 0);
+  // Surplus loads re-read the wave's last chunk (its first one when the wave
+  // has no chunk: c0 < C always holds), never outside the tensor.  All loads
+  // are issued up front, tile by tile (each tile's chunks are one contiguous
+  // run of memory; measured faster than interleaving the tiles chunk by chunk).
 #pragma unroll
-    for (int rt = 0; rt < R; ++rt)
+  for (int rt = 0; rt < R; ++rt)
+#pragma unroll
+    for (int i = 0; i < NCK; ++i) {
+      const int ii = i < nck ? i : (nck > 0 ? nck - 1 : 0);
       load_chunk<FMT>(qbase[rt] + (size_t)ii * F::QB, sbase[rt] + (size_t)ii * F::SB, qlane, slane, ch[rt][i]);
-  };
-  // PF chunks are requested up front; chunk i + PF is requested once chunk i
-  // has been consumed
-#ifdef GQ_GEMV_PF
-  constexpr int PF = GQ_GEMV_PF < NCK ? GQ_GEMV_PF : NCK;
-#else
-  constexpr int PF = NCK;
-#endif
-#pragma unroll
-  for (int i = 0; i < PF; ++i) issue(i);
+    }
   __builtin_amdgcn_sched_barrier(0);
 
   // ---- 3. activation limbs --------------------------------------------------
@@ -278,11 +292,6 @@ k_gemv_q(const GemvFuse fz, const float *__restrict__ x, const int8_t *__restric
   const int8_t *zero;
   int lds_ld, scl_ld, kbase;  // limb row stride, scale row stride (blocks), slice origin
   if constexpr (!PREP) {
-#if defined(GQ_EXPERIMENT) && GQ_EXPERIMENT == 1
-    constexpr bool kStage = false;  // skip the activation split (wrong results)
-#else
-    constexpr bool kStage = true;
-#endif
     const XlLayout L = xl_layout(F::CK * ((C + KSPLIT - 1) / KSPLIT), NBC);
     unsigned char *base = gq_dyn_lds + (size_t)wave * L.wave_bytes;
     int8_t *lm = reinterpret_cast<int8_t *>(base);
@@ -325,7 +334,7 @@ k_gemv_q(const GemvFuse fz, const float *__restrict__ x, const int8_t *__restric
       }
     }
 #pragma unroll
-    for (int i = 0; i < (kStage ? NBC * TPR : 0); ++i) {
+    for (int i = 0; i < NBC * TPR; ++i) {
       const int b = i / TPR, e8 = lane + 64 * (i % TPR);
       float v[8] = {xv[i][0].x, xv[i][0].y, xv[i][0].z, xv[i][0].w, xv[i][1].x, xv[i][1].y, xv[i][1].z, xv[i][1].w};
       if constexpr (FUSE > 0) {
@@ -343,17 +352,15 @@ k_gemv_q(const GemvFuse fz, const float *__restrict__ x, const int8_t *__restric
         v[e] = xin[i] ? v[e] : 0.f;
         amax = fmaxf(amax, fabsf(v[e]));
       }
-      amax = fmaxf(amax, __shfl_xor(amax, 1, 64));
-      amax = fmaxf(amax, __shfl_xor(amax, 2, 64));
-      const float inv = amax > 0.f ? 127.0f / amax : 0.f;
+      amax = quad_max(amax);
+      // 127 / amax to one ulp: a (represented) limb split needs no correctly
+      // rounded quotient, the scale sx below is what the products use
+      const float inv = amax > 0.f ? 127.0f * __builtin_amdgcn_rcpf(amax) : 0.f;
       const float sx = amax * (1.0f / 127.0f);
       uint32_t la[2], lb[2];
       // block sum of the represented values: offsets and mins then act on
       // exactly the activation the integer products see
-      float s = split8(v, inv, la, lb);
-      s += __shfl_xor(s, 1, 64);
-      s += __shfl_xor(s, 2, 64);
-      s *= sx * (1.0f / 254.0f);
+      const float s = (float)quad_sum(split8(v, inv, la, lb)) * (sx * (1.0f / 254.0f));
       if (8 * e8 < L.lk) {
         *reinterpret_cast<gq_u2 *>(lm + (2 * b) * L.lk + 8 * e8) = gq_u2{la[0], la[1]};
         *reinterpret_cast<gq_u2 *>(lm + (2 * b + 1) * L.lk + 8 * e8) = gq_u2{lb[0], lb[1]};
@@ -403,35 +410,10 @@ k_gemv_q(const GemvFuse fz, const float *__restrict__ x, const int8_t *__restric
 #pragma unroll
       for (int v = 0; v < NBC; ++v) acc[rt][mt][v] = cor[rt][mt][v] = 0.f;
 
-#if defined(GQ_EXPERIMENT) && GQ_EXPERIMENT == 2
-  {  // memory only: fold the loaded words, skip all compute
-    uint32_t acc2 = 0;
-#pragma unroll
-    for (int i = 0; i < NCK; ++i)
-#pragma unroll
-      for (int rt = 0; rt < R; ++rt) {
-        if constexpr (FMT == GQ_FMT_Q4_0) {
-          acc2 ^= ch[rt][i].q[0] ^ ch[rt][i].q[1] ^ ch[rt][i].q[2] ^ ch[rt][i].q[3] ^ ch[rt][i].d;
-        } else if constexpr (FMT == GQ_FMT_Q8_0) {
-          acc2 ^= ch[rt][i].q0[0] ^ ch[rt][i].q0[1] ^ ch[rt][i].q0[2] ^ ch[rt][i].q0[3] ^ ch[rt][i].d;
-          acc2 ^= ch[rt][i].q1[0] ^ ch[rt][i].q1[1] ^ ch[rt][i].q1[2] ^ ch[rt][i].q1[3];
-        } else {
-          acc2 ^= ch[rt][i].qa[0] ^ ch[rt][i].qa[1] ^ ch[rt][i].qa[2] ^ ch[rt][i].qa[3] ^ ch[rt][i].meta[0];
-          acc2 ^= ch[rt][i].qb[0] ^ ch[rt][i].qb[1] ^ ch[rt][i].qb[2] ^ ch[rt][i].qb[3] ^ ch[rt][i].meta[1];
-          acc2 ^= ch[rt][i].meta[2] ^ ch[rt][i].meta[3];
-        }
-      }
-    if (acc2 == 0x9E3779B9u && r == 0) y[0] = 1.0f;
-    return;
-  }
-#endif
   // ---- 4. consume the chunks -------------------------------------------------
-#if defined(GQ_EXPERIMENT) && GQ_EXPERIMENT == 4
-  for (int rep = 0; rep < 2; ++rep)  // twice the consume work (timing probe)
-#endif
-#pragma unroll
-  for (int i = 0; i < NCK; ++i) {
-    if (i < nck)
+  // Chunk i of this wave; with a full chunk list (the common case) the loop
+  // is straight-line code, so the waits on the weight loads stay in order.
+  auto consume = [&](int i) {
 #pragma unroll
     for (int m = 0; m < F::STEPS; ++m) {
       const int koff = i * F::CK + 64 * m;
@@ -481,7 +463,14 @@ k_gemv_q(const GemvFuse fz, const float *__restrict__ x, const int8_t *__restric
         }
       }
     }
-    if (i + PF < NCK) issue(i + PF);
+  };
+  if (nck == NCK) {
+#pragma unroll
+    for (int i = 0; i < NCK; ++i) consume(i);
+  } else {
+#pragma unroll
+    for (int i = 0; i < NCK; ++i)
+      if (i < nck) consume(i);
   }
 
   // ---- 5. reduce: lane groups (4 combinations), then the KSPLIT waves --------
@@ -493,17 +482,9 @@ k_gemv_q(const GemvFuse fz, const float *__restrict__ x, const int8_t *__restric
     for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
       for (int v = 0; v < NBC; ++v) {
-        float p = acc[rt][mt][v] - OFF * cor[rt][mt][v];
-        p += __shfl_xor(p, 16, 64);
-        p += __shfl_xor(p, 32, 64);
-        part[rt][mt][v] = p;
+        part[rt][mt][v] = sum_lane_groups(acc[rt][mt][v] - OFF * cor[rt][mt][v]);
       }
-#if defined(GQ_EXPERIMENT) && GQ_EXPERIMENT == 3
-  constexpr bool kReduce = false;  // every wave stores its partial (wrong results)
-#else
-  constexpr bool kReduce = true;
-#endif
-  if constexpr (KSPLIT > 1 && kReduce) {
+  if constexpr (KSPLIT > 1) {
     __shared__ float red[KSPLIT][R * MT * NBC][16];
     if (g == 0) {
 #pragma unroll
