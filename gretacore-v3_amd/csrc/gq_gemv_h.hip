@@ -11,11 +11,11 @@
 // fp16 (rows >= batch are zero).  The MFMA accumulates across blocks in fp32,
 // so no per-block work remains.
 //
-// A wave takes its K slice in groups of NCK chunks: it issues every weight
-// load of the group, converts the activations of its MFMA k-positions to fp16
-// registers (shared by the R row tiles of the workgroup), and consumes the
-// chunks as they arrive.  The KSPLIT waves' partial sums are reduced in LDS.
+// The activations are staged once per workgroup, window by window, as fp16 A
+// fragments in LDS and shared by the workgroup's row tiles (k_gemv_h below).
 #include <stdlib.h>
+
+#include <type_traits>
 
 #include "gq_internal.h"
 
@@ -25,15 +25,15 @@ template <int FMT>
 struct HFmt;
 template <>
 struct HFmt<GQ_FMT_Q4_0> {
-  static constexpr int CK = 128, QB = 1024, SB = 128, STEPS = 2, NCK = 4;
+  static constexpr int CK = 128, QB = 1024, SB = 128, STEPS = 2;
 };
 template <>
 struct HFmt<GQ_FMT_Q8_0> {
-  static constexpr int CK = 128, QB = 2048, SB = 128, STEPS = 2, NCK = 4;
+  static constexpr int CK = 128, QB = 2048, SB = 128, STEPS = 2;
 };
 template <>
 struct HFmt<GQ_FMT_Q4_K> {
-  static constexpr int CK = 256, QB = 2048, SB = 256, STEPS = 4, NCK = 2;
+  static constexpr int CK = 256, QB = 2048, SB = 256, STEPS = 4;
 };
 
 template <int FMT>
@@ -143,119 +143,167 @@ GQ_DEV gq_f4 mfma16h(const gq_half8 &a, const gq_half8 &b, const gq_f4 &c) {
   return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
 }
 
-// 16 consecutive fp32 -> 2 fp16 A fragments (zeros where `in` is false)
-GQ_DEV void x16_to_frags(const float *p, bool in, gq_half8 &f0, gq_half8 &f1) {
-  gq_f4 v[4];
-#pragma unroll
-  for (int i = 0; i < 4; ++i) v[i] = in ? *reinterpret_cast<const gq_f4 *>(p + 4 * i) : gq_f4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-  for (int i = 0; i < 8; ++i) {
-    f0[i] = (_Float16)v[i >> 2][i & 3];
-    f1[i] = (_Float16)v[2 + (i >> 2)][i & 3];
-  }
-}
+// Activation staging window: kWin consecutive k of every K part, converted to
+// fp16 A fragments in LDS once per workgroup and shared by its TW row tiles.
+constexpr int kWin = 256;
+constexpr int kWinBytes = kWin / 64 * 2 * 64 * 16;  // [64-k step][half][lane][8 x fp16]
 
-template <int FMT, int R, int KSPLIT>
-__global__ void __launch_bounds__(64 * KSPLIT)
+// Workgroup = TW row tiles x KS parts of K, one wave per (tile, part).  The
+// waves of a part walk their K range window by window: weights are loaded two
+// windows ahead into registers, the activations of the next window are loaded
+// (fp32, coalesced runs of 8) while the current window is consumed, then
+// converted into the other LDS buffer; one barrier per window.  A lane (g, r)
+// of the A fragment for 64-k step m, half j holds x[r][64 m + 16 g + 8 j + 0..7]
+// (rows >= batch are zero), matching the weights dequant_step gives lane
+// (g, r).  The KS parts' partial sums are reduced in LDS at the end.
+template <int FMT, int TW, int KS>
+__global__ void __launch_bounds__(64 * TW * KS)
 k_gemv_h(const uint8_t *__restrict__ w, size_t sc_off, const float *__restrict__ x, float *__restrict__ y, int N,
-         int K, int C, int nb) {
+         int K, int C, int nb, int NI) {
   using F = HFmt<FMT>;
-  constexpr int NCK = F::NCK;
+  constexpr int WC = kWin / F::CK;                   // chunks per window
+  constexpr int NT = 64 * TW * KS;                   // threads
+  constexpr int RPT = (KS * 16 * (kWin / 8)) / NT;   // x runs of 8 per thread per window
+  static_assert(RPT * NT == KS * 16 * (kWin / 8), "runs must divide evenly");
+  __shared__ __attribute__((aligned(16))) unsigned char xs[2][KS][kWinBytes];
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int tt = wave % TW, part = wave / TW;
   const int g = lane >> 4, r = lane & 15;
-  const size_t tile0 = (size_t)blockIdx.x * R;
   const int ntiles = (int)gq_tiles(N);
-  const int c0 = (C * wave) / KSPLIT, c1 = (C * (wave + 1)) / KSPLIT;
-  const int nck = c1 - c0;  // chunks of this wave, consumed in groups of NCK
-
+  const size_t tile = (size_t)blockIdx.x * TW + tt;
+  const size_t tb = (tile < (size_t)ntiles ? tile : (size_t)ntiles - 1) * (size_t)C;
+  const int c0 = (C * part) / KS, c1 = (C * (part + 1)) / KS;  // this wave's chunks (c0 < c1: KS <= C)
   const uint32_t qlane = 16u * (uint32_t)lane;
   const uint32_t slane = (FMT == GQ_FMT_Q4_K) ? 16u * (uint32_t)r : 8u * (uint32_t)r + 4u * (uint32_t)(g >> 1);
-  size_t tbase[R];
+
+  // weights of window `it` (chunks past the part re-read its last chunk)
+  auto load_win = [&](int it, HChunk<FMT> (&ch)[WC]) {
 #pragma unroll
-  for (int rt = 0; rt < R; ++rt) {
-    const size_t t = (tile0 + rt < (size_t)ntiles) ? tile0 + rt : (size_t)ntiles - 1;
-    tbase[rt] = t * (size_t)C;
+    for (int j = 0; j < WC; ++j) {
+      int ci = c0 + it * WC + j;
+      ci = ci < c1 ? ci : c1 - 1;
+      load_hchunk<FMT>(w + (tb + ci) * F::QB, w + sc_off + (tb + ci) * F::SB, qlane, slane, ch[j]);
+    }
+  };
+  // activations: run u of this thread = (part p, batch row b, 8-run kr); its
+  // source row, first k and end of K range are fixed, each window adds kWin
+  gq_f4 xr[RPT][2];
+  bool xin[RPT];
+  const float *xsrc[RPT];
+  int xk0[RPT], xk1[RPT];
+  uint32_t xdst[RPT];
+#pragma unroll
+  for (int u = 0; u < RPT; ++u) {
+    const int run = (int)threadIdx.x + u * NT;
+    const int kr = run & 31, b = (run >> 5) & 15, p = run >> 9;
+    const int pc0 = (C * p) / KS, pc1 = (C * (p + 1)) / KS;
+    xsrc[u] = x + (size_t)(b < nb ? b : 0) * K;
+    xk0[u] = pc0 * F::CK + 8 * kr;
+    xk1[u] = b < nb ? min(pc1 * F::CK, K) : 0;  // K % 32 == 0: a run is wholly in or out
+    const int o = 8 * kr, m = o >> 6, gq = (o & 63) >> 4, j = (o & 15) >> 3;
+    xdst[u] = (uint32_t)(p * kWinBytes + ((m * 2 + j) * 64 + 16 * gq + b) * 16);
   }
-  const bool brow = r < nb;
-  const float *xr = x + (size_t)(brow ? r : 0) * K;
-
-  gq_f4 acc[R];
+  auto load_x = [&](int it) {
 #pragma unroll
-  for (int rt = 0; rt < R; ++rt) acc[rt] = gq_f4{0.f, 0.f, 0.f, 0.f};
-
-  for (int gb = 0; gb == 0 || gb < nck; gb += NCK) {
-    const int ng = nck - gb < NCK ? nck - gb : NCK;  // chunks in this group (may be 0)
-    // ---- weight loads of the group (clamped, unconditional): surplus loads
-    // re-read the group's last chunk (chunk c0 when the wave has none: c0 < C
-    // always holds), never outside the tensor
-    HChunk<FMT> ch[R][NCK];
-#pragma unroll
-    for (int i = 0; i < NCK; ++i) {
-      const int ci = c0 + gb + (i < ng ? i : (ng > 0 ? ng - 1 : 0));
-#pragma unroll
-      for (int rt = 0; rt < R; ++rt)
-        load_hchunk<FMT>(w + (tbase[rt] + ci) * F::QB, w + sc_off + (tbase[rt] + ci) * F::SB, qlane, slane,
-                         ch[rt][i]);
+    for (int u = 0; u < RPT; ++u) {
+      // unconditional load from a clamped address, zeroed after: no branches
+      const int k = xk0[u] + it * kWin;
+      const bool in = k < xk1[u];
+      const gq_f4 *src = reinterpret_cast<const gq_f4 *>(xsrc[u] + (in ? k : 0));
+      xr[u][0] = src[0];
+      xr[u][1] = src[1];
+      xin[u] = in;
     }
-    // ---- activations: lane (g, row b = r) keeps x[b][k] for the k of its
-    // MFMA slots: per step m, 16 consecutive k at 64 m + 32 (g >> 1) + 16 (g & 1)
-    gq_half8 xa[NCK][F::STEPS][2];
+  };
+  auto store_x = [&](int buf) {
 #pragma unroll
-    for (int i = 0; i < NCK; ++i) {
-      const int ci = c0 + gb + (i < ng ? i : (ng > 0 ? ng - 1 : 0));
+    for (int u = 0; u < RPT; ++u) {
+      gq_half8 h;
 #pragma unroll
-      for (int m = 0; m < F::STEPS; ++m) {
-        const int k = ci * F::CK + 64 * m + 32 * (g >> 1) + 16 * (g & 1);
-        const bool in = brow && k < K;  // K % 32 == 0: a 16-run is wholly in or out
-        x16_to_frags(xr + (in ? k : 0), in, xa[i][m][0], xa[i][m][1]);
+      for (int e = 0; e < 4; ++e) {
+        h[e] = (_Float16)xr[u][0][e];
+        h[4 + e] = (_Float16)xr[u][1][e];
       }
+      gq_u4 hv = __builtin_bit_cast(gq_u4, h);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) hv[e] = xin[u] ? hv[e] : 0u;  // k past the part / K, or b >= batch
+      *reinterpret_cast<gq_u4 *>(&xs[buf][0][0] + xdst[u]) = hv;
     }
-    // ---- consume
+  };
+
+  const int nwin = ((c1 - c0) + WC - 1) / WC;  // this wave's windows (<= NI)
+  HChunk<FMT> w0[WC], w1[WC], w2[WC];
+  load_win(0, w0);
+  load_win(1, w1);  // (a surplus re-read when NI == 1)
+  load_x(0);
+  store_x(0);
+  __syncthreads();
+  gq_f4 acc = gq_f4{0.f, 0.f, 0.f, 0.f};
+  // Window `it` (weights in w0).  PF: the weights of window it + 2 and the
+  // activations of window it + 1 are requested first.  The prefetch choice
+  // is a compile-time constant at every call, so no load sits under a branch
+  // (a branch around a load makes the compiler wait for every load issued
+  // before it).
+  auto window = [&](int it, auto pfw, auto pfx) {
+    if constexpr (decltype(pfw)::value) load_win(it + 2, w2);
+    if constexpr (decltype(pfx)::value) load_x(it + 1);
+    if (it < nwin) {
+      const unsigned char *xb = xs[it & 1][part];
 #pragma unroll
-    for (int i = 0; i < NCK; ++i) {
-      if (i < ng)
+      for (int j = 0; j < WC; ++j) {
+        if (c0 + it * WC + j < c1) {
 #pragma unroll
-        for (int m = 0; m < F::STEPS; ++m)
-#pragma unroll
-          for (int rt = 0; rt < R; ++rt) {
+          for (int m = 0; m < F::STEPS; ++m) {
+            const int ms = j * F::STEPS + m;
+            const gq_half8 a0 = *reinterpret_cast<const gq_half8 *>(xb + ((ms * 2 + 0) * 64 + lane) * 16);
+            const gq_half8 a1 = *reinterpret_cast<const gq_half8 *>(xb + ((ms * 2 + 1) * 64 + lane) * 16);
             gq_half8 b0, b1;
-            dequant_step<FMT>(ch[rt][i], m, 2 * m + (g >> 1), b0, b1);
-            acc[rt] = mfma16h(xa[i][m][0], b0, acc[rt]);
-            acc[rt] = mfma16h(xa[i][m][1], b1, acc[rt]);
+            dequant_step<FMT>(w0[j], m, 2 * m + (g >> 1), b0, b1);
+            acc = mfma16h(a0, b0, acc);
+            acc = mfma16h(a1, b1, acc);
           }
-    }
-  }
-
-  // ---- reduce over the KSPLIT waves; D lane (g, r): batch rows 4g..4g+3, column r
-  if constexpr (KSPLIT > 1) {
-    __shared__ gq_f4 red[KSPLIT][R][64];
-#pragma unroll
-    for (int rt = 0; rt < R; ++rt) red[wave][rt][lane] = acc[rt];
-    __syncthreads();
-    if (wave != 0) return;
-#pragma unroll
-    for (int rt = 0; rt < R; ++rt) {
-      gq_f4 s = red[0][rt][lane];
-#pragma unroll
-      for (int q = 1; q < KSPLIT; ++q) {
-        const gq_f4 v = red[q][rt][lane];
-        s[0] += v[0];
-        s[1] += v[1];
-        s[2] += v[2];
-        s[3] += v[3];
+        }
       }
-      acc[rt] = s;
     }
-  }
+    if constexpr (decltype(pfx)::value) store_x((it + 1) & 1);
+    __syncthreads();
 #pragma unroll
-  for (int rt = 0; rt < R; ++rt) {
-    const size_t row = (tile0 + rt) * 16 + r;
-    if (row >= (size_t)N) continue;
+    for (int j = 0; j < WC; ++j) {
+      w0[j] = w1[j];
+      w1[j] = w2[j];
+    }
+  };
+  using T_ = std::true_type;
+  using F_ = std::false_type;
+  int it = 0;
+  for (; it + 2 < NI; ++it) window(it, T_{}, T_{});
+  if (it + 1 < NI) window(it++, F_{}, T_{});
+  window(it, F_{}, F_{});
+
+  // ---- reduce over the KS parts (LDS reused); D lane (g, r): batch rows 4g..4g+3, column r
+  if constexpr (KS > 1) {
+    gq_f4 *red = reinterpret_cast<gq_f4 *>(&xs[0][0][0]);  // [KS][TW][64]
+    red[(part * TW + tt) * 64 + lane] = acc;
+    __syncthreads();
+    if (part != 0) return;
+    gq_f4 s = red[tt * 64 + lane];
+#pragma unroll
+    for (int q = 1; q < KS; ++q) {
+      const gq_f4 v = red[(q * TW + tt) * 64 + lane];
+      s[0] += v[0];
+      s[1] += v[1];
+      s[2] += v[2];
+      s[3] += v[3];
+    }
+    acc = s;
+  }
+  const size_t row = tile * 16 + r;
+  if (tile < (size_t)ntiles && row < (size_t)N) {
 #pragma unroll
     for (int v = 0; v < 4; ++v) {
       const int b = 4 * g + v;
-      if (b < nb) y[(size_t)b * N + row] = acc[rt][v];
+      if (b < nb) y[(size_t)b * N + row] = acc[v];
     }
   }
 }
@@ -267,46 +315,51 @@ int env_int(const char *name) {
 
 }  // namespace
 
-// Launch plan of the fp16 batch GEMV: R (1 or 2) row tiles per workgroup and
-// KSPLIT (1..8) waves.  chunks_per_wave may exceed NCK: the kernel then
-// consumes them in groups.
+// Launch plan of the fp16 batch GEMV: TW (1, 2 or 4) row tiles and KS (1..8)
+// parts of K per workgroup.  Wide matrices share each staged activation
+// window across 4 (or 2) row tiles; K is split until the grid holds about
+// 3584 waves (3.5 per SIMD; measured best on 14336 x 4096), at most 8 parts
+// (the double-buffered windows take KS x 16 KiB of LDS), at most one part
+// per chunk and at most 16 waves per workgroup.  chunks_per_wave is the
+// longest part.
 int gq_gemv_h_plan(int fmt, size_t N, size_t K, int *R_out, int *ks_out, int *cpw_out) {
   const int f = gq_fmt_is_q4k(fmt) ? GQ_FMT_Q4_K : fmt;
-  const int nck = f == GQ_FMT_Q4_K ? HFmt<GQ_FMT_Q4_K>::NCK : f == GQ_FMT_Q8_0 ? HFmt<GQ_FMT_Q8_0>::NCK
-                                                                                : HFmt<GQ_FMT_Q4_0>::NCK;
   const int C = (int)gq_chunks(f, K);
   const size_t tiles = gq_tiles(N);
-  // two row tiles per workgroup while that still leaves >= 256 workgroups
-  int R = (tiles + 1) / 2 >= 256 ? 2 : 1;
+  int tw = tiles >= 800 ? 4 : tiles >= 400 ? 2 : 1;
   const int er = env_int("GQ_GEMV_H_R");
-  if (er == 1 || er == 2) R = er;
-  // fewest waves (at most 8: a wave keeps ~200 VGPRs) such that each holds at
-  // most NCK chunks; past that a wave consumes its chunks in groups of NCK
+  if (er == 1 || er == 2 || er == 4) tw = er;
   int ks = 1;
-  while (ks < 8 && (C + ks - 1) / ks > nck) ks *= 2;
+  while (ks < 8 && tiles * ks < 3584 && 2 * ks <= C && tw * ks < 16) ks *= 2;
   const int e = env_int("GQ_GEMV_H_KSPLIT");
-  if (e == 1 || e == 2 || e == 4 || e == 8) ks = e;
-  *R_out = R;
+  if ((e == 1 || e == 2 || e == 4 || e == 8) && e <= C) ks = e;
+  if (tw * ks > 16) tw = 16 / ks;
+  *R_out = tw;
   *ks_out = ks;
   *cpw_out = (C + ks - 1) / ks;
   return GQ_OK;
 }
 
 namespace {
-template <int FMT, int R>
-int launch_h_r(const void *packed, const float *x, float *y, int N, int K, int nb, int ks, hipStream_t s) {
+template <int FMT, int TW>
+int launch_h_tw(const void *packed, const float *x, float *y, int N, int K, int nb, int ks, hipStream_t s) {
   const int C = (int)gq_chunks(FMT, K);
-  const size_t wgs = (gq_tiles(N) + R - 1) / R;
+  const size_t wgs = (gq_tiles(N) + TW - 1) / TW;
   const size_t sc_off = gq_sc_plane_offset(FMT, N, K);
   const uint8_t *w = (const uint8_t *)packed;
-#define GQ_LAUNCH_H(KS)                                                                                            \
-  hipLaunchKernelGGL((k_gemv_h<FMT, R, KS>), dim3((unsigned)wgs), dim3(64 * KS), 0, s, w, sc_off, x, y, N, K, C, \
-                     nb)
+  constexpr int WC = kWin / HFmt<FMT>::CK;
+  const int NI = ((C + ks - 1) / ks + WC - 1) / WC;
+#define GQ_LAUNCH_H(KS)                                                                                              \
+  hipLaunchKernelGGL((k_gemv_h<FMT, TW, KS>), dim3((unsigned)wgs), dim3(64 * TW * KS), 0, s, w, sc_off, x, y, N, K, \
+                     C, nb, NI)
   switch (ks) {
   case 1: GQ_LAUNCH_H(1); break;
   case 2: GQ_LAUNCH_H(2); break;
   case 4: GQ_LAUNCH_H(4); break;
-  default: GQ_LAUNCH_H(8); break;
+  default:
+    if constexpr (TW <= 2) GQ_LAUNCH_H(8);
+    else return GQ_ERR_INVALID_ARGS;
+    break;
   }
 #undef GQ_LAUNCH_H
   return gq_last_launch();
@@ -314,10 +367,11 @@ int launch_h_r(const void *packed, const float *x, float *y, int N, int K, int n
 
 template <int FMT>
 int launch_h(const void *packed, const float *x, float *y, int N, int K, int nb, hipStream_t s) {
-  int R, ks, cpw;
-  GQ_TRY(gq_gemv_h_plan(FMT, N, K, &R, &ks, &cpw));
-  if (R == 2) return launch_h_r<FMT, 2>(packed, x, y, N, K, nb, ks, s);
-  return launch_h_r<FMT, 1>(packed, x, y, N, K, nb, ks, s);
+  int tw, ks, cpw;
+  GQ_TRY(gq_gemv_h_plan(FMT, N, K, &tw, &ks, &cpw));
+  if (tw == 4) return launch_h_tw<FMT, 4>(packed, x, y, N, K, nb, ks, s);
+  if (tw == 2) return launch_h_tw<FMT, 2>(packed, x, y, N, K, nb, ks, s);
+  return launch_h_tw<FMT, 1>(packed, x, y, N, K, nb, ks, s);
 }
 }  // namespace
 

@@ -19,43 +19,43 @@ SHAPES = [(1, 32), (100, 288), (17, 96), (33, 160), (1, 256), (100, 256), (1, 76
           (4096, 4096), (14336, 4096), (4096, 14336), (1024, 4096), (128256, 4096), (7, 256), (40, 512)]
 
 
-NCK_H = {gq.FMT_Q4_0: 4, gq.FMT_Q8_0: 4, gq.FMT_Q4_K: 2, gq.FMT_Q4_K_GGML: 2}
 SB = {gq.FMT_Q4_0: 128, gq.FMT_Q8_0: 128, gq.FMT_Q4_K: 256, gq.FMT_Q4_K_GGML: 256}
-RMAX_H = {gq.FMT_Q4_0: 2, gq.FMT_Q8_0: 2, gq.FMT_Q4_K: 2, gq.FMT_Q4_K_GGML: 2}
+KWIN = 256  # k per activation staging window of the fp16 batch kernel
 
 
 def emulate_h(fmt, n, k, batch):
-    """Replays k_gemv_h's chunk-group and address arithmetic on the host."""
-    R, ks, cpw = gq.gemv_plan(fmt, n, k, batch)
-    assert R in (1, 2) and R <= RMAX_H[fmt] and ks in (1, 2, 4, 8)
+    """Replays k_gemv_h's window, chunk and address arithmetic on the host:
+    workgroup = TW row tiles x KS parts of K, weights prefetched two windows
+    ahead (clamped to the part's last chunk), activation runs of 8 per
+    thread and window."""
+    TW, KS, cpw = gq.gemv_plan(fmt, n, k, batch)
+    assert TW in (1, 2, 4) and KS in (1, 2, 4, 8) and TW * KS <= 16
     C = -(-k // CK[fmt])
+    assert KS <= C
     tiles = -(-n // 16)
-    assert cpw == -(-C // ks)
-    steps = CK[fmt] // 64
-    wgs = -(-tiles // R)
-    nck_g = NCK_H[fmt]
-    for wave in range(ks):
-        c0, c1 = C * wave // ks, C * (wave + 1) // ks
-        nck = c1 - c0
-        assert 0 <= c0 < C and c1 <= C
-        gb = 0
-        while gb == 0 or gb < nck:
-            ng = min(nck_g, nck - gb)
-            for i in range(nck_g):
-                ci = c0 + gb + (i if i < ng else (ng - 1 if ng > 0 else 0))
-                assert 0 <= ci < C
+    wc = KWIN // CK[fmt]
+    assert cpw == -(-C // KS)
+    NI = -(-cpw // wc)
+    wgs = -(-tiles // TW)
+    # LDS: two buffers of KS windows (8 KiB each) must fit the 160 KiB
+    assert 2 * KS * 8192 <= 160 * 1024
+    for part in range(KS):
+        c0, c1 = C * part // KS, C * (part + 1) // KS
+        assert 0 <= c0 < c1 <= C
+        for it in range(max(NI, 2)):  # windows loaded: 0, 1 and it + 2 < NI
+            for j in range(wc):
+                ci = min(c0 + it * wc + j, c1 - 1)
                 for blk in (0, wgs - 1):
-                    for rt in range(R):
-                        t = min(blk * R + rt, tiles - 1)
+                    for tt in range(TW):
+                        t = min(blk * TW + tt, tiles - 1)
                         chunk = t * C + ci
                         assert chunk * QB[fmt] + QB[fmt] <= tiles * C * QB[fmt]
                         assert chunk * SB[fmt] + SB[fmt] <= tiles * C * SB[fmt]
-                for m in range(steps):
-                    for g in range(4):
-                        kk = ci * CK[fmt] + 64 * m + 32 * (g >> 1) + 16 * (g & 1)
-                        if kk < k:
-                            assert kk + 16 <= k  # a 16-element run is read only when wholly inside
-            gb += nck_g
+        for it in range(NI):
+            for kr in range(32):
+                kk = c0 * CK[fmt] + 8 * kr + it * KWIN
+                if kk < min(c1 * CK[fmt], k):
+                    assert kk + 8 <= k  # a run of 8 is read only when wholly inside
 
 
 def emulate(fmt, n, k, batch):
