@@ -201,9 +201,9 @@ GQ_DEV void store_w(const WRec<FMT> &rec, int tl, int lane, int step, _Float16 *
 // logical chunk from 8 (16) different bank groups, for 32 or 64 LDS banks.
 GQ_DEV int a_swz(int row) { return (row ^ ((row >> 3) & 3)) & 7; }
 
-template <int BM>
+template <int BM, int NW = 8>
 GQ_DEV void load_a_lds(const _Float16 *a16, int lda, int M, int m0, int step, int wave, int lane, _Float16 *As) {
-  constexpr int PER_WAVE = BM / 64;  // instructions per wave per K step
+  constexpr int PER_WAVE = BM / (8 * NW);  // instructions per wave per K step (NW waves)
 #pragma unroll
   for (int i = 0; i < PER_WAVE; ++i) {
     const int row0 = 8 * (wave * PER_WAVE + i);
@@ -302,25 +302,19 @@ k_gemm_t16(const uint8_t *__restrict__ w, uint32_t sc_off, const _Float16 *__res
   const int brow = (BN / 4) * wn + (lane & 31);
   const int sw = a_swz(lane & 31);  // == a_swz(arow + 32 i): row bases are multiples of 32
 
-  // One K step on LDS buffer BUF: first the weight records of step + 1
-  // (register stage BUF ^ 1, loaded one step ago) are dequantized into weight
-  // buffer BUF ^ 1; then the A tile of step + 1 is requested (LDS DMA into A
-  // buffer BUF ^ 1) and the records of step + 2 (into register stage BUF,
-  // consumed one step ago); then the MFMAs.  The two waves of a SIMD overlap
-  // one's dequantization with the other's MFMAs.
+  // One K step on LDS buffer BUF: the A tile of step + 1 is requested (LDS
+  // DMA into A buffer BUF ^ 1); then, for each of the KS MFMA k-steps, its
+  // MFMAs are issued and a quarter of the weight records of step + 1
+  // (register stage BUF ^ 1, loaded a step ago) is dequantized into weight
+  // buffer BUF ^ 1 while they run; after the last quarter the records of
+  // step + 2 are requested into that register stage.
   auto run_step = [&](int step, auto buf_c) {
     constexpr int BUF = decltype(buf_c)::value;
     using NB = std::integral_constant<int, BUF ^ 1>;
     // the last steps' loads are clamped: loaded, never read
     const int s1 = step + 1 < nsteps ? step + 1 : nsteps - 1;
     const int s2 = step + 2 < nsteps ? step + 2 : nsteps - 1;
-#pragma unroll
-    for (int q = 0; q < KS; ++q) store_w_part(q, s1, BUF ^ 1, NB{});
-    // (the stores only wait for loads issued a step ago)
-    __builtin_amdgcn_sched_barrier(0);
     load_a_lds<BM>(a16, lda, M, m0, s1, wave, lane, As_of(NB{}));
-    load_w_step(s2, BUF);
-    // keep the requests ahead of the MFMAs: they have the whole step to land
     __builtin_amdgcn_sched_barrier(0);
     const _Float16 *As = As_of(buf_c) + arow * BK;
     const _Float16 *Bs = Bs_of(buf_c) + brow * BSTRIDE + 8 * (lane >> 5);
@@ -342,6 +336,12 @@ k_gemm_t16(const uint8_t *__restrict__ w, uint32_t sc_off, const _Float16 *__res
       for (int i = 0; i < TM; ++i)
 #pragma unroll
         for (int j = 0; j < TN; ++j) acc[i][j] = gq_mfma32(af[ks & 1][i], bf[ks & 1][j], acc[i][j]);
+      // dequantize a quarter of the next step's weight records (loaded a step
+      // ago) into the other weight buffer while these MFMAs run
+      store_w_part(ks, s1, BUF ^ 1, NB{});
+      // the records of step + 2 reuse that register stage: request them once
+      // the last quarter has been read
+      if (ks == KS - 1) load_w_step(s2, BUF);
     }
     // the A tile of step + 1 (LDS DMA, issued before the 2 * WR record
     // loads) must land before any wave reads buffer BUF ^ 1
@@ -373,6 +373,248 @@ k_gemm_t16(const uint8_t *__restrict__ w, uint32_t sc_off, const _Float16 *__res
 #pragma unroll
       for (int v = 0; v < 16; ++v) {
         const int m = m0 + (BM / 2) * wm + 32 * i + 8 * (v >> 2) + 4 * (lane >> 5) + (v & 3);
+        if (m < M) {
+          if constexpr (CBF16)
+            reinterpret_cast<uint16_t *>(c)[(size_t)m * N + n] = f32_to_bf16_rne(acc[i][j][v]);
+          else
+            reinterpret_cast<float *>(c)[(size_t)m * N + n] = acc[i][j][v];
+        }
+      }
+    }
+}
+
+// ---- register-B kernel: 256 x 256 tiles, 4 waves of 128 x 128 ----------------
+// The weight operand never goes through LDS: each wave loads, for each of its
+// four 32-column blocks, the T16 code groups of its columns and dequantizes
+// them straight into v_mfma_f32_32x32x16_f16 B fragments.  Only the
+// activation tile is staged in LDS (LDS DMA, double-buffered, swizzled).
+//
+// k order inside a 64-k step: MFMA k-step ks (16 k) takes, in lane half kh,
+// the 8 k at 32 (ks >> 1) + 16 kh + 8 (ks & 1).  For the weights this is T16
+// lane slot g = 2 (ks >> 1) + kh, code-group slots 8 (ks & 1) .. + 7 (one
+// dword of the group); for the activations it is 16-byte chunk
+// 4 (ks >> 1) + 2 kh + (ks & 1) of the row -- the same k on both sides.  All
+// eight k of a fragment lie in 32-block (ks >> 1) of the step.
+template <int FMT, int NJ>
+struct RStep;
+template <int NJ>
+struct RStep<GQ_FMT_Q4_0, NJ> {
+  gq_u2 q[NJ][2];  // [column block][g = kh or 2 + kh]: the step's 8-byte code groups
+  gq_u2 d[NJ];     // d0 d2 | d1 d3 of the column's chunk
+};
+template <int NJ>
+struct RStep<GQ_FMT_Q8_0, NJ> {
+  gq_u4 q[NJ][2];  // 16 int8 per lane slot
+  gq_u2 d[NJ];
+};
+template <int NJ>
+struct RStep<GQ_FMT_Q4_K, NJ> {
+  gq_u2 q[NJ][2];
+  gq_u4 meta[NJ];  // d, dmin, W1, W2, W3 of the column's super-block
+};
+
+template <int FMT, int NJ>
+GQ_DEV void load_rstep(const uint8_t *w, const uint32_t (&qo)[NJ], const uint32_t (&so)[NJ], int step,
+                       RStep<FMT, NJ> &st) {
+#pragma unroll
+  for (int j = 0; j < NJ; ++j) {
+    if constexpr (FMT == GQ_FMT_Q4_0) {
+      const uint8_t *b = w + ((size_t)(step >> 1) << 10) + 8 * (step & 1);
+      st.q[j][0] = gq_ld8(b + qo[j]);
+      st.q[j][1] = gq_ld8(b + qo[j] + 512);
+      st.d[j] = gq_ld8(w + (size_t)(step >> 1) * 128 + so[j]);
+    } else if constexpr (FMT == GQ_FMT_Q8_0) {
+      const uint8_t *b = w + ((size_t)(step >> 1) << 11) + ((step & 1) << 10);
+      st.q[j][0] = gq_ld16(b + qo[j]);
+      st.q[j][1] = gq_ld16(b + qo[j] + 512);
+      st.d[j] = gq_ld8(w + (size_t)(step >> 1) * 128 + so[j]);
+    } else {
+      const int m = step & 3;
+      const uint8_t *b = w + ((size_t)(step >> 2) << 11) + ((m >> 1) << 10) + 8 * (m & 1);
+      st.q[j][0] = gq_ld8(b + qo[j]);
+      st.q[j][1] = gq_ld8(b + qo[j] + 512);
+      st.meta[j] = gq_ld16(w + (size_t)(step >> 2) * 256 + so[j]);
+    }
+  }
+}
+
+// Q4_K: the fp16 factors of the sub-block 2 (step & 3) + h of column block j
+// (sc, -1024 sc, d, -dmin m), decoded once per K step.
+struct QKf {
+  gq_half2 sc2, nsc2, d2, mn2;
+};
+template <int NJ>
+GQ_DEV void q4k_factors(const RStep<GQ_FMT_Q4_K, NJ> &st, int step, QKf (&f)[NJ][2]) {
+#pragma unroll
+  for (int j = 0; j < NJ; ++j) {
+    const uint32_t mv[4] = {st.meta[j][0], st.meta[j][1], st.meta[j][2], st.meta[j][3]};
+    const float d = gq_h2f(mv[0] & 0xFFFFu), dmin = gq_h2f(mv[0] >> 16);
+    const _Float16 hd = (_Float16)d;  // exact: d came from fp16 (NaN aside)
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      uint32_t sc, mn;
+      gq_q4k_meta_codes(mv, 2 * (step & 3) + h, &sc, &mn);
+      const _Float16 hsc = (_Float16)(float)sc, hnsc = (_Float16)(-1024.0f * (float)sc);
+      const _Float16 hmin = (_Float16)(-(dmin * (float)mn));
+      f[j][h] = QKf{gq_half2{hsc, hsc}, gq_half2{hnsc, hnsc}, gq_half2{hd, hd}, gq_half2{hmin, hmin}};
+    }
+  }
+}
+
+// B fragment of column block j, MFMA k-step ks, K step `step`: 8 fp16 values
+// (c - bias) * scale (Q4_K: d sc c - dmin m, factors from q4k_factors), each
+// rounded once.
+template <int FMT, int NJ>
+GQ_DEV gq_half8 rfrag(const RStep<FMT, NJ> &st, int j, int ks, int step, const QKf *qk) {
+  const int h = ks >> 1;
+  gq_half2 p[4];
+  if constexpr (FMT == GQ_FMT_Q8_0) {
+    const gq_u4 &q = st.q[j][h];
+    const uint32_t w0 = q[2 * (ks & 1)] ^ 0x80808080u, w1 = q[2 * (ks & 1) + 1] ^ 0x80808080u;
+    const uint32_t db = st.d[j][h];
+    const gq_half2 d2 = h2_of_bits16((step & 1) ? (db >> 16) : db);
+    const gq_half2 off = {(_Float16)-1152.0f, (_Float16)-1152.0f};
+    bytes_to_magic(w0, p[0], p[1]);
+    bytes_to_magic(w1, p[2], p[3]);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) p[i] = (p[i] + off) * d2;
+  } else {
+    const uint32_t w = st.q[j][h][ks & 1];
+    bytes_to_magic(w & 0x0F0F0F0Fu, p[0], p[1]);
+    bytes_to_magic((w >> 4) & 0x0F0F0F0Fu, p[2], p[3]);
+    if constexpr (FMT == GQ_FMT_Q4_0) {
+      const uint32_t db = st.d[j][h];
+      const gq_half2 d2 = h2_of_bits16((step & 1) ? (db >> 16) : db);
+      const gq_half2 off = {(_Float16)-1032.0f, (_Float16)-1032.0f};
+#pragma unroll
+      for (int i = 0; i < 4; ++i) p[i] = (p[i] + off) * d2;
+    } else {
+      const QKf &f = qk[h];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) p[i] = __builtin_elementwise_fma(__builtin_elementwise_fma(p[i], f.sc2, f.nsc2), f.d2, f.mn2);
+    }
+  }
+  gq_half8 o;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    o[2 * i] = p[i][0];
+    o[2 * i + 1] = p[i][1];
+  }
+  return o;
+}
+
+// Workgroup tile BM x BN, WM x WN waves; a wave owns (BM / WM) x (BN / WN) of C
+// (TM x NJ MFMA tiles of 32 x 32).  256 x 256 with 2 x 4 waves: two waves per SIMD.
+template <int FMT, int CBF16, int BM, int BN, int WM, int WN>
+__global__ void __launch_bounds__(64 * WM * WN) __attribute__((amdgpu_waves_per_eu(WM * WN / 4, WM * WN / 4)))
+k_gemm_rb(const uint8_t *__restrict__ w, uint32_t sc_off, const _Float16 *__restrict__ a16, int lda,
+          void *__restrict__ c, int M, int N, int C, int nsteps, int tiles_m) {
+  constexpr int KS = BK / 16;
+  constexpr int NW = WM * WN, TM = BM / WM / 32, NJ = BN / WN / 32;  // waves, MFMA tiles per wave
+  static_assert(TM >= 1 && NJ >= 1 && BM % (8 * NW) == 0, "tile shape");
+  __shared__ __attribute__((aligned(16))) _Float16 As_0[BM * BK];
+  __shared__ __attribute__((aligned(16))) _Float16 As_1[BM * BK];
+  auto As_of = [&](auto b) -> _Float16 * { return decltype(b)::value ? As_1 : As_0; };
+  using B0 = std::integral_constant<int, 0>;
+  using B1 = std::integral_constant<int, 1>;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wm = wave / WN, wn = wave % WN;
+  int mt, nt;
+  tile_of(blockIdx.x, gridDim.x, tiles_m, mt, nt);
+  const int m0 = mt * BM, n0 = nt * BN;
+  const int ntiles = (int)gq_tiles(N);
+  const int kh = lane >> 5, r = lane & 15;
+
+  // per column block: byte offsets of this lane's T16 slot g = kh (the slot
+  // 2 + kh is 512 bytes further) and of its row's scales, chunk 0
+  uint32_t qo[NJ], so[NJ];
+#pragma unroll
+  for (int j = 0; j < NJ; ++j) {
+    int t = (n0 + (BN / WN) * wn + 32 * j + (lane & 31)) >> 4;
+    if (t >= ntiles) t = ntiles - 1;  // clamped; those columns are never stored
+    const uint32_t tc = (uint32_t)t * (uint32_t)C;
+    const uint32_t slot = 16u * (16u * (uint32_t)kh + (uint32_t)r);
+    if constexpr (FMT == GQ_FMT_Q4_0) {
+      qo[j] = (tc << 10) + slot;
+      so[j] = sc_off + tc * 128u + 8u * r;
+    } else if constexpr (FMT == GQ_FMT_Q8_0) {
+      qo[j] = (tc << 11) + slot;
+      so[j] = sc_off + tc * 128u + 8u * r;
+    } else {
+      qo[j] = (tc << 11) + slot;
+      so[j] = sc_off + tc * 256u + 16u * r;
+    }
+  }
+
+  gq_f16v acc[TM][NJ];
+#pragma unroll
+  for (int i = 0; i < TM; ++i)
+#pragma unroll
+    for (int j = 0; j < NJ; ++j)
+#pragma unroll
+      for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.f;
+
+  RStep<FMT, NJ> wst[2];
+  const int arow = (BM / WM) * wm + (lane & 31);
+  const int sw = a_swz(lane & 31);
+
+  auto run_step = [&](int step, auto buf_c) {
+    constexpr int BUF = decltype(buf_c)::value;
+    using NB = std::integral_constant<int, BUF ^ 1>;
+    const int s1 = step + 1 < nsteps ? step + 1 : nsteps - 1;
+    const int s2 = step + 2 < nsteps ? step + 2 : nsteps - 1;
+    load_a_lds<BM, NW>(a16, lda, M, m0, s1, wave, lane, As_of(NB{}));
+    __builtin_amdgcn_sched_barrier(0);
+    const _Float16 *As = As_of(buf_c) + arow * BK;
+    RStep<FMT, NJ> &cur = wst[BUF];
+    gq_half8 af[2][TM];
+    auto read_a = [&](int ks, int fb) {
+      const int ch = (4 * (ks >> 1) + 2 * kh + (ks & 1)) ^ sw;
+#pragma unroll
+      for (int i = 0; i < TM; ++i) af[fb][i] = *reinterpret_cast<const gq_half8 *>(As + 32 * i * BK + 8 * ch);
+    };
+    read_a(0, 0);
+    QKf qk[NJ][2];
+    if constexpr (FMT == GQ_FMT_Q4_K) q4k_factors<NJ>(cur, step, qk);
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) {
+      if (ks + 1 < KS) read_a(ks + 1, (ks + 1) & 1);
+#pragma unroll
+      for (int j = 0; j < NJ; ++j) {
+        const gq_half8 bf = rfrag<FMT, NJ>(cur, j, ks, step, qk[j]);
+#pragma unroll
+        for (int i = 0; i < TM; ++i) acc[i][j] = gq_mfma32(af[ks & 1][i], bf, acc[i][j]);
+      }
+    }
+    // the register stage of this step is free: request step + 2 into it
+    load_rstep<FMT, NJ>(w, qo, so, s2, cur);
+    // the A tile of step + 1 (and the weights of step + 1) must have landed;
+    // the 3 NJ loads of step + 2 just issued may stay in flight
+    static_assert(3 * NJ <= 15, "vmcnt immediate");
+    __builtin_amdgcn_s_waitcnt(0x0F70 | (3 * NJ));
+    __syncthreads();
+  };
+
+  load_a_lds<BM, NW>(a16, lda, M, m0, 0, wave, lane, As_0);
+  load_rstep<FMT, NJ>(w, qo, so, 0, wst[0]);
+  load_rstep<FMT, NJ>(w, qo, so, nsteps > 1 ? 1 : 0, wst[1]);
+  __builtin_amdgcn_s_waitcnt(0x0F70);
+  __syncthreads();
+  for (int step = 0; step < nsteps; step += 2) {
+    run_step(step, B0{});
+    run_step(step + 1, B1{});
+  }
+
+#pragma unroll
+  for (int i = 0; i < TM; ++i)
+#pragma unroll
+    for (int j = 0; j < NJ; ++j) {
+      const int n = n0 + (BN / WN) * wn + 32 * j + (lane & 31);
+      if (n >= N) continue;
+#pragma unroll
+      for (int v = 0; v < 16; ++v) {
+        const int m = m0 + (BM / WM) * wm + 32 * i + 8 * (v >> 2) + 4 * (lane >> 5) + (v & 3);
         if (m < M) {
           if constexpr (CBF16)
             reinterpret_cast<uint16_t *>(c)[(size_t)m * N + n] = f32_to_bf16_rne(acc[i][j][v]);
@@ -428,21 +670,47 @@ int launch_cfg(const void *packed, const _Float16 *a16, int lda, void *c, int M,
   return gq_last_launch();
 }
 
-// Tile shape: the largest tile that still gives every CU a workgroup.
-int pick_tile(int M, int N) {
+template <int FMT, int CBF16, int BM, int BN, int WM, int WN>
+int launch_rb(const void *packed, const _Float16 *a16, int lda, void *c, int M, int N, int K, hipStream_t s) {
+  const int C = (int)gq_chunks(FMT, K);
+  const int nsteps = (int)(gq_kpad(FMT, K) / BK);
+  const int tiles_m = (M + BM - 1) / BM, tiles_n = (N + BN - 1) / BN;
+  hipLaunchKernelGGL((k_gemm_rb<FMT, CBF16, BM, BN, WM, WN>), dim3((unsigned)(tiles_m * tiles_n)), dim3(64 * WM * WN),
+                     0, s,
+                     (const uint8_t *)packed, (uint32_t)gq_sc_plane_offset(FMT, N, K), a16, lda, c, M, N, C, nsteps,
+                     tiles_m);
+  return gq_last_launch();
+}
+
+// Kernel and tile shape (measured on MI355X, M = 512 / 2048 x N = 4096 / 14336):
+//   0: register-B kernel, 256 x 256 (448 workgroups at 2048 x 14336)
+//   3: LDS-B kernel, 256 x 256 (Q4_K at that size: its per-fragment
+//      sub-block decoding costs more than the LDS round trip saves)
+//   4: register-B, 256 x 128, for >= 192 workgroups
+//   6: register-B, 128 x 128, smaller problems
+// 1, 2 (LDS-B 256 x 128, 128 x 128) and 5, 7, 8 (other register-B shapes)
+// are kept for tuning through GQ_GEMM_TILE.
+int pick_tile(int fmt, int M, int N) {
   auto wgs = [&](int bm, int bn) { return (long)((M + bm - 1) / bm) * ((N + bn - 1) / bn); };
   if (const char *e = getenv("GQ_GEMM_TILE")) return atoi(e);
-  if (wgs(256, 256) >= 256) return 0;
-  if (wgs(256, 128) >= 256) return 1;
-  return 2;
+  if (wgs(256, 256) >= 384) return fmt == GQ_FMT_Q4_K ? 3 : 0;
+  if (wgs(256, 128) >= 192) return 4;
+  return 6;
 }
 
 template <int FMT, int CBF16>
 int launch_fmt(const void *packed, const _Float16 *a16, int lda, void *c, int M, int N, int K, hipStream_t s) {
-  switch (pick_tile(M, N)) {
-  case 0: return launch_cfg<FMT, CBF16, 256, 256>(packed, a16, lda, c, M, N, K, s);
+  switch (pick_tile(FMT, M, N)) {
+  case 0: return launch_rb<FMT, CBF16, 256, 256, 2, 4>(packed, a16, lda, c, M, N, K, s);
+  case 4: return launch_rb<FMT, CBF16, 256, 128, 2, 4>(packed, a16, lda, c, M, N, K, s);
+  case 5: return launch_rb<FMT, CBF16, 128, 256, 2, 4>(packed, a16, lda, c, M, N, K, s);
+  case 6: return launch_rb<FMT, CBF16, 128, 128, 2, 4>(packed, a16, lda, c, M, N, K, s);
+  case 7: return launch_rb<FMT, CBF16, 128, 128, 2, 2>(packed, a16, lda, c, M, N, K, s);
+  case 8: return launch_rb<FMT, CBF16, 256, 128, 4, 2>(packed, a16, lda, c, M, N, K, s);
+  default: return launch_rb<FMT, CBF16, 128, 128, 2, 4>(packed, a16, lda, c, M, N, K, s);
+  case 3: return launch_cfg<FMT, CBF16, 256, 256>(packed, a16, lda, c, M, N, K, s);
   case 1: return launch_cfg<FMT, CBF16, 256, 128>(packed, a16, lda, c, M, N, K, s);
-  default: return launch_cfg<FMT, CBF16, 128, 128>(packed, a16, lda, c, M, N, K, s);
+  case 2: return launch_cfg<FMT, CBF16, 128, 128>(packed, a16, lda, c, M, N, K, s);
   }
 }
 

@@ -190,3 +190,20 @@ def test_compat_int8_int4_launchers(dev, m):
     y4 = gq.launch_int4_wt(_to_dev(x, dev), _to_dev(p4, dev), _to_dev(s4, dev), _to_dev(hs, dev), m, n, k,
                            head_dim=16).cpu().numpy()
     assert O.rel_l2(y4, ref4) <= 1e-5
+
+
+@pytest.mark.parametrize("tile", [0, 1, 2, 3, 4, 5, 6, 7, 8])
+@pytest.mark.parametrize("fmt", [O.Q4_0, O.Q8_0, O.Q4_K])
+def test_gemm_every_kernel_shape(dev, fmt, tile, monkeypatch):
+    """Each GEMM kernel / tile shape (forced through GQ_GEMM_TILE), on a shape
+    with partial tiles in M and N."""
+    import gq
+    import torch
+    monkeypatch.setenv("GQ_GEMM_TILE", str(tile))
+    m, n, k = 300, 400, 1024
+    w = O.gen_weights(fmt, n, k, seed=60 + tile)
+    a = torch.randn(m, k, generator=torch.Generator().manual_seed(tile)).to(torch.bfloat16)
+    ref = O.gemv(fmt, w, a.float().numpy(), n, k)
+    packed = _to_dev(gq.repack_host(fmt, w, n, k), dev)
+    c = gq.gemm(fmt, packed, a.to(dev), n, k).cpu().numpy()
+    assert O.rel_l2(c, ref) <= TOL
