@@ -105,6 +105,10 @@ int gq_repack_host(int fmt, const void *gguf, size_t N, size_t K, void *packed) 
         for (int eh = 0; eh < 2; ++eh) memcpy(dst + gq_q8_0_half_off(n, b, eh, C), blk + 2 + 16 * eh, 16);
         memcpy(dst + sc + gq_q4_0_d_off(n, b, C), blk, 2);
       }
+  } else if (gq_fmt_is_q6k(fmt)) {
+    const int ggml = fmt == GQ_FMT_Q6_K_GGML;
+    for (size_t n = 0; n < N; ++n)
+      for (size_t s = 0; s < C; ++s) gq_q6k_put(ggml, src + (n * C + s) * 210, dst, dst + sc, n, s, C);
   } else {
     const int ggml = fmt == GQ_FMT_Q4_K_GGML;
     const size_t S = C;
@@ -146,6 +150,10 @@ int gq_unpack_host(int fmt, const void *packed, size_t N, size_t K, void *gguf) 
         for (int eh = 0; eh < 2; ++eh) memcpy(blk + 2 + 16 * eh, src + gq_q8_0_half_off(n, b, eh, C), 16);
         memcpy(blk, src + sc + gq_q4_0_d_off(n, b, C), 2);
       }
+  } else if (gq_fmt_is_q6k(fmt)) {
+    const int ggml = fmt == GQ_FMT_Q6_K_GGML;
+    for (size_t n = 0; n < N; ++n)
+      for (size_t s = 0; s < C; ++s) gq_q6k_get(ggml, src, src + sc, n, s, C, dst + (n * C + s) * 210);
   } else {
     const int ggml = fmt == GQ_FMT_Q4_K_GGML;
     const size_t S = C;
@@ -168,6 +176,13 @@ int gq_unpack_host(int fmt, const void *packed, size_t N, size_t K, void *gguf) 
 int gq_matmul(int fmt, const void *packed, const float *a, float *c, size_t M, size_t N, size_t K, void *stream) {
   if (M >= 1 && M <= GQ_MAX_BATCH)
     return gq_gemv(fmt, packed, a, c, N, K, (int)M, nullptr, 0, stream);
+  if (gq_fmt_is_q6k(fmt)) {  // no Q6_K GEMM: batches of 16 rows through the GEMV
+    for (size_t m0 = 0; m0 < M; m0 += GQ_MAX_BATCH) {
+      const size_t mb = M - m0 < GQ_MAX_BATCH ? M - m0 : GQ_MAX_BATCH;
+      GQ_TRY(gq_gemv(fmt, packed, a + m0 * K, c + m0 * N, N, K, (int)mb, nullptr, 0, stream));
+    }
+    return GQ_OK;
+  }
   return gq_gemm(fmt, packed, a, GQ_DT_F32, c, GQ_DT_F32, M, N, K, nullptr, 0, stream);
 }
 

@@ -619,7 +619,7 @@ extern "C" int gq_gemv_plan(int fmt, size_t N, size_t K, int batch, int *R_out, 
                             int *chunks_per_wave_out) {
   GQ_TRY(gq_check_shape(fmt, N, K));
   GQ_CHECK(batch >= 1 && batch <= GQ_MAX_BATCH, GQ_ERR_UNSUPPORTED);
-  if (batch < gq_gemv_h_min()) return q_plan(fmt, N, K, batch, R_out, ksplit_out, chunks_per_wave_out);
+  if (batch < gq_gemv_h_min() && !gq_fmt_is_q6k(fmt)) return q_plan(fmt, N, K, batch, R_out, ksplit_out, chunks_per_wave_out);
   int R = 1, ks = 1, cpw = 0;
   GQ_TRY(gq_gemv_h_plan(fmt, N, K, &R, &ks, &cpw));
   if (R_out) *R_out = R;
@@ -676,13 +676,14 @@ int gq_gemv_h_min(void) {
 }
 
 extern "C" size_t gq_gemv_workspace_bytes(int fmt, size_t K, int batch) {
-  if (!gq_fmt_valid(fmt) || batch < 1 || batch > GQ_MAX_BATCH || K > GQ_MAX_DIM) return 0;
+  if (!gq_fmt_valid(fmt) || gq_fmt_is_q6k(fmt) || batch < 1 || batch > GQ_MAX_BATCH || K > GQ_MAX_DIM) return 0;
   return gq_xl_bytes(fmt, K, batch) + gq_scl_bytes(fmt, K, batch);
 }
 
 extern "C" int gq_gemv_prep(int fmt, const float *x, size_t K, int batch, void *ws, size_t ws_bytes,
                             void *stream) {
   GQ_TRY(gq_check_shape(fmt, 0, K));
+  GQ_CHECK(!gq_fmt_is_q6k(fmt), GQ_ERR_UNSUPPORTED);
   GQ_CHECK(batch >= 1 && batch <= GQ_MAX_BATCH, GQ_ERR_UNSUPPORTED);
   GQ_CHECK(x && ws, GQ_ERR_INVALID_ARGS);
   GQ_CHECK(ws_bytes >= gq_gemv_workspace_bytes(fmt, K, batch), GQ_ERR_WORKSPACE);
@@ -693,6 +694,7 @@ extern "C" int gq_gemv_prep(int fmt, const float *x, size_t K, int batch, void *
 extern "C" int gq_gemv_prepped(int fmt, const void *packed, const void *ws, float *y, size_t N, size_t K,
                                int batch, void *stream) {
   GQ_TRY(gq_check_shape(fmt, N, K));
+  GQ_CHECK(!gq_fmt_is_q6k(fmt), GQ_ERR_UNSUPPORTED);
   GQ_CHECK(batch >= 1 && batch <= GQ_MAX_BATCH, GQ_ERR_UNSUPPORTED);
   GQ_CHECK(packed && ws && y, GQ_ERR_INVALID_ARGS);
   if (N == 0) return GQ_OK;
@@ -708,7 +710,8 @@ extern "C" int gq_gemv(int fmt, const void *packed, const float *x, float *y, si
   GQ_CHECK(packed && x && y, GQ_ERR_INVALID_ARGS);
   if (N == 0) return GQ_OK;
   if (K == 0) return gq_fill_zero(y, N * batch, (hipStream_t)stream);
-  if (batch >= gq_gemv_h_min())
+  // wide batches, and Q6_K at every batch, run on the fp16 matrix-core kernel
+  if (batch >= gq_gemv_h_min() || gq_fmt_is_q6k(fmt))
     return gq_launch_gemv_h(fmt, packed, x, y, (int)N, (int)K, batch, (hipStream_t)stream);
   if (gq_gemv_fused(batch))
     return dispatch(gq_fmt_is_q4k(fmt) ? GQ_FMT_Q4_K : fmt, packed, x, nullptr, y, (int)N, (int)K, batch,
@@ -777,7 +780,7 @@ int launch_fused_fmt(int fmt, const GemvFuse &fz, size_t wgs, int ks, const floa
 extern "C" int gq_gemv_multi_plan(int fmt, int n_mats, const size_t *N, size_t K, int batch, int *R_out,
                                   int *ksplit_out, int *chunks_per_wave_out) {
   GQ_CHECK(n_mats >= 1 && n_mats <= 4 && N, GQ_ERR_INVALID_ARGS);
-  GQ_CHECK(batch >= 1 && batch <= 4, GQ_ERR_UNSUPPORTED);
+  GQ_CHECK(batch >= 1 && batch <= 4 && !gq_fmt_is_q6k(fmt), GQ_ERR_UNSUPPORTED);
   size_t tiles = 0;
   for (int i = 0; i < n_mats; ++i) {
     GQ_TRY(gq_check_shape(fmt, N[i], K));
@@ -817,7 +820,7 @@ extern "C" int gq_gemv_multi(int fmt, int n_mats, const void *const *packed, con
 extern "C" int gq_gemv_swiglu_plan(int fmt, size_t N, size_t K, int batch, int *ksplit_out,
                                    int *chunks_per_wave_out) {
   GQ_TRY(gq_check_shape(fmt, N, K));
-  GQ_CHECK(batch >= 1 && batch <= 4, GQ_ERR_UNSUPPORTED);
+  GQ_CHECK(batch >= 1 && batch <= 4 && !gq_fmt_is_q6k(fmt), GQ_ERR_UNSUPPORTED);
   const int C = (int)gq_chunks(fmt, K);
   const int ks = ks_for(fmt, gq_tiles(N), C, 2);
   GQ_CHECK(ks > 0, GQ_ERR_UNSUPPORTED);

@@ -35,6 +35,10 @@ template <>
 struct HFmt<GQ_FMT_Q4_K> {
   static constexpr int CK = 256, QB = 2048, SB = 256, STEPS = 4;
 };
+template <>
+struct HFmt<GQ_FMT_Q6_K> {
+  static constexpr int CK = 256, QB = 3072, SB = 288, STEPS = 4;
+};
 
 template <int FMT>
 struct HChunk;
@@ -53,6 +57,13 @@ struct HChunk<GQ_FMT_Q4_K> {
   gq_u4 qa, qb;
   gq_u4 meta;
 };
+template <>
+struct HChunk<GQ_FMT_Q6_K> {
+  gq_u4 qa, qb;  // low-nibble code groups, steps 0,1 and 2,3
+  gq_u4 hi;      // high 2-bit fields, one word per step
+  gq_u4 sc;      // the row's 16 int8 scales
+  uint32_t d;    // the row's fp16 d (low half)
+};
 
 template <int FMT>
 GQ_DEV void load_hchunk(const uint8_t *qp, const uint8_t *sp, uint32_t qo, uint32_t so, HChunk<FMT> &ch) {
@@ -63,10 +74,16 @@ GQ_DEV void load_hchunk(const uint8_t *qp, const uint8_t *sp, uint32_t qo, uint3
     ch.q0 = gq_ld16_nt(qp + qo);
     ch.q1 = gq_ld16_nt(qp + 1024 + qo);
     ch.d = gq_ld4_nt(sp + so);
-  } else {
+  } else if constexpr (FMT == GQ_FMT_Q4_K) {
     ch.qa = gq_ld16_nt(qp + qo);
     ch.qb = gq_ld16_nt(qp + 1024 + qo);
     ch.meta = gq_ld16_nt(sp + so);
+  } else {  // Q6_K: so = 16 r
+    ch.qa = gq_ld16_nt(qp + qo);
+    ch.qb = gq_ld16_nt(qp + 1024 + qo);
+    ch.hi = gq_ld16_nt(qp + 2048 + qo);
+    ch.sc = gq_ld16_nt(sp + so);
+    ch.d = gq_ld4_nt(sp + 256 + 4 * (so >> 5)) >> (16 * ((so >> 4) & 1));
   }
 }
 
@@ -79,12 +96,29 @@ GQ_DEV void magic4(uint32_t u, gq_half2 &lo, gq_half2 &hi) {
 GQ_DEV gq_half2 splat_h(uint32_t b16) { return gq_bits_h2((b16 & 0xFFFFu) * 0x10001u); }
 
 // The 16 weights a lane holds for MFMA step m -> fp16 B fragments (slots
-// 0..7, 8..15).  j is the lane's 32-block within the chunk.
+// 0..7, 8..15).  g is the lane's 16-lane group: its 16 weights are half g & 1
+// of 32-block 2 m + (g >> 1) of the chunk (Q6_K: 16-element scale group 4 m + g).
 template <int FMT>
-GQ_DEV void dequant_step(const HChunk<FMT> &c, int m, int j, gq_half8 &o0, gq_half8 &o1) {
+GQ_DEV void dequant_step(const HChunk<FMT> &c, int m, int g, gq_half8 &o0, gq_half8 &o1) {
+  const int j = 2 * m + (g >> 1);
   uint32_t regs[4];
   gq_half2 off, sc2, nsc2, d2, mn2;
-  if constexpr (FMT == GQ_FMT_Q4_0) {
+  if constexpr (FMT == GQ_FMT_Q6_K) {
+    const gq_u4 &q = (m < 2) ? c.qa : c.qb;
+    const uint32_t w0 = q[2 * (m & 1)], w1 = q[2 * (m & 1) + 1], hw = c.hi[m];
+    regs[0] = w0 & 0x0F0F0F0Fu;
+    regs[1] = (w0 >> 4) & 0x0F0F0F0Fu;
+    regs[2] = w1 & 0x0F0F0F0Fu;
+    regs[3] = (w1 >> 4) & 0x0F0F0F0Fu;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) regs[i] |= ((hw >> (2 * i)) & 0x03030303u) << 4;  // codes 0..63
+    // (c - 32) * (d * scale): the scale product rounded to fp16, then one
+    // rounding of the exact (c - 32) * that
+    const float sc = (float)(int8_t)((c.sc[m] >> (8 * g)) & 0xFFu);
+    const _Float16 hs = (_Float16)(gq_h2f(c.d & 0xFFFFu) * sc);
+    off = gq_half2{(_Float16)-1056.0f, (_Float16)-1056.0f};
+    d2 = gq_half2{hs, hs};
+  } else if constexpr (FMT == GQ_FMT_Q4_0) {
     const uint32_t w0 = c.q[2 * m], w1 = c.q[2 * m + 1];
     regs[0] = w0 & 0x0F0F0F0Fu;
     regs[1] = (w0 >> 4) & 0x0F0F0F0Fu;
@@ -123,7 +157,7 @@ GQ_DEV void dequant_step(const HChunk<FMT> &c, int m, int j, gq_half8 &o0, gq_ha
     magic4(regs[q], lo, hi);
     if constexpr (FMT == GQ_FMT_Q4_K) {
       // (1024 + c) * sc - 1024 sc = c * sc exactly, then one rounding of
-      // c * sc * d - dmin * m
+      // c * sc * d - dmin * m (magic4 of a 6-bit Q6_K code is 1024 + c too)
       lo = __builtin_elementwise_fma(__builtin_elementwise_fma(lo, sc2, nsc2), d2, mn2);
       hi = __builtin_elementwise_fma(__builtin_elementwise_fma(hi, sc2, nsc2), d2, mn2);
     } else {
@@ -175,7 +209,8 @@ k_gemv_h(const uint8_t *__restrict__ w, size_t sc_off, const float *__restrict__
   const size_t tb = (tile < (size_t)ntiles ? tile : (size_t)ntiles - 1) * (size_t)C;
   const int c0 = (C * part) / KS, c1 = (C * (part + 1)) / KS;  // this wave's chunks (c0 < c1: KS <= C)
   const uint32_t qlane = 16u * (uint32_t)lane;
-  const uint32_t slane = (FMT == GQ_FMT_Q4_K) ? 16u * (uint32_t)r : 8u * (uint32_t)r + 4u * (uint32_t)(g >> 1);
+  const uint32_t slane = (FMT == GQ_FMT_Q4_K || FMT == GQ_FMT_Q6_K) ? 16u * (uint32_t)r
+                                                                    : 8u * (uint32_t)r + 4u * (uint32_t)(g >> 1);
 
   // weights of window `it` (chunks past the part re-read its last chunk)
   auto load_win = [&](int it, HChunk<FMT> (&ch)[WC]) {
@@ -259,7 +294,7 @@ k_gemv_h(const uint8_t *__restrict__ w, size_t sc_off, const float *__restrict__
             const gq_half8 a0 = *reinterpret_cast<const gq_half8 *>(xb + ((ms * 2 + 0) * 64 + lane) * 16);
             const gq_half8 a1 = *reinterpret_cast<const gq_half8 *>(xb + ((ms * 2 + 1) * 64 + lane) * 16);
             gq_half8 b0, b1;
-            dequant_step<FMT>(w0[j], m, 2 * m + (g >> 1), b0, b1);
+            dequant_step<FMT>(w0[j], m, g, b0, b1);
             acc = mfma16h(a0, b0, acc);
             acc = mfma16h(a1, b1, acc);
           }
@@ -323,7 +358,7 @@ int env_int(const char *name) {
 // per chunk and at most 16 waves per workgroup.  chunks_per_wave is the
 // longest part.
 int gq_gemv_h_plan(int fmt, size_t N, size_t K, int *R_out, int *ks_out, int *cpw_out) {
-  const int f = gq_fmt_is_q4k(fmt) ? GQ_FMT_Q4_K : fmt;
+  const int f = gq_fmt_is_q4k(fmt) ? GQ_FMT_Q4_K : gq_fmt_is_q6k(fmt) ? GQ_FMT_Q6_K : fmt;
   const int C = (int)gq_chunks(f, K);
   const size_t tiles = gq_tiles(N);
   int tw = tiles >= 800 ? 4 : tiles >= 400 ? 2 : 1;
@@ -376,6 +411,7 @@ int launch_h(const void *packed, const float *x, float *y, int N, int K, int nb,
 }  // namespace
 
 int gq_launch_gemv_h(int fmt, const void *packed, const float *x, float *y, int N, int K, int nb, hipStream_t s) {
+  if (gq_fmt_is_q6k(fmt)) return launch_h<GQ_FMT_Q6_K>(packed, x, y, N, K, nb, s);
   switch (gq_fmt_is_q4k(fmt) ? GQ_FMT_Q4_K : fmt) {
   case GQ_FMT_Q4_0: return launch_h<GQ_FMT_Q4_0>(packed, x, y, N, K, nb, s);
   case GQ_FMT_Q8_0: return launch_h<GQ_FMT_Q8_0>(packed, x, y, N, K, nb, s);

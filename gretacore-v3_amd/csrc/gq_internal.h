@@ -54,7 +54,7 @@ int gq_gemv_h_plan(int fmt, size_t N, size_t K, int *R_out, int *ks_out, int *cp
 int gq_launch_gemv_h(int fmt, const void *packed, const float *x, float *y, int N, int K, int nb, hipStream_t s);
 
 // load-time conversions (gq_loadconv.hip)
-int gq_launch_dequant_q6_k(const void *blocks, size_t n_blocks, float *out, hipStream_t s);
+int gq_launch_dequant_q6_k(const void *blocks, size_t n_blocks, float *out, int ggml, hipStream_t s);
 int gq_launch_f16_to_f32(const void *in, size_t n, float *out, hipStream_t s);
 
 // Library-owned per-device workspace (grown on demand, never shrunk).

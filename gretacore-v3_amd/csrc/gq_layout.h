@@ -32,9 +32,16 @@
 //              byte i of W1 = sc[2i]   | (m[2i]   & 3) << 6
 //              byte i of W2 = sc[2i+1] | (m[2i+1] & 3) << 6
 //              byte i of W3 = (m[2i] >> 2) | (m[2i+1] >> 2) << 4   256 B/chunk
+//  Q6_K: chunk = 1 super-block (256 k).  Codes c = low 4 bits | high 2 bits << 4.
+//    qs plane  [tile][S] 3072 B: the low nibbles as Q4_K code groups (2048 B),
+//              then per lane and MFMA step the 16 high 2-bit fields in one word
+//              [64 lanes][4 steps][4 B]: byte b holds, at bits 2q..2q+1, the
+//              high bits of slot 4q + b (the slot whose low nibble the Q4 code
+//              group extraction puts in byte b of word q)
+//    scale plane [tile][S] 288 B: [16 rows][16 x int8 scale] then [16 rows][fp16 d]
 // Padding blocks (K not a multiple of 128 for Q4_0/Q8_0) carry d = 0 and zero
 // codes, so they add exact zeros.  Bytes per weight are unchanged by the
-// repack: 0.5625 (Q4_0, Q4_K) and 1.0625 (Q8_0).
+// repack: 0.5625 (Q4_0, Q4_K), 1.0625 (Q8_0) and 0.8203 (Q6_K).
 #ifndef GQ_LAYOUT_H
 #define GQ_LAYOUT_H
 #include <stddef.h>
@@ -48,29 +55,38 @@
 
 #define GQ_TILE_ROWS 16
 
-// Format ids: the GGML type ids (weight_loader.cpp:15-33), plus one id for the
-// llama.cpp canonical Q4_K layout.
+// Format ids: the GGML type ids (weight_loader.cpp:15-33), plus one id each for
+// the llama.cpp canonical Q4_K and Q6_K layouts.
 #define GQ_FMT_Q4_0 2
 #define GQ_FMT_Q8_0 8
 #define GQ_FMT_Q4_K 12
+#define GQ_FMT_Q6_K 14
 #define GQ_FMT_Q4_K_GGML 112
+#define GQ_FMT_Q6_K_GGML 114
 
-GQ_LHD int gq_fmt_valid(int fmt) {
-  return fmt == GQ_FMT_Q4_0 || fmt == GQ_FMT_Q8_0 || fmt == GQ_FMT_Q4_K ||
-         fmt == GQ_FMT_Q4_K_GGML;
-}
 GQ_LHD int gq_fmt_is_q4k(int fmt) {
   return fmt == GQ_FMT_Q4_K || fmt == GQ_FMT_Q4_K_GGML;
 }
-GQ_LHD size_t gq_block_elems(int fmt) { return gq_fmt_is_q4k(fmt) ? 256 : 32; }
+GQ_LHD int gq_fmt_is_q6k(int fmt) {
+  return fmt == GQ_FMT_Q6_K || fmt == GQ_FMT_Q6_K_GGML;
+}
+// formats with a T16 layout (repack, dequant of packed data, GEMV)
+GQ_LHD int gq_fmt_valid(int fmt) {
+  return fmt == GQ_FMT_Q4_0 || fmt == GQ_FMT_Q8_0 || gq_fmt_is_q4k(fmt) || gq_fmt_is_q6k(fmt);
+}
+GQ_LHD size_t gq_block_elems(int fmt) { return (gq_fmt_is_q4k(fmt) || gq_fmt_is_q6k(fmt)) ? 256 : 32; }
 GQ_LHD size_t gq_block_bytes(int fmt) {
-  return fmt == GQ_FMT_Q4_0 ? 18 : fmt == GQ_FMT_Q8_0 ? 34 : 144;
+  return fmt == GQ_FMT_Q4_0 ? 18 : fmt == GQ_FMT_Q8_0 ? 34 : gq_fmt_is_q6k(fmt) ? 210 : 144;
 }
 // k elements per T16 chunk
-GQ_LHD size_t gq_chunk_k(int fmt) { return gq_fmt_is_q4k(fmt) ? 256 : 128; }
+GQ_LHD size_t gq_chunk_k(int fmt) { return (gq_fmt_is_q4k(fmt) || gq_fmt_is_q6k(fmt)) ? 256 : 128; }
 // bytes of the qs plane and of the scale plane per (tile, chunk)
-GQ_LHD size_t gq_chunk_qs_bytes(int fmt) { return fmt == GQ_FMT_Q4_0 ? 1024 : 2048; }
-GQ_LHD size_t gq_chunk_sc_bytes(int fmt) { return gq_fmt_is_q4k(fmt) ? 256 : 128; }
+GQ_LHD size_t gq_chunk_qs_bytes(int fmt) {
+  return fmt == GQ_FMT_Q4_0 ? 1024 : gq_fmt_is_q6k(fmt) ? 3072 : 2048;
+}
+GQ_LHD size_t gq_chunk_sc_bytes(int fmt) {
+  return gq_fmt_is_q4k(fmt) ? 256 : gq_fmt_is_q6k(fmt) ? 288 : 128;
+}
 
 GQ_LHD size_t gq_tiles(size_t N) { return (N + GQ_TILE_ROWS - 1) / GQ_TILE_ROWS; }
 GQ_LHD size_t gq_chunks(int fmt, size_t K) {

@@ -46,10 +46,11 @@ __global__ void __launch_bounds__(256) k_f32_to_f16_trunc(const float *__restric
 
 // One thread per 16 outputs (one int8 scale) of a 210-byte Q6_K block:
 // ql[128] | qh[64] | int8 scales[16] | fp16 d; element i takes 4 low bits from
-// ql[i/2] (nibble i%2) and 2 high bits from qh[i/4] (pair i%4);
-// w = (d * (q - 32)) * scales[i/16], each product rounded.
+// ql[i/2] (nibble i%2) and 2 high bits from qh[i/4] (pair i%4) in the
+// reference layout (ggml: gq_q6k_locate); w = (d * (q - 32)) * scales[i/16],
+// each product rounded.
 __global__ void __launch_bounds__(256) k_dequant_q6_k(const uint8_t *__restrict__ src, float *__restrict__ out,
-                                                      size_t ngrp) {
+                                                      size_t ngrp, int ggml) {
   size_t t = (size_t)blockIdx.x * 256 + threadIdx.x;
   if (t >= ngrp) return;
   const uint8_t *b = src + (t >> 4) * 210;
@@ -60,9 +61,7 @@ __global__ void __launch_bounds__(256) k_dequant_q6_k(const uint8_t *__restrict_
 #pragma unroll
   for (int e = 0; e < 16; ++e) {
     const int i = 16 * g + e;
-    const int lo = (b[i >> 1] >> ((i & 1) * 4)) & 0x0F;
-    const int hi = (b[128 + (i >> 2)] >> ((i & 3) * 2)) & 0x03;
-    const float p = d * (float)((lo | (hi << 4)) - 32);
+    const float p = d * (float)((int)gq_q6k_code(ggml, b, i) - 32);
     y[e] = p * sc;
   }
   float4 *o = reinterpret_cast<float4 *>(out + t * 16);
@@ -168,9 +167,9 @@ __global__ void __launch_bounds__(256) k_split_q8_0(const uint8_t *__restrict__ 
 
 }  // namespace
 
-int gq_launch_dequant_q6_k(const void *blocks, size_t n_blocks, float *out, hipStream_t s) {
+int gq_launch_dequant_q6_k(const void *blocks, size_t n_blocks, float *out, int ggml, hipStream_t s) {
   hipLaunchKernelGGL(k_dequant_q6_k, dim3(grid_for(n_blocks * 16)), dim3(256), 0, s, (const uint8_t *)blocks, out,
-                     n_blocks * 16);
+                     n_blocks * 16, ggml);
   return gq_last_launch();
 }
 

@@ -6,6 +6,7 @@
 //         difference rounded separately -> contraction is disabled below)
 //   Q8_0  weight_loader.cpp:703-712 + gemm_kernels.hip:612-616: (float)q * d
 //   Q4_0  GGUF spec (no reference implementation): (float)(q - 8) * d
+//   Q6_K  weight_loader.cpp:158-177: (d * (c - 32)) * scale
 //   fp16  weight_loader.cpp:91-110 (NaN -> Inf)
 #include "gq_internal.h"
 
@@ -104,6 +105,24 @@ k_dequant_t16(int fmt, const uint8_t *__restrict__ w, float *__restrict__ out, i
 #pragma unroll
       for (int s = 0; s < 16; ++s) y[16 * eh + s] = (float)q[s] * d;
     }
+  } else if (fmt == GQ_FMT_Q6_K) {
+    // (d * (c - 32)) * scale, as weight_loader.cpp:158-177 rounds it
+    size_t s = blk >> 3;
+    int j = (int)(blk & 7);
+    const float d = gq_h2f(gq_rd16(scp + gq_q6k_d_off(n, s, C)));
+    const int8_t *scl = reinterpret_cast<const int8_t *>(scp + gq_q6k_sc_off(n, s, C));
+#pragma unroll
+    for (int eh = 0; eh < 2; ++eh) {
+      uint8_t c[16];
+      gq_unpack_codes16(*reinterpret_cast<const uint64_t *>(w + gq_q6k_grp_off(n, s, j, eh, C)), c);
+      const uint32_t hw = *reinterpret_cast<const uint32_t *>(w + gq_q6k_hi_off(n, s, j, eh, C));
+      const float sc = (float)scl[2 * j + eh];
+#pragma unroll
+      for (int e = 0; e < 16; ++e) {
+        const float p = d * (float)((int)(c[e] | (gq_q6k_hi_of(hw, e) << 4)) - 32);
+        y[16 * eh + e] = p * sc;
+      }
+    }
   } else {
     size_t s = blk >> 3;
     int j = (int)(blk & 7);
@@ -188,6 +207,17 @@ k_repack_q4_k(const uint8_t *__restrict__ src, uint8_t *__restrict__ dst, int N,
       *reinterpret_cast<uint64_t *>(dst + gq_q4k_grp_off(n, s, j, eh, S)) = grp[2 * j + eh];
   *reinterpret_cast<gq_u4 *>(dst + gq_sc_plane_offset(GQ_FMT_Q4_K, N, K) + gq_q4k_meta_off(n, s, S)) =
       gq_u4{meta[0], meta[1], meta[2], meta[3]};
+}
+
+// one thread per (padded row, super-block)
+__global__ void __launch_bounds__(256)
+k_repack_q6_k(const uint8_t *__restrict__ src, uint8_t *__restrict__ dst, int N, int K, int ggml) {
+  size_t S = gq_chunks(GQ_FMT_Q6_K, K), Np = gq_tiles(N) * 16;
+  size_t i = (size_t)blockIdx.x * 256 + threadIdx.x;
+  if (i >= Np * S) return;
+  size_t n = i / S, s = i % S;
+  gq_q6k_put(ggml, n < (size_t)N ? src + (n * S + s) * 210 : nullptr, dst,
+             dst + gq_sc_plane_offset(GQ_FMT_Q6_K, N, K), n, s, S);
 }
 
 // ---------------------------------------------------------------------------
@@ -301,12 +331,12 @@ k_quantize_act_q8(const void *__restrict__ a, int a_dtype, int8_t *__restrict__ 
 static unsigned blocks_for(size_t n) { return (unsigned)((n + 255) / 256); }
 
 extern "C" int gq_dequant_gguf(int fmt, const void *blocks, size_t n_blocks, float *out, void *stream) {
-  GQ_CHECK(gq_fmt_valid(fmt) || fmt == GQ_FMT_F16 || fmt == GQ_FMT_Q6_K, GQ_ERR_UNSUPPORTED);
+  GQ_CHECK(gq_fmt_valid(fmt) || fmt == GQ_FMT_F16, GQ_ERR_UNSUPPORTED);
   GQ_CHECK(blocks && out, GQ_ERR_INVALID_ARGS);
   if (n_blocks == 0) return GQ_OK;
   hipStream_t s = (hipStream_t)stream;
   if (fmt == GQ_FMT_F16) return gq_launch_f16_to_f32(blocks, n_blocks, out, s);
-  if (fmt == GQ_FMT_Q6_K) return gq_launch_dequant_q6_k(blocks, n_blocks, out, s);
+  if (gq_fmt_is_q6k(fmt)) return gq_launch_dequant_q6_k(blocks, n_blocks, out, fmt == GQ_FMT_Q6_K_GGML, s);
   const uint8_t *src = (const uint8_t *)blocks;
   if (fmt == GQ_FMT_Q4_0)
     hipLaunchKernelGGL(k_dequant_q4_0, dim3(blocks_for(n_blocks)), dim3(256), 0, s, src, out, n_blocks);
@@ -322,7 +352,7 @@ extern "C" int gq_dequant_packed(int fmt, const void *packed, size_t N, size_t K
   GQ_TRY(gq_check_shape(fmt, N, K));
   GQ_CHECK(packed && out, GQ_ERR_INVALID_ARGS);
   if (N == 0 || K == 0) return GQ_OK;
-  int f = gq_fmt_is_q4k(fmt) ? GQ_FMT_Q4_K : fmt;
+  int f = gq_fmt_is_q4k(fmt) ? GQ_FMT_Q4_K : gq_fmt_is_q6k(fmt) ? GQ_FMT_Q6_K : fmt;
   hipLaunchKernelGGL(k_dequant_t16, dim3(blocks_for(N * (K / 32))), dim3(256), 0, (hipStream_t)stream, f,
                      (const uint8_t *)packed, out, (int)N, (int)K);
   return gq_last_launch();
@@ -340,6 +370,9 @@ extern "C" int gq_repack(int fmt, const void *gguf, size_t N, size_t K, void *pa
     hipLaunchKernelGGL(k_repack_q4_0, dim3(blocks_for(Np * C * 4)), dim3(256), 0, s, src, dst, (int)N, (int)K);
   else if (fmt == GQ_FMT_Q8_0)
     hipLaunchKernelGGL(k_repack_q8_0, dim3(blocks_for(Np * C * 4)), dim3(256), 0, s, src, dst, (int)N, (int)K);
+  else if (gq_fmt_is_q6k(fmt))
+    hipLaunchKernelGGL(k_repack_q6_k, dim3(blocks_for(Np * C)), dim3(256), 0, s, src, dst, (int)N, (int)K,
+                       (int)(fmt == GQ_FMT_Q6_K_GGML));
   else
     hipLaunchKernelGGL(k_repack_q4_k, dim3(blocks_for(Np * C)), dim3(256), 0, s, src, dst, (int)N, (int)K,
                        (int)(fmt == GQ_FMT_Q4_K_GGML));

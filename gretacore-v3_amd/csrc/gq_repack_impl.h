@@ -185,6 +185,48 @@ GQ_HD void gq_q4k_from_groups(int ggml, const uint64_t grp[16], const uint32_t m
     }
 }
 
+// ---- Q6_K ----------------------------------------------------------------
+// Block: ql[128] | qh[64] | int8 scales[16] | fp16 d; code c = low 4 | high 2 << 4,
+// value (d * (c - 32)) * scales[i / 16] (scales in element order in both layouts).
+// Reference (GRETA) layout, weight_loader.cpp:158-177: element i takes its low
+// bits from ql[i/2] (nibble i%2) and its high bits from qh[i/4] (pair i%4).
+// llama.cpp layout (dequantize_row_q6_K): per 128-element half h, l in 0..31,
+// elements 128h + 32k + l take ql[64h + l + 32 (k & 1)] (nibble k >> 1) and
+// qh[32h + l] (pair k).
+GQ_HD void gq_q6k_locate(int ggml, int i, int *li, int *ls, int *hi, int *hs) {
+  if (!ggml) {
+    *li = i >> 1;
+    *ls = 4 * (i & 1);
+    *hi = 128 + (i >> 2);
+    *hs = 2 * (i & 3);
+  } else {
+    const int h = i >> 7, k = (i >> 5) & 3, l = i & 31;
+    *li = 64 * h + l + 32 * (k & 1);
+    *ls = 4 * (k >> 1);
+    *hi = 128 + 32 * h + l;
+    *hs = 2 * k;
+  }
+}
+GQ_HD uint32_t gq_q6k_code(int ggml, const uint8_t *blk, int i) {
+  int li, ls, hi, hs;
+  gq_q6k_locate(ggml, i, &li, &ls, &hi, &hs);
+  return ((blk[li] >> ls) & 15u) | (((blk[hi] >> hs) & 3u) << 4);
+}
+GQ_HD void gq_q6k_set_code(int ggml, uint8_t *blk, int i, uint32_t c) {
+  int li, ls, hi, hs;
+  gq_q6k_locate(ggml, i, &li, &ls, &hi, &hs);
+  blk[li] = (uint8_t)((blk[li] & ~(15u << ls)) | ((c & 15u) << ls));
+  blk[hi] = (uint8_t)((blk[hi] & ~(3u << hs)) | (((c >> 4) & 3u) << hs));
+}
+// The 16 high 2-bit fields of a lane's 16 slots as one word: byte b holds slot
+// 4q + b at bits 2q .. 2q+1.
+GQ_HD uint32_t gq_q6k_pack_hi(const uint8_t codes[16]) {
+  uint32_t w = 0;
+  for (int s = 0; s < 16; ++s) w |= (uint32_t)((codes[s] >> 4) & 3u) << (8 * (s & 3) + 2 * (s >> 2));
+  return w;
+}
+GQ_HD uint32_t gq_q6k_hi_of(uint32_t w, int s) { return (w >> (8 * (s & 3) + 2 * (s >> 2))) & 3u; }
+
 // ---- addressing in the T16 layout ---------------------------------------
 // Within a chunk of a 16-row tile, lane l = 16*g + r (row r) holds, for the
 // int8 MFMA pair m, the 16 elements 16*(g&1) .. +15 of (sub-)block 2m + (g>>1).
@@ -218,4 +260,65 @@ GQ_HD size_t gq_q4k_grp_off(size_t n, size_t s, int j, int eh, size_t S) {
 GQ_HD size_t gq_q4k_meta_off(size_t n, size_t s, size_t S) {
   size_t t = n >> 4, r = n & 15;
   return (t * S + s) * 256 + 16 * r;
+}
+// Q6_K: code group of the low nibbles (sub-block j, half eh) of super-block s
+// of row n (8 bytes), the high-bit word of the same 16 slots (4 bytes), and
+// the row's scales (16 bytes) and d (2 bytes) in the scale plane.
+GQ_HD size_t gq_q6k_grp_off(size_t n, size_t s, int j, int eh, size_t S) {
+  size_t t = n >> 4, r = n & 15;
+  size_t m = (size_t)j >> 1, g = 2 * ((size_t)j & 1) + (size_t)eh;
+  return (t * S + s) * 3072 + ((m >> 1) << 10) + 16 * (16 * g + r) + 8 * (m & 1);
+}
+GQ_HD size_t gq_q6k_hi_off(size_t n, size_t s, int j, int eh, size_t S) {
+  size_t t = n >> 4, r = n & 15;
+  size_t m = (size_t)j >> 1, g = 2 * ((size_t)j & 1) + (size_t)eh;
+  return (t * S + s) * 3072 + 2048 + 16 * (16 * g + r) + 4 * m;
+}
+GQ_HD size_t gq_q6k_sc_off(size_t n, size_t s, size_t S) {
+  size_t t = n >> 4, r = n & 15;
+  return (t * S + s) * 288 + 16 * r;
+}
+GQ_HD size_t gq_q6k_d_off(size_t n, size_t s, size_t S) {
+  size_t t = n >> 4, r = n & 15;
+  return (t * S + s) * 288 + 256 + 2 * r;
+}
+// GGUF Q6_K super-block of row n -> its T16 places (packed: the whole tensor,
+// sc: its scale plane).  Writes every byte it owns, zeros for a null block.
+GQ_HD void gq_q6k_put(int ggml, const uint8_t *blk, uint8_t *packed, uint8_t *sc, size_t n, size_t s, size_t S) {
+  for (int j = 0; j < 8; ++j)
+    for (int eh = 0; eh < 2; ++eh) {
+      uint8_t c[16];
+      for (int e = 0; e < 16; ++e) c[e] = blk ? (uint8_t)gq_q6k_code(ggml, blk, 32 * j + 16 * eh + e) : 0;
+      const uint64_t g = gq_pack_codes16(c);
+      uint8_t *gp = packed + gq_q6k_grp_off(n, s, j, eh, S);
+      for (int b = 0; b < 8; ++b) gp[b] = (uint8_t)(g >> (8 * b));
+      const uint32_t h = gq_q6k_pack_hi(c);
+      uint8_t *hp = packed + gq_q6k_hi_off(n, s, j, eh, S);
+      for (int b = 0; b < 4; ++b) hp[b] = (uint8_t)(h >> (8 * b));
+    }
+  uint8_t *sp = sc + gq_q6k_sc_off(n, s, S);
+  for (int i = 0; i < 16; ++i) sp[i] = blk ? blk[192 + i] : 0;
+  uint8_t *dp = sc + gq_q6k_d_off(n, s, S);
+  dp[0] = blk ? blk[208] : 0;
+  dp[1] = blk ? blk[209] : 0;
+}
+// T16 -> GGUF Q6_K super-block (inverse of gq_q6k_put)
+GQ_HD void gq_q6k_get(int ggml, const uint8_t *packed, const uint8_t *sc, size_t n, size_t s, size_t S, uint8_t *blk) {
+  for (int i = 0; i < 210; ++i) blk[i] = 0;
+  for (int j = 0; j < 8; ++j)
+    for (int eh = 0; eh < 2; ++eh) {
+      const uint8_t *gp = packed + gq_q6k_grp_off(n, s, j, eh, S);
+      uint64_t g = 0;
+      for (int b = 0; b < 8; ++b) g |= (uint64_t)gp[b] << (8 * b);
+      const uint8_t *hp = packed + gq_q6k_hi_off(n, s, j, eh, S);
+      const uint32_t h = (uint32_t)hp[0] | ((uint32_t)hp[1] << 8) | ((uint32_t)hp[2] << 16) | ((uint32_t)hp[3] << 24);
+      uint8_t c[16];
+      gq_unpack_codes16(g, c);
+      for (int e = 0; e < 16; ++e) gq_q6k_set_code(ggml, blk, 32 * j + 16 * eh + e, c[e] | (gq_q6k_hi_of(h, e) << 4));
+    }
+  const uint8_t *sp = sc + gq_q6k_sc_off(n, s, S);
+  for (int i = 0; i < 16; ++i) blk[192 + i] = sp[i];
+  const uint8_t *dp = sc + gq_q6k_d_off(n, s, S);
+  blk[208] = dp[0];
+  blk[209] = dp[1];
 }

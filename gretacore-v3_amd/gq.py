@@ -18,8 +18,10 @@ FMT_Q8_0 = 8
 FMT_Q4_K = 12
 FMT_Q4_K_GGML = 112
 FMT_F16 = 1    # gq_dequant_gguf only
-FMT_Q6_K = 14  # gq_dequant_gguf only
-FORMATS = {"q4_0": FMT_Q4_0, "q8_0": FMT_Q8_0, "q4_k": FMT_Q4_K, "q4_k_ggml": FMT_Q4_K_GGML}
+FMT_Q6_K = 14  # repack / dequant / gemv (no gemm)
+FMT_Q6_K_GGML = 114
+FORMATS = {"q4_0": FMT_Q4_0, "q8_0": FMT_Q8_0, "q4_k": FMT_Q4_K, "q4_k_ggml": FMT_Q4_K_GGML, "q6_k": FMT_Q6_K,
+           "q6_k_ggml": FMT_Q6_K_GGML}
 
 DT_F32, DT_F16, DT_BF16 = 0, 1, 2
 MAX_BATCH = 16
@@ -182,7 +184,7 @@ def repack(fmt: int, d_gguf, n: int, k: int, stream=None):
 def dequant_gguf(fmt: int, d_blocks, n_blocks: int, stream=None):
     import torch
     _require_device(d_blocks)
-    per = 256 if fmt in (FMT_Q4_K, FMT_Q4_K_GGML, FMT_Q6_K) else (1 if fmt == FMT_F16 else 32)
+    per = 256 if fmt in (FMT_Q4_K, FMT_Q4_K_GGML, FMT_Q6_K, FMT_Q6_K_GGML) else (1 if fmt == FMT_F16 else 32)
     out = torch.empty(n_blocks * per, dtype=torch.float32, device=d_blocks.device)
     check(load().gq_dequant_gguf(fmt, _ptr(d_blocks), n_blocks, _ptr(out), _stream(stream)), "gq_dequant_gguf")
     return out

@@ -65,9 +65,9 @@ public:
   // Q4_K_GGML), quant_info().format the GGML type id.  N = shape[1] rows,
   // K = shape[0].
   bool load_tensor_quant(const std::string &name, gcore::rt::hip::Buffer &packed, std::string *err);
-  // Q4_K code layout of this file: false (default) = the reference's layout
-  // (weight_loader.cpp:125-156), true = llama.cpp's.  GQ_Q4K_LAYOUT=ggml in the
-  // environment sets true at open().
+  // k-quant code layouts of this file (Q4_K and Q6_K): false (default) = the
+  // reference's layouts (weight_loader.cpp:125-177), true = llama.cpp's.
+  // GQ_Q4K_LAYOUT=ggml in the environment sets true at open().
   void set_q4k_layout_ggml(bool ggml);
   // Raw tensor bytes (no GPU).
   bool read_raw(const std::string &name, std::vector<uint8_t> &out, std::string *err) const;

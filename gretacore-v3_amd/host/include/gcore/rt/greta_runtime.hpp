@@ -2,7 +2,7 @@
 // Runtime boundary types of the quantized-weight matrix path, with the names
 // and meaning of the reference's L0 interface
 // (src/rt/include/gcore/rt/greta_runtime.hpp:16-97).  Additions are appended
-// only: enum values Q4_0 / Q8_0 / Q4_K_GGML for GGUF-native T16 weights and the
+// only: enum values Q4_0 / Q8_0 / Q4_K_GGML / Q6_K / Q6_K_GGML for GGUF-native T16 weights and the
 // `format` field of GretaQuantInfo (the GGML type id of such weights).
 #include <cstddef>
 #include <cstdint>
@@ -34,6 +34,8 @@ enum class GretaDataType {
   Q4_0 = 8,
   Q8_0 = 9,
   Q4_K_GGML = 10,
+  Q6_K = 11,
+  Q6_K_GGML = 12,
 };
 
 struct GretaQuantInfo {

@@ -8,7 +8,7 @@
 //     per-head scales unless GRETA_PERHEAD_QKV is set to something other than
 //     "1" (:161-163), and force_gemv from the op label and the GRETA_PREFILL_* /
 //     GRETA_WO_LAYOUT_FORCE flags (:316-352).
-//   * B GGUF-native (Q4_0 / Q8_0 / Q4_K / Q4_K_GGML, T16 layout) -> gq_matmul:
+//   * B GGUF-native (Q4_0 / Q8_0 / Q4_K / Q4_K_GGML / Q6_K / Q6_K_GGML, T16 layout) -> gq_matmul:
 //     GEMV kernels for M <= 16, the MFMA GEMM above (added by this library).
 // Unlike the reference (which always returns SUCCESS), launch failures and
 // unsupported operands are reported.
@@ -70,6 +70,8 @@ int gguf_format(const gcore::rt::GretaMemory *B) {
   case GretaDataType::Q8_0: return GQ_FMT_Q8_0;
   case GretaDataType::Q4_K: return GQ_FMT_Q4_K;
   case GretaDataType::Q4_K_GGML: return GQ_FMT_Q4_K_GGML;
+  case GretaDataType::Q6_K: return GQ_FMT_Q6_K;
+  case GretaDataType::Q6_K_GGML: return GQ_FMT_Q6_K_GGML;
   default: return 0;
   }
 }
@@ -131,7 +133,9 @@ GretaResult GretaCompute::gemm(GretaStream *stream, GretaMemory *A, GretaMemory 
   case GretaDataType::Q4_0:
   case GretaDataType::Q8_0:
   case GretaDataType::Q4_K:
-  case GretaDataType::Q4_K_GGML: {
+  case GretaDataType::Q4_K_GGML:
+  case GretaDataType::Q6_K:
+  case GretaDataType::Q6_K_GGML: {
     const int fmt = gguf_format(B);
     size_t need = 0;
     if (gq_packed_size(fmt, N, K, &need) != GQ_OK || B->size() < need) return GretaResult::ERROR_INVALID_ARGS;
@@ -148,6 +152,13 @@ GretaResult GretaCompute::gemm(GretaStream *stream, GretaMemory *A, GretaMemory 
       case GretaDataType::FP16: adt = GQ_DT_F16; break;
       case GretaDataType::BF16: adt = GQ_DT_BF16; break;
       default: return GretaResult::ERROR_INVALID_ARGS;
+      }
+      if (fmt == GQ_FMT_Q6_K || fmt == GQ_FMT_Q6_K_GGML) {  // no Q6_K GEMM: GEMVs over 16-row batches (fp32 A)
+        if (adt != GQ_DT_F32) return GretaResult::ERROR_INVALID_ARGS;
+        audit.route = "GEMV";
+        st = gq_matmul(fmt, B->data(), static_cast<const float *>(A->data()), static_cast<float *>(C->data()), M, N,
+                       K, s);
+        break;
       }
       audit.route = "GEMM";
       st = gq_gemm(fmt, B->data(), A->data(), adt, C->data(), GQ_DT_F32, M, N, K, nullptr, 0, s);

@@ -354,6 +354,8 @@ struct GGUFLoader::Impl {
   }
 
   int q4k_fmt() const { return q4k_ggml ? GQ_FMT_Q4_K_GGML : GQ_FMT_Q4_K; }
+  // the k-quant layout flag covers Q6_K too (a file uses one family of layouts)
+  int q6k_fmt() const { return q4k_ggml ? GQ_FMT_Q6_K_GGML : GQ_FMT_Q6_K; }
 
   // Device dequant of a tensor to fp32 (weight_loader.cpp:517-560 conversions).
   bool to_f32(int idx, const uint8_t *data, size_t n_elem, float *out, std::string *err) const {
@@ -367,7 +369,7 @@ struct GGUFLoader::Impl {
     case T_Q4_0: fmt = GQ_FMT_Q4_0; be = 32; break;
     case T_Q8_0: fmt = GQ_FMT_Q8_0; be = 32; break;
     case T_Q4_K: fmt = q4k_fmt(); be = 256; break;
-    case T_Q6_K: fmt = GQ_FMT_Q6_K; be = 256; break;
+    case T_Q6_K: fmt = q6k_fmt(); be = 256; break;
     default: return set_err(err, "unsupported tensor type " + info.dtype + " for " + info.name), false;
     }
     if (n_elem % be) return set_err(err, "element count not a whole number of blocks: " + info.name), false;
@@ -480,8 +482,12 @@ bool GGUFLoader::plan(const std::string &name, LoadKind kind, LoadPlan *p, std::
     else if (type == T_Q4_K) {
       r.fmt = impl_->q4k_fmt();
       r.type = impl_->q4k_ggml ? DT::Q4_K_GGML : DT::Q4_K;
+    } else if (type == T_Q6_K) {
+      r.fmt = impl_->q6k_fmt();
+      r.type = impl_->q4k_ggml ? DT::Q6_K_GGML : DT::Q6_K;
     } else
-      return set_err(err, "load_tensor_quant: " + name + " is " + t.dtype + " (Q4_0, Q8_0 or Q4_K expected)"),
+      return set_err(err, "load_tensor_quant: " + name + " is " + t.dtype +
+                              " (Q4_0, Q8_0, Q4_K or Q6_K expected)"),
              false;
     if (t.shape.empty()) return set_err(err, "load_tensor_quant: scalar tensor " + name), false;
     r.K = t.shape[0];
@@ -640,7 +646,10 @@ bool GGUFLoader::load_tensor_quant(const std::string &name, gcore::rt::hip::Buff
   if (!plan(name, LoadKind::QUANT, &p, err) || !alloc_buffer(packed, p.bytes, p.type, err)) return false;
   if (!load_into(name, LoadKind::QUANT, p, packed.data(), nullptr, nullptr, err)) return false;
   gcore::rt::GretaQuantInfo q;
-  q.group_size = p.fmt == GQ_FMT_Q4_K || p.fmt == GQ_FMT_Q4_K_GGML ? 256 : 32;
+  q.group_size = (p.fmt == GQ_FMT_Q4_K || p.fmt == GQ_FMT_Q4_K_GGML || p.fmt == GQ_FMT_Q6_K ||
+                  p.fmt == GQ_FMT_Q6_K_GGML)
+                     ? 256
+                     : 32;
   q.format = (uint32_t)p.fmt;
   packed.set_quant_info(q);
   return true;

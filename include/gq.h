@@ -37,14 +37,18 @@ extern "C" {
 #define GQ_ERR_WORKSPACE 4    /* workspace missing or too small */
 #define GQ_ERR_NO_DEVICE 5    /* no usable GPU */
 
-/* weight formats: GGML type ids (weight_loader.cpp:15-33) + a Q4_K variant */
+/* weight formats: GGML type ids (weight_loader.cpp:15-33) + Q4_K / Q6_K variants */
 #define GQ_FMT_Q4_0 2
 #define GQ_FMT_Q8_0 8
 #define GQ_FMT_Q4_K 12       /* reference (GRETA) Q4_K layout, weight_loader.cpp:125-156 */
+#define GQ_FMT_Q6_K 14       /* reference Q6_K layout, weight_loader.cpp:158-177 */
 #define GQ_FMT_Q4_K_GGML 112 /* llama.cpp canonical Q4_K layout */
+#define GQ_FMT_Q6_K_GGML 114 /* llama.cpp canonical Q6_K layout */
 /* accepted by gq_dequant_gguf only (loader conversions) */
 #define GQ_FMT_F16 1         /* one "block" = one fp16 value (weight_loader.cpp:91-110) */
-#define GQ_FMT_Q6_K 14       /* reference Q6_K layout, weight_loader.cpp:158-177 */
+/* Q6_K (both layouts): T16 repack, dequant and gq_gemv (fp16 matrix-core
+   kernel at every batch); gq_gemm, gq_gemv_prep / prepped, gq_gemv_multi and
+   gq_gemv_swiglu return GQ_ERR_UNSUPPORTED for it. */
 
 /* activation / output dtypes */
 #define GQ_DT_F32 0

@@ -106,6 +106,7 @@ size_t gqo_block_elems(int fmt) {
   case GQO_Q4_K:
   case GQO_Q4_K_GGML:
   case GQO_Q6_K:
+  case GQO_Q6_K_GGML:
     return 256;
   default:
     return 0;
@@ -125,6 +126,7 @@ size_t gqo_block_bytes(int fmt) {
   case GQO_Q4_K_GGML:
     return 144;
   case GQO_Q6_K:
+  case GQO_Q6_K_GGML:
     return 210;
   default:
     return 0;
@@ -245,6 +247,25 @@ static void deq_q6_k(const uint8_t *b, float *y) {
   }
 }
 
+/* Q6_K, llama.cpp layout (ggml dequantize_row_q6_K, not part of the
+ * reference): per 128-element half h and l in 0..31, element 128h + 32k + l
+ * takes its low 4 bits from ql[64h + l + 32(k & 1)] (high nibble when k >= 2)
+ * and its high 2 bits from qh[32h + l] (bits 2k, 2k+1); scales in element
+ * order.  Values are rounded as the reference rounds Q6_K: (d * (q-32)) * sc. */
+static void deq_q6_k_ggml(const uint8_t *b, float *y) {
+  const uint8_t *ql = b, *qh = b + 128;
+  const int8_t *sc = (const int8_t *)(b + 192);
+  float d = gqo_fp16_to_fp32(rd16(b + 208));
+  for (int i = 0; i < 256; ++i) {
+    int h = i >> 7, k = (i >> 5) & 3, l = i & 31;
+    int lo = (ql[64 * h + l + 32 * (k & 1)] >> (4 * (k >> 1))) & 0x0F;
+    int hi = (qh[32 * h + l] >> (2 * k)) & 0x03;
+    int q = (lo | (hi << 4)) - 32;
+    volatile float t = d * (float)q;
+    y[i] = t * (float)sc[i / 16];
+  }
+}
+
 int gqo_dequant(int fmt, const uint8_t *blocks, size_t n_blocks, float *out) {
   size_t be = gqo_block_elems(fmt), bb = gqo_block_bytes(fmt);
   if (!be) return 1;
@@ -272,6 +293,9 @@ int gqo_dequant(int fmt, const uint8_t *blocks, size_t n_blocks, float *out) {
       break;
     case GQO_Q6_K:
       deq_q6_k(b, y);
+      break;
+    case GQO_Q6_K_GGML:
+      deq_q6_k_ggml(b, y);
       break;
     default:
       return 1;

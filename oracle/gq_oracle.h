@@ -40,7 +40,8 @@ enum {
   GQO_Q8_0 = 8,
   GQO_Q4_K = 12,      /* reference (GRETA) Q4_K nibble / scale layout */
   GQO_Q6_K = 14,
-  GQO_Q4_K_GGML = 112 /* llama.cpp canonical Q4_K layout */
+  GQO_Q4_K_GGML = 112, /* llama.cpp canonical Q4_K layout */
+  GQO_Q6_K_GGML = 114  /* llama.cpp canonical Q6_K layout */
 };
 
 float gqo_fp16_to_fp32(uint16_t h);

@@ -25,9 +25,9 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 ORACLE_SO = os.path.join(HERE, "_build", "libgqoracle.so")
 REF_SO = os.path.join(HERE, "_ref", "libgqref.so")
 
-Q4_0, Q8_0, Q4_K, Q6_K, Q4_K_GGML = 2, 8, 12, 14, 112
-BLOCK_ELEMS = {Q4_0: 32, Q8_0: 32, Q4_K: 256, Q4_K_GGML: 256, Q6_K: 256}
-BLOCK_BYTES = {Q4_0: 18, Q8_0: 34, Q4_K: 144, Q4_K_GGML: 144, Q6_K: 210}
+Q4_0, Q8_0, Q4_K, Q6_K, Q4_K_GGML, Q6_K_GGML = 2, 8, 12, 14, 112, 114
+BLOCK_ELEMS = {Q4_0: 32, Q8_0: 32, Q4_K: 256, Q4_K_GGML: 256, Q6_K: 256, Q6_K_GGML: 256}
+BLOCK_BYTES = {Q4_0: 18, Q8_0: 34, Q4_K: 144, Q4_K_GGML: 144, Q6_K: 210, Q6_K_GGML: 210}
 
 _lib = None
 _ref = None
@@ -258,7 +258,7 @@ def gen_weights(fmt: int, n: int, k: int, seed: int) -> np.ndarray:
         out[:, 0:2] = _scales16(rng, nb, 0.01).view(np.uint8).reshape(nb, 2)
         out[:, 2:4] = _scales16(rng, nb, 0.01).view(np.uint8).reshape(nb, 2)
         out[:, 4:] = rng.integers(0, 256, size=(nb, 140), dtype=np.uint8)
-    elif fmt == Q6_K:
+    elif fmt in (Q6_K, Q6_K_GGML):
         out[:, :208] = rng.integers(0, 256, size=(nb, 208), dtype=np.uint8)
         out[:, 192:208] = rng.integers(-32, 32, size=(nb, 16), dtype=np.int8).view(np.uint8)
         out[:, 208:210] = _scales16(rng, nb, 0.01).view(np.uint8).reshape(nb, 2)

@@ -56,16 +56,20 @@ def test_status_strings_and_version():
     assert lib.gq_status_string(99) == b"unknown status"
 
 
-@pytest.mark.parametrize("fmt", [gq.FMT_Q4_0, gq.FMT_Q8_0, gq.FMT_Q4_K, gq.FMT_Q4_K_GGML])
+ALL = [gq.FMT_Q4_0, gq.FMT_Q8_0, gq.FMT_Q4_K, gq.FMT_Q4_K_GGML, gq.FMT_Q6_K, gq.FMT_Q6_K_GGML]
+
+
+@pytest.mark.parametrize("fmt", ALL)
 def test_sizes_match_gguf(fmt):
     # bytes per weight are unchanged by the repack when the shape is tile-aligned
     for n, k in [(4096, 4096), (14336, 4096), (4096, 14336), (1024, 4096)]:
         assert gq.packed_size(fmt, n, k) == gq.gguf_bytes(fmt, n, k)
     assert gq.gguf_bytes(gq.FMT_Q4_0, 14336, 4096) == 33030144
     assert gq.gguf_bytes(gq.FMT_Q8_0, 128256, 4096) == 558170112
+    assert gq.gguf_bytes(gq.FMT_Q6_K, 128256, 4096) == 128256 * 16 * 210
 
 
-@pytest.mark.parametrize("fmt", [gq.FMT_Q4_0, gq.FMT_Q8_0, gq.FMT_Q4_K, gq.FMT_Q4_K_GGML])
+@pytest.mark.parametrize("fmt", ALL)
 @pytest.mark.parametrize("shape", [(64, 1024), (7, 256), (40, 512), (1, 4096), (17, 2304)])
 def test_host_repack_roundtrip(fmt, shape):
     n, k = shape
@@ -80,7 +84,7 @@ def test_host_repack_roundtrip(fmt, shape):
 def test_repack_is_a_permutation_of_the_bits():
     # every GGUF byte (and every nibble) lands somewhere: popcount is preserved
     n, k = 32, 1024
-    for fmt in (gq.FMT_Q4_0, gq.FMT_Q8_0, gq.FMT_Q4_K):
+    for fmt in (gq.FMT_Q4_0, gq.FMT_Q8_0, gq.FMT_Q4_K, gq.FMT_Q6_K, gq.FMT_Q6_K_GGML):
         w = O.gen_weights(fmt, n, k, seed=1)
         p = gq.repack_host(fmt, w, n, k)
         assert np.unpackbits(p).sum() == np.unpackbits(w).sum()
@@ -101,6 +105,10 @@ def test_argument_validation():
     assert lib.gq_gemm(gq.FMT_Q4_0, buf, buf, 7, buf, 0, 4, 16, 32, None, 0, None) == 2  # bad dtype
     assert lib.gq_gemv_workspace_bytes(gq.FMT_Q4_0, 4096, 17) == 0
     assert lib.gq_gemv_workspace_bytes(gq.FMT_Q4_0, 4096, 4) > 0
+    # Q6_K: GEMV only (fp16 kernel, no workspace); no GEMM, no split or fused GEMV
+    assert lib.gq_gemv_workspace_bytes(gq.FMT_Q6_K, 4096, 4) == 0
+    assert lib.gq_gemm(gq.FMT_Q6_K, buf, buf, 2, buf, 0, 32, 16, 256, None, 0, None) == 2
+    assert lib.gq_gemv_prep(gq.FMT_Q6_K, buf, 256, 1, buf, 64, None) == 2
     # zero-sized problems are no-ops that need no device
     assert lib.gq_gemv(gq.FMT_Q4_0, buf, buf, buf, 0, 32, 1, None, 0, None) == 0
     assert lib.gq_gemm(gq.FMT_Q4_0, buf, buf, 2, buf, 0, 0, 16, 32, None, 0, None) == 0

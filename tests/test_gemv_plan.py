@@ -12,14 +12,14 @@ import pytest
 import gq
 
 MAXC = {gq.FMT_Q4_0: 8, gq.FMT_Q8_0: 8, gq.FMT_Q4_K: 4, gq.FMT_Q4_K_GGML: 4}
-CK = {gq.FMT_Q4_0: 128, gq.FMT_Q8_0: 128, gq.FMT_Q4_K: 256, gq.FMT_Q4_K_GGML: 256}
-QB = {gq.FMT_Q4_0: 1024, gq.FMT_Q8_0: 2048, gq.FMT_Q4_K: 2048, gq.FMT_Q4_K_GGML: 2048}
+CK = {gq.FMT_Q4_0: 128, gq.FMT_Q8_0: 128, gq.FMT_Q4_K: 256, gq.FMT_Q4_K_GGML: 256, gq.FMT_Q6_K: 256}
+QB = {gq.FMT_Q4_0: 1024, gq.FMT_Q8_0: 2048, gq.FMT_Q4_K: 2048, gq.FMT_Q4_K_GGML: 2048, gq.FMT_Q6_K: 3072}
 
 SHAPES = [(1, 32), (100, 288), (17, 96), (33, 160), (1, 256), (100, 256), (1, 768), (17, 512), (256, 2048),
           (4096, 4096), (14336, 4096), (4096, 14336), (1024, 4096), (128256, 4096), (7, 256), (40, 512)]
 
 
-SB = {gq.FMT_Q4_0: 128, gq.FMT_Q8_0: 128, gq.FMT_Q4_K: 256, gq.FMT_Q4_K_GGML: 256}
+SB = {gq.FMT_Q4_0: 128, gq.FMT_Q8_0: 128, gq.FMT_Q4_K: 256, gq.FMT_Q4_K_GGML: 256, gq.FMT_Q6_K: 288}
 KWIN = 256  # k per activation staging window of the fp16 batch kernel
 
 
@@ -84,14 +84,16 @@ def emulate(fmt, n, k, batch):
 SHAPES_H = SHAPES + [(14336, 14336), (4096, 28672), (16, 65536)]
 
 
-@pytest.mark.parametrize("fmt", [gq.FMT_Q4_0, gq.FMT_Q8_0, gq.FMT_Q4_K])
+@pytest.mark.parametrize("fmt", [gq.FMT_Q4_0, gq.FMT_Q8_0, gq.FMT_Q4_K, gq.FMT_Q6_K])
 @pytest.mark.parametrize("batch", [1, 2, 3, 4, 5, 8, 9, 16])
 def test_gemv_plan_in_bounds(fmt, batch, monkeypatch):
     for n, k in SHAPES_H:
-        if k % (256 if fmt == gq.FMT_Q4_K else 32):
+        if k % (32 if fmt in (gq.FMT_Q4_0, gq.FMT_Q8_0) else 256):
             continue
-        if batch >= 5:
+        if batch >= 5 or fmt == gq.FMT_Q6_K:  # Q6_K: the fp16 kernel at every batch
             emulate_h(fmt, n, k, batch)
+    if fmt == gq.FMT_Q6_K:
+        return
     # the int8 kernel at every batch (the split prep / prepped form uses it)
     monkeypatch.setenv("GQ_GEMV_H_MIN", "17")
     for n, k in SHAPES:

@@ -186,8 +186,10 @@ def test_plans(model_file):
         assert not p["transpose"] and p["bytes"] == 512 * DIM
         p = g.plan("blk.0.ffn_gate.weight", gq.LOAD_QUANT)
         assert (p["fmt"], p["N"], p["K"], p["bytes"]) == (gq.FMT_Q4_0, 512, DIM, gq.packed_size(gq.FMT_Q4_0, 512, DIM))
-        with pytest.raises(gq.GQError, match="Q4_0, Q8_0 or Q4_K"):
-            g.plan("output.weight", gq.LOAD_QUANT)
+        p = g.plan("output.weight", gq.LOAD_QUANT)  # Q6_K: T16 too
+        assert (p["fmt"], p["N"], p["K"]) == (gq.FMT_Q6_K, 48, DIM)
+        with pytest.raises(gq.GQError, match="Q4_0, Q8_0, Q4_K or Q6_K"):
+            g.plan("blk.0.attn_output.weight", gq.LOAD_QUANT)  # F16
         with pytest.raises(gq.GQError, match="not found"):
             g.plan("nope", gq.LOAD_F32)
 
@@ -289,12 +291,14 @@ def test_load_quant_is_the_t16_repack(dev, model_file, ggml):
     with _ours(path) as g:
         g.set_q4k_layout(ggml)
         for name, (sh, gt, fmt, data) in spec.items():
-            if gt not in (W.GGML_Q4_0, W.GGML_Q8_0, W.GGML_Q4_K):
+            if gt not in (W.GGML_Q4_0, W.GGML_Q8_0, W.GGML_Q4_K, W.GGML_Q6_K):
                 continue
             packed, _, _, plan = g.load(name, gq.LOAD_QUANT, device=dev)
             f = plan["fmt"]
             if gt == W.GGML_Q4_K:
                 assert f == (gq.FMT_Q4_K_GGML if ggml else gq.FMT_Q4_K)
+            if gt == W.GGML_Q6_K:
+                assert f == (gq.FMT_Q6_K_GGML if ggml else gq.FMT_Q6_K)
             k = sh[0]
             n = int(np.prod(sh)) // k
             host = gq.repack_host(f, np.frombuffer(data, dtype=np.uint8), n, k)

@@ -9,7 +9,7 @@ import oracle as O
 pytestmark = pytest.mark.gpu
 
 TOL = 1e-3  # rel-L2 bound for GEMV / GEMM vs the fp64 oracle
-FMTS = [O.Q4_0, O.Q8_0, O.Q4_K, O.Q4_K_GGML]
+FMTS = [O.Q4_0, O.Q8_0, O.Q4_K, O.Q4_K_GGML, O.Q6_K, O.Q6_K_GGML]
 
 
 def bitexact(got, ref):
@@ -90,7 +90,7 @@ def test_gemv_ragged_q32(dev, fmt, shape):
     assert err <= TOL, err
 
 
-@pytest.mark.parametrize("fmt", [O.Q4_K, O.Q4_K_GGML])
+@pytest.mark.parametrize("fmt", [O.Q4_K, O.Q4_K_GGML, O.Q6_K, O.Q6_K_GGML])
 @pytest.mark.parametrize("shape", [(100, 256), (1, 768), (17, 512)])
 def test_gemv_ragged_q4k(dev, fmt, shape):
     n, k = shape
@@ -99,6 +99,7 @@ def test_gemv_ragged_q4k(dev, fmt, shape):
 
 
 @pytest.mark.parametrize("fmt,n,k", [(O.Q4_0, 14336, 4096), (O.Q4_0, 4096, 14336), (O.Q8_0, 4096, 4096),
+                                     (O.Q6_K, 32000, 4096),
                                      (O.Q4_K, 14336, 4096)])
 def test_gemv_baseline_shapes(dev, fmt, n, k):
     err = _gemv_case(dev, fmt, n, k, 1, seed=1000 + fmt)
@@ -207,3 +208,14 @@ def test_gemm_every_kernel_shape(dev, fmt, tile, monkeypatch):
     packed = _to_dev(gq.repack_host(fmt, w, n, k), dev)
     c = gq.gemm(fmt, packed, a.to(dev), n, k).cpu().numpy()
     assert O.rel_l2(c, ref) <= TOL
+
+
+def test_q6k_matmul_batches_the_gemv(dev):
+    """Q6_K has no GEMM: gq_matmul runs M > 16 rows as 16-row GEMV batches."""
+    import gq
+    n, k, m = 96, 512, 40
+    w = O.gen_weights(O.Q6_K, n, k, seed=31)
+    a = O.gen_x(m, k, seed=32)
+    packed = _to_dev(gq.repack_host(O.Q6_K, w, n, k), dev)
+    c = gq.matmul(O.Q6_K, packed, _to_dev(a, dev), n, k).cpu().numpy()
+    assert O.rel_l2(c, O.gemv(O.Q6_K, w, a, n, k)) <= TOL

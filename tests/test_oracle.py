@@ -139,6 +139,49 @@ def test_q6k_reference_golden():
     assert bits_equal(O.dequant(O.Q6_K, g["blocks"]), g["out"])
 
 
+def _q6k_block(d, sc, codes, ggml):
+    """Pack 256 six-bit codes into a Q6_K block (the inverse of the two
+    layouts' decoders, written element by element)."""
+    b = np.zeros(210, np.uint8)
+    for i, c in enumerate(codes):
+        lo, hi = int(c) & 15, int(c) >> 4
+        if not ggml:
+            b[i // 2] |= lo << (4 * (i % 2))
+            b[128 + i // 4] |= hi << (2 * (i % 4))
+        else:
+            h, k, l = i // 128, (i // 32) % 4, i % 32
+            b[64 * h + l + 32 * (k % 2)] |= lo << (4 * (k // 2))
+            b[128 + 32 * h + l] |= hi << (2 * k)
+    b[192:208] = np.asarray(sc, np.int8).view(np.uint8)
+    b[208:210] = np.frombuffer(np.float16(d).tobytes(), np.uint8)
+    return b
+
+
+@pytest.mark.parametrize("ggml", [False, True])
+def test_q6k_hand_built_block(ggml):
+    rng = np.random.default_rng(11 + ggml)
+    codes = rng.integers(0, 64, 256)
+    sc = rng.integers(-128, 128, 16)
+    d = 0.25  # exact: every product is exact in fp32
+    got = O.dequant(O.Q6_K_GGML if ggml else O.Q6_K, _q6k_block(d, sc, codes, ggml))
+    want = np.array([(d * (codes[i] - 32)) * sc[i // 16] for i in range(256)], np.float32)
+    assert np.array_equal(got, want)
+
+
+def test_q6k_layouts_differ():
+    w = O.gen_weights(O.Q6_K, 4, 256, seed=3)
+    assert not np.array_equal(O.dequant(O.Q6_K, w), O.dequant(O.Q6_K_GGML, w))
+
+
+def test_q6k_extremes():
+    # codes 0 and 63 -> -32 d sc and 31 d sc; sc = -128 .. 127
+    codes = np.array([0, 63] * 128)
+    sc = np.array([-128, 127] * 8)
+    for ggml in (False, True):
+        y = O.dequant(O.Q6_K_GGML if ggml else O.Q6_K, _q6k_block(1.0, sc, codes, ggml))
+        assert y[0] == 4096.0 and y[1] == -3968.0 and y[16] == -4064.0 and y[17] == 3937.0
+
+
 # ---- Q4_0 / Q8_0 (GGUF spec) ------------------------------------------------------
 def test_q4_0_known_answer():
     # byte j = j | (15 - j) << 4, d = 0.5: y[j] = (j - 8)/2, y[j + 16] = (7 - j)/2
@@ -184,7 +227,7 @@ def test_gemm_ref_golden():
     assert np.array_equal(O.gemm_ref(g["A"], g["B"]), g["C"])
 
 
-@pytest.mark.parametrize("fmt", [O.Q4_0, O.Q8_0, O.Q4_K, O.Q4_K_GGML])
+@pytest.mark.parametrize("fmt", [O.Q4_0, O.Q8_0, O.Q4_K, O.Q4_K_GGML, O.Q6_K, O.Q6_K_GGML])
 def test_gemv_brute_force_tiny(fmt):
     k = O.BLOCK_ELEMS[fmt] * 2
     n, b = 5, 3
