@@ -7,8 +7,9 @@ weight copy; >= 8 distinct copies (>= 264 MB) are rotated so the 256 MB
 Infinity Cache cannot serve them.
 
 Also reported (field "extra"): the other BASELINE configs -- Q4_0 / Q8_0 GEMV
-shapes, Q4_K batch 1/4/8/16, the prefill GEMM TFLOPS at M = 512 / 2048, and one
-full 32-layer Llama-3-8B-shaped decode step (225 GEMVs).
+shapes, Q4_K batch 1/4/8/16, the prefill GEMM TFLOPS at M = 512 / 2048, one
+full 32-layer Llama-3-8B-shaped decode step (225 GEMVs), and the GGUF-native
+load throughput (pinned sliced upload + on-GPU repack).
 
   python bench.py [--steps K] [--warmup W] [--gpus 1] [--headline-only]
 """
@@ -214,6 +215,82 @@ def bench_decode_step(dev, steps, warmup):
     return out
 
 
+def bench_load(dev, layers=8):
+    """GGUF-native load throughput (SURVEY config: loader I/O): a Llama-3-8B
+    shaped file of `layers` Q4_K layers (~1 GB) in the page cache, every matrix
+    loaded with gq_gguf_load(QUANT) (pinned sliced upload + on-GPU T16 repack),
+    against the reference's way of loading: read into pageable memory, a
+    synchronous pageable copy, then the repack.  GB/s of GGUF bytes."""
+    import shutil
+    import tempfile
+
+    import numpy as np
+    import torch
+
+    import gq
+    sys.path.insert(0, os.path.join(ROOT, "tests"))
+    import gguf_writer as W
+    shapes = [("attn_q", 4096, 4096), ("attn_k", 4096, 1024), ("attn_v", 4096, 1024),
+              ("attn_output", 4096, 4096), ("ffn_gate", 4096, 14336), ("ffn_up", 4096, 14336),
+              ("ffn_down", 14336, 4096)]
+    d = tempfile.mkdtemp(prefix="gq_load_")
+    path = os.path.join(d, "model.gguf")
+    try:
+        rng = np.random.default_rng(0)
+        tensors = []
+        for l in range(layers):
+            for nm, k, n in shapes:
+                nb = W.tensor_bytes(W.GGML_Q4_K, [k, n])
+                tensors.append((f"blk.{l}.{nm}.weight", [k, n], W.GGML_Q4_K,
+                                rng.integers(0, 256, nb, dtype=np.uint8).tobytes()))
+        W.write_gguf(path, W.llama_kv(dim=4096, heads=32, heads_kv=8, layers=layers, ff=14336, ctx=2048,
+                                      vocab=["a"], rope=5e5, eps=1e-5), tensors)
+        total = sum(len(t[3]) for t in tensors)
+        names = [t[0] for t in tensors]
+        del tensors
+        with open(path, "rb") as f:  # page cache warm for both paths
+            while f.read(1 << 26):
+                pass
+        g = gq.GGUF(path)
+        info = {t["name"]: t for t in g.tensors()}
+        outs = {nm: torch.empty(g.plan(nm, gq.LOAD_QUANT)["bytes"], dtype=torch.uint8, device=dev) for nm in names}
+
+        def ours():
+            for nm in names:
+                o = outs[nm]
+                g._check(gq.load().gq_gguf_load(g._h, nm.encode(), gq.LOAD_QUANT, gq._ptr(o), o.numel(),
+                                                None, 0, None, 0), "gq_gguf_load")
+            torch.cuda.synchronize()
+
+        def reference_style():
+            res = []
+            with open(path, "rb") as f:
+                for nm in names:
+                    t = info[nm]
+                    f.seek(t["offset"])
+                    host = np.empty(t["size_bytes"], dtype=np.uint8)
+                    f.readinto(host)
+                    raw = torch.from_numpy(host).to(dev)
+                    res.append(gq.repack(gq.FMT_Q4_K, raw, t["shape"][1], t["shape"][0]))
+                    torch.cuda.synchronize()
+            return res
+
+        ours()  # staging buffers allocated here
+        t0 = time.perf_counter()
+        ours()
+        t_ours = time.perf_counter() - t0
+        t0 = time.perf_counter()
+        ref = reference_style()
+        t_ref = time.perf_counter() - t0
+        same = all(torch.equal(outs[nm], r) for nm, r in zip(names, ref))
+        g.close()
+        return {"GBps": round(total / t_ours / 1e9, 2), "ms": round(t_ours * 1e3, 1), "bytes": total,
+                "reference_style_GBps": round(total / t_ref / 1e9, 2), "same_bytes": same,
+                "layers": layers, "format": "Q4_K", "note": "page-cache-warm file; H2D over PCIe"}
+    finally:
+        shutil.rmtree(d, ignore_errors=True)
+
+
 def cpu_baseline(target_s=12.0):
     """The oracle (C restatement of the reference CPU semantics: dequant then
     fp64-accumulated dot, OpenMP over rows) on the host cores, on the headline
@@ -244,6 +321,7 @@ def main():
     ap.add_argument("--headline-only", action="store_true", help="only the headline GEMV (for profiling)")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-decode-step", action="store_true")
+    ap.add_argument("--no-load", action="store_true", help="skip the GGUF load-throughput extra")
     ap.add_argument("--gemm-only", action="store_true",
                     help="only the Q4_0 M=2048 14336x4096 prefill GEMM, --steps times (for profiling)")
     args = ap.parse_args()
@@ -300,6 +378,9 @@ def main():
         if not args.no_decode_step:
             log("[bench] decode step (config 5)")
             extra["decode_step_llama3_8b_q4k"] = bench_decode_step(dev, steps, warmup)
+        if not args.no_load:
+            log("[bench] GGUF-native load")
+            extra["load_quant_q4_k_llama3_8b_8layers"] = bench_load(dev)
     cpu = None
     if not args.no_cpu:
         log("[bench] cpu baseline")

@@ -150,33 +150,35 @@ k_dequant_t16(int fmt, const uint8_t *__restrict__ w, float *__restrict__ out, i
 }
 
 // ---------------------------------------------------------------------------
-// Repack GGUF -> T16.  One thread per (padded row, padded block); positions
-// outside the tensor are written as zeros, so no memset is needed.
+// Repack GGUF -> T16.  One thread per (padded row, padded block) of the rows
+// [row0, row0 + rows) of an N-row tensor (row0 a multiple of 16; src points at
+// row row0 of the GGUF data); positions outside the tensor are written as
+// zeros, so no memset is needed.
 // ---------------------------------------------------------------------------
 __global__ void __launch_bounds__(256)
-k_repack_q4_0(const uint8_t *__restrict__ src, uint8_t *__restrict__ dst, int N, int K) {
-  size_t C = gq_chunks(GQ_FMT_Q4_0, K), nbp = C * 4, Np = gq_tiles(N) * 16;
+k_repack_q4_0(const uint8_t *__restrict__ src, uint8_t *__restrict__ dst, int N, int K, int row0, int rows) {
+  size_t C = gq_chunks(GQ_FMT_Q4_0, K), nbp = C * 4;
   size_t i = (size_t)blockIdx.x * 256 + threadIdx.x;
-  if (i >= Np * nbp) return;
-  size_t n = i / nbp, blk = i % nbp;
+  if (i >= (size_t)rows * nbp) return;
+  size_t r = i / nbp, blk = i % nbp, n = row0 + r;
   size_t nb = (size_t)K / 32;
   uint64_t grp[2] = {0, 0};
   uint32_t d16 = 0;
-  if (n < (size_t)N && blk < nb) gq_q4_0_groups(src + (n * nb + blk) * 18, grp, &d16);
+  if (n < (size_t)N && blk < nb) gq_q4_0_groups(src + (r * nb + blk) * 18, grp, &d16);
   for (int eh = 0; eh < 2; ++eh) *reinterpret_cast<uint64_t *>(dst + gq_q4_0_grp_off(n, blk, eh, C)) = grp[eh];
   *reinterpret_cast<uint16_t *>(dst + gq_sc_plane_offset(GQ_FMT_Q4_0, N, K) + gq_q4_0_d_off(n, blk, C)) =
       (uint16_t)d16;
 }
 
 __global__ void __launch_bounds__(256)
-k_repack_q8_0(const uint8_t *__restrict__ src, uint8_t *__restrict__ dst, int N, int K) {
-  size_t C = gq_chunks(GQ_FMT_Q8_0, K), nbp = C * 4, Np = gq_tiles(N) * 16;
+k_repack_q8_0(const uint8_t *__restrict__ src, uint8_t *__restrict__ dst, int N, int K, int row0, int rows) {
+  size_t C = gq_chunks(GQ_FMT_Q8_0, K), nbp = C * 4;
   size_t i = (size_t)blockIdx.x * 256 + threadIdx.x;
-  if (i >= Np * nbp) return;
-  size_t n = i / nbp, blk = i % nbp;
+  if (i >= (size_t)rows * nbp) return;
+  size_t r = i / nbp, blk = i % nbp, n = row0 + r;
   size_t nb = (size_t)K / 32;
   bool in = n < (size_t)N && blk < nb;
-  const uint8_t *b = src + (n * nb + blk) * 34;
+  const uint8_t *b = src + (r * nb + blk) * 34;
   for (int eh = 0; eh < 2; ++eh) {
     uint32_t wv[4] = {0, 0, 0, 0};
     if (in)
@@ -190,15 +192,16 @@ k_repack_q8_0(const uint8_t *__restrict__ src, uint8_t *__restrict__ dst, int N,
 }
 
 __global__ void __launch_bounds__(256)
-k_repack_q4_k(const uint8_t *__restrict__ src, uint8_t *__restrict__ dst, int N, int K, int ggml) {
-  size_t S = gq_chunks(GQ_FMT_Q4_K, K), Np = gq_tiles(N) * 16;
+k_repack_q4_k(const uint8_t *__restrict__ src, uint8_t *__restrict__ dst, int N, int K, int row0, int rows,
+              int ggml) {
+  size_t S = gq_chunks(GQ_FMT_Q4_K, K);
   size_t i = (size_t)blockIdx.x * 256 + threadIdx.x;
-  if (i >= Np * S) return;
-  size_t n = i / S, s = i % S;
+  if (i >= (size_t)rows * S) return;
+  size_t r = i / S, s = i % S, n = row0 + r;
   uint64_t grp[16];
   uint32_t meta[4] = {0, 0, 0, 0};
   if (n < (size_t)N) {
-    gq_q4k_groups(ggml, src + (n * S + s) * 144, grp, meta);
+    gq_q4k_groups(ggml, src + (r * S + s) * 144, grp, meta);
   } else {
     for (int q = 0; q < 16; ++q) grp[q] = 0;
   }
@@ -211,12 +214,13 @@ k_repack_q4_k(const uint8_t *__restrict__ src, uint8_t *__restrict__ dst, int N,
 
 // one thread per (padded row, super-block)
 __global__ void __launch_bounds__(256)
-k_repack_q6_k(const uint8_t *__restrict__ src, uint8_t *__restrict__ dst, int N, int K, int ggml) {
-  size_t S = gq_chunks(GQ_FMT_Q6_K, K), Np = gq_tiles(N) * 16;
+k_repack_q6_k(const uint8_t *__restrict__ src, uint8_t *__restrict__ dst, int N, int K, int row0, int rows,
+              int ggml) {
+  size_t S = gq_chunks(GQ_FMT_Q6_K, K);
   size_t i = (size_t)blockIdx.x * 256 + threadIdx.x;
-  if (i >= Np * S) return;
-  size_t n = i / S, s = i % S;
-  gq_q6k_put(ggml, n < (size_t)N ? src + (n * S + s) * 210 : nullptr, dst,
+  if (i >= (size_t)rows * S) return;
+  size_t r = i / S, s = i % S, n = row0 + r;
+  gq_q6k_put(ggml, n < (size_t)N ? src + (r * S + s) * 210 : nullptr, dst,
              dst + gq_sc_plane_offset(GQ_FMT_Q6_K, N, K), n, s, S);
 }
 
@@ -358,25 +362,34 @@ extern "C" int gq_dequant_packed(int fmt, const void *packed, size_t N, size_t K
   return gq_last_launch();
 }
 
-extern "C" int gq_repack(int fmt, const void *gguf, size_t N, size_t K, void *packed, void *stream) {
+extern "C" int gq_repack_rows(int fmt, const void *gguf_rows, size_t N, size_t K, size_t row0, size_t rows,
+                              void *packed, void *stream) {
   GQ_TRY(gq_check_shape(fmt, N, K));
-  GQ_CHECK(gguf && packed, GQ_ERR_INVALID_ARGS);
-  if (N == 0 || K == 0) return GQ_OK;
+  GQ_CHECK(gguf_rows && packed, GQ_ERR_INVALID_ARGS);
+  GQ_CHECK(row0 % 16 == 0 && row0 <= N && rows <= N - row0, GQ_ERR_INVALID_ARGS);
+  GQ_CHECK(row0 + rows == N || rows % 16 == 0, GQ_ERR_INVALID_ARGS);  // whole tiles, or the tensor's end
+  if (rows == 0 || K == 0) return GQ_OK;
   hipStream_t s = (hipStream_t)stream;
-  size_t Np = gq_tiles(N) * 16, C = gq_chunks(fmt, K);
-  const uint8_t *src = (const uint8_t *)gguf;
+  // rows padded to whole tiles: the padding rows of the last tile are zeroed
+  const size_t rp = gq_tiles(row0 + rows) * 16 - row0, C = gq_chunks(fmt, K);
+  const uint8_t *src = (const uint8_t *)gguf_rows;
   uint8_t *dst = (uint8_t *)packed;
+  const int n = (int)N, k = (int)K, r0 = (int)row0, r = (int)rp;
   if (fmt == GQ_FMT_Q4_0)
-    hipLaunchKernelGGL(k_repack_q4_0, dim3(blocks_for(Np * C * 4)), dim3(256), 0, s, src, dst, (int)N, (int)K);
+    hipLaunchKernelGGL(k_repack_q4_0, dim3(blocks_for(rp * C * 4)), dim3(256), 0, s, src, dst, n, k, r0, r);
   else if (fmt == GQ_FMT_Q8_0)
-    hipLaunchKernelGGL(k_repack_q8_0, dim3(blocks_for(Np * C * 4)), dim3(256), 0, s, src, dst, (int)N, (int)K);
+    hipLaunchKernelGGL(k_repack_q8_0, dim3(blocks_for(rp * C * 4)), dim3(256), 0, s, src, dst, n, k, r0, r);
   else if (gq_fmt_is_q6k(fmt))
-    hipLaunchKernelGGL(k_repack_q6_k, dim3(blocks_for(Np * C)), dim3(256), 0, s, src, dst, (int)N, (int)K,
+    hipLaunchKernelGGL(k_repack_q6_k, dim3(blocks_for(rp * C)), dim3(256), 0, s, src, dst, n, k, r0, r,
                        (int)(fmt == GQ_FMT_Q6_K_GGML));
   else
-    hipLaunchKernelGGL(k_repack_q4_k, dim3(blocks_for(Np * C)), dim3(256), 0, s, src, dst, (int)N, (int)K,
+    hipLaunchKernelGGL(k_repack_q4_k, dim3(blocks_for(rp * C)), dim3(256), 0, s, src, dst, n, k, r0, r,
                        (int)(fmt == GQ_FMT_Q4_K_GGML));
   return gq_last_launch();
+}
+
+extern "C" int gq_repack(int fmt, const void *gguf, size_t N, size_t K, void *packed, void *stream) {
+  return gq_repack_rows(fmt, gguf, N, K, 0, N, packed, stream);
 }
 
 int gq_launch_prep_x(int fmt, const float *x, void *ws, int B, int K, hipStream_t s) {

@@ -39,6 +39,7 @@ _SIGS = {
     "gq_repack_host": (ctypes.c_int, [ctypes.c_int, _vp, _c_size, _c_size, _vp]),
     "gq_unpack_host": (ctypes.c_int, [ctypes.c_int, _vp, _c_size, _c_size, _vp]),
     "gq_repack": (ctypes.c_int, [ctypes.c_int, _vp, _c_size, _c_size, _vp, _vp]),
+    "gq_repack_rows": (ctypes.c_int, [ctypes.c_int, _vp, _c_size, _c_size, _c_size, _c_size, _vp, _vp]),
     "gq_dequant_gguf": (ctypes.c_int, [ctypes.c_int, _vp, _c_size, _vp, _vp]),
     "gq_dequant_packed": (ctypes.c_int, [ctypes.c_int, _vp, _c_size, _c_size, _vp, _vp]),
     "gq_gemv_workspace_bytes": (_c_size, [ctypes.c_int, _c_size, ctypes.c_int]),
@@ -89,6 +90,17 @@ _SIGS_GGUF = {
     "gq_gguf_read_raw": (ctypes.c_int, [_vp, ctypes.c_char_p, _vp, _c_size]),
     "gq_gguf_plan_load": (ctypes.c_int, [_vp, ctypes.c_char_p, ctypes.c_int, _vp]),
     "gq_gguf_load": (ctypes.c_int, [_vp, ctypes.c_char_p, ctypes.c_int, _vp, _c_size, _vp, _c_size, _vp, _c_size]),
+    # include/gq_greta.h
+    "gq_greta_write": (ctypes.c_int, [_vp, ctypes.c_char_p, ctypes.c_int, ctypes.POINTER(_c_size)]),
+    "gq_greta_open": (ctypes.c_int, [ctypes.c_char_p, ctypes.POINTER(_vp)]),
+    "gq_greta_open_error": (ctypes.c_char_p, []),
+    "gq_greta_close": (None, [_vp]),
+    "gq_greta_error": (ctypes.c_char_p, [_vp]),
+    "gq_greta_tensor_count": (_c_size, [_vp]),
+    "gq_greta_tensor_info": (ctypes.c_int, [_vp, _c_size, _vp]),
+    "gq_greta_find": (ctypes.c_int, [_vp, ctypes.c_char_p, ctypes.POINTER(_c_size)]),
+    "gq_greta_get_config": (ctypes.c_int, [_vp, _vp]),
+    "gq_greta_load": (ctypes.c_int, [_vp, ctypes.c_char_p, _vp, _c_size, _vp, _c_size, _vp, _c_size]),
 }
 _SIGS.update(_SIGS_GGUF)
 
@@ -179,6 +191,14 @@ def repack(fmt: int, d_gguf, n: int, k: int, stream=None):
     out = torch.empty(packed_size(fmt, n, k), dtype=torch.uint8, device=d_gguf.device)
     check(load().gq_repack(fmt, _ptr(d_gguf), n, k, _ptr(out), _stream(stream)), "gq_repack")
     return out
+
+
+def repack_rows(fmt: int, d_gguf_rows, n: int, k: int, row0: int, rows: int, d_packed, stream=None):
+    """Repacks GGUF rows [row0, row0 + rows) into the whole tensor's T16 buffer."""
+    _require_device(d_gguf_rows)
+    _require_device(d_packed)
+    check(load().gq_repack_rows(fmt, _ptr(d_gguf_rows), n, k, row0, rows, _ptr(d_packed), _stream(stream)),
+          "gq_repack_rows")
 
 
 def dequant_gguf(fmt: int, d_blocks, n_blocks: int, stream=None):
@@ -555,3 +575,85 @@ class GGUF:
         if sc is not None:
             sc = sc[:p["scale_bytes"]].view(torch.float32)
         return out, sc, hs, p
+
+
+# ---- .greta files (include/gq_greta.h) ---------------------------------------
+GRETA_INT4, GRETA_Q4_K, GRETA_Q4_0, GRETA_Q8_0, GRETA_Q4_K_GGML, GRETA_Q6_K, GRETA_Q6_K_GGML = 4, 5, 8, 9, 10, 11, 12
+
+
+class _GretaTensor(ctypes.Structure):
+    _fields_ = [("name", ctypes.c_char * 256), ("dtype", ctypes.c_uint32), ("n_dims", ctypes.c_uint32),
+                ("shape", ctypes.c_uint64 * 8), ("group_size", ctypes.c_uint32), ("num_heads", ctypes.c_uint32),
+                ("w_bytes", ctypes.c_uint64), ("s_bytes", ctypes.c_uint64), ("h_bytes", ctypes.c_uint64),
+                ("fmt", ctypes.c_int32), ("N", ctypes.c_uint64), ("K", ctypes.c_uint64)]
+
+
+def greta_write(gguf: "GGUF", path: str, kind: int = LOAD_QUANT) -> int:
+    """Writes a .greta file from an open GGUF: kind LOAD_QUANT (T16 records,
+    host repack) or LOAD_INT4 (the reference tool's INT4 records, on the GPU).
+    Returns the record count."""
+    n = _c_size(0)
+    gguf._check(load().gq_greta_write(gguf._h, os.fsencode(path), kind, ctypes.byref(n)), "gq_greta_write")
+    return n.value
+
+
+class Greta:
+    """.greta file opened through libgq's reader (GretaLoader)."""
+
+    def __init__(self, path: str):
+        lib = load()
+        h = _vp()
+        if lib.gq_greta_open(os.fsencode(path), ctypes.byref(h)) != 0:
+            raise GQError(f"gq_greta_open({path}) failed: {lib.gq_greta_open_error().decode()}")
+        self._h = h
+
+    def close(self):
+        if self._h:
+            load().gq_greta_close(self._h)
+            self._h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *a):
+        self.close()
+
+    def _check(self, st, what):
+        if st != 0:
+            raise GQError(f"{what} failed ({st}): {load().gq_greta_error(self._h).decode()}")
+
+    def tensors(self):
+        lib = load()
+        out = []
+        for i in range(lib.gq_greta_tensor_count(self._h)):
+            t = _GretaTensor()
+            self._check(lib.gq_greta_tensor_info(self._h, i, ctypes.byref(t)), "gq_greta_tensor_info")
+            out.append({"name": t.name.decode(), "dtype": t.dtype, "shape": [int(t.shape[d]) for d in range(t.n_dims)],
+                        "group_size": t.group_size, "num_heads": t.num_heads, "w_bytes": int(t.w_bytes),
+                        "s_bytes": int(t.s_bytes), "h_bytes": int(t.h_bytes), "fmt": t.fmt, "N": int(t.N),
+                        "K": int(t.K)})
+        return out
+
+    def config(self):
+        c = _Config()
+        self._check(load().gq_greta_get_config(self._h, ctypes.byref(c)), "gq_greta_get_config")
+        return {f: getattr(c, f) for f, _ in _Config._fields_}
+
+    def load(self, name: str, device="cuda"):
+        """Returns (w, s, h) uint8 device tensors (None where the record has none)."""
+        import torch
+        t = next(t for t in self.tensors() if t["name"] == name)
+        w = torch.empty(max(t["w_bytes"], 1), dtype=torch.uint8, device=device)
+        s = torch.empty(t["s_bytes"], dtype=torch.uint8, device=device) if t["s_bytes"] else None
+        h = torch.empty(t["h_bytes"], dtype=torch.uint8, device=device) if t["h_bytes"] else None
+        self._check(load().gq_greta_load(self._h, name.encode(), _ptr(w), w.numel(), _ptr(s),
+                                         s.numel() if s is not None else 0, _ptr(h),
+                                         h.numel() if h is not None else 0), "gq_greta_load")
+        return w[:t["w_bytes"]], s, h
+

@@ -2,11 +2,14 @@
 #include <cstring>
 #include <string>
 
+#include "gcore/inference/greta_file.hpp"
 #include "gcore/inference/weight_loader.hpp"
 #include "gq.h"
 #include "gq_gguf.h"
+#include "gq_greta.h"
 
 using gcore::inference::GGUFLoader;
+using gcore::inference::GretaLoader;
 
 struct gq_gguf {
   GGUFLoader loader;
@@ -16,8 +19,27 @@ struct gq_gguf {
   mutable std::string err;
 };
 
+struct gq_greta {
+  GretaLoader loader;
+  mutable std::string err;
+};
+
 namespace {
 thread_local std::string g_open_err;
+thread_local std::string g_greta_open_err;
+
+void fill_config(const gcore::inference::ModelConfig &c, gq_gguf_config *out) {
+  out->dim = c.dim;
+  out->num_heads = c.num_heads;
+  out->num_heads_kv = c.num_heads_kv;
+  out->num_layers = c.num_layers;
+  out->vocab_size = c.vocab_size;
+  out->hidden_dim = c.hidden_dim;
+  out->head_dim = c.head_dim;
+  out->max_seq_len = c.max_seq_len;
+  out->rope_base = c.rope_base;
+  out->rms_eps = c.rms_eps;
+}
 
 bool kind_of(int k, GGUFLoader::LoadKind *out) {
   switch (k) {
@@ -87,17 +109,7 @@ int gq_gguf_find(const gq_gguf *g, const char *name, size_t *index) {
 
 int gq_gguf_get_config(const gq_gguf *g, gq_gguf_config *out) {
   if (!g || !out) return GQ_ERR_INVALID_ARGS;
-  const auto &c = g->config;
-  out->dim = c.dim;
-  out->num_heads = c.num_heads;
-  out->num_heads_kv = c.num_heads_kv;
-  out->num_layers = c.num_layers;
-  out->vocab_size = c.vocab_size;
-  out->hidden_dim = c.hidden_dim;
-  out->head_dim = c.head_dim;
-  out->max_seq_len = c.max_seq_len;
-  out->rope_base = c.rope_base;
-  out->rms_eps = c.rms_eps;
+  fill_config(g->config, out);
   return GQ_OK;
 }
 
@@ -159,6 +171,101 @@ int gq_gguf_load(const gq_gguf *g, const char *name, int kind, void *d_out, size
     return GQ_ERR_INVALID_ARGS;
   }
   if (!g->loader.load_into(name, k, p, d_out, d_scales, d_head_scales, &g->err)) return GQ_ERR_HIP;
+  return GQ_OK;
+}
+
+// ---- .greta files -------------------------------------------------------------
+
+int gq_greta_write(gq_gguf *g, const char *path, int kind, size_t *written) {
+  if (written) *written = 0;
+  if (!g || !path) return GQ_ERR_INVALID_ARGS;
+  gcore::inference::GretaWriteKind k;
+  if (kind == GQ_LOAD_QUANT) k = gcore::inference::GretaWriteKind::T16;
+  else if (kind == GQ_LOAD_INT4) k = gcore::inference::GretaWriteKind::INT4;
+  else return GQ_ERR_UNSUPPORTED;
+  size_t n = 0;
+  if (!gcore::inference::write_greta(g->loader, path, k, &n, &g->err)) return GQ_ERR_INVALID_ARGS;
+  if (written) *written = n;
+  return GQ_OK;
+}
+
+int gq_greta_open(const char *path, gq_greta **out) {
+  if (!out) return GQ_ERR_INVALID_ARGS;
+  *out = nullptr;
+  if (!path) return GQ_ERR_INVALID_ARGS;
+  auto *h = new gq_greta();
+  std::string e;
+  if (!h->loader.open(path, &e)) {
+    g_greta_open_err = e.empty() ? ".greta open failed" : e;
+    delete h;
+    return GQ_ERR_INVALID_ARGS;
+  }
+  g_greta_open_err.clear();
+  *out = h;
+  return GQ_OK;
+}
+
+const char *gq_greta_open_error(void) { return g_greta_open_err.c_str(); }
+
+void gq_greta_close(gq_greta *h) { delete h; }
+
+const char *gq_greta_error(const gq_greta *h) { return h ? h->err.c_str() : ""; }
+
+size_t gq_greta_tensor_count(const gq_greta *h) { return h ? h->loader.records().size() : 0; }
+
+int gq_greta_tensor_info(const gq_greta *h, size_t index, gq_greta_tensor *out) {
+  if (!h || !out || index >= h->loader.records().size()) return GQ_ERR_INVALID_ARGS;
+  const auto &r = h->loader.records()[index];
+  std::memset(out, 0, sizeof(*out));
+  std::strncpy(out->name, r.name.c_str(), sizeof(out->name) - 1);
+  out->dtype = r.dtype;
+  out->n_dims = (uint32_t)r.shape.size();
+  for (size_t i = 0; i < r.shape.size() && i < 8; ++i) out->shape[i] = r.shape[i];
+  out->group_size = r.group_size;
+  out->num_heads = r.num_heads;
+  out->w_bytes = r.w_size;
+  out->s_bytes = r.s_size;
+  out->h_bytes = r.h_size;
+  out->fmt = gcore::inference::greta_fmt_of_dtype(r.dtype);
+  if (out->fmt >= 0 && !r.shape.empty() && r.shape[0]) {
+    uint64_t n = 1;
+    for (uint64_t d : r.shape) n *= d;
+    out->K = r.shape[0];
+    out->N = n / r.shape[0];
+  }
+  return GQ_OK;
+}
+
+int gq_greta_find(const gq_greta *h, const char *name, size_t *index) {
+  if (!h || !name || !index) return GQ_ERR_INVALID_ARGS;
+  const auto &recs = h->loader.records();
+  for (size_t i = 0; i < recs.size(); ++i)
+    if (recs[i].name == name) {
+      *index = i;
+      return GQ_OK;
+    }
+  h->err = std::string("tensor not found: ") + name;
+  return GQ_ERR_INVALID_ARGS;
+}
+
+int gq_greta_get_config(const gq_greta *h, gq_gguf_config *out) {
+  if (!h || !out) return GQ_ERR_INVALID_ARGS;
+  fill_config(h->loader.get_config(), out);
+  return GQ_OK;
+}
+
+int gq_greta_load(const gq_greta *h, const char *name, void *d_w, size_t w_cap, void *d_s, size_t s_cap, void *d_h,
+                  size_t h_cap) {
+  if (!h || !name) return GQ_ERR_INVALID_ARGS;
+  size_t i;
+  if (gq_greta_find(h, name, &i) != GQ_OK) return GQ_ERR_INVALID_ARGS;
+  const auto &r = h->loader.records()[i];
+  if (!d_w || w_cap < r.w_size || (r.s_size && (!d_s || s_cap < r.s_size)) ||
+      (r.h_size && (!d_h || h_cap < r.h_size))) {
+    h->err = "gq_greta_load: destination missing or smaller than the record";
+    return GQ_ERR_INVALID_ARGS;
+  }
+  if (!h->loader.load_into(name, d_w, w_cap, d_s, s_cap, d_h, h_cap, &h->err)) return GQ_ERR_HIP;
   return GQ_OK;
 }
 

@@ -7,6 +7,8 @@
 // scales, T16 repack).
 #include "gcore/inference/weight_loader.hpp"
 
+#include "gcore/inference/greta_file.hpp"
+
 #include <fcntl.h>
 #include <hip/hip_runtime.h>
 #include <sys/mman.h>
@@ -18,6 +20,7 @@
 #include <iostream>
 
 #include "gq.h"
+#include "upload.hpp"
 
 namespace gcore::inference {
 
@@ -192,6 +195,15 @@ struct GGUFLoader::Impl {
   size_t data_offset = 0;
   bool loaded = false;
   bool q4k_ggml = false;
+  std::unique_ptr<Uploader> up;  // pinned staging ring, created at the first load
+
+  Uploader &uploader() {
+    if (!up) up = std::make_unique<Uploader>();
+    return *up;
+  }
+  bool upload(void *dst, const uint8_t *src, size_t bytes, std::string *err) {
+    return uploader().copy(dst, src, bytes, err);
+  }
 
   ~Impl() { close(); }
   void close() {
@@ -358,10 +370,10 @@ struct GGUFLoader::Impl {
   int q6k_fmt() const { return q4k_ggml ? GQ_FMT_Q6_K_GGML : GQ_FMT_Q6_K; }
 
   // Device dequant of a tensor to fp32 (weight_loader.cpp:517-560 conversions).
-  bool to_f32(int idx, const uint8_t *data, size_t n_elem, float *out, std::string *err) const {
+  bool to_f32(int idx, const uint8_t *data, size_t n_elem, float *out, std::string *err) {
     const uint32_t t = types[idx];
     const TensorInfo &info = tensors[idx];
-    if (t == T_F32) return hip_ok(hipMemcpy(out, data, n_elem * 4, hipMemcpyHostToDevice), "hipMemcpy", err);
+    if (t == T_F32) return upload(out, data, n_elem * 4, err);
     int fmt;
     size_t be;
     switch (t) {
@@ -375,7 +387,7 @@ struct GGUFLoader::Impl {
     if (n_elem % be) return set_err(err, "element count not a whole number of blocks: " + info.name), false;
     DevMem raw;
     if (!raw.alloc(info.size_bytes, err)) return false;
-    if (!hip_ok(hipMemcpy(raw.p, data, info.size_bytes, hipMemcpyHostToDevice), "hipMemcpy", err)) return false;
+    if (!upload(raw.p, data, info.size_bytes, err)) return false;
     if (!gq_ok(gq_dequant_gguf(fmt, raw.p, n_elem / be, out, nullptr), "dequant", err)) return false;
     return hip_ok(hipStreamSynchronize(nullptr), "dequant", err);
   }
@@ -516,12 +528,10 @@ bool GGUFLoader::load_into(const std::string &name, LoadKind kind, const LoadPla
   };
 
   if (kind == LoadKind::QUANT) {
-    DevMem raw;
+    // sliced upload, each slice repacked into `out` while the next is copied
     const size_t rb = impl_->tensors[idx].size_bytes;
-    if (!raw.alloc(rb, err)) return false;
-    if (!hip_ok(hipMemcpy(raw.p, data, rb, hipMemcpyHostToDevice), "hipMemcpy", err)) return false;
-    if (!gq_ok(gq_repack(p.fmt, raw.p, p.N, p.K, out, nullptr), "repack", err)) return false;
-    return hip_ok(hipStreamSynchronize(nullptr), "repack", err);
+    if (p.N == 0 || rb % p.N) return set_err(err, "load_tensor_quant: ragged rows in " + name), false;
+    return impl_->uploader().repack(p.fmt, data, p.N, p.K, rb / p.N, out, err);
   }
   if (kind == LoadKind::F32) return impl_->to_f32(idx, data, n, (float *)out, err);
 
@@ -530,7 +540,7 @@ bool GGUFLoader::load_into(const std::string &name, LoadKind kind, const LoadPla
     const size_t rb = impl_->tensors[idx].size_bytes;
     if (n % 32) return set_err(err, "element count not a whole number of blocks: " + name), false;
     if (!raw.alloc(rb, err)) return false;
-    if (!hip_ok(hipMemcpy(raw.p, data, rb, hipMemcpyHostToDevice), "hipMemcpy", err)) return false;
+    if (!impl_->upload(raw.p, data, rb, err)) return false;
     if (!gq_ok(gq_split_q8_0(raw.p, n / 32, (int8_t *)out, (float *)scales, nullptr), "Q8_0 split", err))
       return false;
     return hip_ok(hipStreamSynchronize(nullptr), "Q8_0 split", err);
@@ -540,10 +550,10 @@ bool GGUFLoader::load_into(const std::string &name, LoadKind kind, const LoadPla
     // stored fp16 is uploaded as is (weight_loader.cpp:596-597): fp16
     // subnormals survive, unlike the fp32 -> fp16 truncation of other types
     const size_t rb = n * 2;
-    if (!p.transpose) return hip_ok(hipMemcpy(out, data, rb, hipMemcpyHostToDevice), "hipMemcpy", err);
+    if (!p.transpose) return impl_->upload(out, data, rb, err);
     DevMem h;
     if (!h.alloc(rb, err)) return false;
-    if (!hip_ok(hipMemcpy(h.p, data, rb, hipMemcpyHostToDevice), "hipMemcpy", err)) return false;
+    if (!impl_->upload(h.p, data, rb, err)) return false;
     if (!gq_ok(gq_transpose_kv(2, h.p, dm, kv, out, nullptr), "GQA transpose", err)) return false;
     if (!hip_ok(hipStreamSynchronize(nullptr), "GQA transpose", err)) return false;
     note_transpose();
@@ -658,6 +668,13 @@ bool GGUFLoader::load_tensor_quant(const std::string &name, gcore::rt::hip::Buff
 std::unique_ptr<WeightLoader> create_weight_loader(const std::string &path, std::string *err) {
   if (path.find(".gguf") != std::string::npos) {
     auto l = std::make_unique<GGUFLoader>();
+    if (!l->open(path, err)) return nullptr;
+    return l;
+  }
+  // the reference's factory knows only .gguf (:1043-1053); .greta files are
+  // read by GretaLoader
+  if (path.find(".greta") != std::string::npos) {
+    auto l = std::make_unique<GretaLoader>();
     if (!l->open(path, err)) return nullptr;
     return l;
   }

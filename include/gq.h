@@ -78,6 +78,16 @@ int gq_repack_host(int fmt, const void *gguf, size_t N, size_t K, void *packed);
 int gq_unpack_host(int fmt, const void *packed, size_t N, size_t K, void *gguf);
 /* Device: same as gq_repack_host on device buffers. */
 int gq_repack(int fmt, const void *d_gguf, size_t N, size_t K, void *d_packed, void *stream);
+/* Device, one slice of rows: d_gguf_rows holds the GGUF rows [row0, row0 +
+ * rows) of an N x K tensor; their T16 tiles are written into d_packed, the
+ * whole tensor's buffer (gq_packed_size(N, K) bytes).  row0 is a multiple of
+ * 16 and rows is too unless the slice ends the tensor (the last tile's padding
+ * rows are then zeroed).  Slices may run in any order; together they give
+ * gq_repack's result.  Lets a loader repack a tensor while later slices are
+ * still in flight from the host (replaces the whole-tensor hipMemcpy of
+ * src/inference/src/weight_loader.cpp:532-534). */
+int gq_repack_rows(int fmt, const void *d_gguf_rows, size_t N, size_t K, size_t row0, size_t rows,
+                   void *d_packed, void *stream);
 
 /* ---- dequantization (bit-exact with the reference semantics) -------------- */
 /* n_blocks raw GGUF blocks -> fp32 (n_blocks * 32 or * 256 values; F16:

@@ -109,6 +109,11 @@ def test_argument_validation():
     assert lib.gq_gemv_workspace_bytes(gq.FMT_Q6_K, 4096, 4) == 0
     assert lib.gq_gemm(gq.FMT_Q6_K, buf, buf, 2, buf, 0, 32, 16, 256, None, 0, None) == 2
     assert lib.gq_gemv_prep(gq.FMT_Q6_K, buf, 256, 1, buf, 64, None) == 2
+    # row slices: whole tiles from a multiple of 16, or the tensor's end
+    assert lib.gq_repack_rows(gq.FMT_Q4_0, buf, 40, 32, 8, 16, buf, None) == 1   # row0 not a tile start
+    assert lib.gq_repack_rows(gq.FMT_Q4_0, buf, 40, 32, 0, 8, buf, None) == 1    # partial tile mid-tensor
+    assert lib.gq_repack_rows(gq.FMT_Q4_0, buf, 40, 32, 32, 16, buf, None) == 1  # past the end
+    assert lib.gq_repack_rows(gq.FMT_Q4_0, buf, 40, 32, 32, 0, buf, None) == 0   # empty slice: no-op
     # zero-sized problems are no-ops that need no device
     assert lib.gq_gemv(gq.FMT_Q4_0, buf, buf, buf, 0, 32, 1, None, 0, None) == 0
     assert lib.gq_gemm(gq.FMT_Q4_0, buf, buf, 2, buf, 0, 0, 16, 32, None, 0, None) == 0

@@ -309,3 +309,39 @@ def test_load_quant_is_the_t16_repack(dev, model_file, ggml):
             y = gq.gemv(f, packed, torch.from_numpy(x).to(dev), n, k).cpu().numpy()
             ref = O.gemv(f, np.frombuffer(data, dtype=np.uint8), x, n, k)
             assert O.rel_l2(y, ref) <= 1e-3
+
+
+@pytest.mark.gpu
+def test_sliced_upload_with_many_slices(dev, tmp_path, monkeypatch):
+    """Tensors several times larger than the staging slice (1 MiB here, a ring
+    of 2 slots) load bit-identically: every slot is reused, the last slice is
+    short and the row count is not a multiple of 16."""
+    import gq
+    monkeypatch.setenv("GQ_LOAD_SLICE_MB", "1")
+    monkeypatch.setenv("GQ_LOAD_SLOTS", "2")
+    monkeypatch.setenv("GQ_LOAD_THREADS", "3")
+    specs = [("a.weight", [4096, 1000], W.GGML_Q4_0, O.Q4_0), ("b.weight", [2048, 1000], W.GGML_Q6_K, O.Q6_K),
+             ("c.weight", [1024, 900], W.GGML_Q8_0, O.Q8_0), ("d.weight", [3000, 700], W.GGML_F32, None),
+             ("e.weight", [4096, 300], W.GGML_F16, None)]
+    tensors = [(nm, sh, gt, _tensor_data(nm, sh, gt, f, 7 + i)) for i, (nm, sh, gt, f) in enumerate(specs)]
+    path = _write(tmp_path, "big.gguf", W.llama_kv(dim=DIM, heads=HEADS, heads_kv=HEADS_KV, layers=1, ff=512,
+                                                   ctx=2048, vocab=VOCAB, rope=1e4, eps=1e-5), tensors)
+    with _ours(path) as g:
+        for (nm, sh, gt, f), (_, _, _, data) in zip(specs, tensors):
+            raw = np.frombuffer(data, dtype=np.uint8)
+            k, n = sh[0], int(np.prod(sh)) // sh[0]
+            if f is not None:
+                packed, _, _, plan = g.load(nm, gq.LOAD_QUANT, device=dev)
+                assert _bits_equal(packed.cpu().numpy(), gq.repack_host(f, raw, n, k)), nm
+                f32, _, _, _ = g.load(nm, gq.LOAD_F32, device=dev)
+                assert _bits_equal(f32.cpu().numpy(), O.dequant(f, raw)), nm
+            elif gt == W.GGML_F32:
+                f32, _, _, _ = g.load(nm, gq.LOAD_F32, device=dev)
+                assert _bits_equal(f32.cpu().numpy(), raw), nm
+            else:
+                f16, _, _, _ = g.load(nm, gq.LOAD_F16, device=dev)
+                assert _bits_equal(f16.cpu().numpy(), raw), nm
+        q8, s8, _, _ = g.load("c.weight", gq.LOAD_INT8, device=dev)
+        blk = np.frombuffer(tensors[2][3], dtype=np.uint8).reshape(-1, 34)  # Q8_0 split as stored
+        assert _bits_equal(q8.cpu().numpy(), blk[:, 2:].copy())
+        assert _bits_equal(s8.cpu().numpy(), O.fp16_to_fp32(blk[:, :2].copy().view(np.uint16).ravel()))

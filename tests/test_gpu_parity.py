@@ -65,6 +65,21 @@ def test_repack_device_matches_host_and_dequant(dev, fmt, shape):
     assert bitexact(back, ref)
 
 
+@pytest.mark.parametrize("fmt", FMTS)
+def test_repack_rows_slices_in_any_order(dev, fmt):
+    """Row slices repacked out of order into one buffer give the whole-tensor
+    repack, including the zeroed padding rows of a ragged last tile."""
+    import gq
+    import torch
+    n, k = 40, 1024
+    w = O.gen_weights(fmt, n, k, seed=8 + fmt)
+    rb = w.size // n
+    out = torch.full((gq.packed_size(fmt, n, k),), 0xAB, dtype=torch.uint8, device=dev)
+    for r0, rows in [(32, 8), (0, 16), (16, 16)]:
+        gq.repack_rows(fmt, _to_dev(w[r0 * rb:(r0 + rows) * rb], dev), n, k, r0, rows, out)
+    assert np.array_equal(out.cpu().numpy(), gq.repack_host(fmt, w, n, k))
+
+
 def _gemv_case(dev, fmt, n, k, batch, seed):
     import gq
     w = O.gen_weights(fmt, n, k, seed=seed)
