@@ -1,7 +1,9 @@
 // gq_capi.cpp -- host side of the C ABI: status reporting, sizes, the host
 // (CPU) repack used by the loader, the library-owned workspace and the
 // GretaCompute::gemm-style routing entry.
+#include <algorithm>
 #include <mutex>
+#include <thread>
 #include <string.h>
 #include <vector>
 
@@ -78,17 +80,13 @@ int gq_packed_size(int fmt, size_t N, size_t K, size_t *bytes) {
 }
 
 // Host repack: the same per-block functions the device kernel uses.
-int gq_repack_host(int fmt, const void *gguf, size_t N, size_t K, void *packed) {
-  GQ_TRY(gq_check_shape(fmt, N, K));
-  GQ_CHECK(gguf && packed, GQ_ERR_INVALID_ARGS);
-  if (N == 0 || K == 0) return GQ_OK;
-  const uint8_t *src = (const uint8_t *)gguf;
-  uint8_t *dst = (uint8_t *)packed;
+namespace {
+// Repacks the GGUF rows [n0, n1) (whole tiles) into the T16 buffer.
+void repack_host_rows(int fmt, const uint8_t *src, uint8_t *dst, size_t N, size_t K, size_t n0, size_t n1) {
   const size_t C = gq_chunks(fmt, K), sc = gq_sc_plane_offset(fmt, N, K);
-  memset(dst, 0, gq_packed_bytes(fmt, N, K));
   if (fmt == GQ_FMT_Q4_0) {
     const size_t nb = K / 32;
-    for (size_t n = 0; n < N; ++n)
+    for (size_t n = n0; n < n1; ++n)
       for (size_t b = 0; b < nb; ++b) {
         uint64_t grp[2];
         uint32_t d16;
@@ -99,7 +97,7 @@ int gq_repack_host(int fmt, const void *gguf, size_t N, size_t K, void *packed) 
       }
   } else if (fmt == GQ_FMT_Q8_0) {
     const size_t nb = K / 32;
-    for (size_t n = 0; n < N; ++n)
+    for (size_t n = n0; n < n1; ++n)
       for (size_t b = 0; b < nb; ++b) {
         const uint8_t *blk = src + (n * nb + b) * 34;
         for (int eh = 0; eh < 2; ++eh) memcpy(dst + gq_q8_0_half_off(n, b, eh, C), blk + 2 + 16 * eh, 16);
@@ -107,21 +105,46 @@ int gq_repack_host(int fmt, const void *gguf, size_t N, size_t K, void *packed) 
       }
   } else if (gq_fmt_is_q6k(fmt)) {
     const int ggml = fmt == GQ_FMT_Q6_K_GGML;
-    for (size_t n = 0; n < N; ++n)
+    for (size_t n = n0; n < n1; ++n)
       for (size_t s = 0; s < C; ++s) gq_q6k_put(ggml, src + (n * C + s) * 210, dst, dst + sc, n, s, C);
   } else {
     const int ggml = fmt == GQ_FMT_Q4_K_GGML;
-    const size_t S = C;
-    for (size_t n = 0; n < N; ++n)
-      for (size_t s = 0; s < S; ++s) {
+    for (size_t n = n0; n < n1; ++n)
+      for (size_t s = 0; s < C; ++s) {
         uint64_t grp[16];
         uint32_t meta[4];
-        gq_q4k_groups(ggml, src + (n * S + s) * 144, grp, meta);
+        gq_q4k_groups(ggml, src + (n * C + s) * 144, grp, meta);
         for (int j = 0; j < 8; ++j)
-          for (int eh = 0; eh < 2; ++eh) memcpy(dst + gq_q4k_grp_off(n, s, j, eh, S), &grp[2 * j + eh], 8);
-        memcpy(dst + sc + gq_q4k_meta_off(n, s, S), meta, 16);
+          for (int eh = 0; eh < 2; ++eh) memcpy(dst + gq_q4k_grp_off(n, s, j, eh, C), &grp[2 * j + eh], 8);
+        memcpy(dst + sc + gq_q4k_meta_off(n, s, C), meta, 16);
       }
   }
+}
+}  // namespace
+
+int gq_repack_host(int fmt, const void *gguf, size_t N, size_t K, void *packed) {
+  GQ_TRY(gq_check_shape(fmt, N, K));
+  GQ_CHECK(gguf && packed, GQ_ERR_INVALID_ARGS);
+  if (N == 0 || K == 0) return GQ_OK;
+  const uint8_t *src = (const uint8_t *)gguf;
+  uint8_t *dst = (uint8_t *)packed;
+  memset(dst, 0, gq_packed_bytes(fmt, N, K));  // padding rows and blocks
+  // row tiles split over host threads (each tile's bytes are written by one)
+  const size_t tiles = gq_tiles(N);
+  const size_t bytes = gq_packed_bytes(fmt, N, K);
+  size_t nt = std::min<size_t>(std::max(1u, std::thread::hardware_concurrency()), 16);
+  nt = std::min(nt, std::max<size_t>(1, bytes >> 22));  // >= 4 MiB per thread
+  nt = std::min(nt, tiles);
+  if (nt <= 1) {
+    repack_host_rows(fmt, src, dst, N, K, 0, N);
+    return GQ_OK;
+  }
+  std::vector<std::thread> th;
+  for (size_t t = 0; t < nt; ++t) {
+    const size_t n0 = std::min(N, tiles * t / nt * 16), n1 = std::min(N, tiles * (t + 1) / nt * 16);
+    if (n0 < n1) th.emplace_back(repack_host_rows, fmt, src, dst, N, K, n0, n1);
+  }
+  for (auto &x : th) x.join();
   return GQ_OK;
 }
 
