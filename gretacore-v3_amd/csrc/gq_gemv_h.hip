@@ -95,14 +95,103 @@ GQ_DEV void magic4(uint32_t u, gq_half2 &lo, gq_half2 &hi) {
 
 GQ_DEV gq_half2 splat_h(uint32_t b16) { return gq_bits_h2((b16 & 0xFFFFu) * 0x10001u); }
 
-// The 16 weights a lane holds for MFMA step m -> fp16 B fragments (slots
-// 0..7, 8..15).  g is the lane's 16-lane group: its 16 weights are half g & 1
-// of 32-block 2 m + (g >> 1) of the chunk (Q6_K: 16-element scale group 4 m + g).
+// 4-bit codes straight to fp16: OR-ing a code into the low mantissa bits of
+// 1024.0 (0x6400) gives 1024 + q.  Of a code-group word (slots 0..3 in the
+// low nibbles of bytes 0..3, slots 4..7 in the high nibbles) four and-or ops
+// give the halves (s0, s2), (s4, s6) * 16, (s1, s3), (s5, s7) * 16 -- the high
+// nibbles come out as 1024 + 16 q.  Formats that use this order stage their
+// activations in the same order, with the "* 16" positions divided by 16
+// (exact), so each product is unchanged (kQ4Perm, kQ4Div16).
+// The magic is held in a VGPR (mg): a VOP3 and-or can then take the mask as its
+// one scalar operand and stays a single instruction.
+GQ_DEV uint32_t magic_h2_vgpr() {
+  uint32_t v;
+  asm volatile("v_mov_b32 %0, 0x64006400" : "=v"(v));
+  return v;
+}
+GQ_DEV void nib_halves(uint32_t w, uint32_t mg, gq_half2 (&p)[4]) {
+  const uint32_t v = w >> 8;
+  p[0] = gq_bits_h2((w & 0x000F000Fu) | mg);
+  p[1] = gq_bits_h2((w & 0x00F000F0u) | mg);
+  p[2] = gq_bits_h2((v & 0x000F000Fu) | mg);
+  p[3] = gq_bits_h2((v & 0x00F000F0u) | mg);
+}
+// B fragment element e of a 4-bit format holds slot kQ4Perm[e]; elements with
+// kQ4Div16 set are 16 x the weight
+constexpr int kQ4Perm[8] = {0, 2, 4, 6, 1, 3, 5, 7};
+constexpr bool kQ4Div16[8] = {false, false, true, true, false, false, true, true};
 template <int FMT>
-GQ_DEV void dequant_step(const HChunk<FMT> &c, int m, int g, gq_half8 &o0, gq_half8 &o1) {
+constexpr bool kNibOrder = FMT == GQ_FMT_Q4_0 || FMT == GQ_FMT_Q4_K;
+
+GQ_DEV _Float16 bits_h(uint32_t b16) { return __builtin_bit_cast(_Float16, (uint16_t)(b16 & 0xFFFFu)); }
+
+// The 16 weights a lane holds for MFMA step m -> fp16 B fragments (slots
+// 0..7, 8..15; for the 4-bit formats in nib_halves order).  g is the lane's
+// 16-lane group: its 16 weights are half g & 1 of 32-block 2 m + (g >> 1) of
+// the chunk (Q6_K: 16-element scale group 4 m + g).
+template <int FMT>
+GQ_DEV void dequant_step(const HChunk<FMT> &c, int m, int g, uint32_t mg, gq_half8 &o0, gq_half8 &o1) {
+  if constexpr (FMT == GQ_FMT_Q4_0 || FMT == GQ_FMT_Q4_K) {
+    uint32_t w0, w1;
+    gq_half2 a1, b1, a16, b16;  // (h * a + b) per pair; then * d2 + m2 (Q4_K)
+    gq_half2 d2, m1, m16;
+    if constexpr (FMT == GQ_FMT_Q4_0) {
+      w0 = c.q[2 * m];
+      w1 = c.q[2 * m + 1];
+      // (q - 8) * d: the subtraction is exact, the product rounds once (and
+      // 16 (q - 8) * d is 16 x that rounding)
+      const _Float16 d = bits_h(m ? (c.d >> 16) : c.d);
+      a1 = gq_half2{(_Float16)1.0f, (_Float16)1.0f};
+      b1 = gq_half2{(_Float16)-1032.0f, (_Float16)-1032.0f};
+      a16 = a1;
+      b16 = gq_half2{(_Float16)-1152.0f, (_Float16)-1152.0f};
+      d2 = gq_half2{d, d};
+    } else {
+      const gq_u4 &q = (m < 2) ? c.qa : c.qb;
+      w0 = q[2 * (m & 1)];
+      w1 = q[2 * (m & 1) + 1];
+      const uint32_t mv[4] = {c.meta[0], c.meta[1], c.meta[2], c.meta[3]};
+      uint32_t sc, mn;
+      gq_q4k_meta_codes(mv, 2 * m + (g >> 1), &sc, &mn);
+      // (1024 + q) * sc - 1024 sc = q * sc exactly (<= 945; 16 q sc <= 15120,
+      // a multiple of 16: exact too), then one rounding of q sc d - dmin m
+      const _Float16 hsc = (_Float16)(float)sc;
+      const _Float16 dmin = bits_h(mv[0] >> 16);
+      const _Float16 hm = (_Float16)(-((float)dmin * (float)mn));
+      a1 = gq_half2{hsc, hsc};
+      b1 = gq_half2{(_Float16)(-1024.0f * (float)sc), (_Float16)(-1024.0f * (float)sc)};
+      a16 = a1;
+      b16 = b1;
+      const _Float16 d = bits_h(mv[0]);
+      d2 = gq_half2{d, d};
+      m1 = gq_half2{hm, hm};
+      m16 = gq_half2{(_Float16)(16.0f * (float)hm), (_Float16)(16.0f * (float)hm)};
+    }
+#pragma unroll
+    for (int hw = 0; hw < 2; ++hw) {
+      gq_half2 p[4];
+      nib_halves(hw ? w1 : w0, mg, p);
+      gq_half8 &o = hw ? o1 : o0;
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const bool x16 = q & 1;
+        gq_half2 t;
+        if constexpr (FMT == GQ_FMT_Q4_0) {
+          t = (p[q] + (x16 ? b16 : b1)) * d2;
+        } else {
+          t = __builtin_elementwise_fma(__builtin_elementwise_fma(p[q], x16 ? a16 : a1, x16 ? b16 : b1), d2,
+                                        x16 ? m16 : m1);
+        }
+        o[2 * q] = t[0];
+        o[2 * q + 1] = t[1];
+      }
+    }
+    return;
+  } else {
   const int j = 2 * m + (g >> 1);
+  (void)j;
   uint32_t regs[4];
-  gq_half2 off, sc2, nsc2, d2, mn2;
+  gq_half2 off, d2;
   if constexpr (FMT == GQ_FMT_Q6_K) {
     const gq_u4 &q = (m < 2) ? c.qa : c.qb;
     const uint32_t w0 = q[2 * (m & 1)], w1 = q[2 * (m & 1) + 1], hw = c.hi[m];
@@ -115,61 +204,29 @@ GQ_DEV void dequant_step(const HChunk<FMT> &c, int m, int g, gq_half8 &o0, gq_ha
     // (c - 32) * (d * scale): the scale product rounded to fp16, then one
     // rounding of the exact (c - 32) * that
     const float sc = (float)(int8_t)((c.sc[m] >> (8 * g)) & 0xFFu);
-    const _Float16 hs = (_Float16)(gq_h2f(c.d & 0xFFFFu) * sc);
+    const _Float16 hs = (_Float16)((float)bits_h(c.d) * sc);
     off = gq_half2{(_Float16)-1056.0f, (_Float16)-1056.0f};
     d2 = gq_half2{hs, hs};
-  } else if constexpr (FMT == GQ_FMT_Q4_0) {
-    const uint32_t w0 = c.q[2 * m], w1 = c.q[2 * m + 1];
-    regs[0] = w0 & 0x0F0F0F0Fu;
-    regs[1] = (w0 >> 4) & 0x0F0F0F0Fu;
-    regs[2] = w1 & 0x0F0F0F0Fu;
-    regs[3] = (w1 >> 4) & 0x0F0F0F0Fu;
-    off = gq_half2{(_Float16)-1032.0f, (_Float16)-1032.0f};
-    d2 = splat_h(m ? (c.d >> 16) : c.d);
-  } else if constexpr (FMT == GQ_FMT_Q8_0) {
+  } else {  // Q8_0
     const gq_u4 &q = m ? c.q1 : c.q0;
 #pragma unroll
     for (int i = 0; i < 4; ++i) regs[i] = q[i] ^ 0x80808080u;
     off = gq_half2{(_Float16)-1152.0f, (_Float16)-1152.0f};
     d2 = splat_h(m ? (c.d >> 16) : c.d);
-  } else {
-    const gq_u4 &q = (m < 2) ? c.qa : c.qb;
-    const uint32_t w0 = q[2 * (m & 1)], w1 = q[2 * (m & 1) + 1];
-    regs[0] = w0 & 0x0F0F0F0Fu;
-    regs[1] = (w0 >> 4) & 0x0F0F0F0Fu;
-    regs[2] = w1 & 0x0F0F0F0Fu;
-    regs[3] = (w1 >> 4) & 0x0F0F0F0Fu;
-    const uint32_t mv[4] = {c.meta[0], c.meta[1], c.meta[2], c.meta[3]};
-    uint32_t sc, mn;
-    gq_q4k_meta_codes(mv, j, &sc, &mn);
-    const float d = gq_h2f(mv[0] & 0xFFFFu), dmin = gq_h2f(mv[0] >> 16);
-    const _Float16 hd = (_Float16)d;  // exact: d came from fp16 (NaN aside)
-    const _Float16 hsc = (_Float16)(float)sc, hnsc = (_Float16)(-1024.0f * (float)sc);
-    const _Float16 hmin = (_Float16)(-(dmin * (float)mn));
-    sc2 = gq_half2{hsc, hsc};
-    nsc2 = gq_half2{hnsc, hnsc};
-    d2 = gq_half2{hd, hd};
-    mn2 = gq_half2{hmin, hmin};
   }
 #pragma unroll
   for (int q = 0; q < 4; ++q) {
     gq_half2 lo, hi;
     magic4(regs[q], lo, hi);
-    if constexpr (FMT == GQ_FMT_Q4_K) {
-      // (1024 + c) * sc - 1024 sc = c * sc exactly, then one rounding of
-      // c * sc * d - dmin * m (magic4 of a 6-bit Q6_K code is 1024 + c too)
-      lo = __builtin_elementwise_fma(__builtin_elementwise_fma(lo, sc2, nsc2), d2, mn2);
-      hi = __builtin_elementwise_fma(__builtin_elementwise_fma(hi, sc2, nsc2), d2, mn2);
-    } else {
-      lo = (lo + off) * d2;  // exact (q - bias), one rounding of the product
-      hi = (hi + off) * d2;
-    }
+    lo = (lo + off) * d2;  // exact (q - bias), one rounding of the product
+    hi = (hi + off) * d2;
     gq_half8 &o = (q < 2) ? o0 : o1;
     const int b = 4 * (q & 1);
     o[b] = lo[0];
     o[b + 1] = lo[1];
     o[b + 2] = hi[0];
     o[b + 3] = hi[1];
+  }
   }
 }
 
@@ -188,6 +245,7 @@ constexpr int kWinBytes = kWin / 64 * 2 * 64 * 16;  // [64-k step][half][lane][8
 // (fp32, coalesced runs of 8) while the current window is consumed, then
 // converted into the other LDS buffer; one barrier per window.  A lane (g, r)
 // of the A fragment for 64-k step m, half j holds x[r][64 m + 16 g + 8 j + 0..7]
+// (4-bit formats: in kQ4Perm order, the kQ4Div16 elements divided by 16)
 // (rows >= batch are zero), matching the weights dequant_step gives lane
 // (g, r).  The KS parts' partial sums are reduced in LDS at the end.
 template <int FMT, int TW, int KS>
@@ -255,10 +313,14 @@ k_gemv_h(const uint8_t *__restrict__ w, size_t sc_off, const float *__restrict__
 #pragma unroll
     for (int u = 0; u < RPT; ++u) {
       gq_half8 h;
+      const float xv[8] = {xr[u][0][0], xr[u][0][1], xr[u][0][2], xr[u][0][3],
+                           xr[u][1][0], xr[u][1][1], xr[u][1][2], xr[u][1][3]};
 #pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        h[e] = (_Float16)xr[u][0][e];
-        h[4 + e] = (_Float16)xr[u][1][e];
+      for (int e = 0; e < 8; ++e) {
+        if constexpr (kNibOrder<FMT>)  // the weights' order, "x 16" positions divided by 16
+          h[e] = kQ4Div16[e] ? (_Float16)(xv[kQ4Perm[e]] * 0.0625f) : (_Float16)xv[kQ4Perm[e]];
+        else
+          h[e] = (_Float16)xv[e];
       }
       gq_u4 hv = __builtin_bit_cast(gq_u4, h);
 #pragma unroll
@@ -268,13 +330,14 @@ k_gemv_h(const uint8_t *__restrict__ w, size_t sc_off, const float *__restrict__
   };
 
   const int nwin = ((c1 - c0) + WC - 1) / WC;  // this wave's windows (<= NI)
+  const uint32_t mg = magic_h2_vgpr();
   HChunk<FMT> w0[WC], w1[WC], w2[WC];
   load_win(0, w0);
   load_win(1, w1);  // (a surplus re-read when NI == 1)
   load_x(0);
   store_x(0);
   __syncthreads();
-  gq_f4 acc = gq_f4{0.f, 0.f, 0.f, 0.f};
+  gq_f4 acc = gq_f4{0.f, 0.f, 0.f, 0.f}, acc2 = acc;  // chains of halves 0 and 1
   // Window `it` (weights in w0).  PF: the weights of window it + 2 and the
   // activations of window it + 1 are requested first.  The prefetch choice
   // is a compile-time constant at every call, so no load sits under a branch
@@ -294,9 +357,9 @@ k_gemv_h(const uint8_t *__restrict__ w, size_t sc_off, const float *__restrict__
             const gq_half8 a0 = *reinterpret_cast<const gq_half8 *>(xb + ((ms * 2 + 0) * 64 + lane) * 16);
             const gq_half8 a1 = *reinterpret_cast<const gq_half8 *>(xb + ((ms * 2 + 1) * 64 + lane) * 16);
             gq_half8 b0, b1;
-            dequant_step<FMT>(w0[j], m, g, b0, b1);
+            dequant_step<FMT>(w0[j], m, g, mg, b0, b1);
             acc = mfma16h(a0, b0, acc);
-            acc = mfma16h(a1, b1, acc);
+            acc2 = mfma16h(a1, b1, acc2);
           }
         }
       }
@@ -315,6 +378,8 @@ k_gemv_h(const uint8_t *__restrict__ w, size_t sc_off, const float *__restrict__
   for (; it + 2 < NI; ++it) window(it, T_{}, T_{});
   if (it + 1 < NI) window(it++, F_{}, T_{});
   window(it, F_{}, F_{});
+#pragma unroll
+  for (int v = 0; v < 4; ++v) acc[v] += acc2[v];
 
   // ---- reduce over the KS parts (LDS reused); D lane (g, r): batch rows 4g..4g+3, column r
   if constexpr (KS > 1) {
@@ -343,6 +408,142 @@ k_gemv_h(const uint8_t *__restrict__ w, size_t sc_off, const float *__restrict__
   }
 }
 
+// One-stage variant for K parts that fit: every wave issues the loads of ALL
+// its chunks up front (like the int8 GEMV), the workgroup stages its whole
+// activation range once (x loads are issued before the weight loads, so waiting
+// for them never waits for a weight), one barrier, then each wave consumes its
+// chunks in arrival order with no further synchronisation.  NCK (chunks per
+// wave) and the LDS size KS * NCK * CK * 32 bytes are compile-time; the host
+// picks this kernel only where both fit.
+template <int FMT, int TW, int KS, int NCK>
+__global__ void __launch_bounds__(64 * TW * KS)
+k_gemv_h1(const uint8_t *__restrict__ w, size_t sc_off, const float *__restrict__ x, float *__restrict__ y, int N,
+          int K, int C, int nb) {
+  using F = HFmt<FMT>;
+  constexpr int NT = 64 * TW * KS;
+  constexpr int PK = NCK * F::CK;                // k per part (padded)
+  constexpr int PB = PK * 32;                    // LDS bytes per part: [PK/64][2][64][16]
+  constexpr int RUNS = KS * 16 * (PK / 8);       // 8-element x runs
+  constexpr int RPT = (RUNS + NT - 1) / NT;
+  __shared__ __attribute__((aligned(16))) unsigned char xs[KS * PB];
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int tt = wave % TW, part = wave / TW;
+  const int g = lane >> 4, r = lane & 15;
+  const int ntiles = (int)gq_tiles(N);
+  const size_t tile = (size_t)blockIdx.x * TW + tt;
+  const size_t tb = (tile < (size_t)ntiles ? tile : (size_t)ntiles - 1) * (size_t)C;
+  const int c0 = (C * part) / KS, c1 = (C * (part + 1)) / KS;  // c0 < c1 (KS <= C)
+  const int nck = c1 - c0;                                     // <= NCK (host-checked)
+  const uint32_t qlane = 16u * (uint32_t)lane;
+  const uint32_t slane = (FMT == GQ_FMT_Q4_K || FMT == GQ_FMT_Q6_K) ? 16u * (uint32_t)r
+                                                                    : 8u * (uint32_t)r + 4u * (uint32_t)(g >> 1);
+
+  // ---- 1. activation loads (the workgroup's whole range), then weights -------
+  gq_f4 xr[RPT][2];
+  bool xin[RPT];
+  uint32_t xdst[RPT];
+#pragma unroll
+  for (int u = 0; u < RPT; ++u) {
+    const int run = (int)threadIdx.x + u * NT;
+    const int kr = run % (PK / 8), b = (run / (PK / 8)) % 16, p = run / (16 * (PK / 8));
+    const int pc0 = (C * p) / KS, pc1 = (C * (p + 1)) / KS;
+    const int k = pc0 * F::CK + 8 * kr;
+    const bool in = run < RUNS && b < nb && k < pc1 * F::CK && k < K;  // K % 32 == 0: runs are whole
+    const gq_f4 *src = reinterpret_cast<const gq_f4 *>(x + (in ? (size_t)b * K + k : 0));
+    xr[u][0] = src[0];
+    xr[u][1] = src[1];
+    xin[u] = in;
+    const int o = 8 * kr, ms = o >> 6, gq = (o & 63) >> 4, j = (o & 15) >> 3;
+    xdst[u] = run < RUNS ? (uint32_t)(p * PB + ((ms * 2 + j) * 64 + 16 * gq + b) * 16) : 0xFFFFFFFFu;
+  }
+  __builtin_amdgcn_sched_barrier(0);
+  HChunk<FMT> ch[NCK];
+#pragma unroll
+  for (int i = 0; i < NCK; ++i) {
+    const int ci = c0 + i < c1 ? c0 + i : c1 - 1;  // surplus loads re-read the last chunk
+    load_hchunk<FMT>(w + (tb + ci) * F::QB, w + sc_off + (tb + ci) * F::SB, qlane, slane, ch[i]);
+  }
+  __builtin_amdgcn_sched_barrier(0);
+
+  // ---- 2. activations -> fp16 A fragments in LDS --------------------------------
+#pragma unroll
+  for (int u = 0; u < RPT; ++u) {
+    if (RUNS % NT != 0 && xdst[u] == 0xFFFFFFFFu) continue;
+    const float xv[8] = {xr[u][0][0], xr[u][0][1], xr[u][0][2], xr[u][0][3],
+                         xr[u][1][0], xr[u][1][1], xr[u][1][2], xr[u][1][3]};
+    gq_half8 h;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      if constexpr (kNibOrder<FMT>)
+        h[e] = kQ4Div16[e] ? (_Float16)(xv[kQ4Perm[e]] * 0.0625f) : (_Float16)xv[kQ4Perm[e]];
+      else
+        h[e] = (_Float16)xv[e];
+    }
+    gq_u4 hv = __builtin_bit_cast(gq_u4, h);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) hv[e] = xin[u] ? hv[e] : 0u;
+    *reinterpret_cast<gq_u4 *>(xs + xdst[u]) = hv;
+  }
+  __syncthreads();
+
+  // ---- 3. consume ------------------------------------------------------------------
+  const uint32_t mg = magic_h2_vgpr();
+  const unsigned char *xb = xs + part * PB;
+  // two accumulator chains (halves 0 and 1 of each step), summed at the end
+  gq_f4 acc = gq_f4{0.f, 0.f, 0.f, 0.f}, acc2 = acc;
+  auto consume = [&](int i) {
+#pragma unroll
+    for (int m = 0; m < F::STEPS; ++m) {
+      const int ms = i * F::STEPS + m;
+      const gq_half8 a0 = *reinterpret_cast<const gq_half8 *>(xb + ((ms * 2 + 0) * 64 + lane) * 16);
+      const gq_half8 a1 = *reinterpret_cast<const gq_half8 *>(xb + ((ms * 2 + 1) * 64 + lane) * 16);
+      gq_half8 b0, b1;
+      dequant_step<FMT>(ch[i], m, g, mg, b0, b1);
+      acc = mfma16h(a0, b0, acc);
+      acc2 = mfma16h(a1, b1, acc2);
+    }
+  };
+  if (nck == NCK) {
+#pragma unroll
+    for (int i = 0; i < NCK; ++i) consume(i);
+  } else {
+#pragma unroll
+    for (int i = 0; i < NCK; ++i)
+      if (i < nck) consume(i);
+  }
+
+#pragma unroll
+  for (int v = 0; v < 4; ++v) acc[v] += acc2[v];
+
+  // ---- 4. reduce over the KS parts (LDS reused) ---------------------------------
+  if constexpr (KS > 1) {
+    __syncthreads();
+    gq_f4 *red = reinterpret_cast<gq_f4 *>(xs);  // [KS][TW][64]
+    red[(part * TW + tt) * 64 + lane] = acc;
+    __syncthreads();
+    if (part != 0) return;
+    gq_f4 sum = red[tt * 64 + lane];
+#pragma unroll
+    for (int q = 1; q < KS; ++q) {
+      const gq_f4 v = red[(q * TW + tt) * 64 + lane];
+      sum[0] += v[0];
+      sum[1] += v[1];
+      sum[2] += v[2];
+      sum[3] += v[3];
+    }
+    acc = sum;
+  }
+  const size_t row = tile * 16 + r;
+  if (tile < (size_t)ntiles && row < (size_t)N) {
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+      const int b = 4 * g + v;
+      if (b < nb) y[(size_t)b * N + row] = acc[v];
+    }
+  }
+}
+
 int env_int(const char *name) {
   const char *e = getenv(name);
   return e ? atoi(e) : 0;
@@ -357,6 +558,41 @@ int env_int(const char *name) {
 // (the double-buffered windows take KS x 16 KiB of LDS), at most one part
 // per chunk and at most 16 waves per workgroup.  chunks_per_wave is the
 // longest part.
+// Plan of the one-stage kernel (k_gemv_h1), or GQ_ERR_UNSUPPORTED where it does
+// not apply: 16 waves per workgroup as TW row tiles x (16 / TW) K parts, the
+// activations of all of K in LDS (32 bytes per k: K padded to whole parts must
+// stay within 128 KiB) and each wave's chunks in registers (kH1MaxChunks).  TW
+// is the largest that still gives every CU a workgroup.  GQ_GEMV_H1=0 turns
+// the kernel off, =1 forces it wherever it fits.
+int gq_gemv_h1_plan(int fmt, size_t N, size_t K, int *R_out, int *ks_out, int *cpw_out) {
+  const int f = gq_fmt_is_q4k(fmt) ? GQ_FMT_Q4_K : gq_fmt_is_q6k(fmt) ? GQ_FMT_Q6_K : fmt;
+  const int e = env_int("GQ_GEMV_H1");
+  if (e == 0 && getenv("GQ_GEMV_H1")) return GQ_ERR_UNSUPPORTED;
+  // measured: a win for the 4-bit formats on grids of up to 512 row tiles
+  // (e.g. 4096 x 4096 at batch 8: 7.6 vs 8.7 us), even at 14336 rows, and a
+  // loss for the register-heavy Q8_0 / Q6_K chunks
+  if (e != 1 && (f == GQ_FMT_Q8_0 || f == GQ_FMT_Q6_K || gq_tiles(N) > 512)) return GQ_ERR_UNSUPPORTED;
+  const int C = (int)gq_chunks(f, K);
+  const int CK = f == GQ_FMT_Q4_K || f == GQ_FMT_Q6_K ? 256 : 128;
+  const int maxc = f == GQ_FMT_Q4_0 || f == GQ_FMT_Q8_0 ? 8 : 4;
+  const size_t tiles = gq_tiles(N);
+  int tw = 8;
+  while (tw > 1 && (tiles + tw - 1) / tw < 224) tw /= 2;
+  const int ks = 16 / tw;
+  if (ks > C) return GQ_ERR_UNSUPPORTED;
+  int nck = (C + ks - 1) / ks;
+  int nckp = nck <= 1 ? 1 : nck <= 2 ? 2 : nck <= 4 ? 4 : 8;
+  if (nckp > maxc) return GQ_ERR_UNSUPPORTED;
+  if ((size_t)ks * nckp * CK * 32 > 128 * 1024) return GQ_ERR_UNSUPPORTED;
+  // one workgroup per CU (its LDS): more than one round of workgroups only
+  // when forced
+  if (e != 1 && (tiles + tw - 1) / tw > 256) return GQ_ERR_UNSUPPORTED;
+  *R_out = tw;
+  *ks_out = ks;
+  *cpw_out = nck;
+  return GQ_OK;
+}
+
 int gq_gemv_h_plan(int fmt, size_t N, size_t K, int *R_out, int *ks_out, int *cpw_out) {
   const int f = gq_fmt_is_q4k(fmt) ? GQ_FMT_Q4_K : gq_fmt_is_q6k(fmt) ? GQ_FMT_Q6_K : fmt;
   const int C = (int)gq_chunks(f, K);
@@ -400,9 +636,41 @@ int launch_h_tw(const void *packed, const float *x, float *y, int N, int K, int 
   return gq_last_launch();
 }
 
+// chunk registers a wave may hold in the one-stage kernel
+template <int FMT>
+constexpr int kH1MaxChunks = (FMT == GQ_FMT_Q4_0) ? 8 : (FMT == GQ_FMT_Q8_0) ? 8 : 4;
+
+template <int FMT, int TW, int KS>
+int launch_h1_nck(const void *packed, const float *x, float *y, int N, int K, int nb, int nck, hipStream_t s) {
+  const int C = (int)gq_chunks(FMT, K);
+  const size_t wgs = (gq_tiles(N) + TW - 1) / TW;
+  const size_t sc_off = gq_sc_plane_offset(FMT, N, K);
+  const uint8_t *w = (const uint8_t *)packed;
+  // instantiated only where the activations fit the LDS (KS * NCK * CK * 32 bytes)
+#define GQ_LAUNCH_H1(NCK)                                                                                          \
+  if constexpr (NCK <= kH1MaxChunks<FMT> && KS * NCK * HFmt<FMT>::CK * 32 <= 128 * 1024) {                         \
+    hipLaunchKernelGGL((k_gemv_h1<FMT, TW, KS, NCK>), dim3((unsigned)wgs), dim3(64 * TW * KS), 0, s, w, sc_off, x, \
+                       y, N, K, C, nb);                                                                            \
+    return gq_last_launch();                                                                                       \
+  }                                                                                                                \
+  return GQ_ERR_INVALID_ARGS;
+  if (nck <= 1) { GQ_LAUNCH_H1(1) }
+  if (nck <= 2) { GQ_LAUNCH_H1(2) }
+  if (nck <= 4) { GQ_LAUNCH_H1(4) }
+  if (nck <= 8) { GQ_LAUNCH_H1(8) }
+  return GQ_ERR_INVALID_ARGS;
+#undef GQ_LAUNCH_H1
+}
+
 template <int FMT>
 int launch_h(const void *packed, const float *x, float *y, int N, int K, int nb, hipStream_t s) {
   int tw, ks, cpw;
+  if (gq_gemv_h1_plan(FMT, N, K, &tw, &ks, &cpw) == GQ_OK) {
+    if (tw == 1) return launch_h1_nck<FMT, 1, 16>(packed, x, y, N, K, nb, cpw, s);
+    if (tw == 2) return launch_h1_nck<FMT, 2, 8>(packed, x, y, N, K, nb, cpw, s);
+    if (tw == 4) return launch_h1_nck<FMT, 4, 4>(packed, x, y, N, K, nb, cpw, s);
+    return launch_h1_nck<FMT, 8, 2>(packed, x, y, N, K, nb, cpw, s);
+  }
   GQ_TRY(gq_gemv_h_plan(FMT, N, K, &tw, &ks, &cpw));
   if (tw == 4) return launch_h_tw<FMT, 4>(packed, x, y, N, K, nb, ks, s);
   if (tw == 2) return launch_h_tw<FMT, 2>(packed, x, y, N, K, nb, ks, s);

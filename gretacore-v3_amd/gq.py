@@ -119,6 +119,12 @@ def load(path: str | None = None):
     p = path or LIB_PATH
     if not os.path.exists(p):
         raise GQError(f"libgq.so not built: {p} missing (run __graft_entry__.build())")
+    # PyTorch's HIP runtime must be loaded before libgq's (same soname): with
+    # the order reversed, libgq's HIP calls report no device on this image
+    try:
+        import torch  # noqa: F401
+    except ImportError:
+        pass
     lib = ctypes.CDLL(p)
     for name, (res, args) in _SIGS.items():
         fn = getattr(lib, name)

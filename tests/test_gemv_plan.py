@@ -58,6 +58,64 @@ def emulate_h(fmt, n, k, batch):
                     assert kk + 8 <= k  # a run of 8 is read only when wholly inside
 
 
+def h1_plan(fmt, n, k):
+    """The one-stage fp16 kernel's plan (k_gemv_h1), or None where gq_gemv
+    uses the windowed kernel: 4-bit formats, <= 512 row tiles, 16 waves as TW
+    tiles x 16 / TW parts, the activations of all of K in 128 KiB of LDS."""
+    if fmt not in (gq.FMT_Q4_0, gq.FMT_Q4_K):
+        return None
+    C = -(-k // CK[fmt])
+    tiles = -(-n // 16)
+    if tiles > 512:
+        return None
+    tw = 8
+    while tw > 1 and -(-tiles // tw) < 224:
+        tw //= 2
+    ks = 16 // tw
+    if ks > C:
+        return None
+    nck = -(-C // ks)
+    nckp = 1 if nck <= 1 else 2 if nck <= 2 else 4 if nck <= 4 else 8
+    if nckp > (8 if fmt == gq.FMT_Q4_0 else 4) or ks * nckp * CK[fmt] * 32 > 128 * 1024:
+        return None
+    if -(-tiles // tw) > 256:
+        return None
+    return tw, ks, nck
+
+
+def emulate_h1(fmt, n, k, batch, plan):
+    """Replays k_gemv_h1's chunk, activation-run and LDS arithmetic."""
+    TW, KS, nck_max = plan
+    C = -(-k // CK[fmt])
+    tiles = -(-n // 16)
+    wgs = -(-tiles // TW)
+    nckp = 1 if nck_max <= 1 else 2 if nck_max <= 2 else 4 if nck_max <= 4 else 8
+    PK = nckp * CK[fmt]
+    PB = PK * 32
+    assert KS * PB <= 128 * 1024
+    for part in range(KS):
+        c0, c1 = C * part // KS, C * (part + 1) // KS
+        assert 0 <= c0 < c1 <= C and c1 - c0 <= nckp
+        for i in range(nckp):
+            ci = min(c0 + i, c1 - 1)
+            for blk in (0, wgs - 1):
+                for tt in range(TW):
+                    t = min(blk * TW + tt, tiles - 1)
+                    assert (t * C + ci + 1) * QB[fmt] <= tiles * C * QB[fmt]
+                    assert (t * C + ci + 1) * SB[fmt] <= tiles * C * SB[fmt]
+    runs = KS * 16 * (PK // 8)
+    for run in range(runs):
+        kr, b, p = run % (PK // 8), (run // (PK // 8)) % 16, run // (16 * (PK // 8))
+        pc0, pc1 = C * p // KS, C * (p + 1) // KS
+        kk = pc0 * CK[fmt] + 8 * kr
+        if b < batch and kk < pc1 * CK[fmt] and kk < k:
+            assert kk + 8 <= k
+        o = 8 * kr
+        ms, g, j = o >> 6, (o & 63) >> 4, (o & 15) >> 3
+        dst = p * PB + ((ms * 2 + j) * 64 + 16 * g + b) * 16
+        assert 0 <= dst and dst + 16 <= KS * PB
+
+
 def emulate(fmt, n, k, batch):
     """Replays the int8 kernel's chunk/address arithmetic on the host."""
     R, ks, cpw = gq.gemv_plan(fmt, n, k, batch)
@@ -91,7 +149,12 @@ def test_gemv_plan_in_bounds(fmt, batch, monkeypatch):
         if k % (32 if fmt in (gq.FMT_Q4_0, gq.FMT_Q8_0) else 256):
             continue
         if batch >= 5 or fmt == gq.FMT_Q6_K:  # Q6_K: the fp16 kernel at every batch
-            emulate_h(fmt, n, k, batch)
+            p1 = h1_plan(fmt, n, k)
+            if p1 is not None:
+                assert gq.gemv_plan(fmt, n, k, batch) == p1
+                emulate_h1(fmt, n, k, batch, p1)
+            else:
+                emulate_h(fmt, n, k, batch)
     if fmt == gq.FMT_Q6_K:
         return
     # the int8 kernel at every batch (the split prep / prepped form uses it)

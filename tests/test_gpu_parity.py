@@ -234,3 +234,23 @@ def test_q6k_matmul_batches_the_gemv(dev):
     packed = _to_dev(gq.repack_host(O.Q6_K, w, n, k), dev)
     c = gq.matmul(O.Q6_K, packed, _to_dev(a, dev), n, k).cpu().numpy()
     assert O.rel_l2(c, O.gemv(O.Q6_K, w, a, n, k)) <= TOL
+
+
+def test_binding_loads_before_torch(dev):
+    """gq imported and loaded before torch in a fresh process still reaches the
+    device (libgq and torch must share one HIP runtime)."""
+    import os
+    import subprocess
+    import sys
+    root = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+    code = ("import sys; sys.path[:0] = [%r, %r]\n"
+            "import gq, numpy as np\n"
+            "gq.load()\n"
+            "import torch\n"
+            "w = np.zeros(gq.gguf_bytes(gq.FMT_Q8_0, 16, 32), np.uint8)\n"
+            "p = torch.from_numpy(gq.repack_host(gq.FMT_Q8_0, w, 16, 32)).cuda()\n"
+            "y = gq.gemv(gq.FMT_Q8_0, p, torch.ones(1, 32, device='cuda'), 16, 32)\n"
+            "assert float(y.abs().sum()) == 0.0\n"
+            "print('ok')\n") % (os.path.join(root, "gretacore-v3_amd"), os.path.join(root, "oracle"))
+    out = subprocess.run([sys.executable, "-c", code], capture_output=True, text=True, timeout=300)
+    assert out.returncode == 0 and "ok" in out.stdout, out.stderr[-2000:]
