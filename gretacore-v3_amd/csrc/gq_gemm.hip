@@ -467,6 +467,7 @@ GQ_DEV void q4k_factors(const RStep<GQ_FMT_Q4_K, NJ> &st, int step, QKf (&f)[NJ]
 template <int FMT, int NJ>
 GQ_DEV gq_half8 rfrag(const RStep<FMT, NJ> &st, int j, int ks, int step, const QKf *qk) {
   const int h = ks >> 1;
+
   gq_half2 p[4];
   if constexpr (FMT == GQ_FMT_Q8_0) {
     const gq_u4 &q = st.q[j][h];
