@@ -165,8 +165,10 @@ GQ_DEV void store_w(const WRec<FMT> &rec, int tl, int lane, int step, _Float16 *
     }
   } else {
     const uint32_t mv[4] = {rec.meta[0], rec.meta[1], rec.meta[2], rec.meta[3]};
-    const float d = gq_h2f(mv[0] & 0xFFFFu), dmin = gq_h2f(mv[0] >> 16);
-    const _Float16 hd = (_Float16)d;  // exact: d came from fp16 (NaN aside)
+    // the fp16 bits as they are (the reference's NaN-to-Inf conversion would
+    // compile to branches here)
+    const _Float16 hd = __builtin_bit_cast(_Float16, (uint16_t)(mv[0] & 0xFFFFu));
+    const float dmin = (float)__builtin_bit_cast(_Float16, (uint16_t)(mv[0] >> 16));
     const int j = 2 * (step & 3) + (g >> 1);
     uint32_t sc, mn;
     gq_q4k_meta_codes(mv, j, &sc, &mn);
@@ -448,8 +450,10 @@ GQ_DEV void q4k_factors(const RStep<GQ_FMT_Q4_K, NJ> &st, int step, QKf (&f)[NJ]
 #pragma unroll
   for (int j = 0; j < NJ; ++j) {
     const uint32_t mv[4] = {st.meta[j][0], st.meta[j][1], st.meta[j][2], st.meta[j][3]};
-    const float d = gq_h2f(mv[0] & 0xFFFFu), dmin = gq_h2f(mv[0] >> 16);
-    const _Float16 hd = (_Float16)d;  // exact: d came from fp16 (NaN aside)
+    // the fp16 bits as they are (the reference's NaN-to-Inf conversion would
+    // compile to branches here)
+    const _Float16 hd = __builtin_bit_cast(_Float16, (uint16_t)(mv[0] & 0xFFFFu));
+    const float dmin = (float)__builtin_bit_cast(_Float16, (uint16_t)(mv[0] >> 16));
 #pragma unroll
     for (int h = 0; h < 2; ++h) {
       uint32_t sc, mn;
@@ -467,7 +471,6 @@ GQ_DEV void q4k_factors(const RStep<GQ_FMT_Q4_K, NJ> &st, int step, QKf (&f)[NJ]
 template <int FMT, int NJ>
 GQ_DEV gq_half8 rfrag(const RStep<FMT, NJ> &st, int j, int ks, int step, const QKf *qk) {
   const int h = ks >> 1;
-
   gq_half2 p[4];
   if constexpr (FMT == GQ_FMT_Q8_0) {
     const gq_u4 &q = st.q[j][h];

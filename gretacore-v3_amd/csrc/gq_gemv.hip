@@ -26,6 +26,10 @@
 //    Q8_0 is signed.
 //  * Batch <= 4 stages the activations in-kernel (no workspace, one launch);
 //    batch 5..16 uses a prep kernel that writes the same limbs to a workspace.
+//  * Q6_K (batch 1..2): a lane's 16 k of an MFMA step are one 16-element scale
+//    group, so the A rows are (scale group, limb) x two batch rows and each
+//    lane applies its own group's d * sc; the -32 offset goes through
+//    16-element sums of the represented activation.
 #include <stdlib.h>
 
 #include "gq_internal.h"
@@ -46,6 +50,10 @@ template <>
 struct Fmt<GQ_FMT_Q4_K> {
   static constexpr int CK = 256, QB = 2048, SB = 256, MAXC = 4, STEPS = 4;
 };
+template <>
+struct Fmt<GQ_FMT_Q6_K> {
+  static constexpr int CK = 256, QB = 3072, SB = 288, MAXC = 4, STEPS = 4;
+};
 
 // weight registers of one chunk (one row tile)
 template <int FMT>
@@ -65,6 +73,13 @@ struct Chunk<GQ_FMT_Q4_K> {
   gq_u4 qa, qb;  // steps 0,1 and 2,3
   gq_u4 meta;    // d, dmin, W1, W2, W3 of this lane's row
 };
+template <>
+struct Chunk<GQ_FMT_Q6_K> {
+  gq_u4 qa, qb;  // low-nibble code groups, steps 0,1 and 2,3
+  gq_u4 hi;      // high 2-bit fields, one word per step
+  gq_u4 sc;      // the row's 16 int8 scales
+  uint32_t d;    // the row's fp16 d (low half)
+};
 
 // qp / sp: wave-uniform chunk bases; qo / so: this lane's 32-bit offsets
 template <int FMT>
@@ -77,9 +92,17 @@ GQ_DEV void load_chunk(const uint8_t *qp, const uint8_t *sp, uint32_t qo, uint32
     ch.q1 = gq_ld16_nt(qp + 1024 + qo);
     ch.d = gq_ld4_nt(sp + so);
   } else {
-    ch.qa = gq_ld16_nt(qp + qo);
-    ch.qb = gq_ld16_nt(qp + 1024 + qo);
-    ch.meta = gq_ld16_nt(sp + so);
+    if constexpr (FMT == GQ_FMT_Q4_K) {
+      ch.qa = gq_ld16_nt(qp + qo);
+      ch.qb = gq_ld16_nt(qp + 1024 + qo);
+      ch.meta = gq_ld16_nt(sp + so);
+    } else {  // Q6_K: so = 16 r
+      ch.qa = gq_ld16_nt(qp + qo);
+      ch.qb = gq_ld16_nt(qp + 1024 + qo);
+      ch.hi = gq_ld16_nt(qp + 2048 + qo);
+      ch.sc = gq_ld16_nt(sp + so);
+      ch.d = gq_ld4_nt(sp + 256 + 4 * (so >> 5)) >> (16 * ((so >> 4) & 1));
+    }
   }
 }
 
@@ -257,7 +280,8 @@ k_gemv_q(const GemvFuse fz, const float *__restrict__ x, const int8_t *__restric
   // fixed offset.
   Chunk<FMT> ch[R][NCK];
   const uint32_t qlane = 16u * (uint32_t)lane;
-  const uint32_t slane = (FMT == GQ_FMT_Q4_K) ? 16u * (uint32_t)r : 8u * (uint32_t)r + 4u * (uint32_t)(g >> 1);
+  const uint32_t slane = (FMT == GQ_FMT_Q4_K || FMT == GQ_FMT_Q6_K) ? 16u * (uint32_t)r
+                                                                    : 8u * (uint32_t)r + 4u * (uint32_t)(g >> 1);
   const uint8_t *qbase[R], *sbase[R];
 #pragma unroll
   for (int rt = 0; rt < R; ++rt) {
@@ -360,12 +384,22 @@ k_gemv_q(const GemvFuse fz, const float *__restrict__ x, const int8_t *__restric
       uint32_t la[2], lb[2];
       // block sum of the represented values: offsets and mins then act on
       // exactly the activation the integer products see
-      const float s = (float)quad_sum(split8(v, inv, la, lb)) * (sx * (1.0f / 254.0f));
+      // Q6_K (a scale per 16 elements): the two 16-element sums of the block,
+      // in the float4's second and fourth slots
+      const int t8 = split8(v, inv, la, lb);
+      float s, s_hi = 0.f;
+      if constexpr (FMT == GQ_FMT_Q6_K) {
+        const int p16 = t8 + __builtin_amdgcn_mov_dpp(t8, 0xB1, 0xF, 0xF, false);  // lanes 4j + {0,1} | {2,3}
+        s = (float)p16 * (sx * (1.0f / 254.0f));
+        s_hi = (float)__builtin_amdgcn_mov_dpp(p16, 0x4E, 0xF, 0xF, false) * (sx * (1.0f / 254.0f));
+      } else {
+        s = (float)quad_sum(t8) * (sx * (1.0f / 254.0f));
+      }
       if (8 * e8 < L.lk) {
         *reinterpret_cast<gq_u2 *>(lm + (2 * b) * L.lk + 8 * e8) = gq_u2{la[0], la[1]};
         *reinterpret_cast<gq_u2 *>(lm + (2 * b + 1) * L.lk + 8 * e8) = gq_u2{lb[0], lb[1]};
         if ((lane & 3) == 0)
-          *reinterpret_cast<gq_f4 *>(sc + 4 * (b * nblk + (e8 >> 2))) = gq_f4{sx, s, sx * (1.0f / 254.0f), 0.f};
+          *reinterpret_cast<gq_f4 *>(sc + 4 * (b * nblk + (e8 >> 2))) = gq_f4{sx, s, sx * (1.0f / 254.0f), s_hi};
       }
     }
     __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
@@ -388,8 +422,18 @@ k_gemv_q(const GemvFuse fz, const float *__restrict__ x, const int8_t *__restric
   // A operand: lane (row r, group g) is combination c = r >> 2 = (h, l) of
   // batch row 4 * mt + (r & 3); it carries data only where its lane group
   // covers block h of the MFMA pair ((g >> 1) == h), zeros otherwise.
+  // Q6_K (scales per 16 elements): row r is combination c = r >> 1 = (scale
+  // group q = r >> 2, limb l = (r >> 1) & 1) of batch row r & 1 (two batch
+  // rows per MFMA), with data where the lane group is that scale group
+  // (g == q); D lane (g, r') then holds group g's dots: value v is limb v >> 1
+  // of batch row v & 1.
   const int8_t *abase[MT];
-  {
+  if constexpr (FMT == GQ_FMT_Q6_K) {
+    static_assert(MT == 1 && NBC <= 2, "Q6_K: batch 1..2");
+    const int q = r >> 2, l = (r >> 1) & 1, b = r & 1;
+    const bool act = g == q && b < nb && b < NBC;
+    abase[0] = act ? limbs + (size_t)(2 * b + l) * lds_ld + (k0 - kbase) + 16 * g : zero + (k0 - kbase);
+  } else {
     const int c = r >> 2, h = c >> 1, l = c & 1;
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt) {
@@ -418,6 +462,35 @@ k_gemv_q(const GemvFuse fz, const float *__restrict__ x, const int8_t *__restric
     for (int m = 0; m < F::STEPS; ++m) {
       const int koff = i * F::CK + 64 * m;
       const int blk = (k0 - kbase) / 32 + i * BPC + 2 * m + hp;  // this lane's block, in scale rows
+      if constexpr (FMT == GQ_FMT_Q6_K) {
+        // lane (g, r): scale group 4 m + g of row r; D value v = (limb v >> 1,
+        // batch row v & 1); the 16-element sums give the -32 offset
+        const gq_i4 a0 = *reinterpret_cast<const gq_i4 *>(abase[0] + koff);
+        float sxl[NBC], szl[NBC], s16[NBC];
+#pragma unroll
+        for (int v = 0; v < NBC; ++v) {
+          const gq_f4 f = *reinterpret_cast<const gq_f4 *>(scl + 4 * ((size_t)(v < nb ? v : 0) * scl_ld + blk));
+          sxl[v] = f[0];
+          szl[v] = f[2];
+          s16[v] = (g & 1) ? f[3] : f[1];
+        }
+#pragma unroll
+        for (int rt = 0; rt < R; ++rt) {
+          const Chunk<FMT> &cc = ch[rt][i];
+          const gq_u4 &qq = (m < 2) ? cc.qa : cc.qb;
+          gq_i4 bop = codes16(qq[2 * (m & 1)], qq[2 * (m & 1) + 1]);
+          const uint32_t hw = cc.hi[m];
+#pragma unroll
+          for (int e = 0; e < 4; ++e) bop[e] |= (int)(((hw >> (2 * e)) & 0x03030303u) << 4);  // codes 0..63
+          const float ws = h16lo(cc.d) * (float)(int8_t)((cc.sc[m] >> (8 * g)) & 0xFFu);
+          const gq_i4 D = mfma_i8(a0, bop);
+#pragma unroll
+          for (int v = 0; v < NBC; ++v) {
+            acc[rt][0][v] += (ws * sxl[v]) * (float)D[v] + (ws * szl[v]) * (float)D[2 + v];
+            cor[rt][0][v] += ws * s16[v];
+          }
+        }
+      } else {
       gq_i4 a[MT];
       float2 sv[MT][NBC];
 #pragma unroll
@@ -462,6 +535,7 @@ k_gemv_q(const GemvFuse fz, const float *__restrict__ x, const int8_t *__restric
           }
         }
       }
+      }
     }
   };
   if (nck == NCK) {
@@ -474,7 +548,7 @@ k_gemv_q(const GemvFuse fz, const float *__restrict__ x, const int8_t *__restric
   }
 
   // ---- 5. reduce: lane groups (4 combinations), then the KSPLIT waves --------
-  constexpr float OFF = (FMT == GQ_FMT_Q4_0) ? 8.f : (FMT == GQ_FMT_Q4_K) ? 1.f : 0.f;
+  constexpr float OFF = (FMT == GQ_FMT_Q4_0) ? 8.f : (FMT == GQ_FMT_Q4_K) ? 1.f : (FMT == GQ_FMT_Q6_K) ? 32.f : 0.f;
   float part[R][MT][NBC];
 #pragma unroll
   for (int rt = 0; rt < R; ++rt)
@@ -582,9 +656,11 @@ int launch_r(const void *packed, const float *x, const void *ws, float *y, int N
 static int q_plan(int fmt, size_t N, size_t K, int batch, int *R_out, int *ksplit_out, int *chunks_per_wave_out) {
   GQ_TRY(gq_check_shape(fmt, N, K));
   GQ_CHECK(batch >= 1 && batch <= GQ_MAX_BATCH, GQ_ERR_UNSUPPORTED);
-  const int f = gq_fmt_is_q4k(fmt) ? GQ_FMT_Q4_K : fmt;
-  const int maxc = f == GQ_FMT_Q4_K ? Fmt<GQ_FMT_Q4_K>::MAXC : f == GQ_FMT_Q8_0 ? Fmt<GQ_FMT_Q8_0>::MAXC
-                                                                                  : Fmt<GQ_FMT_Q4_0>::MAXC;
+  const int f = gq_fmt_is_q4k(fmt) ? GQ_FMT_Q4_K : gq_fmt_is_q6k(fmt) ? GQ_FMT_Q6_K : fmt;
+  const int maxc = f == GQ_FMT_Q4_K   ? Fmt<GQ_FMT_Q4_K>::MAXC
+                   : f == GQ_FMT_Q6_K ? Fmt<GQ_FMT_Q6_K>::MAXC
+                   : f == GQ_FMT_Q8_0 ? Fmt<GQ_FMT_Q8_0>::MAXC
+                                      : Fmt<GQ_FMT_Q4_0>::MAXC;
   const int C = (int)gq_chunks(f, K);
   const size_t tiles = gq_tiles(N);
   const int mt = batch <= 4 ? 1 : (batch + 3) / 4;
@@ -615,11 +691,13 @@ static int q_plan(int fmt, size_t N, size_t K, int batch, int *R_out, int *kspli
 
 // The plan of the kernel gq_gemv launches for (fmt, N, K, batch): the int8
 // kernel above, or from batch gq_gemv_h_min() on the fp16 batch kernel.
+static bool gq_gemv_on_h(int fmt, size_t N, size_t K, int batch);
+
 extern "C" int gq_gemv_plan(int fmt, size_t N, size_t K, int batch, int *R_out, int *ksplit_out,
                             int *chunks_per_wave_out) {
   GQ_TRY(gq_check_shape(fmt, N, K));
   GQ_CHECK(batch >= 1 && batch <= GQ_MAX_BATCH, GQ_ERR_UNSUPPORTED);
-  if (batch < gq_gemv_h_min() && !gq_fmt_is_q6k(fmt)) return q_plan(fmt, N, K, batch, R_out, ksplit_out, chunks_per_wave_out);
+  if (!gq_gemv_on_h(fmt, N, K, batch)) return q_plan(fmt, N, K, batch, R_out, ksplit_out, chunks_per_wave_out);
   int R = 1, ks = 1, cpw = 0;
   if (gq_gemv_h1_plan(fmt, N, K, &R, &ks, &cpw) != GQ_OK) GQ_TRY(gq_gemv_h_plan(fmt, N, K, &R, &ks, &cpw));
   if (R_out) *R_out = R;
@@ -655,6 +733,11 @@ int launch_gemv(const void *packed, const float *x, const void *ws, float *y, in
 
 int dispatch(int fmt, const void *packed, const float *x, const void *ws, float *y, int N, int K, int nb,
              hipStream_t s) {
+  if (fmt == GQ_FMT_Q6_K) {  // fused staging, batch 1..2 only
+    if (!x || nb > 2) return GQ_ERR_UNSUPPORTED;
+    return nb == 1 ? launch_shape<GQ_FMT_Q6_K, 1, 1, false>(packed, x, nullptr, y, N, K, nb, s)
+                   : launch_shape<GQ_FMT_Q6_K, 2, 1, false>(packed, x, nullptr, y, N, K, nb, s);
+  }
   switch (fmt) {
   case GQ_FMT_Q4_0: return launch_gemv<GQ_FMT_Q4_0>(packed, x, ws, y, N, K, nb, s);
   case GQ_FMT_Q8_0: return launch_gemv<GQ_FMT_Q8_0>(packed, x, ws, y, N, K, nb, s);
@@ -673,6 +756,19 @@ int gq_gemv_h_min(void) {
   const char *e = getenv("GQ_GEMV_H_MIN");
   const int v = e ? atoi(e) : 0;
   return (v >= 1 && v <= GQ_MAX_BATCH + 1) ? v : 5;
+}
+
+// Which kernel gq_gemv uses: the fp16 batch kernel from gq_gemv_h_min() on,
+// for Q6_K beyond batch 2 (its int8 MFMA rows hold two batch rows), and where
+// K is too long for the int8 kernel's registers (more than 16 waves x MAXC
+// chunks: K > 16384); the int8 kernel otherwise.
+static bool gq_gemv_on_h(int fmt, size_t N, size_t K, int batch) {
+  if (batch >= gq_gemv_h_min() || (gq_fmt_is_q6k(fmt) && batch > 2)) return true;
+  int R = 1, ks = 2, cpw = 0;
+  if (q_plan(fmt, N, K, batch, &R, &ks, &cpw) != GQ_OK) return true;
+  const int f = gq_fmt_is_q4k(fmt) ? GQ_FMT_Q4_K : gq_fmt_is_q6k(fmt) ? GQ_FMT_Q6_K : fmt;
+  const int maxc = (f == GQ_FMT_Q4_K || f == GQ_FMT_Q6_K) ? 4 : 8;
+  return cpw > maxc / R;
 }
 
 extern "C" size_t gq_gemv_workspace_bytes(int fmt, size_t K, int batch) {
@@ -710,12 +806,12 @@ extern "C" int gq_gemv(int fmt, const void *packed, const float *x, float *y, si
   GQ_CHECK(packed && x && y, GQ_ERR_INVALID_ARGS);
   if (N == 0) return GQ_OK;
   if (K == 0) return gq_fill_zero(y, N * batch, (hipStream_t)stream);
-  // wide batches, and Q6_K at every batch, run on the fp16 matrix-core kernel
-  if (batch >= gq_gemv_h_min() || gq_fmt_is_q6k(fmt))
+  // wide batches, and Q6_K beyond batch 2, run on the fp16 matrix-core kernel
+  if (gq_gemv_on_h(fmt, N, K, batch))
     return gq_launch_gemv_h(fmt, packed, x, y, (int)N, (int)K, batch, (hipStream_t)stream);
   if (gq_gemv_fused(batch))
-    return dispatch(gq_fmt_is_q4k(fmt) ? GQ_FMT_Q4_K : fmt, packed, x, nullptr, y, (int)N, (int)K, batch,
-                    (hipStream_t)stream);
+    return dispatch(gq_fmt_is_q4k(fmt) ? GQ_FMT_Q4_K : gq_fmt_is_q6k(fmt) ? GQ_FMT_Q6_K : fmt, packed, x, nullptr,
+                    y, (int)N, (int)K, batch, (hipStream_t)stream);
   size_t need = gq_gemv_workspace_bytes(fmt, K, batch);
   if (!ws) {
     GQ_TRY(gq_default_workspace(need, &ws));

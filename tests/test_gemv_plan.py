@@ -11,7 +11,7 @@ import pytest
 
 import gq
 
-MAXC = {gq.FMT_Q4_0: 8, gq.FMT_Q8_0: 8, gq.FMT_Q4_K: 4, gq.FMT_Q4_K_GGML: 4}
+MAXC = {gq.FMT_Q4_0: 8, gq.FMT_Q8_0: 8, gq.FMT_Q4_K: 4, gq.FMT_Q4_K_GGML: 4, gq.FMT_Q6_K: 4}
 CK = {gq.FMT_Q4_0: 128, gq.FMT_Q8_0: 128, gq.FMT_Q4_K: 256, gq.FMT_Q4_K_GGML: 256, gq.FMT_Q6_K: 256}
 QB = {gq.FMT_Q4_0: 1024, gq.FMT_Q8_0: 2048, gq.FMT_Q4_K: 2048, gq.FMT_Q4_K_GGML: 2048, gq.FMT_Q6_K: 3072}
 
@@ -148,13 +148,18 @@ def test_gemv_plan_in_bounds(fmt, batch, monkeypatch):
     for n, k in SHAPES_H:
         if k % (32 if fmt in (gq.FMT_Q4_0, gq.FMT_Q8_0) else 256):
             continue
-        if batch >= 5 or fmt == gq.FMT_Q6_K:  # Q6_K: the fp16 kernel at every batch
+        # the int8 kernel holds up to 16 waves x MAXC chunks per row tile (K <=
+        # 16384); Q6_K uses it at batch 1..2; the fp16 kernel takes the rest
+        int8_fits = -(-k // CK[fmt]) <= 16 * MAXC[fmt]
+        if batch >= 5 or (fmt == gq.FMT_Q6_K and batch > 2) or not int8_fits:
             p1 = h1_plan(fmt, n, k)
             if p1 is not None:
                 assert gq.gemv_plan(fmt, n, k, batch) == p1
                 emulate_h1(fmt, n, k, batch, p1)
             else:
                 emulate_h(fmt, n, k, batch)
+        elif fmt == gq.FMT_Q6_K:
+            emulate(fmt, n, k, batch)
     if fmt == gq.FMT_Q6_K:
         return
     # the int8 kernel at every batch (the split prep / prepped form uses it)

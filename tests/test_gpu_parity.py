@@ -121,6 +121,14 @@ def test_gemv_baseline_shapes(dev, fmt, n, k):
     assert err <= TOL, err
 
 
+@pytest.mark.parametrize("fmt", [O.Q4_0, O.Q8_0, O.Q4_K, O.Q6_K])
+@pytest.mark.parametrize("batch", [1, 3])
+def test_gemv_long_k_falls_back(dev, fmt, batch):
+    """K beyond the int8 kernel's registers (> 16384) runs on the fp16 kernel."""
+    err = _gemv_case(dev, fmt, 48, 20480, batch, seed=300 + batch)
+    assert err <= TOL, err
+
+
 def test_gemv_special_inputs(dev):
     """All-8 nibbles -> zero weights; one-hot x selects a column."""
     import gq
