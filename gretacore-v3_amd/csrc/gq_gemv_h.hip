@@ -415,15 +415,21 @@ k_gemv_h(const uint8_t *__restrict__ w, size_t sc_off, const float *__restrict__
 // chunks in arrival order with no further synchronisation.  NCK (chunks per
 // wave) and the LDS size KS * NCK * CK * 32 bytes are compile-time; the host
 // picks this kernel only where both fit.
-template <int FMT, int TW, int KS, int NCK>
+//
+// MR (8 or 16) is the number of activation rows staged.  With MR = 8 (batch
+// <= 8) the LDS holds half as much (two workgroups per CU) and the lanes of
+// A rows 8..15 read rows 0..7 again: an A row only feeds the same row of D,
+// and D rows >= batch are never stored.
+template <int FMT, int TW, int KS, int NCK, int MR>
 __global__ void __launch_bounds__(64 * TW * KS)
 k_gemv_h1(const uint8_t *__restrict__ w, size_t sc_off, const float *__restrict__ x, float *__restrict__ y, int N,
           int K, int C, int nb) {
   using F = HFmt<FMT>;
+  static_assert(MR == 8 || MR == 16, "rows staged");
   constexpr int NT = 64 * TW * KS;
   constexpr int PK = NCK * F::CK;                // k per part (padded)
-  constexpr int PB = PK * 32;                    // LDS bytes per part: [PK/64][2][64][16]
-  constexpr int RUNS = KS * 16 * (PK / 8);       // 8-element x runs
+  constexpr int PB = PK * 2 * MR;                // LDS bytes per part: [PK/64][2][4][MR][16]
+  constexpr int RUNS = KS * MR * (PK / 8);       // 8-element x runs
   constexpr int RPT = (RUNS + NT - 1) / NT;
   __shared__ __attribute__((aligned(16))) unsigned char xs[KS * PB];
   const int lane = threadIdx.x & 63;
@@ -446,7 +452,7 @@ k_gemv_h1(const uint8_t *__restrict__ w, size_t sc_off, const float *__restrict_
 #pragma unroll
   for (int u = 0; u < RPT; ++u) {
     const int run = (int)threadIdx.x + u * NT;
-    const int kr = run % (PK / 8), b = (run / (PK / 8)) % 16, p = run / (16 * (PK / 8));
+    const int kr = run % (PK / 8), b = (run / (PK / 8)) % MR, p = run / (MR * (PK / 8));
     const int pc0 = (C * p) / KS, pc1 = (C * (p + 1)) / KS;
     const int k = pc0 * F::CK + 8 * kr;
     const bool in = run < RUNS && b < nb && k < pc1 * F::CK && k < K;  // K % 32 == 0: runs are whole
@@ -455,7 +461,7 @@ k_gemv_h1(const uint8_t *__restrict__ w, size_t sc_off, const float *__restrict_
     xr[u][1] = src[1];
     xin[u] = in;
     const int o = 8 * kr, ms = o >> 6, gq = (o & 63) >> 4, j = (o & 15) >> 3;
-    xdst[u] = run < RUNS ? (uint32_t)(p * PB + ((ms * 2 + j) * 64 + 16 * gq + b) * 16) : 0xFFFFFFFFu;
+    xdst[u] = run < RUNS ? (uint32_t)(p * PB + (((ms * 2 + j) * 4 + gq) * MR + b) * 16) : 0xFFFFFFFFu;
   }
   __builtin_amdgcn_sched_barrier(0);
   HChunk<FMT> ch[NCK];
@@ -489,15 +495,16 @@ k_gemv_h1(const uint8_t *__restrict__ w, size_t sc_off, const float *__restrict_
 
   // ---- 3. consume ------------------------------------------------------------------
   const uint32_t mg = magic_h2_vgpr();
-  const unsigned char *xb = xs + part * PB;
+  // this lane's A row: r (MR = 16) or r & 7 (MR = 8)
+  const unsigned char *xb = xs + part * PB + (g * MR + (r & (MR - 1))) * 16;
   // two accumulator chains (halves 0 and 1 of each step), summed at the end
   gq_f4 acc = gq_f4{0.f, 0.f, 0.f, 0.f}, acc2 = acc;
   auto consume = [&](int i) {
 #pragma unroll
     for (int m = 0; m < F::STEPS; ++m) {
       const int ms = i * F::STEPS + m;
-      const gq_half8 a0 = *reinterpret_cast<const gq_half8 *>(xb + ((ms * 2 + 0) * 64 + lane) * 16);
-      const gq_half8 a1 = *reinterpret_cast<const gq_half8 *>(xb + ((ms * 2 + 1) * 64 + lane) * 16);
+      const gq_half8 a0 = *reinterpret_cast<const gq_half8 *>(xb + (ms * 2 + 0) * 4 * MR * 16);
+      const gq_half8 a1 = *reinterpret_cast<const gq_half8 *>(xb + (ms * 2 + 1) * 4 * MR * 16);
       gq_half8 b0, b1;
       dequant_step<FMT>(ch[i], m, g, mg, b0, b1);
       acc = mfma16h(a0, b0, acc);
@@ -560,33 +567,35 @@ int env_int(const char *name) {
 // longest part.
 // Plan of the one-stage kernel (k_gemv_h1), or GQ_ERR_UNSUPPORTED where it does
 // not apply: 16 waves per workgroup as TW row tiles x (16 / TW) K parts, the
-// activations of all of K in LDS (32 bytes per k: K padded to whole parts must
-// stay within 128 KiB) and each wave's chunks in registers (kH1MaxChunks).  TW
-// is the largest that still gives every CU a workgroup.  GQ_GEMV_H1=0 turns
-// the kernel off, =1 forces it wherever it fits.
-int gq_gemv_h1_plan(int fmt, size_t N, size_t K, int *R_out, int *ks_out, int *cpw_out) {
+// activations of all of K in LDS (MR rows x 2 bytes per k: 8 rows up to batch
+// 8, else 16; at most 128 KiB) and each wave's chunks in registers
+// (kH1MaxChunks).  Workgroups per CU: 2 with 8 rows (<= 64 KiB), else 1; TW is
+// the largest that still gives every slot a workgroup, in one round.  Not for
+// the register-heavy Q8_0 / Q6_K chunks.  GQ_GEMV_H1=0 turns the kernel off,
+// =1 forces it wherever it fits.
+int gq_gemv_h1_plan(int fmt, size_t N, size_t K, int nb, int *R_out, int *ks_out, int *cpw_out) {
   const int f = gq_fmt_is_q4k(fmt) ? GQ_FMT_Q4_K : gq_fmt_is_q6k(fmt) ? GQ_FMT_Q6_K : fmt;
   const int e = env_int("GQ_GEMV_H1");
   if (e == 0 && getenv("GQ_GEMV_H1")) return GQ_ERR_UNSUPPORTED;
-  // measured: a win for the 4-bit formats on grids of up to 512 row tiles
-  // (e.g. 4096 x 4096 at batch 8: 7.6 vs 8.7 us), even at 14336 rows, and a
-  // loss for the register-heavy Q8_0 / Q6_K chunks
-  if (e != 1 && (f == GQ_FMT_Q8_0 || f == GQ_FMT_Q6_K || gq_tiles(N) > 512)) return GQ_ERR_UNSUPPORTED;
+  if (e != 1 && (f == GQ_FMT_Q8_0 || f == GQ_FMT_Q6_K)) return GQ_ERR_UNSUPPORTED;
   const int C = (int)gq_chunks(f, K);
   const int CK = f == GQ_FMT_Q4_K || f == GQ_FMT_Q6_K ? 256 : 128;
   const int maxc = f == GQ_FMT_Q4_0 || f == GQ_FMT_Q8_0 ? 8 : 4;
+  const int mr = nb <= 8 ? 8 : 16;
+  const size_t slots = 256 * (mr == 8 ? 2 : 1);
   const size_t tiles = gq_tiles(N);
   int tw = 8;
-  while (tw > 1 && (tiles + tw - 1) / tw < 224) tw /= 2;
+  while (tw > 1 && (tiles + tw - 1) / tw < slots * 7 / 8) tw /= 2;
   const int ks = 16 / tw;
   if (ks > C) return GQ_ERR_UNSUPPORTED;
-  int nck = (C + ks - 1) / ks;
-  int nckp = nck <= 1 ? 1 : nck <= 2 ? 2 : nck <= 4 ? 4 : 8;
+  const int nck = (C + ks - 1) / ks;
+  const int nckp = nck <= 1 ? 1 : nck <= 2 ? 2 : nck <= 4 ? 4 : nck <= 8 ? 8 : 16;
   if (nckp > maxc) return GQ_ERR_UNSUPPORTED;
-  if ((size_t)ks * nckp * CK * 32 > 128 * 1024) return GQ_ERR_UNSUPPORTED;
-  // one workgroup per CU (its LDS): more than one round of workgroups only
-  // when forced
-  if (e != 1 && (tiles + tw - 1) / tw > 256) return GQ_ERR_UNSUPPORTED;
+  if ((size_t)ks * nckp * CK * 2 * mr > (mr == 8 ? 64 : 128) * 1024) return GQ_ERR_UNSUPPORTED;
+  // 16 rows (one workgroup per CU): measured a win on grids of up to 512 row
+  // tiles only (4096 x 4096: 7.6 vs 8.7 us; 14336 rows: 13.9 vs 13.5 us)
+  if (e != 1 && mr == 16 && tiles > 512) return GQ_ERR_UNSUPPORTED;
+  if (e != 1 && (tiles + tw - 1) / tw > slots) return GQ_ERR_UNSUPPORTED;
   *R_out = tw;
   *ks_out = ks;
   *cpw_out = nck;
@@ -640,7 +649,7 @@ int launch_h_tw(const void *packed, const float *x, float *y, int N, int K, int 
 template <int FMT>
 constexpr int kH1MaxChunks = (FMT == GQ_FMT_Q4_0) ? 8 : (FMT == GQ_FMT_Q8_0) ? 8 : 4;
 
-template <int FMT, int TW, int KS>
+template <int FMT, int TW, int KS, int MR>
 int launch_h1_nck(const void *packed, const float *x, float *y, int N, int K, int nb, int nck, hipStream_t s) {
   const int C = (int)gq_chunks(FMT, K);
   const size_t wgs = (gq_tiles(N) + TW - 1) / TW;
@@ -648,9 +657,9 @@ int launch_h1_nck(const void *packed, const float *x, float *y, int N, int K, in
   const uint8_t *w = (const uint8_t *)packed;
   // instantiated only where the activations fit the LDS (KS * NCK * CK * 32 bytes)
 #define GQ_LAUNCH_H1(NCK)                                                                                          \
-  if constexpr (NCK <= kH1MaxChunks<FMT> && KS * NCK * HFmt<FMT>::CK * 32 <= 128 * 1024) {                         \
-    hipLaunchKernelGGL((k_gemv_h1<FMT, TW, KS, NCK>), dim3((unsigned)wgs), dim3(64 * TW * KS), 0, s, w, sc_off, x, \
-                       y, N, K, C, nb);                                                                            \
+  if constexpr (NCK <= kH1MaxChunks<FMT> && KS * NCK * HFmt<FMT>::CK * 2 * MR <= 128 * 1024) {                     \
+    hipLaunchKernelGGL((k_gemv_h1<FMT, TW, KS, NCK, MR>), dim3((unsigned)wgs), dim3(64 * TW * KS), 0, s, w, sc_off, \
+                       x, y, N, K, C, nb);                                                                         \
     return gq_last_launch();                                                                                       \
   }                                                                                                                \
   return GQ_ERR_INVALID_ARGS;
@@ -665,11 +674,17 @@ int launch_h1_nck(const void *packed, const float *x, float *y, int N, int K, in
 template <int FMT>
 int launch_h(const void *packed, const float *x, float *y, int N, int K, int nb, hipStream_t s) {
   int tw, ks, cpw;
-  if (gq_gemv_h1_plan(FMT, N, K, &tw, &ks, &cpw) == GQ_OK) {
-    if (tw == 1) return launch_h1_nck<FMT, 1, 16>(packed, x, y, N, K, nb, cpw, s);
-    if (tw == 2) return launch_h1_nck<FMT, 2, 8>(packed, x, y, N, K, nb, cpw, s);
-    if (tw == 4) return launch_h1_nck<FMT, 4, 4>(packed, x, y, N, K, nb, cpw, s);
-    return launch_h1_nck<FMT, 8, 2>(packed, x, y, N, K, nb, cpw, s);
+  if (gq_gemv_h1_plan(FMT, N, K, nb, &tw, &ks, &cpw) == GQ_OK) {
+    if (nb <= 8) {
+      if (tw == 1) return launch_h1_nck<FMT, 1, 16, 8>(packed, x, y, N, K, nb, cpw, s);
+      if (tw == 2) return launch_h1_nck<FMT, 2, 8, 8>(packed, x, y, N, K, nb, cpw, s);
+      if (tw == 4) return launch_h1_nck<FMT, 4, 4, 8>(packed, x, y, N, K, nb, cpw, s);
+      return launch_h1_nck<FMT, 8, 2, 8>(packed, x, y, N, K, nb, cpw, s);
+    }
+    if (tw == 1) return launch_h1_nck<FMT, 1, 16, 16>(packed, x, y, N, K, nb, cpw, s);
+    if (tw == 2) return launch_h1_nck<FMT, 2, 8, 16>(packed, x, y, N, K, nb, cpw, s);
+    if (tw == 4) return launch_h1_nck<FMT, 4, 4, 16>(packed, x, y, N, K, nb, cpw, s);
+    return launch_h1_nck<FMT, 8, 2, 16>(packed, x, y, N, K, nb, cpw, s);
   }
   GQ_TRY(gq_gemv_h_plan(FMT, N, K, &tw, &ks, &cpw));
   if (tw == 4) return launch_h_tw<FMT, 4>(packed, x, y, N, K, nb, ks, s);

@@ -58,27 +58,30 @@ def emulate_h(fmt, n, k, batch):
                     assert kk + 8 <= k  # a run of 8 is read only when wholly inside
 
 
-def h1_plan(fmt, n, k):
+def h1_plan(fmt, n, k, batch):
     """The one-stage fp16 kernel's plan (k_gemv_h1), or None where gq_gemv
-    uses the windowed kernel: 4-bit formats, <= 512 row tiles, 16 waves as TW
-    tiles x 16 / TW parts, the activations of all of K in 128 KiB of LDS."""
+    uses the windowed kernel: 4-bit formats, 16 waves as TW tiles x 16 / TW
+    parts, MR (8 up to batch 8, else 16) activation rows of all of K in LDS
+    (64 / 128 KiB: 2 / 1 workgroups per CU), one round of workgroups."""
     if fmt not in (gq.FMT_Q4_0, gq.FMT_Q4_K):
         return None
     C = -(-k // CK[fmt])
     tiles = -(-n // 16)
-    if tiles > 512:
-        return None
+    mr = 8 if batch <= 8 else 16
+    slots = 256 * (2 if mr == 8 else 1)
     tw = 8
-    while tw > 1 and -(-tiles // tw) < 224:
+    while tw > 1 and -(-tiles // tw) < slots * 7 // 8:
         tw //= 2
     ks = 16 // tw
     if ks > C:
         return None
     nck = -(-C // ks)
-    nckp = 1 if nck <= 1 else 2 if nck <= 2 else 4 if nck <= 4 else 8
-    if nckp > (8 if fmt == gq.FMT_Q4_0 else 4) or ks * nckp * CK[fmt] * 32 > 128 * 1024:
+    nckp = 1 if nck <= 1 else 2 if nck <= 2 else 4 if nck <= 4 else 8 if nck <= 8 else 16
+    if nckp > (8 if fmt == gq.FMT_Q4_0 else 4) or ks * nckp * CK[fmt] * 2 * mr > (64 if mr == 8 else 128) * 1024:
         return None
-    if -(-tiles // tw) > 256:
+    if mr == 16 and tiles > 512:
+        return None
+    if -(-tiles // tw) > slots:
         return None
     return tw, ks, nck
 
@@ -89,9 +92,10 @@ def emulate_h1(fmt, n, k, batch, plan):
     C = -(-k // CK[fmt])
     tiles = -(-n // 16)
     wgs = -(-tiles // TW)
+    mr = 8 if batch <= 8 else 16
     nckp = 1 if nck_max <= 1 else 2 if nck_max <= 2 else 4 if nck_max <= 4 else 8
     PK = nckp * CK[fmt]
-    PB = PK * 32
+    PB = PK * 2 * mr
     assert KS * PB <= 128 * 1024
     for part in range(KS):
         c0, c1 = C * part // KS, C * (part + 1) // KS
@@ -103,17 +107,25 @@ def emulate_h1(fmt, n, k, batch, plan):
                     t = min(blk * TW + tt, tiles - 1)
                     assert (t * C + ci + 1) * QB[fmt] <= tiles * C * QB[fmt]
                     assert (t * C + ci + 1) * SB[fmt] <= tiles * C * SB[fmt]
-    runs = KS * 16 * (PK // 8)
+    runs = KS * mr * (PK // 8)
     for run in range(runs):
-        kr, b, p = run % (PK // 8), (run // (PK // 8)) % 16, run // (16 * (PK // 8))
+        kr, b, p = run % (PK // 8), (run // (PK // 8)) % mr, run // (mr * (PK // 8))
         pc0, pc1 = C * p // KS, C * (p + 1) // KS
         kk = pc0 * CK[fmt] + 8 * kr
         if b < batch and kk < pc1 * CK[fmt] and kk < k:
             assert kk + 8 <= k
         o = 8 * kr
         ms, g, j = o >> 6, (o & 63) >> 4, (o & 15) >> 3
-        dst = p * PB + ((ms * 2 + j) * 64 + 16 * g + b) * 16
+        dst = p * PB + (((ms * 2 + j) * 4 + g) * mr + b) * 16
         assert 0 <= dst and dst + 16 <= KS * PB
+    # A reads: lane (g, r) at step ms, half j reads row r & (mr - 1)
+    for part in range(KS):
+        for ms in range(PK // 64):
+            for j in range(2):
+                for g in range(4):
+                    for r in range(16):
+                        off = part * PB + (g * mr + (r & (mr - 1))) * 16 + (ms * 2 + j) * 4 * mr * 16
+                        assert off + 16 <= KS * PB
 
 
 def emulate(fmt, n, k, batch):
@@ -152,7 +164,7 @@ def test_gemv_plan_in_bounds(fmt, batch, monkeypatch):
         # 16384); Q6_K uses it at batch 1..2; the fp16 kernel takes the rest
         int8_fits = -(-k // CK[fmt]) <= 16 * MAXC[fmt]
         if batch >= 5 or (fmt == gq.FMT_Q6_K and batch > 2) or not int8_fits:
-            p1 = h1_plan(fmt, n, k)
+            p1 = h1_plan(fmt, n, k, batch)
             if p1 is not None:
                 assert gq.gemv_plan(fmt, n, k, batch) == p1
                 emulate_h1(fmt, n, k, batch, p1)

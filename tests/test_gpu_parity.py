@@ -121,6 +121,17 @@ def test_gemv_baseline_shapes(dev, fmt, n, k):
     assert err <= TOL, err
 
 
+@pytest.mark.parametrize("fmt", [O.Q4_0, O.Q4_K])
+@pytest.mark.parametrize("shape,batch", [((4096, 4096), 8), ((4096, 4096), 12), ((7168, 2048), 6),
+                                         ((14336, 1024), 16), ((1000, 4096), 5), ((2048, 14336), 7)])
+def test_gemv_batch_kernel_plans(dev, fmt, shape, batch):
+    """Shapes that take each batch-kernel plan: one-stage with 8 and with 16
+    staged rows, the windowed kernel, ragged rows, long K."""
+    n, k = shape
+    err = _gemv_case(dev, fmt, n, k, batch, seed=400 + batch)
+    assert err <= TOL, err
+
+
 @pytest.mark.parametrize("fmt", [O.Q4_0, O.Q8_0, O.Q4_K, O.Q6_K])
 @pytest.mark.parametrize("batch", [1, 3])
 def test_gemv_long_k_falls_back(dev, fmt, batch):
