@@ -349,6 +349,9 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-decode-step", action="store_true")
     ap.add_argument("--no-load", action="store_true", help="skip the GGUF load-throughput extra")
+    ap.add_argument("--only", default=None,
+                    help="only the named GEMV config of the 'extra' field (e.g. q6_k_lm_head_128256x4096_b1), "
+                         "after a 64 MiB copy for counter calibration (for profiling)")
     ap.add_argument("--gemm-only", action="store_true",
                     help="only the Q4_0 M=2048 14336x4096 prefill GEMM, --steps times (for profiling)")
     args = ap.parse_args()
@@ -368,7 +371,13 @@ def main():
         r = bench_gemm(O.Q4_0, 2048, 14336, 4096, steps, warmup, dev)
         print(json.dumps({"gemm_q4_0_m2048_14336x4096": r}), flush=True)
         return
-    if args.headline_only:
+    gemv_cfgs = [("q8_0_4096x4096_b1", O.Q8_0, 4096, 4096, 1, 1001),
+                 ("q8_0_lm_head_128256x4096_b1", O.Q8_0, 128256, 4096, 1, 1005),
+                 ("q6_k_lm_head_128256x4096_b1", O.Q6_K, 128256, 4096, 1, 1006),
+                 ("q4_0_4096x4096_b1", O.Q4_0, 4096, 4096, 1, 1002),
+                 ("q4_0_4096x14336_b1", O.Q4_0, 4096, 14336, 1, 1002)]
+    gemv_cfgs += [(f"q4_k_14336x4096_b{b}", O.Q4_K, 14336, 4096, b, 1003) for b in (1, 4, 8, 16)]
+    if args.headline_only or args.only:
         # a plain copy of known size, so profiler byte counters can be
         # calibrated against the GEMV dispatches of the same run
         src = torch.empty(64 << 20, dtype=torch.uint8, device=dev).fill_(1)
@@ -377,18 +386,21 @@ def main():
             torch.bitwise_not(src, out=dst)  # reads 64 MiB, writes 64 MiB
         torch.cuda.synchronize()
         del src, dst
+    if args.only:
+        cfg = [c for c in gemv_cfgs if c[0] == args.only]
+        if not cfg:
+            print(f"--only: unknown config {args.only}; one of {[c[0] for c in gemv_cfgs]}", file=sys.stderr)
+            sys.exit(2)
+        name, fmt, n, k, b, seed = cfg[0]
+        c = GemvCase(fmt, n, k, b, wseed=seed, xseed=seed + 1000, dev=dev)
+        print(json.dumps({name: bench_gemv(c, steps, warmup)}), flush=True)
+        return
     log("[bench] headline: Q4_0 GEMV 14336x4096 batch 1")
     head = GemvCase(O.Q4_0, 14336, 4096, 1, wseed=1002, xseed=2002, dev=dev)
     h = bench_gemv(head, steps, warmup)
     log(f"[bench] headline {h}")
     extra = {}
     if not args.headline_only:
-        gemv_cfgs = [("q8_0_4096x4096_b1", O.Q8_0, 4096, 4096, 1, 1001),
-                     ("q8_0_lm_head_128256x4096_b1", O.Q8_0, 128256, 4096, 1, 1005),
-                     ("q6_k_lm_head_128256x4096_b1", O.Q6_K, 128256, 4096, 1, 1006),
-                     ("q4_0_4096x4096_b1", O.Q4_0, 4096, 4096, 1, 1002),
-                     ("q4_0_4096x14336_b1", O.Q4_0, 4096, 14336, 1, 1002)]
-        gemv_cfgs += [(f"q4_k_14336x4096_b{b}", O.Q4_K, 14336, 4096, b, 1003) for b in (1, 4, 8, 16)]
         for name, fmt, n, k, b, seed in gemv_cfgs:
             log(f"[bench] {name}")
             c = GemvCase(fmt, n, k, b, wseed=seed, xseed=seed + 1000, dev=dev)
