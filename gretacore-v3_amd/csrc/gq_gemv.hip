@@ -491,50 +491,51 @@ k_gemv_q(const GemvFuse fz, const float *__restrict__ x, const int8_t *__restric
           }
         }
       } else {
-      gq_i4 a[MT];
-      float2 sv[MT][NBC];
-#pragma unroll
-      for (int mt = 0; mt < MT; ++mt) {
-        a[mt] = *reinterpret_cast<const gq_i4 *>(abase[mt] + koff);
-#pragma unroll
-        for (int v = 0; v < NBC; ++v) {
-          const int b = 4 * mt + v;
-          sv[mt][v] = *reinterpret_cast<const float2 *>(scl + 4 * ((size_t)(b < nb ? b : 0) * scl_ld + blk) + 2 * lp);
-        }
-      }
-#pragma unroll
-      for (int rt = 0; rt < R; ++rt) {
-        const Chunk<FMT> &cc = ch[rt][i];
-        gq_i4 bop;
-        float ws, wm = 0.f;  // weight scale and offset/min factor of block (2m + h')
-        if constexpr (FMT == GQ_FMT_Q4_0) {
-          bop = codes16(cc.q[2 * m], cc.q[2 * m + 1]);
-          ws = m ? h16hi(cc.d) : h16lo(cc.d);
-          wm = ws;
-        } else if constexpr (FMT == GQ_FMT_Q8_0) {
-          const gq_u4 &qq = m ? cc.q1 : cc.q0;
-          bop = gq_i4{(int)qq[0], (int)qq[1], (int)qq[2], (int)qq[3]};
-          ws = m ? h16hi(cc.d) : h16lo(cc.d);
-        } else {
-          const uint32_t w0 = (m < 2) ? cc.qa[2 * (m & 1)] : cc.qb[2 * (m & 1)];
-          const uint32_t w1 = (m < 2) ? cc.qa[2 * (m & 1) + 1] : cc.qb[2 * (m & 1) + 1];
-          bop = codes16(w0, w1);
-          const uint32_t wsc = hp ? cc.meta[2] : cc.meta[1];
-          const uint32_t byte = (wsc >> (8 * m)) & 0xFFu;
-          const uint32_t b3 = (cc.meta[3] >> (8 * m + 4 * hp)) & 15u;
-          ws = h16lo(cc.meta[0]) * (float)(byte & 63u);
-          wm = h16hi(cc.meta[0]) * (float)((byte >> 6) | (b3 << 2));
-        }
+        gq_i4 a[MT];
+        float2 sv[MT][NBC];
 #pragma unroll
         for (int mt = 0; mt < MT; ++mt) {
-          const gq_i4 D = mfma_i8(a[mt], bop);
+          a[mt] = *reinterpret_cast<const gq_i4 *>(abase[mt] + koff);
 #pragma unroll
           for (int v = 0; v < NBC; ++v) {
-            acc[rt][mt][v] += (ws * sv[mt][v].x) * (float)D[v];
-            if constexpr (FMT != GQ_FMT_Q8_0) cor[rt][mt][v] += wm * sv[mt][v].y;
+            const int b = 4 * mt + v;
+            sv[mt][v] =
+                *reinterpret_cast<const float2 *>(scl + 4 * ((size_t)(b < nb ? b : 0) * scl_ld + blk) + 2 * lp);
           }
         }
-      }
+#pragma unroll
+        for (int rt = 0; rt < R; ++rt) {
+          const Chunk<FMT> &cc = ch[rt][i];
+          gq_i4 bop;
+          float ws, wm = 0.f;  // weight scale and offset/min factor of block (2m + h')
+          if constexpr (FMT == GQ_FMT_Q4_0) {
+            bop = codes16(cc.q[2 * m], cc.q[2 * m + 1]);
+            ws = m ? h16hi(cc.d) : h16lo(cc.d);
+            wm = ws;
+          } else if constexpr (FMT == GQ_FMT_Q8_0) {
+            const gq_u4 &qq = m ? cc.q1 : cc.q0;
+            bop = gq_i4{(int)qq[0], (int)qq[1], (int)qq[2], (int)qq[3]};
+            ws = m ? h16hi(cc.d) : h16lo(cc.d);
+          } else {
+            const uint32_t w0 = (m < 2) ? cc.qa[2 * (m & 1)] : cc.qb[2 * (m & 1)];
+            const uint32_t w1 = (m < 2) ? cc.qa[2 * (m & 1) + 1] : cc.qb[2 * (m & 1) + 1];
+            bop = codes16(w0, w1);
+            const uint32_t wsc = hp ? cc.meta[2] : cc.meta[1];
+            const uint32_t byte = (wsc >> (8 * m)) & 0xFFu;
+            const uint32_t b3 = (cc.meta[3] >> (8 * m + 4 * hp)) & 15u;
+            ws = h16lo(cc.meta[0]) * (float)(byte & 63u);
+            wm = h16hi(cc.meta[0]) * (float)((byte >> 6) | (b3 << 2));
+          }
+#pragma unroll
+          for (int mt = 0; mt < MT; ++mt) {
+            const gq_i4 D = mfma_i8(a[mt], bop);
+#pragma unroll
+            for (int v = 0; v < NBC; ++v) {
+              acc[rt][mt][v] += (ws * sv[mt][v].x) * (float)D[v];
+              if constexpr (FMT != GQ_FMT_Q8_0) cor[rt][mt][v] += wm * sv[mt][v].y;
+            }
+          }
+        }
       }
     }
   };
@@ -714,7 +715,8 @@ int launch_shape(const void *packed, const float *x, const void *ws, float *y, i
   GQ_TRY(q_plan(FMT, N, K, nb, &R, &ks, &cpw));
   if (cpw > Fmt<FMT>::MAXC / R) return GQ_ERR_INVALID_ARGS;  // the kernel's register budget
   if (R == 2) return launch_r<FMT, NBC, MT, 2, PREP, false>(packed, x, ws, y, N, K, nb, ks, s);
-  if (!PREP && cpw <= Fmt<FMT>::MAXC / 2) return launch_r<FMT, NBC, MT, 1, PREP, true>(packed, x, ws, y, N, K, nb, ks, s);
+  if (!PREP && cpw <= Fmt<FMT>::MAXC / 2)
+    return launch_r<FMT, NBC, MT, 1, PREP, true>(packed, x, ws, y, N, K, nb, ks, s);
   return launch_r<FMT, NBC, MT, 1, PREP, false>(packed, x, ws, y, N, K, nb, ks, s);
 }
 

@@ -395,7 +395,8 @@ bool GretaLoader::load_tensor_quant(const std::string &name, gcore::rt::hip::Buf
   const GretaRecord *r = impl_->find(name);
   if (!r) return fail(err, "tensor not found: " + name);
   const int fmt = greta_fmt_of_dtype(r->dtype);
-  if (fmt < 0) return fail(err, "load_tensor_quant: " + name + " is " + dtype_name(r->dtype) + " (a T16 record expected)");
+  if (fmt < 0)
+    return fail(err, "load_tensor_quant: " + name + " is " + dtype_name(r->dtype) + " (a T16 record expected)");
   if (!packed.allocate(r->w_size, gcore::rt::hip::BufferUsage::DeviceOnly, (GretaDataType)r->dtype, err))
     return false;
   if (!load_into(name, packed.data(), r->w_size, nullptr, 0, nullptr, 0, err)) return false;
