@@ -1,10 +1,11 @@
 // Drives the C++ host mirror end to end, as a caller of the reference's
 // interfaces would: create_weight_loader -> GGUFLoader::load_tensor_quant /
-// load_tensor_int8 / load_tensor_int4 -> GretaCompute::gemm on a
+// load_tensor_int8 / load_tensor_int4 (or, for a .greta file, GretaLoader's
+// load_tensor_quant / load_tensor_int4) -> GretaCompute::gemm on a
 // GretaStreamHip.  Test infrastructure: tests/test_host_mirror.py runs it and
 // checks the result file against the oracle.
 //
-// usage: greta_compute_driver <file.gguf> <tensor> <quant|int8|int4> <M>
+// usage: greta_compute_driver <file.gguf|file.greta> <tensor> <quant|int8|int4> <M>
 //                             <a.f32> <c.f32> [op_label] [a_dtype f32|f16|bf16]
 // A is read as M x K float32 (converted to the requested A dtype on the host),
 // C written as M x N float32.  Prints "route=<GEMV|GEMM> quant=<mode>".
@@ -17,6 +18,7 @@
 #include <vector>
 
 #include "gcore/compute/greta_compute.hpp"
+#include "gcore/inference/greta_file.hpp"
 #include "gcore/inference/weight_loader.hpp"
 #include "gcore/rt/hip/buffer.hpp"
 #include "gcore/rt/hip/greta_runtime_hip.hpp"
@@ -47,7 +49,8 @@ int main(int argc, char **argv) {
   auto wl = inference::create_weight_loader(path, &err);
   if (!wl) return fail("open: " + err);
   auto *gg = dynamic_cast<inference::GGUFLoader *>(wl.get());
-  if (!gg) return fail("not a GGUF loader");
+  auto *gr = dynamic_cast<inference::GretaLoader *>(wl.get());
+  if (!gg && !gr) return fail("neither a GGUF nor a .greta loader");
   size_t K = 0, n_elem = 1;
   for (const auto &t : wl->list_tensors())
     if (t.name == name) {
@@ -58,7 +61,7 @@ int main(int argc, char **argv) {
   const uint32_t N = (uint32_t)(n_elem / K);
 
   rt::hip::Buffer B, scales, head_scales;
-  bool ok = kind == "quant"  ? gg->load_tensor_quant(name, B, &err)
+  bool ok = kind == "quant"  ? (gg ? gg->load_tensor_quant(name, B, &err) : gr->load_tensor_quant(name, B, &err))
             : kind == "int8" ? wl->load_tensor_int8(name, B, scales, &err)
             : kind == "int4" ? wl->load_tensor_int4(name, B, scales, head_scales, &err)
                              : (err = "unknown kind " + kind, false);

@@ -38,8 +38,9 @@ def model(tmp_path_factory):
     return path, spec, d
 
 
-def _run(model, name, kind, M, label="", adt="f32", seed=0):
-    path, spec, d = model
+def _run(model, name, kind, M, label="", adt="f32", seed=0, path=None):
+    gguf_path, spec, d = model
+    path = path or gguf_path
     sh = spec[name][0]
     K = sh[0]
     N = int(np.prod(sh)) // K
@@ -105,3 +106,34 @@ def test_int4_force_gemv_label(dev, model, monkeypatch):
     monkeypatch.setenv("GRETA_WO_LAYOUT_FORCE", "row")
     a, c, route, N, K = _run(model, "blk.0.attn_q.weight", "int4", 64, label="attn_o_prefill", seed=3)
     assert route == "GEMV"
+
+
+@pytest.mark.parametrize("M", [1, 40])
+@pytest.mark.parametrize("name", ["blk.0.ffn_gate.weight", "blk.0.attn_q.weight", "output.weight"])
+def test_gemm_from_greta_cache(dev, model, name, M):
+    """create_weight_loader on a .greta T16 cache -> GretaLoader::load_tensor_quant
+    -> GretaCompute::gemm: the same result as from the GGUF."""
+    import gq
+    gguf_path, spec, d = model
+    cache = str(d / "m.greta")
+    if not os.path.exists(cache):
+        with gq.GGUF(gguf_path) as g:
+            gq.greta_write(g, cache, gq.LOAD_QUANT)
+    a, c, route, N, K = _run(model, name, "quant", M, seed=50 + M, path=cache)
+    _, c_gguf, route2, _, _ = _run(model, name, "quant", M, seed=50 + M)
+    assert route == route2
+    assert np.array_equal(c.view(np.uint32), c_gguf.view(np.uint32))
+
+
+def test_int4_from_reference_format_greta(dev, model):
+    """An INT4 .greta file (the reference tool's records) through
+    GretaLoader::load_tensor_int4 -> GretaCompute::gemm equals the GGUF INT4 load."""
+    import gq
+    gguf_path, spec, d = model
+    cache = str(d / "m_int4.greta")
+    with gq.GGUF(gguf_path) as g:
+        gq.greta_write(g, cache, gq.LOAD_INT4)
+    for name in ("blk.0.attn_q.weight", "blk.0.attn_k.weight"):
+        a, c, route, N, K = _run(model, name, "int4", 8, seed=5, path=cache)
+        _, c_gguf, _, _, _ = _run(model, name, "int4", 8, seed=5)
+        assert np.array_equal(c.view(np.uint32), c_gguf.view(np.uint32)), name
