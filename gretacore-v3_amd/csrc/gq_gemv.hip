@@ -700,7 +700,7 @@ extern "C" int gq_gemv_plan(int fmt, size_t N, size_t K, int batch, int *R_out, 
   GQ_CHECK(batch >= 1 && batch <= GQ_MAX_BATCH, GQ_ERR_UNSUPPORTED);
   if (!gq_gemv_on_h(fmt, N, K, batch)) return q_plan(fmt, N, K, batch, R_out, ksplit_out, chunks_per_wave_out);
   int R = 1, ks = 1, cpw = 0;
-  if (gq_gemv_h1_plan(fmt, N, K, batch, &R, &ks, &cpw) != GQ_OK) GQ_TRY(gq_gemv_h_plan(fmt, N, K, &R, &ks, &cpw));
+  if (gq_gemv_h1_plan(fmt, N, K, batch, &R, &ks, &cpw) != GQ_OK) GQ_TRY(gq_gemv_h_plan(fmt, N, K, batch, &R, &ks, &cpw));
   if (R_out) *R_out = R;
   if (ksplit_out) *ksplit_out = ks;
   if (chunks_per_wave_out) *chunks_per_wave_out = cpw;

@@ -237,7 +237,6 @@ GQ_DEV gq_f4 mfma16h(const gq_half8 &a, const gq_half8 &b, const gq_f4 &c) {
 // Activation staging window: kWin consecutive k of every K part, converted to
 // fp16 A fragments in LDS once per workgroup and shared by its TW row tiles.
 constexpr int kWin = 256;
-constexpr int kWinBytes = kWin / 64 * 2 * 64 * 16;  // [64-k step][half][lane][8 x fp16]
 
 // Workgroup = TW row tiles x KS parts of K, one wave per (tile, part).  The
 // waves of a part walk their K range window by window: weights are loaded two
@@ -247,17 +246,21 @@ constexpr int kWinBytes = kWin / 64 * 2 * 64 * 16;  // [64-k step][half][lane][8
 // of the A fragment for 64-k step m, half j holds x[r][64 m + 16 g + 8 j + 0..7]
 // (4-bit formats: in kQ4Perm order, the kQ4Div16 elements divided by 16)
 // (rows >= batch are zero), matching the weights dequant_step gives lane
-// (g, r).  The KS parts' partial sums are reduced in LDS at the end.
-template <int FMT, int TW, int KS>
+// (g, r).  The KS parts' partial sums are reduced in LDS at the end.  MR
+// activation rows are staged, as in k_gemv_h1 (MR = 8 up to batch 8: A rows
+// 8..15 re-read rows 0..7, their D rows are never stored).
+template <int FMT, int TW, int KS, int MR>
 __global__ void __launch_bounds__(64 * TW * KS)
 k_gemv_h(const uint8_t *__restrict__ w, size_t sc_off, const float *__restrict__ x, float *__restrict__ y, int N,
          int K, int C, int nb, int NI) {
   using F = HFmt<FMT>;
+  static_assert(MR == 8 || MR == 16, "rows staged");
   constexpr int WC = kWin / F::CK;                   // chunks per window
   constexpr int NT = 64 * TW * KS;                   // threads
-  constexpr int RPT = (KS * 16 * (kWin / 8)) / NT;   // x runs of 8 per thread per window
-  static_assert(RPT * NT == KS * 16 * (kWin / 8), "runs must divide evenly");
-  __shared__ __attribute__((aligned(16))) unsigned char xs[2][KS][kWinBytes];
+  constexpr int WB = kWin * 2 * MR;                  // LDS bytes per part and window: [kWin/64][2][4][MR][16]
+  constexpr int RPT = (KS * MR * (kWin / 8)) / NT;   // x runs of 8 per thread per window
+  static_assert(RPT >= 1 && RPT * NT == KS * MR * (kWin / 8), "runs must divide evenly");
+  __shared__ __attribute__((aligned(16))) unsigned char xs[2][KS][WB];
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int tt = wave % TW, part = wave / TW;
@@ -289,13 +292,13 @@ k_gemv_h(const uint8_t *__restrict__ w, size_t sc_off, const float *__restrict__
 #pragma unroll
   for (int u = 0; u < RPT; ++u) {
     const int run = (int)threadIdx.x + u * NT;
-    const int kr = run & 31, b = (run >> 5) & 15, p = run >> 9;
+    const int kr = run & 31, b = (run >> 5) % MR, p = run / (32 * MR);
     const int pc0 = (C * p) / KS, pc1 = (C * (p + 1)) / KS;
     xsrc[u] = x + (size_t)(b < nb ? b : 0) * K;
     xk0[u] = pc0 * F::CK + 8 * kr;
     xk1[u] = b < nb ? min(pc1 * F::CK, K) : 0;  // K % 32 == 0: a run is wholly in or out
     const int o = 8 * kr, m = o >> 6, gq = (o & 63) >> 4, j = (o & 15) >> 3;
-    xdst[u] = (uint32_t)(p * kWinBytes + ((m * 2 + j) * 64 + 16 * gq + b) * 16);
+    xdst[u] = (uint32_t)(p * WB + (((m * 2 + j) * 4 + gq) * MR + b) * 16);
   }
   auto load_x = [&](int it) {
 #pragma unroll
@@ -347,15 +350,15 @@ k_gemv_h(const uint8_t *__restrict__ w, size_t sc_off, const float *__restrict__
     if constexpr (decltype(pfw)::value) load_win(it + 2, w2);
     if constexpr (decltype(pfx)::value) load_x(it + 1);
     if (it < nwin) {
-      const unsigned char *xb = xs[it & 1][part];
+      const unsigned char *xb = xs[it & 1][part] + (g * MR + (r & (MR - 1))) * 16;  // this lane's A row
 #pragma unroll
       for (int j = 0; j < WC; ++j) {
         if (c0 + it * WC + j < c1) {
 #pragma unroll
           for (int m = 0; m < F::STEPS; ++m) {
             const int ms = j * F::STEPS + m;
-            const gq_half8 a0 = *reinterpret_cast<const gq_half8 *>(xb + ((ms * 2 + 0) * 64 + lane) * 16);
-            const gq_half8 a1 = *reinterpret_cast<const gq_half8 *>(xb + ((ms * 2 + 1) * 64 + lane) * 16);
+            const gq_half8 a0 = *reinterpret_cast<const gq_half8 *>(xb + (ms * 2 + 0) * 4 * MR * 16);
+            const gq_half8 a1 = *reinterpret_cast<const gq_half8 *>(xb + (ms * 2 + 1) * 4 * MR * 16);
             gq_half8 b0, b1;
             dequant_step<FMT>(w0[j], m, g, mg, b0, b1);
             acc = mfma16h(a0, b0, acc);
@@ -602,13 +605,14 @@ int gq_gemv_h1_plan(int fmt, size_t N, size_t K, int nb, int *R_out, int *ks_out
   return GQ_OK;
 }
 
-int gq_gemv_h_plan(int fmt, size_t N, size_t K, int *R_out, int *ks_out, int *cpw_out) {
+int gq_gemv_h_plan(int fmt, size_t N, size_t K, int nb, int *R_out, int *ks_out, int *cpw_out) {
   const int f = gq_fmt_is_q4k(fmt) ? GQ_FMT_Q4_K : gq_fmt_is_q6k(fmt) ? GQ_FMT_Q6_K : fmt;
   const int C = (int)gq_chunks(f, K);
   const size_t tiles = gq_tiles(N);
   int tw = tiles >= 800 ? 4 : tiles >= 400 ? 2 : 1;
   const int er = env_int("GQ_GEMV_H_R");
   if (er == 1 || er == 2 || er == 4) tw = er;
+  (void)nb;  // batch-independent (a 16-way split of 8-row windows measured slower than 8)
   int ks = 1;
   while (ks < 8 && tiles * ks < 3584 && 2 * ks <= C && tw * ks < 16) ks *= 2;
   const int e = env_int("GQ_GEMV_H_KSPLIT");
@@ -621,7 +625,7 @@ int gq_gemv_h_plan(int fmt, size_t N, size_t K, int *R_out, int *ks_out, int *cp
 }
 
 namespace {
-template <int FMT, int TW>
+template <int FMT, int TW, int MR>
 int launch_h_tw(const void *packed, const float *x, float *y, int N, int K, int nb, int ks, hipStream_t s) {
   const int C = (int)gq_chunks(FMT, K);
   const size_t wgs = (gq_tiles(N) + TW - 1) / TW;
@@ -629,15 +633,20 @@ int launch_h_tw(const void *packed, const float *x, float *y, int N, int K, int 
   const uint8_t *w = (const uint8_t *)packed;
   constexpr int WC = kWin / HFmt<FMT>::CK;
   const int NI = ((C + ks - 1) / ks + WC - 1) / WC;
-#define GQ_LAUNCH_H(KS)                                                                                              \
-  hipLaunchKernelGGL((k_gemv_h<FMT, TW, KS>), dim3((unsigned)wgs), dim3(64 * TW * KS), 0, s, w, sc_off, x, y, N, K, \
-                     C, nb, NI)
+  // x runs must spread evenly over the threads (TW <= MR / 2)
+#define GQ_LAUNCH_H(KS)                                                                                               \
+  if constexpr (2 * TW <= MR) {                                                                                       \
+    hipLaunchKernelGGL((k_gemv_h<FMT, TW, KS, MR>), dim3((unsigned)wgs), dim3(64 * TW * KS), 0, s, w, sc_off, x, y, \
+                       N, K, C, nb, NI);                                                                              \
+  } else {                                                                                                            \
+    return GQ_ERR_INVALID_ARGS;                                                                                       \
+  }
   switch (ks) {
   case 1: GQ_LAUNCH_H(1); break;
   case 2: GQ_LAUNCH_H(2); break;
   case 4: GQ_LAUNCH_H(4); break;
   default:
-    if constexpr (TW <= 2) GQ_LAUNCH_H(8);
+    if constexpr (TW <= 2) { GQ_LAUNCH_H(8); }
     else return GQ_ERR_INVALID_ARGS;
     break;
   }
@@ -686,10 +695,15 @@ int launch_h(const void *packed, const float *x, float *y, int N, int K, int nb,
     if (tw == 4) return launch_h1_nck<FMT, 4, 4, 16>(packed, x, y, N, K, nb, cpw, s);
     return launch_h1_nck<FMT, 8, 2, 16>(packed, x, y, N, K, nb, cpw, s);
   }
-  GQ_TRY(gq_gemv_h_plan(FMT, N, K, &tw, &ks, &cpw));
-  if (tw == 4) return launch_h_tw<FMT, 4>(packed, x, y, N, K, nb, ks, s);
-  if (tw == 2) return launch_h_tw<FMT, 2>(packed, x, y, N, K, nb, ks, s);
-  return launch_h_tw<FMT, 1>(packed, x, y, N, K, nb, ks, s);
+  GQ_TRY(gq_gemv_h_plan(FMT, N, K, nb, &tw, &ks, &cpw));
+  if (nb <= 8) {
+    if (tw == 4) return launch_h_tw<FMT, 4, 8>(packed, x, y, N, K, nb, ks, s);
+    if (tw == 2) return launch_h_tw<FMT, 2, 8>(packed, x, y, N, K, nb, ks, s);
+    return launch_h_tw<FMT, 1, 8>(packed, x, y, N, K, nb, ks, s);
+  }
+  if (tw == 4) return launch_h_tw<FMT, 4, 16>(packed, x, y, N, K, nb, ks, s);
+  if (tw == 2) return launch_h_tw<FMT, 2, 16>(packed, x, y, N, K, nb, ks, s);
+  return launch_h_tw<FMT, 1, 16>(packed, x, y, N, K, nb, ks, s);
 }
 }  // namespace
 

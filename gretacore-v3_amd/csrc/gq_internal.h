@@ -50,7 +50,7 @@ int gq_launch_prep_x(int fmt, const float *x, void *ws, int B, int K, hipStream_
 
 // fp16 batch GEMV (gq_gemv_h.hip)
 int gq_gemv_h_min(void);
-int gq_gemv_h_plan(int fmt, size_t N, size_t K, int *R_out, int *ks_out, int *cpw_out);
+int gq_gemv_h_plan(int fmt, size_t N, size_t K, int nb, int *R_out, int *ks_out, int *cpw_out);
 int gq_gemv_h1_plan(int fmt, size_t N, size_t K, int nb, int *R_out, int *ks_out, int *cpw_out);
 int gq_launch_gemv_h(int fmt, const void *packed, const float *x, float *y, int N, int K, int nb, hipStream_t s);
 

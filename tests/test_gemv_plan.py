@@ -26,10 +26,12 @@ KWIN = 256  # k per activation staging window of the fp16 batch kernel
 def emulate_h(fmt, n, k, batch):
     """Replays k_gemv_h's window, chunk and address arithmetic on the host:
     workgroup = TW row tiles x KS parts of K, weights prefetched two windows
-    ahead (clamped to the part's last chunk), activation runs of 8 per
-    thread and window."""
+    ahead (clamped to the part's last chunk), MR (8 up to batch 8, else 16)
+    activation rows staged per window in runs of 8."""
     TW, KS, cpw = gq.gemv_plan(fmt, n, k, batch)
+    mr = 8 if batch <= 8 else 16
     assert TW in (1, 2, 4) and KS in (1, 2, 4, 8) and TW * KS <= 16
+    assert 2 * TW <= mr  # x runs spread evenly over the threads
     C = -(-k // CK[fmt])
     assert KS <= C
     tiles = -(-n // 16)
@@ -37,8 +39,8 @@ def emulate_h(fmt, n, k, batch):
     assert cpw == -(-C // KS)
     NI = -(-cpw // wc)
     wgs = -(-tiles // TW)
-    # LDS: two buffers of KS windows (8 KiB each) must fit the 160 KiB
-    assert 2 * KS * 8192 <= 160 * 1024
+    WB = KWIN * 2 * mr  # LDS bytes per part and window
+    assert 2 * KS * WB <= 160 * 1024
     for part in range(KS):
         c0, c1 = C * part // KS, C * (part + 1) // KS
         assert 0 <= c0 < c1 <= C
@@ -56,6 +58,12 @@ def emulate_h(fmt, n, k, batch):
                 kk = c0 * CK[fmt] + 8 * kr + it * KWIN
                 if kk < min(c1 * CK[fmt], k):
                     assert kk + 8 <= k  # a run of 8 is read only when wholly inside
+    for run in range(KS * mr * 32):  # x runs of a window and their LDS destinations
+        kr, b, p = run & 31, (run >> 5) % mr, run // (32 * mr)
+        o = 8 * kr
+        m, g, j = o >> 6, (o & 63) >> 4, (o & 15) >> 3
+        dst = p * WB + (((m * 2 + j) * 4 + g) * mr + b) * 16
+        assert 0 <= dst and dst + 16 <= KS * WB
 
 
 def h1_plan(fmt, n, k, batch):
