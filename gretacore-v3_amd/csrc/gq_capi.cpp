@@ -18,6 +18,7 @@ struct DeviceWorkspace {
 };
 std::mutex g_ws_mutex;
 std::vector<DeviceWorkspace> g_ws;
+std::vector<int> g_cus;
 }  // namespace
 
 int gq_hip_status(hipError_t e) {
@@ -47,6 +48,25 @@ int gq_default_workspace(size_t bytes, void **ptr) {
   }
   *ptr = w.ptr;
   return GQ_OK;
+}
+
+int gq_device_cus(void) {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) {
+    (void)hipGetLastError();
+    return 0;
+  }
+  std::lock_guard<std::mutex> lock(g_ws_mutex);
+  if ((size_t)dev >= g_cus.size()) g_cus.resize(dev + 1, -1);
+  if (g_cus[dev] < 0) {
+    int n = 0;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) {
+      (void)hipGetLastError();
+      n = 0;
+    }
+    g_cus[dev] = n;
+  }
+  return g_cus[dev];
 }
 
 extern "C" {

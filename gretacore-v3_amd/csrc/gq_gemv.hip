@@ -654,7 +654,8 @@ int launch_r(const void *packed, const float *x, const void *ws, float *y, int N
 // the activation staging per weight) and KSPLIT waves, so that every wave holds
 // at most MAXC / R chunks and the grid has enough waves to keep HBM busy.
 // Every wave's chunk range [C*w/KSPLIT, C*(w+1)/KSPLIT) lies inside [0, C).
-static int q_plan(int fmt, size_t N, size_t K, int batch, int *R_out, int *ksplit_out, int *chunks_per_wave_out) {
+static int q_plan(int fmt, size_t N, size_t K, int batch, int *R_out, int *ksplit_out, int *chunks_per_wave_out,
+                  bool single = true) {
   GQ_TRY(gq_check_shape(fmt, N, K));
   GQ_CHECK(batch >= 1 && batch <= GQ_MAX_BATCH, GQ_ERR_UNSUPPORTED);
   const int f = gq_fmt_is_q4k(fmt) ? GQ_FMT_Q4_K : gq_fmt_is_q6k(fmt) ? GQ_FMT_Q6_K : fmt;
@@ -666,6 +667,18 @@ static int q_plan(int fmt, size_t N, size_t K, int batch, int *R_out, int *kspli
   const size_t tiles = gq_tiles(N);
   const int mt = batch <= 4 ? 1 : (batch + 3) / 4;
   int R = (tiles >= 512 && C >= 4) ? 2 : 1;
+  if (R == 2 && single) {
+    // one-tile workgroups of a single matrix (the multi-matrix kernel holds
+    // registers for twice the chunks, too many for three workgroups per CU)
+    // run best where every CU holds the same number of
+    // tiles or at most three (measured, Q4_0 / Q4_K / Q8_0 at K = 4096:
+    // 10240 rows 6.1 vs 6.9 us, 16384 rows 7.7 vs 8.1 us); two-tile ones
+    // where the tiles per CU fall in between (14336 rows: 7.4 vs 7.8 us)
+    const int cus0 = gq_device_cus();
+    const size_t cus = cus0 > 0 ? (size_t)cus0 : 256;
+    const size_t rounds = (tiles + cus - 1) / cus;
+    if (rounds <= 3 || (tiles % cus == 0 && rounds <= 8)) R = 1;
+  }
   const int er = env_int("GQ_GEMV_R");
   if (er == 1 || er == 2) R = er;
   if ((C + 15) / 16 > maxc / 2) R = 1;  // very long K: keep every register for chunks
@@ -885,7 +898,7 @@ extern "C" int gq_gemv_multi_plan(int fmt, int n_mats, const size_t *N, size_t K
     tiles += gq_tiles(N[i]);
   }
   int R = 1, ks = 2, cpw = 0;
-  GQ_TRY(q_plan(fmt, tiles * 16, K, batch, &R, &ks, &cpw));
+  GQ_TRY(q_plan(fmt, tiles * 16, K, batch, &R, &ks, &cpw, false));
   if (R_out) *R_out = R;
   if (ksplit_out) *ksplit_out = ks;
   if (chunks_per_wave_out) *chunks_per_wave_out = cpw;

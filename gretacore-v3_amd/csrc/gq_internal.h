@@ -60,3 +60,5 @@ int gq_launch_f16_to_f32(const void *in, size_t n, float *out, hipStream_t s);
 
 // Library-owned per-device workspace (grown on demand, never shrunk).
 int gq_default_workspace(size_t bytes, void **ptr);
+// Compute units of the current device (cached per device; 0 without a device).
+int gq_device_cus(void);
