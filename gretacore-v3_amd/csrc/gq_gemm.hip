@@ -509,7 +509,10 @@ GQ_DEV gq_half8 rfrag(const RStep<FMT, NJ> &st, int j, int ks, int step, const Q
 
 // Workgroup tile BM x BN, WM x WN waves; a wave owns (BM / WM) x (BN / WN) of C
 // (TM x NJ MFMA tiles of 32 x 32).  256 x 256 with 2 x 4 waves: two waves per SIMD.
-template <int FMT, int CBF16, int BM, int BN, int WM, int WN>
+// AD: how many K steps ahead the activation tile is requested (1: two LDS
+// buffers; 2: three, for grids whose short steps would otherwise wait on each
+// tile's full load latency).  The weights are requested two steps ahead.
+template <int FMT, int CBF16, int BM, int BN, int WM, int WN, int AD = 1>
 __global__ void __launch_bounds__(64 * WM * WN) __attribute__((amdgpu_waves_per_eu(WM * WN / 4, WM * WN / 4)))
 k_gemm_rb(const uint8_t *__restrict__ w, uint32_t sc_off, const _Float16 *__restrict__ a16, int lda,
           void *__restrict__ c, int M, int N, int C, int nsteps, int tiles_m) {
@@ -518,9 +521,16 @@ k_gemm_rb(const uint8_t *__restrict__ w, uint32_t sc_off, const _Float16 *__rest
   static_assert(TM >= 1 && NJ >= 1 && BM % (8 * NW) == 0, "tile shape");
   __shared__ __attribute__((aligned(16))) _Float16 As_0[BM * BK];
   __shared__ __attribute__((aligned(16))) _Float16 As_1[BM * BK];
-  auto As_of = [&](auto b) -> _Float16 * { return decltype(b)::value ? As_1 : As_0; };
+  __shared__ __attribute__((aligned(16))) _Float16 As_2[AD == 2 ? BM * BK : 8];
+  static_assert(AD == 1 || AD == 2, "activation prefetch distance");
+  auto As_of = [&](auto b) -> _Float16 * {
+    constexpr int v = decltype(b)::value;
+    return v == 0 ? As_0 : v == 1 ? As_1 : As_2;
+  };
   using B0 = std::integral_constant<int, 0>;
   using B1 = std::integral_constant<int, 1>;
+  using B2 = std::integral_constant<int, 2>;
+  constexpr int NA = BM / (8 * NW);  // activation-tile loads per thread and K step
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int wm = wave / WN, wn = wave % WN;
@@ -563,15 +573,16 @@ k_gemm_rb(const uint8_t *__restrict__ w, uint32_t sc_off, const _Float16 *__rest
   const int arow = (BM / WM) * wm + (lane & 31);
   const int sw = a_swz(lane & 31);
 
-  auto run_step = [&](int step, auto buf_c) {
+  auto run_step = [&](int step, auto buf_c, auto wbuf_c) {
     constexpr int BUF = decltype(buf_c)::value;
-    using NB = std::integral_constant<int, BUF ^ 1>;
-    const int s1 = step + 1 < nsteps ? step + 1 : nsteps - 1;
+    // the buffer the activation tile of step + AD goes to
+    using NB = std::integral_constant<int, AD == 1 ? (BUF ^ 1) : (BUF + 2) % 3>;
+    const int s1 = step + AD < nsteps ? step + AD : nsteps - 1;
     const int s2 = step + 2 < nsteps ? step + 2 : nsteps - 1;
     load_a_lds<BM, NW>(a16, lda, M, m0, s1, wave, lane, As_of(NB{}));
     __builtin_amdgcn_sched_barrier(0);
     const _Float16 *As = As_of(buf_c) + arow * BK;
-    RStep<FMT, NJ> &cur = wst[BUF];
+    RStep<FMT, NJ> &cur = wst[decltype(wbuf_c)::value];
     gq_half8 af[2][TM];
     auto read_a = [&](int ks, int fb) {
       const int ch = (4 * (ks >> 1) + 2 * kh + (ks & 1)) ^ sw;
@@ -593,21 +604,41 @@ k_gemm_rb(const uint8_t *__restrict__ w, uint32_t sc_off, const _Float16 *__rest
     }
     // the register stage of this step is free: request step + 2 into it
     load_rstep<FMT, NJ>(w, qo, so, s2, cur);
-    // the A tile of step + 1 (and the weights of step + 1) must have landed;
-    // the 3 NJ loads of step + 2 just issued may stay in flight
-    static_assert(3 * NJ <= 15, "vmcnt immediate");
-    __builtin_amdgcn_s_waitcnt(0x0F70 | (3 * NJ));
+    // the A tile and the weights of step + 1 must have landed; the 3 NJ weight
+    // loads of step + 2 just issued (AD = 2: and the activation tile of
+    // step + 2 before them) may stay in flight
+    constexpr int pend = 3 * NJ + (AD == 2 ? NA : 0);
+    static_assert(pend <= 63, "vmcnt immediate");
+    __builtin_amdgcn_s_waitcnt(0x0F70 | (pend & 15) | ((pend >> 4) << 14));
     __syncthreads();
   };
 
   load_a_lds<BM, NW>(a16, lda, M, m0, 0, wave, lane, As_0);
   load_rstep<FMT, NJ>(w, qo, so, 0, wst[0]);
-  load_rstep<FMT, NJ>(w, qo, so, nsteps > 1 ? 1 : 0, wst[1]);
-  __builtin_amdgcn_s_waitcnt(0x0F70);
-  __syncthreads();
-  for (int step = 0; step < nsteps; step += 2) {
-    run_step(step, B0{});
-    run_step(step + 1, B1{});
+  if constexpr (AD == 1) {
+    load_rstep<FMT, NJ>(w, qo, so, nsteps > 1 ? 1 : 0, wst[1]);
+    __builtin_amdgcn_s_waitcnt(0x0F70);
+    __syncthreads();
+    for (int step = 0; step < nsteps; step += 2) {
+      run_step(step, B0{}, B0{});
+      run_step(step + 1, B1{}, B1{});
+    }
+  } else {
+    load_a_lds<BM, NW>(a16, lda, M, m0, nsteps > 1 ? 1 : 0, wave, lane, As_1);
+    load_rstep<FMT, NJ>(w, qo, so, nsteps > 1 ? 1 : 0, wst[1]);
+    constexpr int pend = 3 * NJ + NA;  // step 1's tile and weights may stay in flight
+    __builtin_amdgcn_s_waitcnt(0x0F70 | (pend & 15) | ((pend >> 4) << 14));
+    __syncthreads();
+    // buffers rotate with period 3, weight stages with period 2: unrolled by 6
+    // (nsteps is even; a step past the end is skipped by every wave alike)
+    for (int step = 0; step < nsteps; step += 6) {
+      run_step(step, B0{}, B0{});
+      run_step(step + 1, B1{}, B1{});
+      if (step + 2 < nsteps) run_step(step + 2, B2{}, B0{});
+      if (step + 3 < nsteps) run_step(step + 3, B0{}, B1{});
+      if (step + 4 < nsteps) run_step(step + 4, B1{}, B0{});
+      if (step + 5 < nsteps) run_step(step + 5, B2{}, B1{});
+    }
   }
 
 #pragma unroll
@@ -674,15 +705,24 @@ int launch_cfg(const void *packed, const _Float16 *a16, int lda, void *c, int M,
   return gq_last_launch();
 }
 
+// ad_default: the activation prefetch distance of the shape (GQ_GEMM_AD=1|2
+// overrides it, for tuning)
 template <int FMT, int CBF16, int BM, int BN, int WM, int WN>
-int launch_rb(const void *packed, const _Float16 *a16, int lda, void *c, int M, int N, int K, hipStream_t s) {
+int launch_rb(const void *packed, const _Float16 *a16, int lda, void *c, int M, int N, int K, hipStream_t s,
+              int ad_default = 1) {
   const int C = (int)gq_chunks(FMT, K);
   const int nsteps = (int)(gq_kpad(FMT, K) / BK);
   const int tiles_m = (M + BM - 1) / BM, tiles_n = (N + BN - 1) / BN;
-  hipLaunchKernelGGL((k_gemm_rb<FMT, CBF16, BM, BN, WM, WN>), dim3((unsigned)(tiles_m * tiles_n)), dim3(64 * WM * WN),
-                     0, s,
-                     (const uint8_t *)packed, (uint32_t)gq_sc_plane_offset(FMT, N, K), a16, lda, c, M, N, C, nsteps,
-                     tiles_m);
+  const char *e = getenv("GQ_GEMM_AD");
+  const int ad = e ? atoi(e) : ad_default;
+  if (ad == 2)
+    hipLaunchKernelGGL((k_gemm_rb<FMT, CBF16, BM, BN, WM, WN, 2>), dim3((unsigned)(tiles_m * tiles_n)),
+                       dim3(64 * WM * WN), 0, s, (const uint8_t *)packed, (uint32_t)gq_sc_plane_offset(FMT, N, K), a16,
+                       lda, c, M, N, C, nsteps, tiles_m);
+  else
+    hipLaunchKernelGGL((k_gemm_rb<FMT, CBF16, BM, BN, WM, WN>), dim3((unsigned)(tiles_m * tiles_n)),
+                       dim3(64 * WM * WN), 0, s, (const uint8_t *)packed, (uint32_t)gq_sc_plane_offset(FMT, N, K), a16,
+                       lda, c, M, N, C, nsteps, tiles_m);
   return gq_last_launch();
 }
 
@@ -690,8 +730,10 @@ int launch_rb(const void *packed, const _Float16 *a16, int lda, void *c, int M, 
 //   0: register-B kernel, 256 x 256 (448 workgroups at 2048 x 14336)
 //   3: LDS-B kernel, 256 x 256 (Q4_K at that size: its per-fragment
 //      sub-block decoding costs more than the LDS round trip saves)
-//   4: register-B, 256 x 128, for >= 192 workgroups
-//   6: register-B, 128 x 128, smaller problems
+//   4: register-B, 256 x 128, for >= 192 workgroups (activation tile two K
+//      steps ahead: 4-6 % faster at 512 x 14336 and 2048 x 4096)
+//   6: register-B, 128 x 128, smaller problems (Q4_K: activation tile two K
+//      steps ahead, 62 -> 56 us at 512 x 4096)
 // 1, 2 (LDS-B 256 x 128, 128 x 128) and 5, 7, 8 (other register-B shapes)
 // are kept for tuning through GQ_GEMM_TILE.
 int pick_tile(int fmt, int M, int N) {
@@ -706,9 +748,9 @@ template <int FMT, int CBF16>
 int launch_fmt(const void *packed, const _Float16 *a16, int lda, void *c, int M, int N, int K, hipStream_t s) {
   switch (pick_tile(FMT, M, N)) {
   case 0: return launch_rb<FMT, CBF16, 256, 256, 2, 4>(packed, a16, lda, c, M, N, K, s);
-  case 4: return launch_rb<FMT, CBF16, 256, 128, 2, 4>(packed, a16, lda, c, M, N, K, s);
+  case 4: return launch_rb<FMT, CBF16, 256, 128, 2, 4>(packed, a16, lda, c, M, N, K, s, 2);
   case 5: return launch_rb<FMT, CBF16, 128, 256, 2, 4>(packed, a16, lda, c, M, N, K, s);
-  case 6: return launch_rb<FMT, CBF16, 128, 128, 2, 4>(packed, a16, lda, c, M, N, K, s);
+  case 6: return launch_rb<FMT, CBF16, 128, 128, 2, 4>(packed, a16, lda, c, M, N, K, s, FMT == GQ_FMT_Q4_K ? 2 : 1);
   case 7: return launch_rb<FMT, CBF16, 128, 128, 2, 2>(packed, a16, lda, c, M, N, K, s);
   case 8: return launch_rb<FMT, CBF16, 256, 128, 4, 2>(packed, a16, lda, c, M, N, K, s);
   default: return launch_rb<FMT, CBF16, 128, 128, 2, 4>(packed, a16, lda, c, M, N, K, s);
