@@ -183,6 +183,18 @@ GQ_DEV int quad_sum(int v) {
   v += __builtin_amdgcn_mov_dpp(v, 0xB1, 0xF, 0xF, false);
   return v + __builtin_amdgcn_mov_dpp(v, 0x4E, 0xF, 0xF, false);
 }
+// Sum over the whole wave, every lane receiving it: quads (DPP lane ^ 1,
+// lane ^ 2), then the mirrored quad of each 8-lane half (row_half_mirror) and
+// the mirrored half of each 16-lane row (row_mirror), then the 16-lane groups
+// (sum_lane_groups).
+GQ_DEV float sum_lane_groups(float p);
+GQ_DEV float wave_sum(float v) {
+  v += __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0xB1, 0xF, 0xF, false));
+  v += __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x4E, 0xF, 0xF, false));
+  v += __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x141, 0xF, 0xF, false));
+  v += __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x140, 0xF, 0xF, false));
+  return sum_lane_groups(v);
+}
 // Sum over the four 16-lane groups (lane, lane ^ 16, lane ^ 32, lane ^ 48):
 // each permlane swap returns the pair (own, partner) in some order.
 GQ_DEV float sum_lane_groups(float p) {
@@ -343,8 +355,7 @@ k_gemv_q(const GemvFuse fz, const float *__restrict__ x, const int8_t *__restric
         }
 #pragma unroll
         for (int b = 0; b < NBC; ++b) {
-#pragma unroll
-          for (int o = 1; o < 64; o <<= 1) ss[b] += __shfl_xor(ss[b], o, 64);
+          ss[b] = wave_sum(ss[b]);
           if (lane == 0) ssred[wave][b] = ss[b];
         }
         __syncthreads();
@@ -654,8 +665,7 @@ int launch_r(const void *packed, const float *x, const void *ws, float *y, int N
 // the activation staging per weight) and KSPLIT waves, so that every wave holds
 // at most MAXC / R chunks and the grid has enough waves to keep HBM busy.
 // Every wave's chunk range [C*w/KSPLIT, C*(w+1)/KSPLIT) lies inside [0, C).
-static int q_plan(int fmt, size_t N, size_t K, int batch, int *R_out, int *ksplit_out, int *chunks_per_wave_out,
-                  bool single = true) {
+static int q_plan(int fmt, size_t N, size_t K, int batch, int *R_out, int *ksplit_out, int *chunks_per_wave_out) {
   GQ_TRY(gq_check_shape(fmt, N, K));
   GQ_CHECK(batch >= 1 && batch <= GQ_MAX_BATCH, GQ_ERR_UNSUPPORTED);
   const int f = gq_fmt_is_q4k(fmt) ? GQ_FMT_Q4_K : gq_fmt_is_q6k(fmt) ? GQ_FMT_Q6_K : fmt;
@@ -667,10 +677,8 @@ static int q_plan(int fmt, size_t N, size_t K, int batch, int *R_out, int *kspli
   const size_t tiles = gq_tiles(N);
   const int mt = batch <= 4 ? 1 : (batch + 3) / 4;
   int R = (tiles >= 512 && C >= 4) ? 2 : 1;
-  if (R == 2 && single) {
-    // one-tile workgroups of a single matrix (the multi-matrix kernel holds
-    // registers for twice the chunks, too many for three workgroups per CU)
-    // run best where every CU holds the same number of
+  if (R == 2) {
+    // one-tile workgroups run best where every CU holds the same number of
     // tiles or at most three (measured, Q4_0 / Q4_K / Q8_0 at K = 4096:
     // 10240 rows 6.1 vs 6.9 us, 16384 rows 7.7 vs 8.1 us); two-tile ones
     // where the tiles per CU fall in between (14336 rows: 7.4 vs 7.8 us)
@@ -850,14 +858,18 @@ int ks_for(int fmt, size_t wgs, int C, int R) {
   return ks;
 }
 
-template <int FMT, int NBC, int R, int FUSE>
+// HALF: register room for MAXC / R / 2 chunks per wave where the plan needs no
+// more (fewer surplus loads, fewer registers)
+template <int FMT, int NBC, int R, int FUSE, bool HALF>
 int launch_fused_nbc(const GemvFuse &fz, size_t wgs, int ks, const float *x, int K, int nb, hipStream_t s) {
   using F = Fmt<FMT>;
+  constexpr int NCKT = F::MAXC / R / (HALF ? 2 : 1);
   const int C = (int)gq_chunks(FMT, K);
   const int Kp = (int)gq_kpad(FMT, K);
+  if ((C + ks - 1) / ks > NCKT) return GQ_ERR_INVALID_ARGS;
   const size_t lds = (size_t)ks * xl_layout(F::CK * ((C + ks - 1) / ks), NBC).wave_bytes;
 #define GQ_LAUNCH_F(KS)                                                                                        \
-  hipLaunchKernelGGL((k_gemv_q<FMT, NBC, 1, R, F::MAXC / R, KS, false, FUSE>), dim3((unsigned)wgs), dim3(64 * KS), \
+  hipLaunchKernelGGL((k_gemv_q<FMT, NBC, 1, R, NCKT, KS, false, FUSE>), dim3((unsigned)wgs), dim3(64 * KS), \
                      lds, s, fz, x, nullptr, nullptr, K, C, Kp, nb)
   switch (ks) {
   case 2: GQ_LAUNCH_F(2); break;
@@ -869,11 +881,20 @@ int launch_fused_nbc(const GemvFuse &fz, size_t wgs, int ks, const float *x, int
   return gq_last_launch();
 }
 
+template <int FMT, int R, int FUSE, bool HALF>
+int launch_fused_h(const GemvFuse &fz, size_t wgs, int ks, const float *x, int K, int nb, hipStream_t s) {
+  if (nb == 1) return launch_fused_nbc<FMT, 1, R, FUSE, HALF>(fz, wgs, ks, x, K, nb, s);
+  if (nb == 2) return launch_fused_nbc<FMT, 2, R, FUSE, HALF>(fz, wgs, ks, x, K, nb, s);
+  return launch_fused_nbc<FMT, 4, R, FUSE, HALF>(fz, wgs, ks, x, K, nb, s);
+}
+
 template <int FMT, int R, int FUSE>
 int launch_fused(const GemvFuse &fz, size_t wgs, int ks, const float *x, int K, int nb, hipStream_t s) {
-  if (nb == 1) return launch_fused_nbc<FMT, 1, R, FUSE>(fz, wgs, ks, x, K, nb, s);
-  if (nb == 2) return launch_fused_nbc<FMT, 2, R, FUSE>(fz, wgs, ks, x, K, nb, s);
-  return launch_fused_nbc<FMT, 4, R, FUSE>(fz, wgs, ks, x, K, nb, s);
+  const int C = (int)gq_chunks(FMT, K);
+  if constexpr (R == 1) {  // (one-tile workgroups: a half list still stages whole 512-k slices)
+    if ((C + ks - 1) / ks <= Fmt<FMT>::MAXC / 2) return launch_fused_h<FMT, 1, FUSE, true>(fz, wgs, ks, x, K, nb, s);
+  }
+  return launch_fused_h<FMT, R, FUSE, false>(fz, wgs, ks, x, K, nb, s);
 }
 
 template <int R, int FUSE>
@@ -898,7 +919,7 @@ extern "C" int gq_gemv_multi_plan(int fmt, int n_mats, const size_t *N, size_t K
     tiles += gq_tiles(N[i]);
   }
   int R = 1, ks = 2, cpw = 0;
-  GQ_TRY(q_plan(fmt, tiles * 16, K, batch, &R, &ks, &cpw, false));
+  GQ_TRY(q_plan(fmt, tiles * 16, K, batch, &R, &ks, &cpw));
   if (R_out) *R_out = R;
   if (ksplit_out) *ksplit_out = ks;
   if (chunks_per_wave_out) *chunks_per_wave_out = cpw;
