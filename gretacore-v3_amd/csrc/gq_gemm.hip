@@ -789,6 +789,18 @@ extern "C" int gq_gemm(int fmt, const void *packed, const void *a, int a_dtype, 
   // the kernel addresses the packed tensor with 32-bit offsets
   GQ_CHECK(gq_packed_bytes(fmt, N, K) < ((size_t)1 << 32), GQ_ERR_INVALID_ARGS);
   hipStream_t s = (hipStream_t)stream;
+  // 17..48 rows: the GEMM's smallest tile (128 x 128) pads M to 128 and gives
+  // N / 128 workgroups, each walking all of K (45-55 us at 4096 x 4096 or
+  // 14336 x 4096 whatever M); the batch GEMV over groups of 16 rows spreads
+  // over every CU (M = 32: 16 / 27 us)
+  if (M > GQ_MAX_BATCH && M <= 3 * GQ_MAX_BATCH && a_dtype == GQ_DT_F32 && c_dtype == GQ_DT_F32) {
+    for (size_t m0 = 0; m0 < M; m0 += GQ_MAX_BATCH) {
+      const size_t mb = M - m0 < GQ_MAX_BATCH ? M - m0 : GQ_MAX_BATCH;
+      GQ_TRY(gq_gemv(fmt, packed, (const float *)a + m0 * K, (float *)c + m0 * N, N, K, (int)mb, nullptr, 0,
+                     stream));
+    }
+    return GQ_OK;
+  }
   const size_t Kp = gq_kpad(fmt, K);
   const _Float16 *a16 = (const _Float16 *)a;
   if (a_dtype != GQ_DT_F16 || Kp != K) {

@@ -183,11 +183,27 @@ def test_gemm_f32_activations_and_matmul_routing(dev):
     fmt, n, k = O.Q4_0, 96, 512
     w = O.gen_weights(fmt, n, k, seed=77)
     packed = _to_dev(gq.repack_host(fmt, w, n, k), dev)
-    for m in (1, 5, 16, 17, 48):
+    for m in (1, 5, 16, 17, 33, 48, 49):
         a = O.gen_x(m, k, seed=m)
         ref = O.gemv(fmt, w, a, n, k)
         c = gq.matmul(fmt, packed, _to_dev(a, dev), n, k).cpu().numpy()
         assert O.rel_l2(c, ref) <= TOL, m
+
+
+@pytest.mark.parametrize("fmt", [O.Q4_0, O.Q8_0, O.Q4_K])
+@pytest.mark.parametrize("m", [17, 20, 36, 48])
+def test_gemm_small_m_runs_gemv_groups(dev, fmt, m):
+    """gq_gemm with 16 < M <= 48 (f32 A and C) through 16-row GEMV groups,
+    the last group ragged (1..16 rows: int8 or fp16 GEMV kernel)."""
+    import gq
+    import torch
+    n, k = 200, 1024
+    w = O.gen_weights(fmt, n, k, seed=80 + m)
+    a = O.gen_x(m, k, seed=90 + m)
+    ref = O.gemv(fmt, w, a, n, k)
+    packed = _to_dev(gq.repack_host(fmt, w, n, k), dev)
+    c = gq.gemm(fmt, packed, _to_dev(a, dev), n, k, out_dtype=torch.float32).cpu().numpy()
+    assert O.rel_l2(c, ref) <= TOL
 
 
 def test_q8_i8_path(dev):
