@@ -509,28 +509,40 @@ GQ_DEV gq_half8 rfrag(const RStep<FMT, NJ> &st, int j, int ks, int step, const Q
 
 // Workgroup tile BM x BN, WM x WN waves; a wave owns (BM / WM) x (BN / WN) of C
 // (TM x NJ MFMA tiles of 32 x 32).  256 x 256 with 2 x 4 waves: two waves per SIMD.
-// AD: how many K steps ahead the activation tile is requested (1: two LDS
-// buffers; 2: three, for grids whose short steps would otherwise wait on each
-// tile's full load latency).  The weights are requested two steps ahead.
-template <int FMT, int CBF16, int BM, int BN, int WM, int WN, int AD = 1>
+// PD: pipeline depth.  The activation tile of step s + PD - 1 is requested
+// into one of PD LDS buffers when step s starts, and the weights of step
+// s + PD into the register stage step s has just used (PD stages), so a
+// step waits on loads issued PD - 1 steps earlier: depth 2 for large tiles,
+// 3 or 4 for grids whose short steps would otherwise wait out each load's
+// latency.
+template <int FMT, int CBF16, int BM, int BN, int WM, int WN, int PD = 2>
 __global__ void __launch_bounds__(64 * WM * WN) __attribute__((amdgpu_waves_per_eu(WM * WN / 4, WM * WN / 4)))
 k_gemm_rb(const uint8_t *__restrict__ w, uint32_t sc_off, const _Float16 *__restrict__ a16, int lda,
           void *__restrict__ c, int M, int N, int C, int nsteps, int tiles_m) {
   constexpr int KS = BK / 16;
   constexpr int NW = WM * WN, TM = BM / WM / 32, NJ = BN / WN / 32;  // waves, MFMA tiles per wave
   static_assert(TM >= 1 && NJ >= 1 && BM % (8 * NW) == 0, "tile shape");
+  static_assert(PD >= 2 && PD <= 4, "pipeline depth");
+  // one array per buffer: the buffer index is a compile-time constant
+  // everywhere, so no wait for an in-flight DMA into another buffer is needed
   __shared__ __attribute__((aligned(16))) _Float16 As_0[BM * BK];
   __shared__ __attribute__((aligned(16))) _Float16 As_1[BM * BK];
-  __shared__ __attribute__((aligned(16))) _Float16 As_2[AD == 2 ? BM * BK : 8];
-  static_assert(AD == 1 || AD == 2, "activation prefetch distance");
+  __shared__ __attribute__((aligned(16))) _Float16 As_2[PD >= 3 ? BM * BK : 8];
+  __shared__ __attribute__((aligned(16))) _Float16 As_3[PD >= 4 ? BM * BK : 8];
   auto As_of = [&](auto b) -> _Float16 * {
     constexpr int v = decltype(b)::value;
-    return v == 0 ? As_0 : v == 1 ? As_1 : As_2;
+    return v == 0 ? As_0 : v == 1 ? As_1 : v == 2 ? As_2 : As_3;
   };
   using B0 = std::integral_constant<int, 0>;
   using B1 = std::integral_constant<int, 1>;
   using B2 = std::integral_constant<int, 2>;
+  using B3 = std::integral_constant<int, 3>;
   constexpr int NA = BM / (8 * NW);  // activation-tile loads per thread and K step
+  // loads a step may leave in flight at its end: the activation tiles of
+  // steps s + 2 .. s + PD - 1 and the weights of steps s + 2 .. s + PD
+  constexpr int pend = (PD - 2) * NA + (PD - 1) * 3 * NJ;
+  static_assert(pend <= 63, "vmcnt immediate");
+  constexpr int kWaitPend = 0x0F70 | (pend & 15) | ((pend >> 4) << 14);
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int wm = wave / WN, wn = wave % WN;
@@ -569,20 +581,21 @@ k_gemm_rb(const uint8_t *__restrict__ w, uint32_t sc_off, const _Float16 *__rest
 #pragma unroll
       for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.f;
 
-  RStep<FMT, NJ> wst[2];
+  RStep<FMT, NJ> wst[PD];
   const int arow = (BM / WM) * wm + (lane & 31);
   const int sw = a_swz(lane & 31);
 
-  auto run_step = [&](int step, auto buf_c, auto wbuf_c) {
+  // step `step` (buffer and register stage step % PD); steps past the end
+  // are skipped by every wave alike
+  auto run_step = [&](int step, auto buf_c) {
     constexpr int BUF = decltype(buf_c)::value;
-    // the buffer the activation tile of step + AD goes to
-    using NB = std::integral_constant<int, AD == 1 ? (BUF ^ 1) : (BUF + 2) % 3>;
-    const int s1 = step + AD < nsteps ? step + AD : nsteps - 1;
-    const int s2 = step + 2 < nsteps ? step + 2 : nsteps - 1;
+    using NB = std::integral_constant<int, (BUF + PD - 1) % PD>;  // buffer of step + PD - 1
+    const int s1 = step + PD - 1 < nsteps ? step + PD - 1 : nsteps - 1;
+    const int s2 = step + PD < nsteps ? step + PD : nsteps - 1;
     load_a_lds<BM, NW>(a16, lda, M, m0, s1, wave, lane, As_of(NB{}));
     __builtin_amdgcn_sched_barrier(0);
     const _Float16 *As = As_of(buf_c) + arow * BK;
-    RStep<FMT, NJ> &cur = wst[decltype(wbuf_c)::value];
+    RStep<FMT, NJ> &cur = wst[BUF];
     gq_half8 af[2][TM];
     auto read_a = [&](int ks, int fb) {
       const int ch = (4 * (ks >> 1) + 2 * kh + (ks & 1)) ^ sw;
@@ -602,43 +615,34 @@ k_gemm_rb(const uint8_t *__restrict__ w, uint32_t sc_off, const _Float16 *__rest
         for (int i = 0; i < TM; ++i) acc[i][j] = gq_mfma32(af[ks & 1][i], bf, acc[i][j]);
       }
     }
-    // the register stage of this step is free: request step + 2 into it
+    // the register stage of this step is free: request step + PD into it
     load_rstep<FMT, NJ>(w, qo, so, s2, cur);
-    // the A tile and the weights of step + 1 must have landed; the 3 NJ weight
-    // loads of step + 2 just issued (AD = 2: and the activation tile of
-    // step + 2 before them) may stay in flight
-    constexpr int pend = 3 * NJ + (AD == 2 ? NA : 0);
-    static_assert(pend <= 63, "vmcnt immediate");
-    __builtin_amdgcn_s_waitcnt(0x0F70 | (pend & 15) | ((pend >> 4) << 14));
+    // the activation tile and the weights of step + 1 must have landed
+    __builtin_amdgcn_s_waitcnt(kWaitPend);
     __syncthreads();
   };
 
-  load_a_lds<BM, NW>(a16, lda, M, m0, 0, wave, lane, As_0);
-  load_rstep<FMT, NJ>(w, qo, so, 0, wst[0]);
-  if constexpr (AD == 1) {
-    load_rstep<FMT, NJ>(w, qo, so, nsteps > 1 ? 1 : 0, wst[1]);
-    __builtin_amdgcn_s_waitcnt(0x0F70);
-    __syncthreads();
-    for (int step = 0; step < nsteps; step += 2) {
-      run_step(step, B0{}, B0{});
-      run_step(step + 1, B1{}, B1{});
-    }
-  } else {
-    load_a_lds<BM, NW>(a16, lda, M, m0, nsteps > 1 ? 1 : 0, wave, lane, As_1);
-    load_rstep<FMT, NJ>(w, qo, so, nsteps > 1 ? 1 : 0, wst[1]);
-    constexpr int pend = 3 * NJ + NA;  // step 1's tile and weights may stay in flight
-    __builtin_amdgcn_s_waitcnt(0x0F70 | (pend & 15) | ((pend >> 4) << 14));
-    __syncthreads();
-    // buffers rotate with period 3, weight stages with period 2: unrolled by 6
-    // (nsteps is even; a step past the end is skipped by every wave alike)
-    for (int step = 0; step < nsteps; step += 6) {
-      run_step(step, B0{}, B0{});
-      run_step(step + 1, B1{}, B1{});
-      if (step + 2 < nsteps) run_step(step + 2, B2{}, B0{});
-      if (step + 3 < nsteps) run_step(step + 3, B0{}, B1{});
-      if (step + 4 < nsteps) run_step(step + 4, B1{}, B0{});
-      if (step + 5 < nsteps) run_step(step + 5, B2{}, B1{});
-    }
+  // prologue: tiles 0 .. PD - 2 and weights 0 .. PD - 1 requested; step 0's
+  // must land
+  auto prime = [&](auto b) {
+    constexpr int i = decltype(b)::value;
+    const int st = i < nsteps ? i : nsteps - 1;
+    if constexpr (i < PD - 1) load_a_lds<BM, NW>(a16, lda, M, m0, st, wave, lane, As_of(b));
+    load_rstep<FMT, NJ>(w, qo, so, st, wst[i]);
+  };
+  prime(B0{});
+  prime(B1{});
+  if constexpr (PD >= 3) prime(B2{});
+  if constexpr (PD >= 4) prime(B3{});
+  __builtin_amdgcn_s_waitcnt(kWaitPend);
+  __syncthreads();
+  for (int step = 0; step < nsteps; step += PD) {
+    run_step(step, B0{});
+    if (step + 1 < nsteps) run_step(step + 1, B1{});
+    if constexpr (PD >= 3)
+      if (step + 2 < nsteps) run_step(step + 2, B2{});
+    if constexpr (PD >= 4)
+      if (step + 3 < nsteps) run_step(step + 3, B3{});
   }
 
 #pragma unroll
@@ -705,54 +709,63 @@ int launch_cfg(const void *packed, const _Float16 *a16, int lda, void *c, int M,
   return gq_last_launch();
 }
 
-// ad_default: the activation prefetch distance of the shape (GQ_GEMM_AD=1|2
-// overrides it, for tuning)
+// pd_default: the pipeline depth of the shape (GQ_GEMM_PD=2|3|4 overrides it,
+// for tuning)
 template <int FMT, int CBF16, int BM, int BN, int WM, int WN>
 int launch_rb(const void *packed, const _Float16 *a16, int lda, void *c, int M, int N, int K, hipStream_t s,
-              int ad_default = 1) {
+              int pd_default = 4) {
   const int C = (int)gq_chunks(FMT, K);
   const int nsteps = (int)(gq_kpad(FMT, K) / BK);
   const int tiles_m = (M + BM - 1) / BM, tiles_n = (N + BN - 1) / BN;
-  const char *e = getenv("GQ_GEMM_AD");
-  const int ad = e ? atoi(e) : ad_default;
-  if (ad == 2)
-    hipLaunchKernelGGL((k_gemm_rb<FMT, CBF16, BM, BN, WM, WN, 2>), dim3((unsigned)(tiles_m * tiles_n)),
-                       dim3(64 * WM * WN), 0, s, (const uint8_t *)packed, (uint32_t)gq_sc_plane_offset(FMT, N, K), a16,
-                       lda, c, M, N, C, nsteps, tiles_m);
-  else
-    hipLaunchKernelGGL((k_gemm_rb<FMT, CBF16, BM, BN, WM, WN>), dim3((unsigned)(tiles_m * tiles_n)),
-                       dim3(64 * WM * WN), 0, s, (const uint8_t *)packed, (uint32_t)gq_sc_plane_offset(FMT, N, K), a16,
-                       lda, c, M, N, C, nsteps, tiles_m);
+  const char *e = getenv("GQ_GEMM_PD");
+  const int pd = e ? atoi(e) : pd_default;
+#define GQ_LAUNCH_RB(PD)                                                                                        \
+  hipLaunchKernelGGL((k_gemm_rb<FMT, CBF16, BM, BN, WM, WN, PD>), dim3((unsigned)(tiles_m * tiles_n)),          \
+                     dim3(64 * WM * WN), 0, s, (const uint8_t *)packed, (uint32_t)gq_sc_plane_offset(FMT, N, K), \
+                     a16, lda, c, M, N, C, nsteps, tiles_m)
+  if (pd == 4) GQ_LAUNCH_RB(4);
+  else if (pd == 3) GQ_LAUNCH_RB(3);
+  else GQ_LAUNCH_RB(2);
+#undef GQ_LAUNCH_RB
   return gq_last_launch();
 }
 
-// Kernel and tile shape (measured on MI355X, M = 512 / 2048 x N = 4096 / 14336):
+// Kernel and tile shape (measured on MI355X, M = 64 .. 2048 x N = 4096 / 14336):
 //   0: register-B kernel, 256 x 256 (448 workgroups at 2048 x 14336)
 //   3: LDS-B kernel, 256 x 256 (Q4_K at that size: its per-fragment
 //      sub-block decoding costs more than the LDS round trip saves)
-//   4: register-B, 256 x 128, for >= 192 workgroups (activation tile two K
-//      steps ahead: 4-6 % faster at 512 x 14336 and 2048 x 4096)
-//   6: register-B, 128 x 128, smaller problems (Q4_K: activation tile two K
-//      steps ahead, 62 -> 56 us at 512 x 4096)
-// 1, 2 (LDS-B 256 x 128, 128 x 128) and 5, 7, 8 (other register-B shapes)
-// are kept for tuning through GQ_GEMM_TILE.
+//   4: register-B, 256 x 128, for >= 192 workgroups
+//   6: register-B, 128 x 128, for >= 192 workgroups (1024 x 4096, 256 x 14336)
+//   9: register-B, 128 x 64 (4 waves), for >= 192 workgroups (512 x 4096:
+//      50 vs 56 us with 128 x 128; 128 x 14336: 48 vs 54 us)
+//  11: register-B, 64 x 64 (4 waves), smaller problems (M <= 256 at N = 4096:
+//      40-43 us vs 49-53)
+// The register-B kernel runs with pipeline depth 4 (1-3 % faster than 2 on
+// the shapes measured), except 256 x 256: depth 2 (at 4 the Q8_0 and Q4_K
+// instances spill registers; Q4_0 gains nothing).  1, 2 (LDS-B 256 x 128, 128 x 128) and 5, 7, 8, 10
+// (other register-B shapes) are kept for tuning through GQ_GEMM_TILE.
 int pick_tile(int fmt, int M, int N) {
   auto wgs = [&](int bm, int bn) { return (long)((M + bm - 1) / bm) * ((N + bn - 1) / bn); };
   if (const char *e = getenv("GQ_GEMM_TILE")) return atoi(e);
   if (wgs(256, 256) >= 384) return fmt == GQ_FMT_Q4_K ? 3 : 0;
   if (wgs(256, 128) >= 192) return 4;
-  return 6;
+  if (wgs(128, 128) >= 192) return 6;
+  if (wgs(128, 64) >= 192) return 9;
+  return 11;
 }
 
 template <int FMT, int CBF16>
 int launch_fmt(const void *packed, const _Float16 *a16, int lda, void *c, int M, int N, int K, hipStream_t s) {
   switch (pick_tile(FMT, M, N)) {
-  case 0: return launch_rb<FMT, CBF16, 256, 256, 2, 4>(packed, a16, lda, c, M, N, K, s);
-  case 4: return launch_rb<FMT, CBF16, 256, 128, 2, 4>(packed, a16, lda, c, M, N, K, s, 2);
+  case 0: return launch_rb<FMT, CBF16, 256, 256, 2, 4>(packed, a16, lda, c, M, N, K, s, 2);
+  case 4: return launch_rb<FMT, CBF16, 256, 128, 2, 4>(packed, a16, lda, c, M, N, K, s);
   case 5: return launch_rb<FMT, CBF16, 128, 256, 2, 4>(packed, a16, lda, c, M, N, K, s);
-  case 6: return launch_rb<FMT, CBF16, 128, 128, 2, 4>(packed, a16, lda, c, M, N, K, s, FMT == GQ_FMT_Q4_K ? 2 : 1);
+  case 6: return launch_rb<FMT, CBF16, 128, 128, 2, 4>(packed, a16, lda, c, M, N, K, s);
   case 7: return launch_rb<FMT, CBF16, 128, 128, 2, 2>(packed, a16, lda, c, M, N, K, s);
   case 8: return launch_rb<FMT, CBF16, 256, 128, 4, 2>(packed, a16, lda, c, M, N, K, s);
+  case 9: return launch_rb<FMT, CBF16, 128, 64, 2, 2>(packed, a16, lda, c, M, N, K, s);
+  case 10: return launch_rb<FMT, CBF16, 64, 128, 2, 4>(packed, a16, lda, c, M, N, K, s);
+  case 11: return launch_rb<FMT, CBF16, 64, 64, 2, 2>(packed, a16, lda, c, M, N, K, s);
   default: return launch_rb<FMT, CBF16, 128, 128, 2, 4>(packed, a16, lda, c, M, N, K, s);
   case 3: return launch_cfg<FMT, CBF16, 256, 256>(packed, a16, lda, c, M, N, K, s);
   case 1: return launch_cfg<FMT, CBF16, 256, 128>(packed, a16, lda, c, M, N, K, s);

@@ -243,17 +243,18 @@ def test_compat_int8_int4_launchers(dev, m):
     assert O.rel_l2(y4, ref4) <= 1e-5
 
 
-@pytest.mark.parametrize("tile,ad", [(0, 1), (0, 2), (1, 1), (2, 1), (3, 1), (4, 1), (4, 2), (5, 1), (5, 2),
-                                     (6, 1), (6, 2), (7, 1), (7, 2), (8, 1), (8, 2)])
+@pytest.mark.parametrize("tile,pd", [(0, 2), (0, 4), (1, 2), (2, 2), (3, 2), (4, 2), (4, 3), (4, 4), (5, 4),
+                                     (6, 2), (6, 3), (6, 4), (7, 4), (8, 4), (9, 3), (9, 4), (10, 4), (11, 2),
+                                     (11, 4)])
 @pytest.mark.parametrize("fmt", [O.Q4_0, O.Q8_0, O.Q4_K])
-def test_gemm_every_kernel_shape(dev, fmt, tile, ad, monkeypatch):
+def test_gemm_every_kernel_shape(dev, fmt, tile, pd, monkeypatch):
     """Each GEMM kernel / tile shape (forced through GQ_GEMM_TILE) and, for the
-    register-B kernel, each activation prefetch distance (GQ_GEMM_AD), on a
-    shape with partial tiles in M and N."""
+    register-B kernel, pipeline depths (GQ_GEMM_PD), on a shape with partial
+    tiles in M and N."""
     import gq
     import torch
     monkeypatch.setenv("GQ_GEMM_TILE", str(tile))
-    monkeypatch.setenv("GQ_GEMM_AD", str(ad))
+    monkeypatch.setenv("GQ_GEMM_PD", str(pd))
     m, n, k = 300, 400, 1024
     w = O.gen_weights(fmt, n, k, seed=60 + tile)
     a = torch.randn(m, k, generator=torch.Generator().manual_seed(tile)).to(torch.bfloat16)
@@ -264,14 +265,14 @@ def test_gemm_every_kernel_shape(dev, fmt, tile, ad, monkeypatch):
 
 
 @pytest.mark.parametrize("fmt,k", [(O.Q4_0, 128), (O.Q8_0, 384), (O.Q4_K, 256), (O.Q4_K, 768), (O.Q4_0, 1536)])
-@pytest.mark.parametrize("ad", [1, 2])
-def test_gemm_short_k_loops(dev, fmt, k, ad, monkeypatch):
-    """K step counts of 2..24: the unrolled step loops' guarded tails for both
-    activation prefetch distances (128 x 128 and 256 x 128 tiles)."""
+@pytest.mark.parametrize("pd", [2, 3, 4])
+def test_gemm_short_k_loops(dev, fmt, k, pd, monkeypatch):
+    """K step counts of 2..24 (fewer steps than the pipeline is deep, and the
+    unrolled step loops' guarded tails) for each pipeline depth."""
     import gq
     import torch
-    monkeypatch.setenv("GQ_GEMM_AD", str(ad))
-    for tile in (4, 6):
+    monkeypatch.setenv("GQ_GEMM_PD", str(pd))
+    for tile in (4, 6, 11):
         monkeypatch.setenv("GQ_GEMM_TILE", str(tile))
         m, n = 200, 160
         w = O.gen_weights(fmt, n, k, seed=70 + k)
@@ -279,7 +280,7 @@ def test_gemm_short_k_loops(dev, fmt, k, ad, monkeypatch):
         ref = O.gemv(fmt, w, a.float().numpy(), n, k)
         packed = _to_dev(gq.repack_host(fmt, w, n, k), dev)
         c = gq.gemm(fmt, packed, a.to(dev), n, k).cpu().numpy()
-        assert O.rel_l2(c, ref) <= TOL, (tile, ad)
+        assert O.rel_l2(c, ref) <= TOL, (tile, pd)
 
 
 def test_q6k_matmul_batches_the_gemv(dev):
