@@ -408,7 +408,7 @@ def main():
             del c
             torch.cuda.empty_cache()
         for fmt, fname in ((O.Q4_0, "q4_0"), (O.Q8_0, "q8_0"), (O.Q4_K, "q4_k")):
-            for m in (512, 2048):
+            for m in (64, 512, 2048):
                 for n in (4096, 14336):
                     name = f"gemm_{fname}_m{m}_{n}x4096"
                     log(f"[bench] {name}")

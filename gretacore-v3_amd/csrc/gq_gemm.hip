@@ -666,8 +666,11 @@ k_gemm_rb(const uint8_t *__restrict__ w, uint32_t sc_off, const _Float16 *__rest
 
 // Activations -> fp16 [M][ldo] (ldo >= K, columns K..ldo-1 zero), 8 per thread.
 // bf16 -> fp16 is exact inside fp16's range; fp32 rounds to nearest even.
+// q4perm: each run of 8 in the order of the 4-bit B fragments of the skinny
+// GEMM (element e holds k slot {0,2,4,6,1,3,5,7}[e], elements 2, 3, 6, 7
+// divided by 16 -- exact, before the one rounding to fp16).
 __global__ void __launch_bounds__(256) k_a_to_f16(const void *__restrict__ a, int a_dtype, _Float16 *__restrict__ o,
-                                                  int M, int K, int ldo) {
+                                                  int M, int K, int ldo, int q4perm) {
   const size_t i = (size_t)blockIdx.x * 256 + threadIdx.x;
   const int per_row = ldo / 8;
   if (i >= (size_t)M * per_row) return;
@@ -694,6 +697,24 @@ __global__ void __launch_bounds__(256) k_a_to_f16(const void *__restrict__ a, in
       h[q] = (_Float16)v0[q];
       h[4 + q] = (_Float16)v1[q];
     }
+  }
+  if (q4perm) {
+    // from the values themselves (fp32 for f32 input: one rounding)
+    float v[8];
+    if (k0 >= K) {
+#pragma unroll
+      for (int q = 0; q < 8; ++q) v[q] = 0.f;
+    } else if (a_dtype == GQ_DT_F32) {
+      const float *f = reinterpret_cast<const float *>(a) + m * K + k0;
+#pragma unroll
+      for (int q = 0; q < 8; ++q) v[q] = f[q];
+    } else {
+#pragma unroll
+      for (int q = 0; q < 8; ++q) v[q] = (float)h[q];
+    }
+    constexpr int perm[8] = {0, 2, 4, 6, 1, 3, 5, 7};
+#pragma unroll
+    for (int e = 0; e < 8; ++e) h[e] = (_Float16)((e & 2) ? v[perm[e]] * 0.0625f : v[perm[e]]);
   }
   *reinterpret_cast<gq_half8 *>(o + m * ldo + k0) = h;
 }
@@ -786,7 +807,7 @@ extern "C" size_t gq_gemm_workspace_bytes(int fmt, size_t M, size_t K) {
   // activations other than fp16 with K == padded K are first written as fp16
   // [M][padded K]
   if (!gq_fmt_valid(fmt) || gq_fmt_is_q6k(fmt) || M > GQ_MAX_DIM || K > GQ_MAX_DIM) return 0;
-  return gq_align256(M * gq_kpad(fmt, K) * 2);
+  return gq_align256(M * (gq_kpad(fmt, K) + 8) * 2);
 }
 
 extern "C" int gq_gemm(int fmt, const void *packed, const void *a, int a_dtype, void *c, int c_dtype, size_t M,
@@ -802,19 +823,34 @@ extern "C" int gq_gemm(int fmt, const void *packed, const void *a, int a_dtype, 
   // the kernel addresses the packed tensor with 32-bit offsets
   GQ_CHECK(gq_packed_bytes(fmt, N, K) < ((size_t)1 << 32), GQ_ERR_INVALID_ARGS);
   hipStream_t s = (hipStream_t)stream;
-  // 17..48 rows: the GEMM's smallest tile (128 x 128) pads M to 128 and gives
-  // N / 128 workgroups, each walking all of K (45-55 us at 4096 x 4096 or
-  // 14336 x 4096 whatever M); the batch GEMV over groups of 16 rows spreads
-  // over every CU (M = 32: 16 / 27 us)
-  if (M > GQ_MAX_BATCH && M <= 3 * GQ_MAX_BATCH && a_dtype == GQ_DT_F32 && c_dtype == GQ_DT_F32) {
-    for (size_t m0 = 0; m0 < M; m0 += GQ_MAX_BATCH) {
-      const size_t mb = M - m0 < GQ_MAX_BATCH ? M - m0 : GQ_MAX_BATCH;
-      GQ_TRY(gq_gemv(fmt, packed, (const float *)a + m0 * K, (float *)c + m0 * N, N, K, (int)mb, nullptr, 0,
-                     stream));
-    }
-    return GQ_OK;
-  }
+  // Few rows: the tiled GEMM gives N / 64 .. N / 128 workgroups, each walking
+  // all of K (37-55 us at 4096 x 4096 or 14336 x 4096 for any M <= 256); the
+  // skinny kernel takes the shapes gq_gemm_skinny_plan accepts (4096 x 4096:
+  // 10 / 14 / 16 us at M = 17 / 64 / 128; 14336 x 4096: 19 / 27 us at
+  // M = 17 / 64).
   const size_t Kp = gq_kpad(fmt, K);
+  int sk_ct = 0, sk_nck = 0;
+  if (gq_gemm_skinny_plan(fmt, M, N, K, &sk_ct, &sk_nck) == GQ_OK) {
+    // A in the skinny kernel's order, always through the workspace, rows 16
+    // bytes longer than a multiple of 4 KiB: each A load reads 16 rows, and at
+    // a 4 KiB-multiple stride they fall into the same L2 channel (64 x 4096:
+    // 19.9 -> 14.9 us; the tiled GEMM is 2-7 % slower with the padding and
+    // keeps the plain stride)
+    const size_t ldo = Kp + 8;
+    const size_t need = gq_gemm_workspace_bytes(fmt, M, K);
+    if (!ws) {
+      GQ_TRY(gq_default_workspace(need, &ws));
+      ws_bytes = need;
+    }
+    GQ_CHECK(ws_bytes >= need, GQ_ERR_WORKSPACE);
+    const size_t n8 = M * (ldo / 8);
+    const int q4 = fmt == GQ_FMT_Q4_0 || gq_fmt_is_q4k(fmt);
+    hipLaunchKernelGGL(k_a_to_f16, dim3((unsigned)((n8 + 255) / 256)), dim3(256), 0, s, a, a_dtype, (_Float16 *)ws,
+                       (int)M, (int)K, (int)ldo, q4);
+    GQ_TRY(gq_last_launch());
+    return gq_launch_gemm_skinny(fmt, packed, (const _Float16 *)ws, (int)ldo, c, c_dtype == GQ_DT_BF16, (int)M, (int)N,
+                                 (int)K, s);
+  }
   const _Float16 *a16 = (const _Float16 *)a;
   if (a_dtype != GQ_DT_F16 || Kp != K) {
     const size_t need = gq_gemm_workspace_bytes(fmt, M, K);
@@ -825,7 +861,7 @@ extern "C" int gq_gemm(int fmt, const void *packed, const void *a, int a_dtype, 
     GQ_CHECK(ws_bytes >= need, GQ_ERR_WORKSPACE);
     const size_t n8 = M * (Kp / 8);
     hipLaunchKernelGGL(k_a_to_f16, dim3((unsigned)((n8 + 255) / 256)), dim3(256), 0, s, a, a_dtype, (_Float16 *)ws,
-                       (int)M, (int)K, (int)Kp);
+                       (int)M, (int)K, (int)Kp, 0);
     GQ_TRY(gq_last_launch());
     a16 = (const _Float16 *)ws;
   }

@@ -554,6 +554,150 @@ k_gemv_h1(const uint8_t *__restrict__ w, size_t sc_off, const float *__restrict_
   }
 }
 
+// Skinny GEMM (M <= 256): C[m][n] = sum_k A[m][k] W[n][k] for few rows of A.
+// The tiled GEMM walks K in 64-element steps, each waiting on loads requested a
+// few steps earlier, on grids of few workgroups; here a workgroup takes CT row
+// tiles of W (16 output columns each) and a block of 64 rows of A, and splits
+// K over its KW = 8 waves like the GEMV: each wave requests all of its chunks
+// (at most NCK) of the CT tiles up front, streams its A fragments straight
+// from global memory (no LDS: no two waves share them) one 64-k step ahead,
+// and issues MT x CT x 2 v_mfma_f32_16x16x32_f16 per step on weights
+// dequantized once (dequant_step).  The KW partial tiles are added in LDS.
+// A is fp16 [M][lda] in the B fragments' order: for the 4-bit formats each
+// aligned run of 8 k holds slots kQ4Perm with the kQ4Div16 slots divided by 16
+// (k_a_to_f16 with q4perm).  Rows >= M read row M - 1 and are not stored.
+template <int FMT, int CT, int NCK, bool CBF16>
+__global__ void __launch_bounds__(512) k_gemm_sk(const uint8_t *__restrict__ w, size_t sc_off,
+                                                 const _Float16 *__restrict__ a16, int lda, void *__restrict__ c,
+                                                 int M, int N, int C) {
+  using F = HFmt<FMT>;
+  constexpr int KW = 8, MT = 4;
+  constexpr int NS = NCK * F::STEPS;  // 64-k steps per wave (static bound)
+  __shared__ gq_f4 red[KW][CT * MT][64];
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int g = lane >> 4, r = lane & 15;
+  const int ntiles = (int)gq_tiles(N);
+  const int m0 = (int)blockIdx.y * 16 * MT;
+  const int c0 = (C * wave) / KW, c1 = (C * (wave + 1)) / KW;
+  const int nck = c1 - c0;  // <= NCK (host-checked); 0 when C < KW
+  const int clast = nck > 0 ? c1 - 1 : c0;  // last chunk a load may name (c0 < C always)
+  const uint32_t qlane = 16u * (uint32_t)lane;
+  const uint32_t slane = (FMT == GQ_FMT_Q4_K || FMT == GQ_FMT_Q6_K) ? 16u * (uint32_t)r
+                                                                    : 8u * (uint32_t)r + 4u * (uint32_t)(g >> 1);
+  // weights: every chunk of the wave, tile by tile (surplus loads re-read the
+  // last chunk)
+  HChunk<FMT> ch[CT][NCK];
+#pragma unroll
+  for (int ct = 0; ct < CT; ++ct) {
+    const int t0 = (int)blockIdx.x * CT + ct;
+    const size_t tb = (size_t)(t0 < ntiles ? t0 : ntiles - 1) * (size_t)C;
+#pragma unroll
+    for (int i = 0; i < NCK; ++i) {
+      const int ci = c0 + i <= clast ? c0 + i : clast;
+      load_hchunk<FMT>(w + (tb + ci) * F::QB, w + sc_off + (tb + ci) * F::SB, qlane, slane, ch[ct][i]);
+    }
+  }
+  // this lane's A rows: 16 mt + r of the block, k offset 16 g
+  const _Float16 *arow[MT];
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt) {
+    const int row = m0 + 16 * mt + r;
+    arow[mt] = a16 + (size_t)(row < M ? row : M - 1) * lda + 16 * g;
+  }
+  // A fragments of step s: chunk s / STEPS of the wave, 64-k step s % STEPS,
+  // halves j = 0, 1 (k + 8 j)
+  auto load_a = [&](int s, gq_half8 (&af)[2][MT]) {
+    const int i = s / F::STEPS, ci = c0 + i <= clast ? c0 + i : clast;
+    const int k = ci * F::CK + 64 * (s % F::STEPS);
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) {
+      af[0][mt] = *reinterpret_cast<const gq_half8 *>(arow[mt] + k);
+      af[1][mt] = *reinterpret_cast<const gq_half8 *>(arow[mt] + k + 8);
+    }
+  };
+  gq_f4 acc[CT][MT];
+#pragma unroll
+  for (int ct = 0; ct < CT; ++ct)
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) acc[ct][mt] = gq_f4{0.f, 0.f, 0.f, 0.f};
+  const uint32_t mg = magic_h2_vgpr();
+  // A fragments requested AP steps ahead (ring of AP + 1; 2 and 3 measured no
+  // faster)
+  constexpr int AP = 1;
+  gq_half8 abuf[AP + 1][2][MT];
+#pragma unroll
+  for (int s = 0; s < AP && s < NS; ++s) load_a(s, abuf[s]);
+#pragma unroll
+  for (int s = 0; s < NS; ++s) {
+    if (s + AP < NS) load_a(s + AP, abuf[(s + AP) % (AP + 1)]);
+    // keep the prefetch ahead of this step's work (the scheduler would
+    // otherwise sink it below the MFMAs that wait on the current fragments)
+    __builtin_amdgcn_sched_barrier(0);
+    const int i = s / F::STEPS, m = s % F::STEPS;
+    // steps past the wave's chunks multiply zeros (no branch: a branch here
+    // makes the compiler wait for every load in flight)
+    const uint32_t live = i < nck ? 0xFFFFFFFFu : 0u;
+#pragma unroll
+    for (int ct = 0; ct < CT; ++ct) {
+      gq_half8 b0, b1;
+      dequant_step<FMT>(ch[ct][i], m, g, mg, b0, b1);
+      gq_u4 u0 = __builtin_bit_cast(gq_u4, b0), u1 = __builtin_bit_cast(gq_u4, b1);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        u0[e] &= live;
+        u1[e] &= live;
+      }
+      b0 = __builtin_bit_cast(gq_half8, u0);
+      b1 = __builtin_bit_cast(gq_half8, u1);
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt) {
+        acc[ct][mt] = mfma16h(abuf[s % (AP + 1)][0][mt], b0, acc[ct][mt]);
+        acc[ct][mt] = mfma16h(abuf[s % (AP + 1)][1][mt], b1, acc[ct][mt]);
+      }
+    }
+  }
+  // partial tiles of the KW waves; wave p adds up pair p (and p + KW, ...)
+#pragma unroll
+  for (int ct = 0; ct < CT; ++ct)
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) red[wave][ct * MT + mt][lane] = acc[ct][mt];
+  __syncthreads();
+  for (int p = wave; p < CT * MT; p += KW) {
+    gq_f4 sum = red[0][p][lane];
+#pragma unroll
+    for (int q = 1; q < KW; ++q) {
+      const gq_f4 v = red[q][p][lane];
+      sum[0] += v[0];
+      sum[1] += v[1];
+      sum[2] += v[2];
+      sum[3] += v[3];
+    }
+    const int ct = p / MT, mt = p % MT;
+    const int t0 = (int)blockIdx.x * CT + ct;
+    const int col = t0 * 16 + r;
+    if (t0 >= ntiles || col >= N) continue;
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+      const int row = m0 + 16 * mt + 4 * g + v;
+      if (row >= M) continue;
+      if constexpr (CBF16) {
+        uint32_t u = __float_as_uint(sum[v]);
+        uint16_t hb;
+        if ((u & 0x7F800000u) == 0x7F800000u) {
+          hb = (uint16_t)((u >> 16) | ((u & 0xFFFFu) ? 0x40u : 0u));
+        } else {
+          u += 0x7FFFu + ((u >> 16) & 1u);
+          hb = (uint16_t)(u >> 16);
+        }
+        reinterpret_cast<uint16_t *>(c)[(size_t)row * N + col] = hb;
+      } else {
+        reinterpret_cast<float *>(c)[(size_t)row * N + col] = sum[v];
+      }
+    }
+  }
+}
+
 int env_int(const char *name) {
   const char *e = getenv(name);
   return e ? atoi(e) : 0;
@@ -713,5 +857,72 @@ int gq_launch_gemv_h(int fmt, const void *packed, const float *x, float *y, int 
   case GQ_FMT_Q4_0: return launch_h<GQ_FMT_Q4_0>(packed, x, y, N, K, nb, s);
   case GQ_FMT_Q8_0: return launch_h<GQ_FMT_Q8_0>(packed, x, y, N, K, nb, s);
   default: return launch_h<GQ_FMT_Q4_K>(packed, x, y, N, K, nb, s);
+  }
+}
+
+// Skinny GEMM plan: M <= 256, a chunk list of at most 4 per wave (K <= 4096
+// for Q4_0 / Q8_0, 8192 for Q4_K), CT = 2 row tiles per workgroup where that
+// still gives every CU a workgroup, and at most two workgroups per CU in all
+// (each reads its 64 rows of A whole: measured slower than the tiled GEMM
+// beyond that, e.g. 128 x 14336: 54 vs 45 us).  GQ_ERR_UNSUPPORTED otherwise
+// (the tiled GEMM takes the shape).  GQ_GEMM_SKINNY=0, or a tiled shape forced
+// through GQ_GEMM_TILE, turns the kernel off.
+int gq_gemm_skinny_plan(int fmt, size_t M, size_t N, size_t K, int *ct_out, int *nck_out) {
+  const char *e = getenv("GQ_GEMM_SKINNY");
+  if ((e && e[0] == '0') || getenv("GQ_GEMM_TILE")) return GQ_ERR_UNSUPPORTED;  // (a forced tiled shape)
+  if (gq_fmt_is_q6k(fmt) || M == 0 || M > 256 || N == 0 || K == 0) return GQ_ERR_UNSUPPORTED;
+  const int f = gq_fmt_is_q4k(fmt) ? GQ_FMT_Q4_K : fmt;
+  const int C = (int)gq_chunks(f, K);
+  const int nck = (C + 7) / 8;
+  const int nckp = nck <= 1 ? 1 : nck <= 2 ? 2 : nck <= 4 ? 4 : 0;
+  if (nckp == 0) return GQ_ERR_UNSUPPORTED;
+  const size_t tiles = gq_tiles(N), gy = (M + 63) / 64;
+  const int cus0 = gq_device_cus();
+  const size_t cus = cus0 > 0 ? (size_t)cus0 : 256;
+  const int ct = ((tiles + 1) / 2) * gy >= cus ? 2 : 1;
+  if (((tiles + ct - 1) / ct) * gy > 2 * cus) return GQ_ERR_UNSUPPORTED;
+  *ct_out = ct;
+  *nck_out = nckp;
+  return GQ_OK;
+}
+
+namespace {
+template <int FMT, int CT, bool CBF16>
+int launch_sk(const void *packed, const _Float16 *a16, int lda, void *c, int M, int N, int K, int nck,
+              hipStream_t s) {
+  const int C = (int)gq_chunks(FMT, K);
+  const dim3 grid((unsigned)((gq_tiles(N) + CT - 1) / CT), (unsigned)((M + 63) / 64));
+  const size_t sc_off = gq_sc_plane_offset(FMT, N, K);
+  const uint8_t *w = (const uint8_t *)packed;
+  if (nck <= 1)
+    hipLaunchKernelGGL((k_gemm_sk<FMT, CT, 1, CBF16>), grid, dim3(512), 0, s, w, sc_off, a16, lda, c, M, N, C);
+  else if (nck <= 2)
+    hipLaunchKernelGGL((k_gemm_sk<FMT, CT, 2, CBF16>), grid, dim3(512), 0, s, w, sc_off, a16, lda, c, M, N, C);
+  else
+    hipLaunchKernelGGL((k_gemm_sk<FMT, CT, 4, CBF16>), grid, dim3(512), 0, s, w, sc_off, a16, lda, c, M, N, C);
+  return gq_last_launch();
+}
+template <int FMT, bool CBF16>
+int launch_sk_ct(const void *packed, const _Float16 *a16, int lda, void *c, int M, int N, int K, int ct, int nck,
+                 hipStream_t s) {
+  return ct == 2 ? launch_sk<FMT, 2, CBF16>(packed, a16, lda, c, M, N, K, nck, s)
+                 : launch_sk<FMT, 1, CBF16>(packed, a16, lda, c, M, N, K, nck, s);
+}
+template <int FMT>
+int launch_sk_fmt(const void *packed, const _Float16 *a16, int lda, void *c, int cbf16, int M, int N, int K, int ct,
+                  int nck, hipStream_t s) {
+  return cbf16 ? launch_sk_ct<FMT, true>(packed, a16, lda, c, M, N, K, ct, nck, s)
+               : launch_sk_ct<FMT, false>(packed, a16, lda, c, M, N, K, ct, nck, s);
+}
+}  // namespace
+
+int gq_launch_gemm_skinny(int fmt, const void *packed, const _Float16 *a16, int lda, void *c, int cbf16, int M, int N,
+                          int K, hipStream_t s) {
+  int ct = 1, nck = 1;
+  GQ_TRY(gq_gemm_skinny_plan(fmt, (size_t)M, (size_t)N, (size_t)K, &ct, &nck));
+  switch (gq_fmt_is_q4k(fmt) ? GQ_FMT_Q4_K : fmt) {
+  case GQ_FMT_Q4_0: return launch_sk_fmt<GQ_FMT_Q4_0>(packed, a16, lda, c, cbf16, M, N, K, ct, nck, s);
+  case GQ_FMT_Q8_0: return launch_sk_fmt<GQ_FMT_Q8_0>(packed, a16, lda, c, cbf16, M, N, K, ct, nck, s);
+  default: return launch_sk_fmt<GQ_FMT_Q4_K>(packed, a16, lda, c, cbf16, M, N, K, ct, nck, s);
   }
 }

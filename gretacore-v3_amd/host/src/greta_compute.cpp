@@ -9,8 +9,7 @@
 //     "1" (:161-163), and force_gemv from the op label and the GRETA_PREFILL_* /
 //     GRETA_WO_LAYOUT_FORCE flags (:316-352).
 //   * B GGUF-native (Q4_0 / Q8_0 / Q4_K / Q4_K_GGML / Q6_K / Q6_K_GGML, T16 layout) -> gq_matmul:
-//     GEMV kernels for M <= 16, gq_gemm above (added by this library; it runs
-//     16-row GEMV groups up to M = 48 for FP32 A).
+//     GEMV kernels for M <= 16, gq_gemm above (added by this library).
 // Unlike the reference (which always returns SUCCESS), launch failures and
 // unsupported operands are reported.
 #include "gcore/compute/greta_compute.hpp"

@@ -161,10 +161,9 @@ int gq_gemv_swiglu_plan(int fmt, size_t N, size_t K, int batch, int *ksplit, int
 /* ---- prefill GEMM: C[m][n] = sum_k A[m][k] * W[n][k] ------------------------ */
 /* A is [M][K] of a_dtype (GQ_DT_BF16 / F16 / F32), C is [M][N] of c_dtype
  * (GQ_DT_F32 or GQ_DT_BF16).  Computes on f16 MFMA (v_mfma_f32_32x32x16_f16)
- * with fp32 accumulation, weights dequantized into fp16 fragments.  For
- * 16 < M <= 48 with f32 A and C the rows go through the batch GEMV in groups
- * of 16 (no workspace used), which reads the weights once per group but
- * spreads over every CU. */
+ * with fp32 accumulation, weights dequantized into fp16 fragments.  Few rows
+ * (M <= 256 where the grid stays within two workgroups per CU) run on a
+ * skinny kernel that splits K over the waves of a workgroup. */
 size_t gq_gemm_workspace_bytes(int fmt, size_t M, size_t K);
 int gq_gemm(int fmt, const void *d_packed, const void *d_a, int a_dtype, void *d_c, int c_dtype, size_t M,
             size_t N, size_t K, void *d_workspace, size_t workspace_bytes, void *stream);
@@ -177,8 +176,7 @@ int gq_gemm_q8_i8(const void *d_packed_q8, const int8_t *d_qa, const float *d_da
                   size_t N, size_t K, void *stream);
 
 /* ---- GretaCompute::gemm routing for GGUF-native B (greta_compute_hip.cpp:148)
- * M <= 16 -> GEMV kernels, otherwise gq_gemm (16-row GEMV groups up to M = 48,
- * the MFMA GEMM above).  A f32 [M][K], C f32. */
+ * M <= 16 -> GEMV kernels, otherwise gq_gemm.  A f32 [M][K], C f32. */
 int gq_matmul(int fmt, const void *d_packed, const float *d_a, float *d_c, size_t M, size_t N, size_t K,
               void *stream);
 

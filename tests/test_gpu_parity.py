@@ -192,9 +192,9 @@ def test_gemm_f32_activations_and_matmul_routing(dev):
 
 @pytest.mark.parametrize("fmt", [O.Q4_0, O.Q8_0, O.Q4_K])
 @pytest.mark.parametrize("m", [17, 20, 36, 48])
-def test_gemm_small_m_runs_gemv_groups(dev, fmt, m):
-    """gq_gemm with 16 < M <= 48 (f32 A and C) through 16-row GEMV groups,
-    the last group ragged (1..16 rows: int8 or fp16 GEMV kernel)."""
+def test_gemm_small_m_f32(dev, fmt, m):
+    """gq_gemm with 16 < M <= 48, f32 A and C (the skinny kernel, one partial
+    64-row block)."""
     import gq
     import torch
     n, k = 200, 1024
@@ -281,6 +281,29 @@ def test_gemm_short_k_loops(dev, fmt, k, pd, monkeypatch):
         packed = _to_dev(gq.repack_host(fmt, w, n, k), dev)
         c = gq.gemm(fmt, packed, a.to(dev), n, k).cpu().numpy()
         assert O.rel_l2(c, ref) <= TOL, (tile, pd)
+
+
+@pytest.mark.parametrize("fmt", [O.Q4_0, O.Q8_0, O.Q4_K, O.Q4_K_GGML])
+@pytest.mark.parametrize("m,n,k", [(49, 200, 1024), (64, 4096, 4096), (100, 520, 2048), (256, 96, 512),
+                                   (130, 1000, 256)])
+def test_gemm_skinny(dev, fmt, m, n, k):
+    """49 <= M <= 256: the skinny GEMM (K split over a workgroup's waves, A in
+    the fragments' order), partial 64-row blocks and ragged row tiles, with
+    bf16 and f32 activations and f32 / bf16 output."""
+    import gq
+    import torch
+    if fmt == O.Q8_0 and k > 4096:
+        pytest.skip("chunk list")
+    w = O.gen_weights(fmt, n, k, seed=110 + m)
+    a = torch.randn(m, k, generator=torch.Generator().manual_seed(m + n))
+    packed = _to_dev(gq.repack_host(fmt, w, n, k), dev)
+    for adt in (torch.bfloat16, torch.float32):
+        aa = a.to(adt)
+        ref = O.gemv(fmt, w, aa.float().numpy(), n, k)
+        c = gq.gemm(fmt, packed, aa.to(dev), n, k).cpu().numpy()
+        assert O.rel_l2(c, ref) <= TOL, adt
+        cb = gq.gemm(fmt, packed, aa.to(dev), n, k, out_dtype=torch.bfloat16).float().cpu().numpy()
+        assert O.rel_l2(cb, ref) <= 5e-3, adt
 
 
 def test_q6k_matmul_batches_the_gemv(dev):
