@@ -219,7 +219,9 @@ int gq_unpack_host(int fmt, const void *packed, size_t N, size_t K, void *gguf) 
 int gq_matmul(int fmt, const void *packed, const float *a, float *c, size_t M, size_t N, size_t K, void *stream) {
   if (M >= 1 && M <= GQ_MAX_BATCH)
     return gq_gemv(fmt, packed, a, c, N, K, (int)M, nullptr, 0, stream);
-  if (gq_fmt_is_q6k(fmt)) {  // no Q6_K GEMM: batches of 16 rows through the GEMV
+  int ct = 0, nck = 0;
+  if (gq_fmt_is_q6k(fmt) && gq_gemm_skinny_plan(fmt, M, N, K, &ct, &nck) != GQ_OK) {
+    // K too long for the skinny kernel: batches of 16 rows through the GEMV
     for (size_t m0 = 0; m0 < M; m0 += GQ_MAX_BATCH) {
       const size_t mb = M - m0 < GQ_MAX_BATCH ? M - m0 : GQ_MAX_BATCH;
       GQ_TRY(gq_gemv(fmt, packed, a + m0 * K, c + m0 * N, N, K, (int)mb, nullptr, 0, stream));

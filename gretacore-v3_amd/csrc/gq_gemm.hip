@@ -804,16 +804,16 @@ int launch_gemm(const void *packed, const _Float16 *a16, int lda, void *c, int c
 }  // namespace
 
 extern "C" size_t gq_gemm_workspace_bytes(int fmt, size_t M, size_t K) {
-  // activations other than fp16 with K == padded K are first written as fp16
-  // [M][padded K]
-  if (!gq_fmt_valid(fmt) || gq_fmt_is_q6k(fmt) || M > GQ_MAX_DIM || K > GQ_MAX_DIM) return 0;
+  // activations are first written as fp16 [M][padded K (+ 8 for the skinny
+  // kernel)] unless they are fp16 of the padded width already (tiled kernel)
+  if (!gq_fmt_valid(fmt) || M > GQ_MAX_DIM || K > GQ_MAX_DIM) return 0;
   return gq_align256(M * (gq_kpad(fmt, K) + 8) * 2);
 }
 
 extern "C" int gq_gemm(int fmt, const void *packed, const void *a, int a_dtype, void *c, int c_dtype, size_t M,
                        size_t N, size_t K, void *ws, size_t ws_bytes, void *stream) {
   GQ_TRY(gq_check_shape(fmt, N, K));
-  GQ_CHECK(!gq_fmt_is_q6k(fmt), GQ_ERR_UNSUPPORTED);  // Q6_K: gq_gemv (gq_matmul batches it)
+
   GQ_CHECK(M <= GQ_MAX_DIM, GQ_ERR_INVALID_ARGS);
   GQ_CHECK(a_dtype == GQ_DT_F32 || a_dtype == GQ_DT_F16 || a_dtype == GQ_DT_BF16, GQ_ERR_UNSUPPORTED);
   GQ_CHECK(c_dtype == GQ_DT_F32 || c_dtype == GQ_DT_BF16, GQ_ERR_UNSUPPORTED);
@@ -851,6 +851,8 @@ extern "C" int gq_gemm(int fmt, const void *packed, const void *a, int a_dtype, 
     return gq_launch_gemm_skinny(fmt, packed, (const _Float16 *)ws, (int)ldo, c, c_dtype == GQ_DT_BF16, (int)M, (int)N,
                                  (int)K, s);
   }
+  // Q6_K has no tiled kernel (gq_matmul runs the batch GEMV per 16 rows)
+  GQ_CHECK(!gq_fmt_is_q6k(fmt), GQ_ERR_UNSUPPORTED);
   const _Float16 *a16 = (const _Float16 *)a;
   if (a_dtype != GQ_DT_F16 || Kp != K) {
     const size_t need = gq_gemm_workspace_bytes(fmt, M, K);

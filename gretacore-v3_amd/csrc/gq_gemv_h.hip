@@ -860,8 +860,8 @@ int gq_launch_gemv_h(int fmt, const void *packed, const float *x, float *y, int 
   }
 }
 
-// Skinny GEMM plan: M <= 256, a chunk list of at most 4 per wave (K <= 4096
-// for Q4_0 / Q8_0, 8192 for Q4_K), CT = 2 row tiles per workgroup where that
+// Skinny GEMM plan: M <= 256 (Q6_K: any M), a chunk list of at most 4 per wave
+// (K <= 4096 for Q4_0 / Q8_0, 8192 for Q4_K; Q6_K 2, K <= 4096), CT = 2 row tiles per workgroup where that
 // still gives every CU a workgroup, and at most two workgroups per CU in all
 // (each reads its 64 rows of A whole: measured slower than the tiled GEMM
 // beyond that, e.g. 128 x 14336: 54 vs 45 us).  GQ_ERR_UNSUPPORTED otherwise
@@ -870,17 +870,20 @@ int gq_launch_gemv_h(int fmt, const void *packed, const float *x, float *y, int 
 int gq_gemm_skinny_plan(int fmt, size_t M, size_t N, size_t K, int *ct_out, int *nck_out) {
   const char *e = getenv("GQ_GEMM_SKINNY");
   if ((e && e[0] == '0') || getenv("GQ_GEMM_TILE")) return GQ_ERR_UNSUPPORTED;  // (a forced tiled shape)
-  if (gq_fmt_is_q6k(fmt) || M == 0 || M > 256 || N == 0 || K == 0) return GQ_ERR_UNSUPPORTED;
-  const int f = gq_fmt_is_q4k(fmt) ? GQ_FMT_Q4_K : fmt;
+  // Q6_K (no tiled GEMM; the alternative is the batch GEMV per 16 rows): any
+  // M, at most 2 chunks per wave (K <= 4096; its chunks take 17 registers)
+  const bool q6 = gq_fmt_is_q6k(fmt);
+  if (M == 0 || (!q6 && M > 256) || N == 0 || K == 0) return GQ_ERR_UNSUPPORTED;
+  const int f = gq_fmt_is_q4k(fmt) ? GQ_FMT_Q4_K : q6 ? GQ_FMT_Q6_K : fmt;
   const int C = (int)gq_chunks(f, K);
   const int nck = (C + 7) / 8;
   const int nckp = nck <= 1 ? 1 : nck <= 2 ? 2 : nck <= 4 ? 4 : 0;
-  if (nckp == 0) return GQ_ERR_UNSUPPORTED;
+  if (nckp == 0 || (q6 && nckp > 2)) return GQ_ERR_UNSUPPORTED;
   const size_t tiles = gq_tiles(N), gy = (M + 63) / 64;
   const int cus0 = gq_device_cus();
   const size_t cus = cus0 > 0 ? (size_t)cus0 : 256;
   const int ct = ((tiles + 1) / 2) * gy >= cus ? 2 : 1;
-  if (((tiles + ct - 1) / ct) * gy > 2 * cus) return GQ_ERR_UNSUPPORTED;
+  if (!q6 && ((tiles + ct - 1) / ct) * gy > 2 * cus) return GQ_ERR_UNSUPPORTED;
   *ct_out = ct;
   *nck_out = nckp;
   return GQ_OK;
@@ -898,8 +901,10 @@ int launch_sk(const void *packed, const _Float16 *a16, int lda, void *c, int M, 
     hipLaunchKernelGGL((k_gemm_sk<FMT, CT, 1, CBF16>), grid, dim3(512), 0, s, w, sc_off, a16, lda, c, M, N, C);
   else if (nck <= 2)
     hipLaunchKernelGGL((k_gemm_sk<FMT, CT, 2, CBF16>), grid, dim3(512), 0, s, w, sc_off, a16, lda, c, M, N, C);
-  else
+  else if constexpr (FMT != GQ_FMT_Q6_K)
     hipLaunchKernelGGL((k_gemm_sk<FMT, CT, 4, CBF16>), grid, dim3(512), 0, s, w, sc_off, a16, lda, c, M, N, C);
+  else
+    return GQ_ERR_UNSUPPORTED;
   return gq_last_launch();
 }
 template <int FMT, bool CBF16>
@@ -920,6 +925,7 @@ int gq_launch_gemm_skinny(int fmt, const void *packed, const _Float16 *a16, int 
                           int K, hipStream_t s) {
   int ct = 1, nck = 1;
   GQ_TRY(gq_gemm_skinny_plan(fmt, (size_t)M, (size_t)N, (size_t)K, &ct, &nck));
+  if (gq_fmt_is_q6k(fmt)) return launch_sk_fmt<GQ_FMT_Q6_K>(packed, a16, lda, c, cbf16, M, N, K, ct, nck, s);
   switch (gq_fmt_is_q4k(fmt) ? GQ_FMT_Q4_K : fmt) {
   case GQ_FMT_Q4_0: return launch_sk_fmt<GQ_FMT_Q4_0>(packed, a16, lda, c, cbf16, M, N, K, ct, nck, s);
   case GQ_FMT_Q8_0: return launch_sk_fmt<GQ_FMT_Q8_0>(packed, a16, lda, c, cbf16, M, N, K, ct, nck, s);

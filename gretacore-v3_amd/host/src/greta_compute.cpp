@@ -153,9 +153,11 @@ GretaResult GretaCompute::gemm(GretaStream *stream, GretaMemory *A, GretaMemory 
       case GretaDataType::BF16: adt = GQ_DT_BF16; break;
       default: return GretaResult::ERROR_INVALID_ARGS;
       }
-      if (fmt == GQ_FMT_Q6_K || fmt == GQ_FMT_Q6_K_GGML) {  // no Q6_K GEMM: GEMVs over 16-row batches (fp32 A)
+      if (fmt == GQ_FMT_Q6_K || fmt == GQ_FMT_Q6_K_GGML) {
+        // gq_matmul: the skinny GEMM (K <= 4096), else GEMVs over 16-row
+        // batches (fp32 A)
         if (adt != GQ_DT_F32) return GretaResult::ERROR_INVALID_ARGS;
-        audit.route = "GEMV";
+        audit.route = K <= 4096 ? "GEMM" : "GEMV";
         st = gq_matmul(fmt, B->data(), static_cast<const float *>(A->data()), static_cast<float *>(C->data()), M, N,
                        K, s);
         break;

@@ -46,9 +46,11 @@ extern "C" {
 #define GQ_FMT_Q6_K_GGML 114 /* llama.cpp canonical Q6_K layout */
 /* accepted by gq_dequant_gguf only (loader conversions) */
 #define GQ_FMT_F16 1         /* one "block" = one fp16 value (weight_loader.cpp:91-110) */
-/* Q6_K (both layouts): T16 repack, dequant and gq_gemv (int8 matrix-core
-   kernel at batch 1..2, fp16 above); gq_gemm, gq_gemv_prep / prepped, gq_gemv_multi and
-   gq_gemv_swiglu return GQ_ERR_UNSUPPORTED for it. */
+/* Q6_K (both layouts): T16 repack, dequant, gq_gemv (int8 matrix-core
+   kernel at batch 1..2, fp16 above) and gq_gemm for K <= 4096 (skinny kernel,
+   any M); gq_gemm with longer K, gq_gemv_prep / prepped, gq_gemv_multi and
+   gq_gemv_swiglu return GQ_ERR_UNSUPPORTED for it (gq_matmul then runs 16-row
+   GEMV batches). */
 
 /* activation / output dtypes */
 #define GQ_DT_F32 0

@@ -105,9 +105,10 @@ def test_argument_validation():
     assert lib.gq_gemm(gq.FMT_Q4_0, buf, buf, 7, buf, 0, 4, 16, 32, None, 0, None) == 2  # bad dtype
     assert lib.gq_gemv_workspace_bytes(gq.FMT_Q4_0, 4096, 17) == 0
     assert lib.gq_gemv_workspace_bytes(gq.FMT_Q4_0, 4096, 4) > 0
-    # Q6_K: GEMV only (fp16 kernel, no workspace); no GEMM, no split or fused GEMV
+    # Q6_K: GEMV (fp16 kernel, no workspace), GEMM for K <= 4096 only, no split
+    # or fused GEMV
     assert lib.gq_gemv_workspace_bytes(gq.FMT_Q6_K, 4096, 4) == 0
-    assert lib.gq_gemm(gq.FMT_Q6_K, buf, buf, 2, buf, 0, 32, 16, 256, None, 0, None) == 2
+    assert lib.gq_gemm(gq.FMT_Q6_K, buf, buf, 2, buf, 0, 32, 16, 4608, None, 0, None) == 2
     assert lib.gq_gemv_prep(gq.FMT_Q6_K, buf, 256, 1, buf, 64, None) == 2
     # row slices: whole tiles from a multiple of 16, or the tensor's end
     assert lib.gq_repack_rows(gq.FMT_Q4_0, buf, 40, 32, 8, 16, buf, None) == 1   # row0 not a tile start

@@ -306,15 +306,40 @@ def test_gemm_skinny(dev, fmt, m, n, k):
         assert O.rel_l2(cb, ref) <= 5e-3, adt
 
 
-def test_q6k_matmul_batches_the_gemv(dev):
-    """Q6_K has no GEMM: gq_matmul runs M > 16 rows as 16-row GEMV batches."""
+@pytest.mark.parametrize("k", [512, 4608])
+def test_q6k_matmul(dev, k):
+    """Q6_K, M > 16: gq_matmul runs the skinny GEMM (K <= 4096) or 16-row GEMV
+    batches (longer K)."""
     import gq
-    n, k, m = 96, 512, 40
+    n, m = 96, 40
     w = O.gen_weights(O.Q6_K, n, k, seed=31)
     a = O.gen_x(m, k, seed=32)
     packed = _to_dev(gq.repack_host(O.Q6_K, w, n, k), dev)
     c = gq.matmul(O.Q6_K, packed, _to_dev(a, dev), n, k).cpu().numpy()
     assert O.rel_l2(c, O.gemv(O.Q6_K, w, a, n, k)) <= TOL
+
+
+@pytest.mark.parametrize("fmt", [O.Q6_K, O.Q6_K_GGML])
+@pytest.mark.parametrize("m,n", [(17, 300), (100, 2048), (300, 160)])
+def test_gemm_q6k_skinny(dev, fmt, m, n):
+    """gq_gemm on Q6_K (skinny kernel at any M, K <= 4096), bf16 A, f32 and
+    bf16 C; longer K is refused."""
+    import gq
+    import torch
+    k = 1024
+    w = O.gen_weights(fmt, n, k, seed=33 + m)
+    a = torch.randn(m, k, generator=torch.Generator().manual_seed(m)).to(torch.bfloat16)
+    ref = O.gemv(fmt, w, a.float().numpy(), n, k)
+    packed = _to_dev(gq.repack_host(fmt, w, n, k), dev)
+    c = gq.gemm(fmt, packed, a.to(dev), n, k).cpu().numpy()
+    assert O.rel_l2(c, ref) <= TOL
+    cb = gq.gemm(fmt, packed, a.to(dev), n, k, out_dtype=torch.bfloat16).float().cpu().numpy()
+    assert O.rel_l2(cb, ref) <= 5e-3
+    k2 = 4608
+    w2 = O.gen_weights(fmt, 32, k2, seed=34)
+    p2 = _to_dev(gq.repack_host(fmt, w2, 32, k2), dev)
+    with pytest.raises(gq.GQError):
+        gq.gemm(fmt, p2, torch.zeros(20, k2, dtype=torch.bfloat16, device=dev), 32, k2)
 
 
 def test_binding_loads_before_torch(dev):

@@ -77,6 +77,16 @@ def test_gemm_gguf_native(dev, model, name, M, adt):
     assert O.rel_l2(c, ref) <= TOL
 
 
+@pytest.mark.parametrize("M", [1, 40])
+def test_gemm_q6k_output(dev, model, M):
+    """Q6_K output.weight through GretaCompute::gemm: GEMV up to 16 rows, the
+    skinny GEMM above (fp32 A)."""
+    a, c, route, N, K = _run(model, "output.weight", "quant", M, seed=70 + M)
+    assert route == ("GEMV" if M <= 16 else "GEMM")
+    sh, fmt, raw = model[1]["output.weight"]
+    assert O.rel_l2(c, O.gemv(fmt, raw, a, N, K)) <= TOL
+
+
 @pytest.mark.parametrize("M", [1, 8, 33, 64])
 @pytest.mark.parametrize("name", ["blk.0.attn_q.weight", "blk.0.attn_k.weight", "output.weight"])
 @pytest.mark.parametrize("kind", ["int8", "int4"])
