@@ -351,7 +351,8 @@ def main():
     ap.add_argument("--no-load", action="store_true", help="skip the GGUF load-throughput extra")
     ap.add_argument("--only", default=None,
                     help="only the named GEMV config of the 'extra' field (e.g. q6_k_lm_head_128256x4096_b1), "
-                         "after a 64 MiB copy for counter calibration (for profiling)")
+                         "after a 64 MiB copy for counter calibration; or one GEMM "
+                         "(gemm_<fmt>_m<M>_<N>x<K>), or decode_step_llama3_8b_q4k (for profiling)")
     ap.add_argument("--gemm-only", action="store_true",
                     help="only the Q4_0 M=2048 14336x4096 prefill GEMM, --steps times (for profiling)")
     args = ap.parse_args()
@@ -386,10 +387,27 @@ def main():
             torch.bitwise_not(src, out=dst)  # reads 64 MiB, writes 64 MiB
         torch.cuda.synchronize()
         del src, dst
+    if args.only and args.only.startswith("gemm_"):
+        # gemm_<fmt>_m<M>_<N>x<K>, e.g. gemm_q4_0_m64_4096x4096
+        try:
+            fname, rest = args.only[5:].rsplit("_m", 1)
+            m_s, nk = rest.split("_", 1)
+            n_s, k_s = nk.split("x")
+            fmt = {"q4_0": O.Q4_0, "q8_0": O.Q8_0, "q4_k": O.Q4_K, "q6_k": O.Q6_K}[fname]
+            m, n, k = int(m_s), int(n_s), int(k_s)
+        except (ValueError, KeyError):
+            print(f"--only: cannot parse {args.only} (gemm_<q4_0|q8_0|q4_k|q6_k>_m<M>_<N>x<K>)", file=sys.stderr)
+            sys.exit(2)
+        print(json.dumps({args.only: bench_gemm(fmt, m, n, k, steps, warmup, dev)}), flush=True)
+        return
+    if args.only == "decode_step_llama3_8b_q4k":
+        print(json.dumps({args.only: bench_decode_step(dev, steps, warmup)}), flush=True)
+        return
     if args.only:
         cfg = [c for c in gemv_cfgs if c[0] == args.only]
         if not cfg:
-            print(f"--only: unknown config {args.only}; one of {[c[0] for c in gemv_cfgs]}", file=sys.stderr)
+            print(f"--only: unknown config {args.only}; one of {[c[0] for c in gemv_cfgs]}, "
+                  "gemm_<fmt>_m<M>_<N>x<K> or decode_step_llama3_8b_q4k", file=sys.stderr)
             sys.exit(2)
         name, fmt, n, k, b, seed = cfg[0]
         c = GemvCase(fmt, n, k, b, wseed=seed, xseed=seed + 1000, dev=dev)
