@@ -557,8 +557,9 @@ k_gemv_h1(const uint8_t *__restrict__ w, size_t sc_off, const float *__restrict_
 // Skinny GEMM (M <= 256): C[m][n] = sum_k A[m][k] W[n][k] for few rows of A.
 // The tiled GEMM walks K in 64-element steps, each waiting on loads requested a
 // few steps earlier, on grids of few workgroups; here a workgroup takes CT row
-// tiles of W (16 output columns each) and a block of 64 rows of A, and splits
-// K over its KW = 8 waves like the GEMV: each wave requests all of its chunks
+// tiles of W (16 output columns each) and a block of 16 MT rows of A (64; 32
+// in the 16-wave variant), and splits K over its KW waves (8; 16 for long K)
+// like the GEMV: each wave requests all of its chunks
 // (at most NCK) of the CT tiles up front, streams its A fragments straight
 // from global memory (no LDS: no two waves share them) one 64-k step ahead,
 // and issues MT x CT x 2 v_mfma_f32_16x16x32_f16 per step on weights
@@ -566,12 +567,11 @@ k_gemv_h1(const uint8_t *__restrict__ w, size_t sc_off, const float *__restrict_
 // A is fp16 [M][lda] in the B fragments' order: for the 4-bit formats each
 // aligned run of 8 k holds slots kQ4Perm with the kQ4Div16 slots divided by 16
 // (k_a_to_f16 with q4perm).  Rows >= M read row M - 1 and are not stored.
-template <int FMT, int CT, int NCK, bool CBF16>
-__global__ void __launch_bounds__(512) k_gemm_sk(const uint8_t *__restrict__ w, size_t sc_off,
-                                                 const _Float16 *__restrict__ a16, int lda, void *__restrict__ c,
-                                                 int M, int N, int C) {
+template <int FMT, int CT, int NCK, bool CBF16, int KW = 8, int MT = 4>
+__global__ void __launch_bounds__(64 * KW) k_gemm_sk(const uint8_t *__restrict__ w, size_t sc_off,
+                                                     const _Float16 *__restrict__ a16, int lda, void *__restrict__ c,
+                                                     int M, int N, int C) {
   using F = HFmt<FMT>;
-  constexpr int KW = 8, MT = 4;
   constexpr int NS = NCK * F::STEPS;  // 64-k steps per wave (static bound)
   __shared__ gq_f4 red[KW][CT * MT][64];
   const int lane = threadIdx.x & 63;
@@ -861,7 +861,8 @@ int gq_launch_gemv_h(int fmt, const void *packed, const float *x, float *y, int 
 }
 
 // Skinny GEMM plan: M <= 256 (Q6_K: any M), a chunk list of at most 4 per wave
-// (K <= 4096 for Q4_0 / Q8_0, 8192 for Q4_K; Q6_K 2, K <= 4096), CT = 2 row tiles per workgroup where that
+// of 8 (K <= 4096 for Q4_0 / Q8_0, 8192 for Q4_K; Q6_K 2, K <= 4096) or, for
+// Q4_0 / Q4_K, 8 per wave of 16 (K <= 16384 / 32768; *nck_out = 16 + chunks), CT = 2 row tiles per workgroup where that
 // still gives every CU a workgroup, and at most two workgroups per CU in all
 // (each reads its 64 rows of A whole: measured slower than the tiled GEMM
 // beyond that, e.g. 128 x 14336: 54 vs 45 us).  GQ_ERR_UNSUPPORTED otherwise
@@ -877,13 +878,24 @@ int gq_gemm_skinny_plan(int fmt, size_t M, size_t N, size_t K, int *ct_out, int 
   const int f = gq_fmt_is_q4k(fmt) ? GQ_FMT_Q4_K : q6 ? GQ_FMT_Q6_K : fmt;
   const int C = (int)gq_chunks(f, K);
   const int nck = (C + 7) / 8;
-  const int nckp = nck <= 1 ? 1 : nck <= 2 ? 2 : nck <= 4 ? 4 : 0;
-  if (nckp == 0 || (q6 && nckp > 2)) return GQ_ERR_UNSUPPORTED;
+  int nckp = nck <= 1 ? 1 : nck <= 2 ? 2 : nck <= 4 ? 4 : 0;
+  if (q6 && nckp > 2) return GQ_ERR_UNSUPPORTED;
   const size_t tiles = gq_tiles(N), gy = (M + 63) / 64;
   const int cus0 = gq_device_cus();
   const size_t cus = cus0 > 0 ? (size_t)cus0 : 256;
-  const int ct = ((tiles + 1) / 2) * gy >= cus ? 2 : 1;
-  if (!q6 && ((tiles + ct - 1) / ct) * gy > 2 * cus) return GQ_ERR_UNSUPPORTED;
+  int ct = ((tiles + 1) / 2) * gy >= cus ? 2 : 1;
+  size_t wgs = ((tiles + ct - 1) / ct) * gy;
+  if (nckp == 0) {
+    // long K: 16 waves (four per SIMD, so half the registers) on 32-row
+    // blocks of A, one row tile, up to 8 chunks each for Q4_0 (K <= 16384)
+    // and 4 for Q4_K (K <= 16384)
+    const int n16 = (C + 15) / 16;
+    if (q6 || f == GQ_FMT_Q8_0 || n16 > (f == GQ_FMT_Q4_0 ? 8 : 4)) return GQ_ERR_UNSUPPORTED;
+    nckp = 16 + (n16 <= 4 ? 4 : 8);  // 16 + chunks: the 16-wave variant
+    ct = 1;
+    wgs = tiles * ((M + 31) / 32);
+  }
+  if (!q6 && wgs > 2 * cus) return GQ_ERR_UNSUPPORTED;
   *ct_out = ct;
   *nck_out = nckp;
   return GQ_OK;
@@ -897,6 +909,21 @@ int launch_sk(const void *packed, const _Float16 *a16, int lda, void *c, int M, 
   const dim3 grid((unsigned)((gq_tiles(N) + CT - 1) / CT), (unsigned)((M + 63) / 64));
   const size_t sc_off = gq_sc_plane_offset(FMT, N, K);
   const uint8_t *w = (const uint8_t *)packed;
+  if (nck > 16) {  // 16-wave variant (4-bit formats, one row tile, 32-row blocks)
+    if constexpr (CT == 1 && (FMT == GQ_FMT_Q4_0 || FMT == GQ_FMT_Q4_K)) {
+      const dim3 g2((unsigned)gq_tiles(N), (unsigned)((M + 31) / 32));
+      if (nck == 20)
+        hipLaunchKernelGGL((k_gemm_sk<FMT, 1, 4, CBF16, 16, 2>), g2, dim3(1024), 0, s, w, sc_off, a16, lda, c, M, N,
+                           C);
+      else if constexpr (FMT == GQ_FMT_Q4_0)
+        hipLaunchKernelGGL((k_gemm_sk<FMT, 1, 8, CBF16, 16, 2>), g2, dim3(1024), 0, s, w, sc_off, a16, lda, c, M, N,
+                           C);
+      else
+        return GQ_ERR_UNSUPPORTED;
+      return gq_last_launch();
+    }
+    return GQ_ERR_UNSUPPORTED;
+  }
   if (nck <= 1)
     hipLaunchKernelGGL((k_gemm_sk<FMT, CT, 1, CBF16>), grid, dim3(512), 0, s, w, sc_off, a16, lda, c, M, N, C);
   else if (nck <= 2)

@@ -285,15 +285,14 @@ def test_gemm_short_k_loops(dev, fmt, k, pd, monkeypatch):
 
 @pytest.mark.parametrize("fmt", [O.Q4_0, O.Q8_0, O.Q4_K, O.Q4_K_GGML])
 @pytest.mark.parametrize("m,n,k", [(49, 200, 1024), (64, 4096, 4096), (100, 520, 2048), (256, 96, 512),
-                                   (130, 1000, 256)])
+                                   (130, 1000, 256), (40, 300, 14336), (70, 48, 8192)])
 def test_gemm_skinny(dev, fmt, m, n, k):
-    """49 <= M <= 256: the skinny GEMM (K split over a workgroup's waves, A in
-    the fragments' order), partial 64-row blocks and ragged row tiles, with
-    bf16 and f32 activations and f32 / bf16 output."""
+    """Few rows: the skinny GEMM (K split over a workgroup's 8 waves, or 16 on
+    32-row blocks for long K; A in the fragments' order), partial row blocks
+    and ragged row tiles, with bf16 and f32 activations and f32 / bf16 output
+    (Q8_0 with long K takes the tiled kernel)."""
     import gq
     import torch
-    if fmt == O.Q8_0 and k > 4096:
-        pytest.skip("chunk list")
     w = O.gen_weights(fmt, n, k, seed=110 + m)
     a = torch.randn(m, k, generator=torch.Generator().manual_seed(m + n))
     packed = _to_dev(gq.repack_host(fmt, w, n, k), dev)
