@@ -833,9 +833,10 @@ extern "C" int gq_gemm(int fmt, const void *packed, const void *a, int a_dtype, 
   if (gq_gemm_skinny_plan(fmt, M, N, K, &sk_ct, &sk_nck) == GQ_OK) {
     // A in the skinny kernel's order, always through the workspace, rows 16
     // bytes longer than a multiple of 4 KiB: each A load reads 16 rows, and at
-    // a 4 KiB-multiple stride they fall into the same L2 channel (64 x 4096:
-    // 19.9 -> 14.9 us; the tiled GEMM is 2-7 % slower with the padding and
-    // keeps the plain stride)
+    // a 4 KiB-multiple stride they collide in the memory hierarchy (64 x 4096:
+    // 19.9 -> 14.9 us; pads of 128 or 256 bytes measured no faster than none,
+    // so the collision is not one of whole cache lines; the tiled GEMM gains
+    // from no pad and keeps the plain stride)
     const size_t ldo = Kp + 8;
     const size_t need = gq_gemm_workspace_bytes(fmt, M, K);
     if (!ws) {
