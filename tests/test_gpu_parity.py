@@ -318,6 +318,21 @@ def test_q6k_matmul(dev, k):
     assert O.rel_l2(c, O.gemv(O.Q6_K, w, a, n, k)) <= TOL
 
 
+@pytest.mark.parametrize("fmt", [O.Q4_0, O.Q8_0])
+@pytest.mark.parametrize("m,n,k", [(50, 33, 96), (33, 17, 288), (1, 16, 32), (7, 40, 160)])
+def test_gemm_skinny_ragged_k(dev, fmt, m, n, k):
+    """Skinny GEMM with K not a multiple of the 128-element chunk (zero-padded
+    activations past K), fewer chunks than waves, and M below one row tile."""
+    import gq
+    import torch
+    w = O.gen_weights(fmt, n, k, seed=120 + k)
+    a = torch.randn(m, k, generator=torch.Generator().manual_seed(k)).to(torch.bfloat16)
+    ref = O.gemv(fmt, w, a.float().numpy(), n, k)
+    packed = _to_dev(gq.repack_host(fmt, w, n, k), dev)
+    c = gq.gemm(fmt, packed, a.to(dev), n, k).cpu().numpy()
+    assert O.rel_l2(c, ref) <= TOL
+
+
 @pytest.mark.parametrize("fmt", [O.Q6_K, O.Q6_K_GGML])
 @pytest.mark.parametrize("m,n", [(17, 300), (100, 2048), (300, 160)])
 def test_gemm_q6k_skinny(dev, fmt, m, n):
