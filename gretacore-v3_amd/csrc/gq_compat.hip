@@ -97,9 +97,118 @@ k_compat_gemv(const TA *__restrict__ a, const uint8_t *__restrict__ b, float *__
   }
 }
 
+// Streaming form for K % 16 == 0 and group sizes that are multiples of 16 (a
+// lane's 16 k then share one scale): a wave takes RW = 4 rows and walks K in
+// 1024-k segments, 16 k per lane; per segment it loads the MB activation rows'
+// 16 values once (float4 loads) for all its rows, each row's 16 weights with
+// one 16- (INT8) or 8-byte (INT4) load and one scale, and accumulates
+// s * sum(q * x) in fp32.  The sum over a lane's 16 terms is then scaled once
+// where the reference scales each weight: the result differs only by fp32
+// rounding order.
+template <int MB, int RW, typename TA, bool INT4>
+__global__ void __launch_bounds__(256)
+k_compat_gemv_seg(const TA *__restrict__ a, const uint8_t *__restrict__ b, float *__restrict__ c,
+                  const float *__restrict__ scales, const float *__restrict__ head_scales, int M, int N, int K,
+                  int lda, int ldc, int gs, int head_dim) {
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int n0 = ((int)blockIdx.x * 4 + wave) * RW;
+  if (n0 >= N) return;
+  const int m_base = (int)blockIdx.y * MB;
+  const int mcount = min(MB, M - m_base);
+  float acc[RW][MB];
+#pragma unroll
+  for (int r = 0; r < RW; ++r)
+#pragma unroll
+    for (int i = 0; i < MB; ++i) acc[r][i] = 0.f;
+  const TA *arow[MB];
+#pragma unroll
+  for (int i = 0; i < MB; ++i) arow[i] = a + (size_t)(m_base + (i < mcount ? i : 0)) * lda;
+#pragma unroll 2
+  for (int k0 = 16 * lane; k0 < K; k0 += 1024) {
+    float xv[MB][16];
+#pragma unroll
+    for (int i = 0; i < MB; ++i) {
+      if constexpr (sizeof(TA) == 4) {
+        const gq_f4 *p = reinterpret_cast<const gq_f4 *>(reinterpret_cast<const float *>(arow[i]) + k0);
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          const gq_f4 v = p[q];
+          xv[i][4 * q] = v[0];
+          xv[i][4 * q + 1] = v[1];
+          xv[i][4 * q + 2] = v[2];
+          xv[i][4 * q + 3] = v[3];
+        }
+      } else {
+        const gq_half8 *p = reinterpret_cast<const gq_half8 *>(reinterpret_cast<const _Float16 *>(arow[i]) + k0);
+#pragma unroll
+        for (int q = 0; q < 2; ++q) {
+          const gq_half8 v = p[q];
+#pragma unroll
+          for (int e = 0; e < 8; ++e) xv[i][8 * q + e] = (float)v[e];
+        }
+      }
+    }
+#pragma unroll
+    for (int r = 0; r < RW; ++r) {
+      const int n = n0 + r < N ? n0 + r : N - 1;  // (rows past N are computed, never stored)
+      const size_t idx = (size_t)n * K + k0;
+      float wv[16];
+      if constexpr (INT4) {
+        const gq_u2 p = gq_ld8(b + idx / 2);
+#pragma unroll
+        for (int e = 0; e < 16; ++e) {
+          const uint32_t byte = (p[e >> 3] >> (8 * ((e >> 1) & 3))) & 0xFFu;
+          const int v = (int)((e & 1) ? (byte >> 4) : (byte & 15u));
+          wv[e] = (float)((v ^ 8) - 8);
+        }
+      } else {
+        const gq_u4 p = gq_ld16(b + idx);
+#pragma unroll
+        for (int e = 0; e < 16; ++e) wv[e] = (float)(int8_t)((p[e >> 2] >> (8 * (e & 3))) & 0xFFu);
+      }
+      const float sc = scales ? scales[idx / gs] : 1.0f;
+#pragma unroll
+      for (int i = 0; i < MB; ++i) {
+        float d = 0.f;
+#pragma unroll
+        for (int e = 0; e < 16; ++e) d += xv[i][e] * wv[e];
+        acc[r][i] += sc * d;
+      }
+    }
+  }
+#pragma unroll
+  for (int r = 0; r < RW; ++r) {
+    const int n = n0 + r;
+    const float h = (head_scales && head_dim > 0 && n < N) ? head_scales[n / head_dim] : 1.0f;
+#pragma unroll
+    for (int i = 0; i < MB; ++i) {
+      const float sum = wave_sum(acc[r][i]);
+      if (lane == 0 && n < N && i < mcount) c[(size_t)(m_base + i) * ldc + n] = sum * h;
+    }
+  }
+}
+
 template <typename TA, bool INT4>
 int launch_compat(hipStream_t s, const TA *a, const uint8_t *b, float *c, const float *sc, const float *hs, int M,
                   int N, int K, int lda, int ldc, int gs, int hd) {
+  const bool seg = K % 16 == 0 && (!sc || gs % 16 == 0) && lda % (sizeof(TA) == 4 ? 4 : 8) == 0 &&
+                   (uintptr_t)a % 16 == 0 && (uintptr_t)b % 16 == 0;
+  if (seg) {
+    // MB activation rows per pass (the passes re-read the weights)
+    const int mb = M >= 4 ? 4 : M >= 2 ? 2 : 1;
+    dim3 grid((unsigned)((N + 15) / 16), (unsigned)((M + mb - 1) / mb));
+    if (mb == 4)
+      hipLaunchKernelGGL((k_compat_gemv_seg<4, 4, TA, INT4>), grid, dim3(256), 0, s, a, b, c, sc, hs, M, N, K, lda,
+                         ldc, gs, hd);
+    else if (mb == 2)
+      hipLaunchKernelGGL((k_compat_gemv_seg<2, 4, TA, INT4>), grid, dim3(256), 0, s, a, b, c, sc, hs, M, N, K, lda,
+                         ldc, gs, hd);
+    else
+      hipLaunchKernelGGL((k_compat_gemv_seg<1, 4, TA, INT4>), grid, dim3(256), 0, s, a, b, c, sc, hs, M, N, K, lda,
+                         ldc, gs, hd);
+    return gq_last_launch();
+  }
   dim3 grid((unsigned)((N + 3) / 4));
   for (int m = 0; m < M; m += 8)
     hipLaunchKernelGGL((k_compat_gemv<8, TA, INT4>), grid, dim3(256), 0, s, a, b, c, sc, hs, M, N, K, lda, ldc,

@@ -226,6 +226,7 @@ def test_q8_i8_path(dev):
 
 @pytest.mark.parametrize("m", [1, 4, 40])
 def test_compat_int8_int4_launchers(dev, m):
+    """Reference INT8 / INT4 launchers on the streaming GEMV (K % 16 == 0)."""
     import gq
     n, k = 64, 256
     rng = np.random.default_rng(m)
@@ -241,6 +242,35 @@ def test_compat_int8_int4_launchers(dev, m):
     y4 = gq.launch_int4_wt(_to_dev(x, dev), _to_dev(p4, dev), _to_dev(s4, dev), _to_dev(hs, dev), m, n, k,
                            head_dim=16).cpu().numpy()
     assert O.rel_l2(y4, ref4) <= 1e-5
+
+
+@pytest.mark.parametrize("m,n,k,gs,hd", [(1, 70, 1040, 32, 10), (3, 33, 4096, 64, 0), (9, 16, 48, 16, 8),
+                                         (5, 40, 100, 20, 0), (2, 24, 1024, 32, 8)])
+def test_compat_launchers_shapes(dev, m, n, k, gs, hd):
+    """Reference launchers: ragged rows, K past one 1024-k segment, other group
+    sizes (K or gs not a multiple of 16: the per-element fallback kernel), head
+    scales, fp16 activations for INT4."""
+    import gq
+    import torch
+    rng = np.random.default_rng(n + k)
+    wf = rng.standard_normal((n, k)).astype(np.float32) * 0.05
+    x = O.gen_x(m, k, seed=k)
+    q8 = rng.integers(-127, 128, size=(n, k), dtype=np.int8)
+    s = (rng.random(n * k // gs).astype(np.float32) + 0.5) * 0.01
+    ref8 = O.gemm_int8_wt(x, q8, s, m, n, k, gs)
+    y8 = gq.launch_int8_wt(_to_dev(x, dev), _to_dev(q8, dev), _to_dev(s, dev), m, n, k, group_size=gs)
+    assert O.rel_l2(y8.cpu().numpy(), ref8) <= 1e-5
+    p4 = rng.integers(0, 256, size=(n * k // 2,), dtype=np.uint8)
+    hs = (rng.random(max(1, n // hd) if hd else 1).astype(np.float32) + 0.5) if hd else None
+    ref4 = O.gemm_int4_wt(x, p4, s, hs, m, n, k, gs, hd)
+    y4 = gq.launch_int4_wt(_to_dev(x, dev), _to_dev(p4, dev), _to_dev(s, dev),
+                           _to_dev(hs, dev) if hs is not None else None, m, n, k, group_size=gs, head_dim=hd)
+    assert O.rel_l2(y4.cpu().numpy(), ref4) <= 1e-5
+    xh = x.astype(np.float16)
+    ref4h = O.gemm_int4_wt(xh.astype(np.float32), p4, s, hs, m, n, k, gs, hd)
+    y4h = gq.launch_int4_wt(_to_dev(xh, dev), _to_dev(p4, dev), _to_dev(s, dev),
+                            _to_dev(hs, dev) if hs is not None else None, m, n, k, group_size=gs, head_dim=hd)
+    assert O.rel_l2(y4h.cpu().numpy(), ref4h) <= 1e-5
 
 
 @pytest.mark.parametrize("tile,pd", [(0, 2), (0, 4), (1, 2), (2, 2), (3, 2), (4, 2), (4, 3), (4, 4), (5, 4),
