@@ -7,9 +7,9 @@
 // with fp32 accumulation, written in the mathematical ("row") layout
 // c[m*ldc + n].  Rows of a are lda apart.  M, N or K == 0 returns at once.
 //
-// One wave per output row n: lanes stream the row's weights with 16-byte loads
-// (16 int8 / 32 nibbles per lane per step) and accumulate all M activation
-// rows at once (M <= 32 per pass), reducing with DPP-backed shuffles.
+// Up to 32 rows (and with force_gemv) the GEMV in fp32, as the reference's
+// GEMV kernels; above, the reference's MFMA route on fp16 operands through
+// gq_gemm (compat_gemm_route).
 #include "gq_internal.h"
 
 namespace {
@@ -216,6 +216,73 @@ int launch_compat(hipStream_t s, const TA *a, const uint8_t *b, float *c, const 
   return gq_last_launch();
 }
 
+// Reference INT8 / INT4 rows -> GGUF Q8_0 / Q4_0 blocks for the MFMA GEMM
+// route, one thread per 32-block: d = fp16(s * h) (the group's scale times the
+// row's head scale), INT8 codes as they are, INT4 codes q (two's complement,
+// even k in the low nibble) as q + 8 in Q4_0's order (low nibbles k 0..15,
+// high nibbles k 16..31).  gs % 32 == 0 and K % 32 == 0 (host-checked).
+template <bool INT4>
+__global__ void __launch_bounds__(256)
+k_compat_to_gguf(const uint8_t *__restrict__ b, const float *__restrict__ scales, const float *__restrict__ hs,
+                 uint8_t *__restrict__ out, int N, int K, int gs, int head_dim) {
+  const size_t blk = (size_t)blockIdx.x * 256 + threadIdx.x;
+  const size_t nblk = (size_t)N * (K / 32);
+  if (blk >= nblk) return;
+  const int n = (int)(blk / (size_t)(K / 32));
+  const size_t e0 = blk * 32;  // first element (n * K + 32 j)
+  float sc = scales ? scales[e0 / gs] : 1.0f;
+  if (hs && head_dim > 0) sc *= hs[n / head_dim];
+  const uint16_t d = __builtin_bit_cast(uint16_t, (_Float16)sc);
+  if constexpr (INT4) {
+    uint8_t *o = out + blk * 18;
+    o[0] = (uint8_t)(d & 0xFF);
+    o[1] = (uint8_t)(d >> 8);
+    const uint8_t *p = b + e0 / 2;
+    uint8_t u[32];
+#pragma unroll
+    for (int j = 0; j < 16; ++j) {
+      const uint8_t byte = p[j];
+      u[2 * j] = (uint8_t)(((byte & 15) ^ 8));      // q + 8 for q in -8..7
+      u[2 * j + 1] = (uint8_t)(((byte >> 4) ^ 8));
+    }
+#pragma unroll
+    for (int j = 0; j < 16; ++j) o[2 + j] = (uint8_t)(u[j] | (u[j + 16] << 4));
+  } else {
+    uint8_t *o = out + blk * 34;
+    o[0] = (uint8_t)(d & 0xFF);
+    o[1] = (uint8_t)(d >> 8);
+    const uint8_t *p = b + e0;
+#pragma unroll
+    for (int j = 0; j < 32; ++j) o[2 + j] = p[j];
+  }
+}
+
+// The reference's MFMA route (M > 32 without force_gemv: gemm_kernels.hip:
+// 910-942, 742-760) computes on fp16 operands (A and w * s rounded to fp16);
+// here the weights become Q8_0 / Q4_0 blocks (d = fp16(s * h)), are repacked
+// into T16 and go through gq_gemm.  Needs lda == K, ldc == N, K % 32 == 0 and
+// gs % 32 == 0; the library's per-device workspace holds the converted
+// weights (the launchers have no workspace argument).  GQ_ERR_UNSUPPORTED
+// when a condition fails (the caller then runs the GEMV).
+template <bool INT4>
+int compat_gemm_route(hipStream_t s, const void *a, int a_dtype, const uint8_t *b, float *c, const float *sc,
+                      const float *hs, int M, int N, int K, int lda, int ldc, int gs, int hd) {
+  if (M <= 32 || lda != K || ldc != N || K % 32 || (sc && gs % 32)) return GQ_ERR_UNSUPPORTED;
+  const int fmt = INT4 ? GQ_FMT_Q4_0 : GQ_FMT_Q8_0;
+  const size_t nblk = (size_t)N * (K / 32);
+  const size_t gguf = gq_align256(nblk * (INT4 ? 18 : 34));
+  const size_t packed = gq_align256(gq_packed_bytes(fmt, N, K));
+  const size_t gws = gq_gemm_workspace_bytes(fmt, M, K);
+  void *ws = nullptr;
+  GQ_TRY(gq_default_workspace(gguf + packed + gws, &ws));
+  uint8_t *wg = (uint8_t *)ws, *wp = wg + gguf, *wa = wp + packed;
+  hipLaunchKernelGGL((k_compat_to_gguf<INT4>), dim3((unsigned)((nblk + 255) / 256)), dim3(256), 0, s, b, sc, hs, wg,
+                     N, K, gs, hd);
+  GQ_TRY(gq_last_launch());
+  GQ_TRY(gq_repack(fmt, wg, N, K, wp, s));
+  return gq_gemm(fmt, wp, a, a_dtype, c, GQ_DT_F32, M, N, K, wa, gws, s);
+}
+
 }  // namespace
 
 extern "C" int gq_launch_gemm_mfma_int8_wt_fp32_acc32(void *stream, const float *a, const int8_t *b, float *c,
@@ -227,8 +294,12 @@ extern "C" int gq_launch_gemm_mfma_int8_wt_fp32_acc32(void *stream, const float 
   GQ_CHECK(a && b && c, GQ_ERR_INVALID_ARGS);
   GQ_CHECK(!scales || group_size > 0, GQ_ERR_INVALID_ARGS);
   GQ_CHECK(M <= GQ_MAX_DIM && N <= GQ_MAX_DIM && K <= GQ_MAX_DIM, GQ_ERR_INVALID_ARGS);
+  const int ld = (int)(lda ? lda : K), lc = (int)(ldc ? ldc : N);
+  const int r = compat_gemm_route<false>((hipStream_t)stream, a, GQ_DT_F32, (const uint8_t *)b, c, scales, nullptr,
+                                         (int)M, (int)N, (int)K, ld, lc, (int)group_size, 0);
+  if (r != GQ_ERR_UNSUPPORTED) return r;
   return launch_compat<float, false>((hipStream_t)stream, a, (const uint8_t *)b, c, scales, nullptr, (int)M, (int)N,
-                                     (int)K, (int)(lda ? lda : K), (int)(ldc ? ldc : N), (int)group_size, 0);
+                                     (int)K, ld, lc, (int)group_size, 0);
 }
 
 extern "C" int gq_launch_gemm_mfma_int4_wt_fp32_acc32(void *stream, const void *a, const int8_t *b, float *c,
@@ -237,13 +308,18 @@ extern "C" int gq_launch_gemm_mfma_int4_wt_fp32_acc32(void *stream, const void *
                                                        uint32_t ldc, uint32_t group_size, uint32_t head_dim,
                                                        int is_fp16_a, int force_gemv) {
   (void)ldb;
-  (void)force_gemv;  // one kernel serves both of the reference's routes
   if (M == 0 || N == 0 || K == 0) return GQ_OK;
   GQ_CHECK(a && b && c, GQ_ERR_INVALID_ARGS);
   GQ_CHECK(!scales || group_size > 0, GQ_ERR_INVALID_ARGS);
   GQ_CHECK(M <= GQ_MAX_DIM && N <= GQ_MAX_DIM && K <= GQ_MAX_DIM, GQ_ERR_INVALID_ARGS);
   hipStream_t s = (hipStream_t)stream;
   const int ld = (int)(lda ? lda : K), lc = (int)(ldc ? ldc : N);
+  if (!force_gemv) {  // the reference's MFMA route for M > 32
+    const int r = compat_gemm_route<true>(s, a, is_fp16_a ? GQ_DT_F16 : GQ_DT_F32, (const uint8_t *)b, c, scales,
+                                          head_scales, (int)M, (int)N, (int)K, ld, lc, (int)group_size,
+                                          (int)head_dim);
+    if (r != GQ_ERR_UNSUPPORTED) return r;
+  }
   if (is_fp16_a)
     return launch_compat<_Float16, true>(s, (const _Float16 *)a, (const uint8_t *)b, c, scales, head_scales, (int)M,
                                          (int)N, (int)K, ld, lc, (int)group_size, (int)head_dim);

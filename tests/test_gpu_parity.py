@@ -226,22 +226,52 @@ def test_q8_i8_path(dev):
 
 @pytest.mark.parametrize("m", [1, 4, 40])
 def test_compat_int8_int4_launchers(dev, m):
-    """Reference INT8 / INT4 launchers on the streaming GEMV (K % 16 == 0)."""
+    """Reference INT8 / INT4 launchers: the fp32 GEMV up to 32 rows (rel-L2
+    1e-5); above, the reference's MFMA route on fp16 operands (weights * scale
+    and A rounded to fp16, as gemm_kernels.hip:820-908 does: rel-L2 1e-3),
+    unless force_gemv."""
     import gq
     n, k = 64, 256
+    tol = 1e-5 if m <= 32 else TOL
     rng = np.random.default_rng(m)
     wf = rng.standard_normal((n, k)).astype(np.float32) * 0.05
     x = O.gen_x(m, k, seed=m + 1)
     q8, s8 = O.requant_int8(wf)
     ref8 = O.gemm_int8_wt(x, q8, s8, m, n, k)
     y8 = gq.launch_int8_wt(_to_dev(x, dev), _to_dev(q8, dev), _to_dev(s8, dev), m, n, k).cpu().numpy()
-    assert O.rel_l2(y8, ref8) <= 1e-5
+    assert O.rel_l2(y8, ref8) <= tol
     p4, s4 = O.requant_int4(wf)
     hs = O.head_scales(wf, 4, 16, k)
     ref4 = O.gemm_int4_wt(x, p4, s4, hs, m, n, k, 32, 16)
     y4 = gq.launch_int4_wt(_to_dev(x, dev), _to_dev(p4, dev), _to_dev(s4, dev), _to_dev(hs, dev), m, n, k,
                            head_dim=16).cpu().numpy()
-    assert O.rel_l2(y4, ref4) <= 1e-5
+    assert O.rel_l2(y4, ref4) <= tol
+    y4g = gq.launch_int4_wt(_to_dev(x, dev), _to_dev(p4, dev), _to_dev(s4, dev), _to_dev(hs, dev), m, n, k,
+                            head_dim=16, force_gemv=True).cpu().numpy()
+    assert O.rel_l2(y4g, ref4) <= 1e-5
+
+
+@pytest.mark.parametrize("m,gs,fp16", [(100, 32, False), (33, 64, True), (300, 32, True), (64, 16, False)])
+def test_compat_mfma_route(dev, m, gs, fp16):
+    """M > 32: INT8 / INT4 weights converted to Q8_0 / Q4_0 blocks (head scales
+    folded into d), repacked and run through gq_gemm; a group size that is not
+    a multiple of 32 keeps the fp32 GEMV."""
+    import gq
+    n, k = 96, 512
+    rng = np.random.default_rng(m + gs)
+    x = O.gen_x(m, k, seed=m)
+    q8 = rng.integers(-127, 128, size=(n, k), dtype=np.int8)
+    s = (rng.random(n * k // gs).astype(np.float32) + 0.5) * 0.01
+    tol = TOL if gs % 32 == 0 else 1e-5
+    y8 = gq.launch_int8_wt(_to_dev(x, dev), _to_dev(q8, dev), _to_dev(s, dev), m, n, k, group_size=gs)
+    assert O.rel_l2(y8.cpu().numpy(), O.gemm_int8_wt(x, q8, s, m, n, k, gs)) <= tol
+    p4 = rng.integers(0, 256, size=(n * k // 2,), dtype=np.uint8)
+    hs = (rng.random(n // 16).astype(np.float32) + 0.5)
+    xa = x.astype(np.float16) if fp16 else x
+    ref4 = O.gemm_int4_wt(xa.astype(np.float32), p4, s, hs, m, n, k, gs, 16)
+    y4 = gq.launch_int4_wt(_to_dev(xa, dev), _to_dev(p4, dev), _to_dev(s, dev), _to_dev(hs, dev), m, n, k,
+                           group_size=gs, head_dim=16)
+    assert O.rel_l2(y4.cpu().numpy(), ref4) <= tol
 
 
 @pytest.mark.parametrize("m,n,k,gs,hd", [(1, 70, 1040, 32, 10), (3, 33, 4096, 64, 0), (9, 16, 48, 16, 8),
