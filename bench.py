@@ -158,6 +158,26 @@ def bench_gemm(fmt, m, n, k, steps, warmup, dev, out_dtype="f32"):
             "rel_l2": err}
 
 
+def bench_compat(dev, m, n=14336, k=4096):
+    """The reference's INT4 / INT8 weight-only launchers (requantized weight
+    formats of load_tensor_int4/int8, fp32 A): one call per step."""
+    import torch
+
+    import gq
+    g = torch.Generator(device="cpu").manual_seed(3000 + m)
+    b8 = torch.randint(-127, 128, (n, k), dtype=torch.int8, generator=g).to(dev)
+    b4 = torch.randint(-128, 128, (n, k // 2), dtype=torch.int8, generator=g).to(dev)
+    sc = (torch.rand(n * k // 32, generator=g) * 0.01).to(dev)
+    a = torch.randn(m, k, generator=g).to(dev)
+    c = torch.empty(m, n, device=dev)
+    t8 = graph_steps(lambda i: gq.launch_int8_wt(a, b8, sc, m, n, k, c=c), 20, 2)
+    t4 = graph_steps(lambda i: gq.launch_int4_wt(a, b4, sc, None, m, n, k, c=c), 20, 2)
+    route = "fp32 GEMV" if m <= 32 else "fp16 MFMA (Q8_0 / Q4_0 conversion + gq_gemm)"
+    return {"int8_us": t8 * 1e6, "int4_us": t4 * 1e6, "route": route,
+            "int8_GBps": (n * k + n * k // 32 * 4) / t8 / 1e9, "int4_GBps": (n * k // 2 + n * k // 32 * 4) / t4 / 1e9,
+            "TFLOPS_int4": 2.0 * m * n * k / t4 / 1e12}
+
+
 def bench_decode_step(dev, steps, warmup):
     """Config 5: 32-layer Llama-3-8B-shaped decode step, Q4_K projections and a
     Q8_0 lm_head: 7 GEMVs per layer + lm_head = 225 single-kernel GEMVs."""
@@ -432,6 +452,10 @@ def main():
                     log(f"[bench] {name}")
                     extra[name] = bench_gemm(fmt, m, n, 4096, steps, warmup, dev)
                     torch.cuda.empty_cache()
+        for m in (1, 512):
+            log(f"[bench] reference INT4/INT8 launchers m={m}")
+            extra[f"compat_launchers_14336x4096_m{m}"] = bench_compat(dev, m)
+            torch.cuda.empty_cache()
         if not args.no_decode_step:
             log("[bench] decode step (config 5)")
             extra["decode_step_llama3_8b_q4k"] = bench_decode_step(dev, steps, warmup)
