@@ -196,7 +196,7 @@ k_compat_gemv_seg(const TA *__restrict__ a, const uint8_t *__restrict__ b, float
 // up front (at most NSEG segments).  The LDS holds 16-byte chunks at
 // c ^ ((c >> 4) & 3) so the four 16-byte reads of a lane's 16 values hit 16
 // different bank groups across each 16 lanes.
-template <int MB, int NSEG, typename TA, bool INT4>
+template <int MB, int NSEG, typename TA, bool INT4, int RW = 1>
 __global__ void __launch_bounds__(1024)
 k_compat_gemv_lds(const TA *__restrict__ a, const uint8_t *__restrict__ b, float *__restrict__ c,
                   const float *__restrict__ scales, const float *__restrict__ head_scales, int M, int N, int K,
@@ -207,21 +207,25 @@ k_compat_gemv_lds(const TA *__restrict__ a, const uint8_t *__restrict__ b, float
   const int wave = threadIdx.x >> 6;
   const int m_base = (int)blockIdx.y * MB;
   const int mcount = min(MB, M - m_base);
-  const int n = (int)blockIdx.x * 16 + wave;
-  const int nr = n < N ? n : N - 1;  // (a row past N is computed, never stored)
+  const int n0 = ((int)blockIdx.x * 16 + wave) * RW;
   const int nseg = (K + 1023) / 1024;
-  // weights and scales of every segment first (clamped, unconditional)
-  gq_u4 w8[INT4 ? 1 : NSEG];
-  gq_u2 w4[INT4 ? NSEG : 1];
-  float sc[NSEG];
+  // weights and scales of every segment of the wave's RW rows first (clamped,
+  // unconditional; a row past N is computed, never stored)
+  gq_u4 w8[RW][INT4 ? 1 : NSEG];
+  gq_u2 w4[RW][INT4 ? NSEG : 1];
+  float sc[RW][NSEG];
 #pragma unroll
-  for (int it = 0; it < NSEG; ++it) {
-    int k0 = 16 * lane + 1024 * it;
-    k0 = k0 < K ? k0 : K - 16;
-    const size_t idx = (size_t)nr * K + k0;
-    if constexpr (INT4) w4[it] = gq_ld8(b + idx / 2);
-    else w8[it] = gq_ld16(b + idx);
-    sc[it] = scales ? scales[idx / gs] : 1.0f;
+  for (int r = 0; r < RW; ++r) {
+    const int nr = n0 + r < N ? n0 + r : N - 1;
+#pragma unroll
+    for (int it = 0; it < NSEG; ++it) {
+      int k0 = 16 * lane + 1024 * it;
+      k0 = k0 < K ? k0 : K - 16;
+      const size_t idx = (size_t)nr * K + k0;
+      if constexpr (INT4) w4[r][it] = gq_ld8(b + idx / 2);
+      else w8[r][it] = gq_ld16(b + idx);
+      sc[r][it] = scales ? scales[idx / gs] : 1.0f;
+    }
   }
   // activations -> LDS
   const int nchunk = K / 4;
@@ -240,43 +244,60 @@ k_compat_gemv_lds(const TA *__restrict__ a, const uint8_t *__restrict__ b, float
     xs[row * nchunk + (ch ^ ((ch >> 4) & 3))] = v;
   }
   __syncthreads();
-  float acc[MB];
+  float acc[RW][MB];
 #pragma unroll
-  for (int i = 0; i < MB; ++i) acc[i] = 0.f;
+  for (int r = 0; r < RW; ++r)
+#pragma unroll
+    for (int i = 0; i < MB; ++i) acc[r][i] = 0.f;
 #pragma unroll
   for (int it = 0; it < NSEG; ++it) {
     const int k0 = 16 * lane + 1024 * it;
     if (it < nseg && k0 < K) {
-      float wv[16];
-      if constexpr (INT4) {
+      float xv[MB][16];
 #pragma unroll
-        for (int e = 0; e < 16; ++e) {
-          const uint32_t byte = (w4[it][e >> 3] >> (8 * ((e >> 1) & 3))) & 0xFFu;
-          const int v = (int)((e & 1) ? (byte >> 4) : (byte & 15u));
-          wv[e] = (float)((v ^ 8) - 8);
-        }
-      } else {
-#pragma unroll
-        for (int e = 0; e < 16; ++e) wv[e] = (float)(int8_t)((w8[it][e >> 2] >> (8 * (e & 3))) & 0xFFu);
-      }
-#pragma unroll
-      for (int i = 0; i < MB; ++i) {
-        float d = 0.f;
+      for (int i = 0; i < MB; ++i)
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
           const int ch = k0 / 4 + j;
           const gq_f4 x4 = xs[i * nchunk + (ch ^ ((ch >> 4) & 3))];
-          d += x4[0] * wv[4 * j] + x4[1] * wv[4 * j + 1] + x4[2] * wv[4 * j + 2] + x4[3] * wv[4 * j + 3];
+          xv[i][4 * j] = x4[0];
+          xv[i][4 * j + 1] = x4[1];
+          xv[i][4 * j + 2] = x4[2];
+          xv[i][4 * j + 3] = x4[3];
         }
-        acc[i] += sc[it] * d;
+#pragma unroll
+      for (int r = 0; r < RW; ++r) {
+        float wv[16];
+        if constexpr (INT4) {
+#pragma unroll
+          for (int e = 0; e < 16; ++e) {
+            const uint32_t byte = (w4[r][it][e >> 3] >> (8 * ((e >> 1) & 3))) & 0xFFu;
+            const int v = (int)((e & 1) ? (byte >> 4) : (byte & 15u));
+            wv[e] = (float)((v ^ 8) - 8);
+          }
+        } else {
+#pragma unroll
+          for (int e = 0; e < 16; ++e) wv[e] = (float)(int8_t)((w8[r][it][e >> 2] >> (8 * (e & 3))) & 0xFFu);
+        }
+#pragma unroll
+        for (int i = 0; i < MB; ++i) {
+          float d = 0.f;
+#pragma unroll
+          for (int e = 0; e < 16; ++e) d += xv[i][e] * wv[e];
+          acc[r][i] += sc[r][it] * d;
+        }
       }
     }
   }
-  const float h = (head_scales && head_dim > 0 && n < N) ? head_scales[n / head_dim] : 1.0f;
 #pragma unroll
-  for (int i = 0; i < MB; ++i) {
-    const float sum = wave_sum(acc[i]);
-    if (lane == 0 && n < N && i < mcount) c[(size_t)(m_base + i) * ldc + n] = sum * h;
+  for (int r = 0; r < RW; ++r) {
+    const int n = n0 + r;
+    const float h = (head_scales && head_dim > 0 && n < N) ? head_scales[n / head_dim] : 1.0f;
+#pragma unroll
+    for (int i = 0; i < MB; ++i) {
+      const float sum = wave_sum(acc[r][i]);
+      if (lane == 0 && n < N && i < mcount) c[(size_t)(m_base + i) * ldc + n] = sum * h;
+    }
   }
 }
 
@@ -290,7 +311,16 @@ int launch_compat(hipStream_t s, const TA *a, const uint8_t *b, float *c, const 
   if (seg && K <= 16384) {
     const int mb = (M >= 4 && K <= 4096) ? 4 : (M >= 2 && K <= 8192) ? 2 : 1;
     const size_t lds = (size_t)mb * K * 4;
-    dim3 grid((unsigned)((N + 15) / 16), (unsigned)((M + mb - 1) / mb));
+    // INT4, one activation row, tall matrices: two rows per wave (twice the
+    // weight bytes in flight per wave; 14336 x 4096: 14.3 -> 13.5 us) while
+    // the grid keeps a workgroup per CU
+    const bool rw2 = INT4 && mb == 1 && K <= 4096 && N >= 8192;
+    dim3 grid((unsigned)((N + (rw2 ? 31 : 15)) / (rw2 ? 32 : 16)), (unsigned)((M + mb - 1) / mb));
+    if (rw2) {
+      hipLaunchKernelGGL((k_compat_gemv_lds<1, 4, TA, INT4, 2>), grid, dim3(1024), lds, s, a, b, c, sc, hs, M, N, K,
+                         lda, ldc, gs, hd);
+      return gq_last_launch();
+    }
 #define GQ_LDS_L(MBV, NS)                                                                                       \
   hipLaunchKernelGGL((k_compat_gemv_lds<MBV, NS, TA, INT4>), grid, dim3(1024), lds, s, a, b, c, sc, hs, M, N, K, \
                      lda, ldc, gs, hd)

@@ -276,7 +276,7 @@ def test_compat_mfma_route(dev, m, gs, fp16):
 
 @pytest.mark.parametrize("m,n,k,gs,hd", [(1, 70, 1040, 32, 10), (3, 33, 4096, 64, 0), (9, 16, 48, 16, 8),
                                          (5, 40, 100, 20, 0), (2, 24, 1024, 32, 8), (2, 40, 8192, 32, 0),
-                                         (1, 20, 14336, 32, 4), (6, 17, 16400, 16, 0)])
+                                         (1, 20, 14336, 32, 4), (6, 17, 16400, 16, 0), (1, 8200, 512, 32, 8)])
 def test_compat_launchers_shapes(dev, m, n, k, gs, hd):
     """Reference launchers: ragged rows, K past one 1024-k segment up to the
     LDS-staged GEMV's 16384 (and beyond: the per-wave form), other group sizes
