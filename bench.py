@@ -221,15 +221,31 @@ def bench_decode_step(dev, steps, warmup):
             gq.gemv(Q4K, L["down"], xs[14336], 4096, 14336, y=ys[4096])
         gq.gemv(Q80, lm_packed, xs[4096], 128256, 4096, y=ys[128256])
 
+    # the fused forms a decode loop calls: RMSNorm folded into the q/k/v and
+    # gate/up launches, gate/up producing silu(gate) * up (the down input)
+    gamma = torch.ones(4096, dtype=torch.float32, device=dev)
+    ya = torch.empty((1, 14336), dtype=torch.float32, device=dev)
+
+    def one_step_fused(_i):
+        for L in layers:
+            gq.gemv_multi(Q4K, [(L["q"], 4096), (L["k"], 1024), (L["v"], 1024)], xs[4096], 4096, gamma=gamma,
+                          ys=[yq, yk, yv])
+            gq.gemv(Q4K, L["o"], xs[4096], 4096, 4096, y=ys[4096])
+            gq.gemv_swiglu(Q4K, L["gate"], L["up"], xs[4096], 14336, 4096, gamma=gamma, y=ya)
+            gq.gemv(Q4K, L["down"], xs[14336], 4096, 14336, y=ys[4096])
+        gq.gemv(Q80, lm_packed, xs[4096], 128256, 4096, y=ys[128256])
+
     t_eager = time_steps(one_step, 3, 1)
     t_graph = graph_steps(one_step, 4, 1)
     t_grouped = graph_steps(one_step_grouped, 4, 1)
+    t_fused = graph_steps(one_step_fused, 4, 1)
     out = {"weight_bytes": wbytes, "gemv_launches": 225, "eager_ms": t_eager * 1e3, "graph_ms": t_graph * 1e3,
            "graph_GBps": wbytes / t_graph / 1e9, "graph_pct_peak": 100.0 * wbytes / t_graph / 1e9 / HBM_PEAK_GBS,
            "projection_steps_per_s": 1.0 / t_graph,
            "grouped_launches": 129, "grouped_graph_ms": t_grouped * 1e3,
            "grouped_GBps": wbytes / t_grouped / 1e9,
-           "grouped_pct_peak": 100.0 * wbytes / t_grouped / 1e9 / HBM_PEAK_GBS}
+           "grouped_pct_peak": 100.0 * wbytes / t_grouped / 1e9 / HBM_PEAK_GBS,
+           "fused_norm_swiglu_graph_ms": t_fused * 1e3}
     del layers, lm_packed
     torch.cuda.empty_cache()
     return out
