@@ -258,6 +258,10 @@ k_gemv_q(const GemvFuse fz, const float *__restrict__ x, const int8_t *__restric
   const int nck = c1 - c0;  // <= NCK (host-checked)
   const int k0 = c0 * F::CK, LK = nck * F::CK;
   const bool norm = FUSE > 0 && fz.gamma != nullptr;
+  float ssw[NBC];                               // this wave's sum of squares per batch row (norm)
+  __shared__ float ssred[FUSE > 0 ? KSPLIT : 1][NBC];  // the waves' sums of squares (norm)
+#pragma unroll
+  for (int b = 0; b < NBC; ++b) ssw[b] = 0.f;
 
   // ---- 1. activation loads (fused path), issued before the weights ----------
   float4 xv[PREP ? 1 : NBC * TPR][2];
@@ -335,14 +339,14 @@ k_gemv_q(const GemvFuse fz, const float *__restrict__ x, const int8_t *__restric
     const int nblk = L.lk / 32;
     for (int o = 16 * lane; o < L.lk; o += 1024)
       *reinterpret_cast<gq_u4 *>(base + L.zero_off + o) = gq_u4{0u, 0u, 0u, 0u};
-    // RMS normalisation (fused entry points): sum of squares of the row over
-    // all waves' slices, then x * inv_rms * gamma
-    float inv_rms[NBC];
-#pragma unroll
-    for (int b = 0; b < NBC; ++b) inv_rms[b] = 1.f;
+    // RMS normalisation (fused entry points): y = inv_rms * (W (x * gamma)),
+    // inv_rms = 1 / sqrt(mean(x^2) + eps) a scalar per batch row, so the
+    // staging multiplies by gamma only (the limb split is per-block scaled,
+    // hence indifferent to the factor) and each wave only records the sum of
+    // squares of its slice; the factor is applied to the finished dot
+    // products, after the reduction barrier the K split needs anyway
     if constexpr (FUSE > 0) {
       if (norm) {
-        __shared__ float ssred[KSPLIT][NBC];
         float ss[NBC];
 #pragma unroll
         for (int b = 0; b < NBC; ++b) ss[b] = 0.f;
@@ -355,16 +359,8 @@ k_gemv_q(const GemvFuse fz, const float *__restrict__ x, const int8_t *__restric
         }
 #pragma unroll
         for (int b = 0; b < NBC; ++b) {
-          ss[b] = wave_sum(ss[b]);
-          if (lane == 0) ssred[wave][b] = ss[b];
-        }
-        __syncthreads();
-#pragma unroll
-        for (int b = 0; b < NBC; ++b) {
-          float t = 0.f;
-#pragma unroll
-          for (int q = 0; q < KSPLIT; ++q) t += ssred[q][b];
-          inv_rms[b] = 1.0f / sqrtf(t / (float)K + fz.eps);
+          ssw[b] = wave_sum(ss[b]);
+          if (lane == 0) ssred[wave][b] = ssw[b];
         }
       }
     }
@@ -378,7 +374,7 @@ k_gemv_q(const GemvFuse fz, const float *__restrict__ x, const int8_t *__restric
           const float gg[8] = {gv[ti][0].x, gv[ti][0].y, gv[ti][0].z, gv[ti][0].w,
                                gv[ti][1].x, gv[ti][1].y, gv[ti][1].z, gv[ti][1].w};
 #pragma unroll
-          for (int e = 0; e < 8; ++e) v[e] = (v[e] * inv_rms[b]) * gg[e];
+          for (int e = 0; e < 8; ++e) v[e] = v[e] * gg[e];
         }
       }
       float amax = 0.f;
@@ -595,6 +591,24 @@ k_gemv_q(const GemvFuse fz, const float *__restrict__ x, const int8_t *__restric
         }
   } else if (g != 0) {
     return;
+  }
+  if constexpr (FUSE > 0) {
+    if (norm) {
+#pragma unroll
+      for (int v = 0; v < NBC; ++v) {
+        float t = ssw[v];
+        if constexpr (KSPLIT > 1) {  // (ordered by the reduction barrier)
+          t = 0.f;
+#pragma unroll
+          for (int q = 0; q < KSPLIT; ++q) t += ssred[q][v];
+        }
+        const float inv = 1.0f / sqrtf(t / (float)K + fz.eps);
+#pragma unroll
+        for (int rt = 0; rt < R; ++rt)
+#pragma unroll
+          for (int mt = 0; mt < MT; ++mt) part[rt][mt][v] *= inv;
+      }
+    }
   }
   if constexpr (FUSE == 2) {
     const size_t row = tile0 * 16 + r;
