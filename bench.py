@@ -1,15 +1,16 @@
 """Benchmark of the GGUF quantized-weight matrix path on one MI355X.
 
-Headline (BASELINE.json metric, configs[1]): Q4_0 decode GEMV, batch 1,
-14336 x 4096, HBM GB/s of whole-job throughput (activation prep + GEMV kernel)
+Headline (the baseline's metric and its configs[1]): Q4_0 decode GEMV,
+batch 1, 14336 x 4096, HBM GB/s of whole-job throughput (one GEMV kernel)
 with the weights already resident in HBM.  A "step" is one GEMV call over one
 weight copy; >= 8 distinct copies (>= 264 MB) are rotated so the 256 MB
 Infinity Cache cannot serve them.
 
-Also reported (field "extra"): the other BASELINE configs -- Q4_0 / Q8_0 GEMV
-shapes, Q4_K batch 1/4/8/16, the prefill GEMM TFLOPS at M = 512 / 2048, one
-full 32-layer Llama-3-8B-shaped decode step (225 GEMVs), and the GGUF-native
-load throughput (pinned sliced upload + on-GPU repack).
+Also reported (field "extra"): the other benchmark configurations -- Q4_0 /
+Q8_0 / Q6_K GEMV shapes, Q4_K batch 1/4/8/16, the prefill GEMM TFLOPS at
+M = 64 / 512 / 2048, the reference-format INT4 / INT8 launchers, one full
+32-layer Llama-3-8B-shaped decode step, and the GGUF-native load throughput
+(pinned sliced upload + on-GPU repack).
 
   python bench.py [--steps K] [--warmup W] [--gpus 1] [--headline-only]
 """
@@ -252,7 +253,7 @@ def bench_decode_step(dev, steps, warmup):
 
 
 def bench_load(dev, layers=8):
-    """GGUF-native load throughput (SURVEY config: loader I/O): a Llama-3-8B
+    """GGUF-native load throughput (the loader I/O row): a Llama-3-8B
     shaped file of `layers` Q4_K layers (~1 GB) in the page cache, every matrix
     loaded with gq_gguf_load(QUANT) (pinned sliced upload + on-GPU T16 repack),
     against the reference's way of loading: read into pageable memory, a

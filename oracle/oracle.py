@@ -5,7 +5,7 @@ TEST INFRASTRUCTURE ONLY: imported by tests/, __graft_entry__.smoke() and
 bench.py's cpu_baseline leg, always as the checker / baseline, never as the
 thing measured or shipped.
 
-Also holds the seeded synthetic GGUF generators for the BASELINE configs:
+Also holds the seeded synthetic GGUF generators for the benchmark configurations:
   Q8_0: q ~ U[-127,127], d = fp16(|N(0,1)| * 0.02)
   Q4_0: nibbles ~ U[0,15], d = fp16(|N(0,1)| * 0.02)
   Q4_K: 12 code bytes ~ U[0,255] (codes U[0,63]), nibbles ~ U[0,15],

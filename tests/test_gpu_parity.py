@@ -1,6 +1,6 @@
 """GPU parity: libgq.so (HIP, gfx950) against the CPU oracle on the same seeded
 inputs.  Dequantization and repack are bit-exact; GEMV/GEMM must be within
-rel-L2 <= 1e-3 of the fp64-accumulated oracle (BASELINE.json north star)."""
+rel-L2 <= 1e-3 of the fp64-accumulated oracle (the north-star tolerance)."""
 import numpy as np
 import pytest
 
