@@ -355,26 +355,82 @@ def bench_load(dev, layers=8):
         shutil.rmtree(d, ignore_errors=True)
 
 
-def cpu_baseline(target_s=12.0):
-    """The oracle (C restatement of the reference CPU semantics: dequant then
-    fp64-accumulated dot, OpenMP over rows) on the host cores, on the headline
-    workload, repeated for ~target_s seconds."""
+def host_cores():
+    """Cores this run may use, as `nproc` reports them (it honours
+    OMP_NUM_THREADS and the CPU affinity mask)."""
+    import subprocess
+    try:
+        return max(1, int(subprocess.run(["nproc"], capture_output=True, text=True, check=True).stdout.strip()))
+    except (OSError, ValueError, subprocess.CalledProcessError):
+        return len(os.sched_getaffinity(0))
+
+
+def _time_cpu_gemv(fmt, n, k, seed, threads, target_s):
+    """Repeated oracle GEMVs (dequant + fp64-accumulated dot, OpenMP over
+    rows) for ~target_s seconds: (seconds per GEMV, repetitions, elapsed)."""
     import oracle as O
-    threads = int(os.environ.get("OMP_NUM_THREADS", "0") or 0) or (os.cpu_count() or 1)
-    n, k = 14336, 4096
-    w = O.gen_weights(O.Q4_0, n, k, seed=1002)
-    x = O.gen_x(1, k, seed=2002)
-    O.gemv(O.Q4_0, w, x, n, k, threads=threads)  # warm
+    w = O.gen_weights(fmt, n, k, seed=seed)
+    x = O.gen_x(1, k, seed=seed + 1000)
+    O.gemv(fmt, w, x, n, k, threads=threads)  # warm
     reps, t0 = 0, time.perf_counter()
     while True:
-        O.gemv(O.Q4_0, w, x, n, k, threads=threads)
+        O.gemv(fmt, w, x, n, k, threads=threads)
         reps += 1
         el = time.perf_counter() - t0
         if el >= target_s:
-            break
-    per = el / reps
-    return {"value": gemv_bytes(O.Q4_0, n, k, 1) / per / 1e9, "unit": "GB/s", "cores": threads, "kind": "port",
-            "sample": f"oracle gqo_gemv Q4_0 {n}x{k} batch 1, {reps} reps in {el:.1f} s ({per * 1e3:.2f} ms/GEMV)"}
+            return el / reps, reps, el
+
+
+def cpu_baseline(target_s=6.0):
+    """The oracle (C restatement of the reference CPU semantics: block dequant
+    as weight_loader.cpp:91-156 / 703-712 and the GGUF spec, then a dot with
+    fp64 accumulation as CpuReference::gemm, cpu_reference.hpp:56-66) on the
+    host cores.  The headline workload (Q4_0 14336 x 4096, batch 1) on all
+    cores gives `value`; the CPU-path configuration (Q8_0 4096 x 4096, batch
+    1, x seed 0) is timed on all cores and on one, and the headline workload
+    on one core too.  About 4 x target_s seconds in all."""
+    import oracle as O
+    cores = host_cores()
+    runs = {}
+    for name, fmt, n, k, seed in (("q4_0_14336x4096_b1", O.Q4_0, 14336, 4096, 1002),
+                                  ("q8_0_4096x4096_b1", O.Q8_0, 4096, 4096, 1001)):
+        for threads in (cores, 1):
+            per, reps, el = _time_cpu_gemv(fmt, n, k, seed, threads, target_s)
+            byts = gemv_bytes(fmt, n, k, 1)
+            runs[f"{name}_{threads}t"] = {"GBps": round(byts / per / 1e9, 3), "ms_per_gemv": round(per * 1e3, 3),
+                                          "threads": threads, "reps": reps, "seconds": round(el, 1)}
+    head = runs[f"q4_0_14336x4096_b1_{cores}t"]
+    return {"value": head["GBps"], "unit": "GB/s", "cores": cores, "kind": "port",
+            "sample": f"oracle gqo_gemv Q4_0 14336x4096 batch 1 on {cores} threads, {head['reps']} reps in "
+                      f"{head['seconds']} s ({head['ms_per_gemv']} ms/GEMV); the other entries of 'runs' are the "
+                      "Q8_0 4096x4096 batch-1 CPU-path configuration and single-thread runs",
+            "runs": runs}
+
+
+def bench_read_ceiling(dev, steps, warmup):
+    """The read ceiling of the headline GEMV: a kernel of the GEMV's grid (its
+    workgroups and waves, every wave issuing all its loads up front) that only
+    streams the same bytes (the T16 Q4_0 14336 x 4096 tensor, rotated copies),
+    and the same grid with no work (the fixed cost of a launch), in the same
+    graph methodology as the GEMV."""
+    import torch
+
+    import gq
+    import oracle as O
+    n, k = 14336, 4096
+    R, ks, _ = gq.gemv_plan(O.Q4_0, n, k, 1)
+    wgs = -(-(-(-n // 16)) // R)
+    nbytes = gq.packed_size(O.Q4_0, n, k)
+    ncopies = max(8, -(-CACHE_DEFEAT_BYTES // nbytes))
+    copies = [torch.randint(0, 256, (nbytes,), dtype=torch.uint8, device=dev) for _ in range(ncopies)]
+    out = torch.empty(wgs * ks, dtype=torch.int32, device=dev)
+    t_read = graph_steps(lambda i: gq.probe_read(copies[i % ncopies], wgs, ks, out), steps, warmup)
+    t_empty = graph_steps(lambda i: gq.probe_empty(wgs, ks), steps, warmup)
+    del copies
+    return {"read_us": round(t_read * 1e6, 3), "read_GBps": round(nbytes / t_read / 1e9, 1),
+            "read_pct_peak": round(100.0 * nbytes / t_read / 1e9 / HBM_PEAK_GBS, 2),
+            "empty_us": round(t_empty * 1e6, 3), "bytes": nbytes, "grid": f"{wgs} workgroups x {ks} waves",
+            "copies": ncopies}
 
 
 def main():
@@ -389,7 +445,8 @@ def main():
     ap.add_argument("--only", default=None,
                     help="only the named GEMV config of the 'extra' field (e.g. q6_k_lm_head_128256x4096_b1), "
                          "after a 64 MiB copy for counter calibration; or one GEMM "
-                         "(gemm_<fmt>_m<M>_<N>x<K>), or decode_step_llama3_8b_q4k (for profiling)")
+                         "(gemm_<fmt>_m<M>_<N>x<K>), read_ceiling (the headline's pure-read and empty kernels), "
+                         "or decode_step_llama3_8b_q4k (for profiling)")
     ap.add_argument("--gemm-only", action="store_true",
                     help="only the Q4_0 M=2048 14336x4096 prefill GEMM, --steps times (for profiling)")
     args = ap.parse_args()
@@ -437,6 +494,9 @@ def main():
             sys.exit(2)
         print(json.dumps({args.only: bench_gemm(fmt, m, n, k, steps, warmup, dev)}), flush=True)
         return
+    if args.only == "read_ceiling":
+        print(json.dumps({args.only: bench_read_ceiling(dev, steps, warmup)}), flush=True)
+        return
     if args.only == "decode_step_llama3_8b_q4k":
         print(json.dumps({args.only: bench_decode_step(dev, steps, warmup)}), flush=True)
         return
@@ -444,7 +504,7 @@ def main():
         cfg = [c for c in gemv_cfgs if c[0] == args.only]
         if not cfg:
             print(f"--only: unknown config {args.only}; one of {[c[0] for c in gemv_cfgs]}, "
-                  "gemm_<fmt>_m<M>_<N>x<K> or decode_step_llama3_8b_q4k", file=sys.stderr)
+                  "gemm_<fmt>_m<M>_<N>x<K>, read_ceiling or decode_step_llama3_8b_q4k", file=sys.stderr)
             sys.exit(2)
         name, fmt, n, k, b, seed = cfg[0]
         c = GemvCase(fmt, n, k, b, wseed=seed, xseed=seed + 1000, dev=dev)
@@ -455,6 +515,10 @@ def main():
     h = bench_gemv(head, steps, warmup)
     log(f"[bench] headline {h}")
     extra = {}
+    log("[bench] read ceiling of the headline grid")
+    rc = bench_read_ceiling(dev, steps, warmup)
+    rc["gemv_over_read"] = round(h["step_us"] / rc["read_us"], 3)
+    extra["read_ceiling_q4_0_14336x4096"] = rc
     if not args.headline_only:
         for name, fmt, n, k, b, seed in gemv_cfgs:
             log(f"[bench] {name}")

@@ -3,7 +3,7 @@
 // formats (weight_loader.cpp:668-1008):
 //   launch_gemm_mfma_int8_wt_fp32_acc32  gemm_kernels.hip:742-760
 //   launch_gemm_mfma_int4_wt_fp32_acc32  gemm_kernels.hip:910-942
-// Semantics: c[m][n] = (sum_k a[m][k] * (w[n][k] * s[(n*K + k)/gs])) * h[n/hd]
+// Semantics: c[m][n] = (sum_k a[m][k] * (w[n][k] * s[idx(n, k)])) * h[n/hd]
 // with fp32 accumulation, written in the mathematical ("row") layout
 // c[m*ldc + n].  Rows of a are lda apart.  M, N or K == 0 returns at once.
 //
@@ -13,6 +13,16 @@
 #include "gq_internal.h"
 
 namespace {
+
+// Scale of weight (n, k).  The reference's two routes index the per-group
+// scales differently: its GEMV kernels (M <= 32 or force_gemv) take
+// s_row = scales + (n*K)/gs and s_row[k/gs] (gemm_kernels.hip:610,615 and
+// 781,796-797), its MFMA kernels (M > 32) scales[(n*K + k)/gs]
+// (gemm_kernels.hip:717, 886).  srow selects the first form; the two agree
+// whenever K % gs == 0.
+GQ_DEV size_t scale_idx(size_t n, size_t K, size_t k, int gs, int srow) {
+  return srow ? (n * K) / (size_t)gs + k / (size_t)gs : (n * K + k) / (size_t)gs;
+}
 
 GQ_DEV float wave_sum(float v) {
 #pragma unroll
@@ -27,7 +37,7 @@ template <int MB, typename TA, bool INT4>
 __global__ void __launch_bounds__(256)
 k_compat_gemv(const TA *__restrict__ a, const uint8_t *__restrict__ b, float *__restrict__ c,
               const float *__restrict__ scales, const float *__restrict__ head_scales, int M, int N, int K,
-              int lda, int ldc, int gs, int head_dim, int m_base) {
+              int lda, int ldc, int gs, int srow, int head_dim, int m_base) {
   const int lane = threadIdx.x & 63;
   const int n = blockIdx.x * 4 + (threadIdx.x >> 6);
   if (n >= N) return;
@@ -55,7 +65,7 @@ k_compat_gemv(const TA *__restrict__ a, const uint8_t *__restrict__ b, float *__
         for (int e = 0; e < 16; ++e) wv[e] = (float)(int8_t)((p[e >> 2] >> (8 * (e & 3))) & 0xFFu);
       }
 #pragma unroll
-      for (int e = 0; e < 16; ++e) wv[e] = wv[e] * (scales ? scales[(row_elems + k0 + e) / gs] : 1.0f);
+      for (int e = 0; e < 16; ++e) wv[e] = wv[e] * (scales ? scales[scale_idx(n, K, k0 + e, gs, srow)] : 1.0f);
     } else {
 #pragma unroll
       for (int e = 0; e < 16; ++e) {
@@ -71,7 +81,7 @@ k_compat_gemv(const TA *__restrict__ a, const uint8_t *__restrict__ b, float *__
           } else {
             q = (int8_t)b[idx];
           }
-          v = (float)q * (scales ? scales[idx / gs] : 1.0f);
+          v = (float)q * (scales ? scales[scale_idx(n, K, k, gs, srow)] : 1.0f);
         }
         wv[e] = v;
       }
@@ -109,7 +119,7 @@ template <int MB, int RW, typename TA, bool INT4>
 __global__ void __launch_bounds__(256)
 k_compat_gemv_seg(const TA *__restrict__ a, const uint8_t *__restrict__ b, float *__restrict__ c,
                   const float *__restrict__ scales, const float *__restrict__ head_scales, int M, int N, int K,
-                  int lda, int ldc, int gs, int head_dim) {
+                  int lda, int ldc, int gs, int srow, int head_dim) {
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
   const int n0 = ((int)blockIdx.x * 4 + wave) * RW;
@@ -167,7 +177,7 @@ k_compat_gemv_seg(const TA *__restrict__ a, const uint8_t *__restrict__ b, float
 #pragma unroll
         for (int e = 0; e < 16; ++e) wv[e] = (float)(int8_t)((p[e >> 2] >> (8 * (e & 3))) & 0xFFu);
       }
-      const float sc = scales ? scales[idx / gs] : 1.0f;
+      const float sc = scales ? scales[scale_idx(n, K, k0, gs, srow)] : 1.0f;
 #pragma unroll
       for (int i = 0; i < MB; ++i) {
         float d = 0.f;
@@ -200,7 +210,7 @@ template <int MB, int NSEG, typename TA, bool INT4, int RW = 1>
 __global__ void __launch_bounds__(1024)
 k_compat_gemv_lds(const TA *__restrict__ a, const uint8_t *__restrict__ b, float *__restrict__ c,
                   const float *__restrict__ scales, const float *__restrict__ head_scales, int M, int N, int K,
-                  int lda, int ldc, int gs, int head_dim) {
+                  int lda, int ldc, int gs, int srow, int head_dim) {
   extern __shared__ __attribute__((aligned(16))) unsigned char lds_raw[];
   gq_f4 *xs = reinterpret_cast<gq_f4 *>(lds_raw);  // [MB][K / 4] chunks, swizzled
   const int lane = threadIdx.x & 63;
@@ -224,7 +234,7 @@ k_compat_gemv_lds(const TA *__restrict__ a, const uint8_t *__restrict__ b, float
       const size_t idx = (size_t)nr * K + k0;
       if constexpr (INT4) w4[r][it] = gq_ld8(b + idx / 2);
       else w8[r][it] = gq_ld16(b + idx);
-      sc[r][it] = scales ? scales[idx / gs] : 1.0f;
+      sc[r][it] = scales ? scales[scale_idx(nr, K, k0, gs, srow)] : 1.0f;
     }
   }
   // activations -> LDS
@@ -303,7 +313,7 @@ k_compat_gemv_lds(const TA *__restrict__ a, const uint8_t *__restrict__ b, float
 
 template <typename TA, bool INT4>
 int launch_compat(hipStream_t s, const TA *a, const uint8_t *b, float *c, const float *sc, const float *hs, int M,
-                  int N, int K, int lda, int ldc, int gs, int hd) {
+                  int N, int K, int lda, int ldc, int gs, int srow, int hd) {
   const bool seg = K % 16 == 0 && (!sc || gs % 16 == 0) && lda % (sizeof(TA) == 4 ? 4 : 8) == 0 &&
                    (uintptr_t)a % 16 == 0 && (uintptr_t)b % 16 == 0;
   // activations staged in LDS per 16-row workgroup (K <= 16384), else read
@@ -318,12 +328,12 @@ int launch_compat(hipStream_t s, const TA *a, const uint8_t *b, float *c, const 
     dim3 grid((unsigned)((N + (rw2 ? 31 : 15)) / (rw2 ? 32 : 16)), (unsigned)((M + mb - 1) / mb));
     if (rw2) {
       hipLaunchKernelGGL((k_compat_gemv_lds<1, 4, TA, INT4, 2>), grid, dim3(1024), lds, s, a, b, c, sc, hs, M, N, K,
-                         lda, ldc, gs, hd);
+                         lda, ldc, gs, srow, hd);
       return gq_last_launch();
     }
 #define GQ_LDS_L(MBV, NS)                                                                                       \
   hipLaunchKernelGGL((k_compat_gemv_lds<MBV, NS, TA, INT4>), grid, dim3(1024), lds, s, a, b, c, sc, hs, M, N, K, \
-                     lda, ldc, gs, hd)
+                     lda, ldc, gs, srow, hd)
     const int nseg = (K + 1023) / 1024;
     if (mb == 4) GQ_LDS_L(4, 4);
     else if (mb == 2) { if (nseg <= 4) GQ_LDS_L(2, 4); else GQ_LDS_L(2, 8); }
@@ -337,19 +347,19 @@ int launch_compat(hipStream_t s, const TA *a, const uint8_t *b, float *c, const 
     dim3 grid((unsigned)((N + 15) / 16), (unsigned)((M + mb - 1) / mb));
     if (mb == 4)
       hipLaunchKernelGGL((k_compat_gemv_seg<4, 4, TA, INT4>), grid, dim3(256), 0, s, a, b, c, sc, hs, M, N, K, lda,
-                         ldc, gs, hd);
+                         ldc, gs, srow, hd);
     else if (mb == 2)
       hipLaunchKernelGGL((k_compat_gemv_seg<2, 4, TA, INT4>), grid, dim3(256), 0, s, a, b, c, sc, hs, M, N, K, lda,
-                         ldc, gs, hd);
+                         ldc, gs, srow, hd);
     else
       hipLaunchKernelGGL((k_compat_gemv_seg<1, 4, TA, INT4>), grid, dim3(256), 0, s, a, b, c, sc, hs, M, N, K, lda,
-                         ldc, gs, hd);
+                         ldc, gs, srow, hd);
     return gq_last_launch();
   }
   dim3 grid((unsigned)((N + 3) / 4));
   for (int m = 0; m < M; m += 8)
     hipLaunchKernelGGL((k_compat_gemv<8, TA, INT4>), grid, dim3(256), 0, s, a, b, c, sc, hs, M, N, K, lda, ldc,
-                       gs, hd, m);
+                       gs, srow, hd, m);
   return gq_last_launch();
 }
 
@@ -435,8 +445,10 @@ extern "C" int gq_launch_gemm_mfma_int8_wt_fp32_acc32(void *stream, const float 
   const int r = compat_gemm_route<false>((hipStream_t)stream, a, GQ_DT_F32, (const uint8_t *)b, c, scales, nullptr,
                                          (int)M, (int)N, (int)K, ld, lc, (int)group_size, 0);
   if (r != GQ_ERR_UNSUPPORTED) return r;
+  // past the MFMA route's conditions the GEMV computes the MFMA route's scale
+  // index for M > 32
   return launch_compat<float, false>((hipStream_t)stream, a, (const uint8_t *)b, c, scales, nullptr, (int)M, (int)N,
-                                     (int)K, ld, lc, (int)group_size, 0);
+                                     (int)K, ld, lc, (int)group_size, M <= 32 ? 1 : 0, 0);
 }
 
 extern "C" int gq_launch_gemm_mfma_int4_wt_fp32_acc32(void *stream, const void *a, const int8_t *b, float *c,
@@ -449,8 +461,13 @@ extern "C" int gq_launch_gemm_mfma_int4_wt_fp32_acc32(void *stream, const void *
   GQ_CHECK(a && b && c, GQ_ERR_INVALID_ARGS);
   GQ_CHECK(!scales || group_size > 0, GQ_ERR_INVALID_ARGS);
   GQ_CHECK(M <= GQ_MAX_DIM && N <= GQ_MAX_DIM && K <= GQ_MAX_DIM, GQ_ERR_INVALID_ARGS);
+  // the reference addresses row n at byte n*(K/2) (gemm_kernels.hip:781, 859)
+  // while its loader packs the flat tensor (weight_loader.cpp:920-957): the
+  // two agree only for even K
+  GQ_CHECK(K % 2 == 0, GQ_ERR_UNSUPPORTED);
   hipStream_t s = (hipStream_t)stream;
   const int ld = (int)(lda ? lda : K), lc = (int)(ldc ? ldc : N);
+  const int srow = (force_gemv || M <= 32) ? 1 : 0;  // the GEMV route's scale index
   if (!force_gemv) {  // the reference's MFMA route for M > 32
     const int r = compat_gemm_route<true>(s, a, is_fp16_a ? GQ_DT_F16 : GQ_DT_F32, (const uint8_t *)b, c, scales,
                                           head_scales, (int)M, (int)N, (int)K, ld, lc, (int)group_size,
@@ -459,7 +476,7 @@ extern "C" int gq_launch_gemm_mfma_int4_wt_fp32_acc32(void *stream, const void *
   }
   if (is_fp16_a)
     return launch_compat<_Float16, true>(s, (const _Float16 *)a, (const uint8_t *)b, c, scales, head_scales, (int)M,
-                                         (int)N, (int)K, ld, lc, (int)group_size, (int)head_dim);
+                                         (int)N, (int)K, ld, lc, (int)group_size, srow, (int)head_dim);
   return launch_compat<float, true>(s, (const float *)a, (const uint8_t *)b, c, scales, head_scales, (int)M, (int)N,
-                                    (int)K, ld, lc, (int)group_size, (int)head_dim);
+                                    (int)K, ld, lc, (int)group_size, srow, (int)head_dim);
 }

@@ -239,7 +239,7 @@ GQ_DEV void tile_of(int id, int G, int tiles_m, int &mt, int &nt) {
 template <int FMT, int CBF16, int BM, int BN>
 __global__ void __launch_bounds__(NTHR) __attribute__((amdgpu_waves_per_eu(2, 2)))
 k_gemm_t16(const uint8_t *__restrict__ w, uint32_t sc_off, const _Float16 *__restrict__ a16, int lda,
-           void *__restrict__ c, int M, int N, int C, int nsteps, int tiles_m) {
+           void *__restrict__ c, const float *__restrict__ rs, int M, int N, int C, int nsteps, int tiles_m) {
   constexpr int TM = BM / 64, TN = BN / 128;  // 32 x 32 MFMA tiles per wave along M and N
   static_assert(TN >= 1, "BN >= 128");
   static_assert(2 * (BN * 4 / NTHR) <= 15, "vmcnt immediate");
@@ -376,10 +376,11 @@ k_gemm_t16(const uint8_t *__restrict__ w, uint32_t sc_off, const _Float16 *__res
       for (int v = 0; v < 16; ++v) {
         const int m = m0 + (BM / 2) * wm + 32 * i + 8 * (v >> 2) + 4 * (lane >> 5) + (v & 3);
         if (m < M) {
+          const float o = rs ? acc[i][j][v] * rs[m] : acc[i][j][v];  // (row scale: an exact power of two)
           if constexpr (CBF16)
-            reinterpret_cast<uint16_t *>(c)[(size_t)m * N + n] = f32_to_bf16_rne(acc[i][j][v]);
+            reinterpret_cast<uint16_t *>(c)[(size_t)m * N + n] = f32_to_bf16_rne(o);
           else
-            reinterpret_cast<float *>(c)[(size_t)m * N + n] = acc[i][j][v];
+            reinterpret_cast<float *>(c)[(size_t)m * N + n] = o;
         }
       }
     }
@@ -518,7 +519,7 @@ GQ_DEV gq_half8 rfrag(const RStep<FMT, NJ> &st, int j, int ks, int step, const Q
 template <int FMT, int CBF16, int BM, int BN, int WM, int WN, int PD = 2>
 __global__ void __launch_bounds__(64 * WM * WN) __attribute__((amdgpu_waves_per_eu(WM * WN / 4, WM * WN / 4)))
 k_gemm_rb(const uint8_t *__restrict__ w, uint32_t sc_off, const _Float16 *__restrict__ a16, int lda,
-          void *__restrict__ c, int M, int N, int C, int nsteps, int tiles_m) {
+          void *__restrict__ c, const float *__restrict__ rs, int M, int N, int C, int nsteps, int tiles_m) {
   constexpr int KS = BK / 16;
   constexpr int NW = WM * WN, TM = BM / WM / 32, NJ = BN / WN / 32;  // waves, MFMA tiles per wave
   static_assert(TM >= 1 && NJ >= 1 && BM % (8 * NW) == 0, "tile shape");
@@ -655,86 +656,106 @@ k_gemm_rb(const uint8_t *__restrict__ w, uint32_t sc_off, const _Float16 *__rest
       for (int v = 0; v < 16; ++v) {
         const int m = m0 + (BM / WM) * wm + 32 * i + 8 * (v >> 2) + 4 * (lane >> 5) + (v & 3);
         if (m < M) {
+          const float o = rs ? acc[i][j][v] * rs[m] : acc[i][j][v];  // (row scale: an exact power of two)
           if constexpr (CBF16)
-            reinterpret_cast<uint16_t *>(c)[(size_t)m * N + n] = f32_to_bf16_rne(acc[i][j][v]);
+            reinterpret_cast<uint16_t *>(c)[(size_t)m * N + n] = f32_to_bf16_rne(o);
           else
-            reinterpret_cast<float *>(c)[(size_t)m * N + n] = acc[i][j][v];
+            reinterpret_cast<float *>(c)[(size_t)m * N + n] = o;
         }
       }
     }
 }
 
-// Activations -> fp16 [M][ldo] (ldo >= K, columns K..ldo-1 zero), 8 per thread.
-// bf16 -> fp16 is exact inside fp16's range; fp32 rounds to nearest even.
+// Activations -> fp16 [M][ldo] (ldo >= K, columns K..ldo-1 zero), one
+// workgroup per row, with a per-row power-of-two scale: the row's largest
+// magnitude is brought into [2^14, 2^15) before the one rounding to fp16, and
+// rs[m] = 2^-s undoes it on the finished dot products (the GEMM epilogues).
+// Multiplying by a power of two is exact, so rows inside fp16's range round
+// as before, while rows with values beyond 65504 (outliers of the
+// down-projection input, bf16 spikes) or far below 1 keep fp16's full
+// relative precision instead of overflowing to Inf or going subnormal.
 // q4perm: each run of 8 in the order of the 4-bit B fragments of the skinny
 // GEMM (element e holds k slot {0,2,4,6,1,3,5,7}[e], elements 2, 3, 6, 7
 // divided by 16 -- exact, before the one rounding to fp16).
-__global__ void __launch_bounds__(256) k_a_to_f16(const void *__restrict__ a, int a_dtype, _Float16 *__restrict__ o,
-                                                  int M, int K, int ldo, int q4perm) {
-  const size_t i = (size_t)blockIdx.x * 256 + threadIdx.x;
-  const int per_row = ldo / 8;
-  if (i >= (size_t)M * per_row) return;
-  const size_t m = i / per_row;
-  const int k0 = (int)(i % per_row) * 8;
-  gq_half8 h;
-  if (k0 >= K) {
-#pragma unroll
-    for (int q = 0; q < 8; ++q) h[q] = (_Float16)0.0f;
-  } else if (a_dtype == GQ_DT_BF16) {
-    const gq_u4 u = gq_ld16(reinterpret_cast<const uint16_t *>(a) + m * K + k0);
+GQ_DEV void load8_f32(const void *a, int a_dtype, size_t off, float (&v)[8]) {
+  if (a_dtype == GQ_DT_BF16) {
+    const gq_u4 u = gq_ld16(reinterpret_cast<const uint16_t *>(a) + off);
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
-      h[2 * q] = (_Float16)__uint_as_float(u[q] << 16);
-      h[2 * q + 1] = (_Float16)__uint_as_float(u[q] & 0xFFFF0000u);
+      v[2 * q] = __uint_as_float(u[q] << 16);
+      v[2 * q + 1] = __uint_as_float(u[q] & 0xFFFF0000u);
     }
   } else if (a_dtype == GQ_DT_F16) {
-    h = *reinterpret_cast<const gq_half8 *>(reinterpret_cast<const _Float16 *>(a) + m * K + k0);
+    const gq_half8 h = *reinterpret_cast<const gq_half8 *>(reinterpret_cast<const _Float16 *>(a) + off);
+#pragma unroll
+    for (int q = 0; q < 8; ++q) v[q] = (float)h[q];
   } else {
-    const float *f = reinterpret_cast<const float *>(a) + m * K + k0;
+    const float *f = reinterpret_cast<const float *>(a) + off;
     const gq_f4 v0 = *reinterpret_cast<const gq_f4 *>(f), v1 = *reinterpret_cast<const gq_f4 *>(f + 4);
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
-      h[q] = (_Float16)v0[q];
-      h[4 + q] = (_Float16)v1[q];
+      v[q] = v0[q];
+      v[4 + q] = v1[q];
     }
   }
-  if (q4perm) {
-    // from the values themselves (fp32 for f32 input: one rounding)
+}
+
+__global__ void __launch_bounds__(256) k_a_to_f16(const void *__restrict__ a, int a_dtype, _Float16 *__restrict__ o,
+                                                  float *__restrict__ rs, int K, int ldo, int q4perm) {
+  __shared__ float wmax[4];
+  const size_t m = blockIdx.x;
+  const int tid = threadIdx.x;
+  // K % 8 == 0 (host-checked), so a run of 8 is all inside or all past K
+  float amax = 0.f;
+  for (int k0 = 8 * tid; k0 < K; k0 += 2048) {
     float v[8];
-    if (k0 >= K) {
+    load8_f32(a, a_dtype, m * K + k0, v);
 #pragma unroll
-      for (int q = 0; q < 8; ++q) v[q] = 0.f;
-    } else if (a_dtype == GQ_DT_F32) {
-      const float *f = reinterpret_cast<const float *>(a) + m * K + k0;
-#pragma unroll
-      for (int q = 0; q < 8; ++q) v[q] = f[q];
-    } else {
-#pragma unroll
-      for (int q = 0; q < 8; ++q) v[q] = (float)h[q];
-    }
-    constexpr int perm[8] = {0, 2, 4, 6, 1, 3, 5, 7};
-#pragma unroll
-    for (int e = 0; e < 8; ++e) h[e] = (_Float16)((e & 2) ? v[perm[e]] * 0.0625f : v[perm[e]]);
+    for (int q = 0; q < 8; ++q) amax = fmaxf(amax, fabsf(v[q]));
   }
-  *reinterpret_cast<gq_half8 *>(o + m * ldo + k0) = h;
+#pragma unroll
+  for (int o2 = 32; o2 > 0; o2 >>= 1) amax = fmaxf(amax, __shfl_xor(amax, o2, 64));
+  if ((tid & 63) == 0) wmax[tid >> 6] = amax;
+  __syncthreads();
+  amax = fmaxf(fmaxf(wmax[0], wmax[1]), fmaxf(wmax[2], wmax[3]));
+  // s = 14 - floor(log2(amax)) from the exponent field (0 for a zero row,
+  // Inf / NaN; clamped so 2^s and 2^-s stay normal floats)
+  const uint32_t eb = (__float_as_uint(amax) >> 23) & 0xFFu;
+  int sh = (eb == 0u || eb == 0xFFu) ? 0 : 14 - ((int)eb - 127);
+  sh = sh < -100 ? -100 : sh > 100 ? 100 : sh;
+  const float f = __uint_as_float((uint32_t)(127 + sh) << 23);
+  if (tid == 0) rs[m] = __uint_as_float((uint32_t)(127 - sh) << 23);
+  constexpr int perm[8] = {0, 2, 4, 6, 1, 3, 5, 7};
+  for (int k0 = 8 * tid; k0 < ldo; k0 += 2048) {
+    float v[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+    if (k0 < K) load8_f32(a, a_dtype, m * K + k0, v);
+    gq_half8 h;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const float x = q4perm ? ((e & 2) ? v[perm[e]] * 0.0625f : v[perm[e]]) : v[e];
+      h[e] = (_Float16)(x * f);
+    }
+    *reinterpret_cast<gq_half8 *>(o + m * ldo + k0) = h;
+  }
 }
 
 template <int FMT, int CBF16, int BM, int BN>
-int launch_cfg(const void *packed, const _Float16 *a16, int lda, void *c, int M, int N, int K, hipStream_t s) {
+int launch_cfg(const void *packed, const _Float16 *a16, int lda, void *c, const float *rs, int M, int N, int K,
+               hipStream_t s) {
   auto kern = k_gemm_t16<FMT, CBF16, BM, BN>;
   const int C = (int)gq_chunks(FMT, K);
   const int nsteps = (int)(gq_kpad(FMT, K) / BK);
   const int tiles_m = (M + BM - 1) / BM, tiles_n = (N + BN - 1) / BN;
   hipLaunchKernelGGL(kern, dim3((unsigned)(tiles_m * tiles_n)), dim3(NTHR), 0, s, (const uint8_t *)packed,
-                     (uint32_t)gq_sc_plane_offset(FMT, N, K), a16, lda, c, M, N, C, nsteps, tiles_m);
+                     (uint32_t)gq_sc_plane_offset(FMT, N, K), a16, lda, c, rs, M, N, C, nsteps, tiles_m);
   return gq_last_launch();
 }
 
 // pd_default: the pipeline depth of the shape (GQ_GEMM_PD=2|3|4 overrides it,
 // for tuning)
 template <int FMT, int CBF16, int BM, int BN, int WM, int WN>
-int launch_rb(const void *packed, const _Float16 *a16, int lda, void *c, int M, int N, int K, hipStream_t s,
-              int pd_default = 4) {
+int launch_rb(const void *packed, const _Float16 *a16, int lda, void *c, const float *rs, int M, int N, int K,
+              hipStream_t s, int pd_default = 4) {
   const int C = (int)gq_chunks(FMT, K);
   const int nsteps = (int)(gq_kpad(FMT, K) / BK);
   const int tiles_m = (M + BM - 1) / BM, tiles_n = (N + BN - 1) / BN;
@@ -743,7 +764,7 @@ int launch_rb(const void *packed, const _Float16 *a16, int lda, void *c, int M, 
 #define GQ_LAUNCH_RB(PD)                                                                                        \
   hipLaunchKernelGGL((k_gemm_rb<FMT, CBF16, BM, BN, WM, WN, PD>), dim3((unsigned)(tiles_m * tiles_n)),          \
                      dim3(64 * WM * WN), 0, s, (const uint8_t *)packed, (uint32_t)gq_sc_plane_offset(FMT, N, K), \
-                     a16, lda, c, M, N, C, nsteps, tiles_m)
+                     a16, lda, c, rs, M, N, C, nsteps, tiles_m)
   if (pd == 4) GQ_LAUNCH_RB(4);
   else if (pd == 3) GQ_LAUNCH_RB(3);
   else GQ_LAUNCH_RB(2);
@@ -776,29 +797,30 @@ int pick_tile(int fmt, int M, int N) {
 }
 
 template <int FMT, int CBF16>
-int launch_fmt(const void *packed, const _Float16 *a16, int lda, void *c, int M, int N, int K, hipStream_t s) {
+int launch_fmt(const void *packed, const _Float16 *a16, int lda, void *c, const float *rs, int M, int N, int K,
+               hipStream_t s) {
   switch (pick_tile(FMT, M, N)) {
-  case 0: return launch_rb<FMT, CBF16, 256, 256, 2, 4>(packed, a16, lda, c, M, N, K, s, 2);
-  case 4: return launch_rb<FMT, CBF16, 256, 128, 2, 4>(packed, a16, lda, c, M, N, K, s);
-  case 5: return launch_rb<FMT, CBF16, 128, 256, 2, 4>(packed, a16, lda, c, M, N, K, s);
-  case 6: return launch_rb<FMT, CBF16, 128, 128, 2, 4>(packed, a16, lda, c, M, N, K, s);
-  case 7: return launch_rb<FMT, CBF16, 128, 128, 2, 2>(packed, a16, lda, c, M, N, K, s);
-  case 8: return launch_rb<FMT, CBF16, 256, 128, 4, 2>(packed, a16, lda, c, M, N, K, s);
-  case 9: return launch_rb<FMT, CBF16, 128, 64, 2, 2>(packed, a16, lda, c, M, N, K, s);
-  case 10: return launch_rb<FMT, CBF16, 64, 128, 2, 4>(packed, a16, lda, c, M, N, K, s);
-  case 11: return launch_rb<FMT, CBF16, 64, 64, 2, 2>(packed, a16, lda, c, M, N, K, s);
-  default: return launch_rb<FMT, CBF16, 128, 128, 2, 4>(packed, a16, lda, c, M, N, K, s);
-  case 3: return launch_cfg<FMT, CBF16, 256, 256>(packed, a16, lda, c, M, N, K, s);
-  case 1: return launch_cfg<FMT, CBF16, 256, 128>(packed, a16, lda, c, M, N, K, s);
-  case 2: return launch_cfg<FMT, CBF16, 128, 128>(packed, a16, lda, c, M, N, K, s);
+  case 0: return launch_rb<FMT, CBF16, 256, 256, 2, 4>(packed, a16, lda, c, rs, M, N, K, s, 2);
+  case 4: return launch_rb<FMT, CBF16, 256, 128, 2, 4>(packed, a16, lda, c, rs, M, N, K, s);
+  case 5: return launch_rb<FMT, CBF16, 128, 256, 2, 4>(packed, a16, lda, c, rs, M, N, K, s);
+  case 6: return launch_rb<FMT, CBF16, 128, 128, 2, 4>(packed, a16, lda, c, rs, M, N, K, s);
+  case 7: return launch_rb<FMT, CBF16, 128, 128, 2, 2>(packed, a16, lda, c, rs, M, N, K, s);
+  case 8: return launch_rb<FMT, CBF16, 256, 128, 4, 2>(packed, a16, lda, c, rs, M, N, K, s);
+  case 9: return launch_rb<FMT, CBF16, 128, 64, 2, 2>(packed, a16, lda, c, rs, M, N, K, s);
+  case 10: return launch_rb<FMT, CBF16, 64, 128, 2, 4>(packed, a16, lda, c, rs, M, N, K, s);
+  case 11: return launch_rb<FMT, CBF16, 64, 64, 2, 2>(packed, a16, lda, c, rs, M, N, K, s);
+  default: return launch_rb<FMT, CBF16, 128, 128, 2, 4>(packed, a16, lda, c, rs, M, N, K, s);
+  case 3: return launch_cfg<FMT, CBF16, 256, 256>(packed, a16, lda, c, rs, M, N, K, s);
+  case 1: return launch_cfg<FMT, CBF16, 256, 128>(packed, a16, lda, c, rs, M, N, K, s);
+  case 2: return launch_cfg<FMT, CBF16, 128, 128>(packed, a16, lda, c, rs, M, N, K, s);
   }
 }
 
 template <int FMT>
-int launch_gemm(const void *packed, const _Float16 *a16, int lda, void *c, int c_dtype, int M, int N, int K,
-                hipStream_t s) {
-  return c_dtype == GQ_DT_BF16 ? launch_fmt<FMT, 1>(packed, a16, lda, c, M, N, K, s)
-                               : launch_fmt<FMT, 0>(packed, a16, lda, c, M, N, K, s);
+int launch_gemm(const void *packed, const _Float16 *a16, int lda, void *c, const float *rs, int c_dtype, int M, int N,
+                int K, hipStream_t s) {
+  return c_dtype == GQ_DT_BF16 ? launch_fmt<FMT, 1>(packed, a16, lda, c, rs, M, N, K, s)
+                               : launch_fmt<FMT, 0>(packed, a16, lda, c, rs, M, N, K, s);
 }
 
 }  // namespace
@@ -806,8 +828,9 @@ int launch_gemm(const void *packed, const _Float16 *a16, int lda, void *c, int c
 extern "C" size_t gq_gemm_workspace_bytes(int fmt, size_t M, size_t K) {
   // activations are first written as fp16 [M][padded K (+ 8 for the skinny
   // kernel)] unless they are fp16 of the padded width already (tiled kernel)
+  // fp16 A, then the M row scales
   if (!gq_fmt_valid(fmt) || M > GQ_MAX_DIM || K > GQ_MAX_DIM) return 0;
-  return gq_align256(M * (gq_kpad(fmt, K) + 8) * 2);
+  return gq_align256(M * (gq_kpad(fmt, K) + 8) * 2) + gq_align256(M * 4);
 }
 
 extern "C" int gq_gemm(int fmt, const void *packed, const void *a, int a_dtype, void *c, int c_dtype, size_t M,
@@ -844,17 +867,18 @@ extern "C" int gq_gemm(int fmt, const void *packed, const void *a, int a_dtype, 
       ws_bytes = need;
     }
     GQ_CHECK(ws_bytes >= need, GQ_ERR_WORKSPACE);
-    const size_t n8 = M * (ldo / 8);
     const int q4 = fmt == GQ_FMT_Q4_0 || gq_fmt_is_q4k(fmt);
-    hipLaunchKernelGGL(k_a_to_f16, dim3((unsigned)((n8 + 255) / 256)), dim3(256), 0, s, a, a_dtype, (_Float16 *)ws,
-                       (int)M, (int)K, (int)ldo, q4);
+    float *rs = (float *)((uint8_t *)ws + gq_align256(M * ldo * 2));
+    hipLaunchKernelGGL(k_a_to_f16, dim3((unsigned)M), dim3(256), 0, s, a, a_dtype, (_Float16 *)ws, rs, (int)K,
+                       (int)ldo, q4);
     GQ_TRY(gq_last_launch());
-    return gq_launch_gemm_skinny(fmt, packed, (const _Float16 *)ws, (int)ldo, c, c_dtype == GQ_DT_BF16, (int)M, (int)N,
+    return gq_launch_gemm_skinny(fmt, packed, (const _Float16 *)ws, (int)ldo, c, rs, c_dtype == GQ_DT_BF16, (int)M, (int)N,
                                  (int)K, s);
   }
   // Q6_K has no tiled kernel (gq_matmul runs the batch GEMV per 16 rows)
   GQ_CHECK(!gq_fmt_is_q6k(fmt), GQ_ERR_UNSUPPORTED);
   const _Float16 *a16 = (const _Float16 *)a;
+  const float *rs = nullptr;  // (fp16 activations of the padded width are used as they are)
   if (a_dtype != GQ_DT_F16 || Kp != K) {
     const size_t need = gq_gemm_workspace_bytes(fmt, M, K);
     if (!ws) {
@@ -862,16 +886,17 @@ extern "C" int gq_gemm(int fmt, const void *packed, const void *a, int a_dtype, 
       ws_bytes = need;
     }
     GQ_CHECK(ws_bytes >= need, GQ_ERR_WORKSPACE);
-    const size_t n8 = M * (Kp / 8);
-    hipLaunchKernelGGL(k_a_to_f16, dim3((unsigned)((n8 + 255) / 256)), dim3(256), 0, s, a, a_dtype, (_Float16 *)ws,
-                       (int)M, (int)K, (int)Kp, 0);
+    float *rsw = (float *)((uint8_t *)ws + gq_align256(M * Kp * 2));
+    hipLaunchKernelGGL(k_a_to_f16, dim3((unsigned)M), dim3(256), 0, s, a, a_dtype, (_Float16 *)ws, rsw, (int)K,
+                       (int)Kp, 0);
     GQ_TRY(gq_last_launch());
     a16 = (const _Float16 *)ws;
+    rs = rsw;
   }
   const int lda = (int)Kp;
   switch (fmt) {
-  case GQ_FMT_Q4_0: return launch_gemm<GQ_FMT_Q4_0>(packed, a16, lda, c, c_dtype, (int)M, (int)N, (int)K, s);
-  case GQ_FMT_Q8_0: return launch_gemm<GQ_FMT_Q8_0>(packed, a16, lda, c, c_dtype, (int)M, (int)N, (int)K, s);
-  default: return launch_gemm<GQ_FMT_Q4_K>(packed, a16, lda, c, c_dtype, (int)M, (int)N, (int)K, s);
+  case GQ_FMT_Q4_0: return launch_gemm<GQ_FMT_Q4_0>(packed, a16, lda, c, rs, c_dtype, (int)M, (int)N, (int)K, s);
+  case GQ_FMT_Q8_0: return launch_gemm<GQ_FMT_Q8_0>(packed, a16, lda, c, rs, c_dtype, (int)M, (int)N, (int)K, s);
+  default: return launch_gemm<GQ_FMT_Q4_K>(packed, a16, lda, c, rs, c_dtype, (int)M, (int)N, (int)K, s);
   }
 }

@@ -795,17 +795,31 @@ int gq_gemv_h_min(void) {
   return (v >= 1 && v <= GQ_MAX_BATCH + 1) ? v : 5;
 }
 
+// LDS bytes of the in-kernel activation staging (batch <= 4) for a plan: one
+// limb region per wave of KSPLIT.
+static size_t q_staging_lds(int fmt, size_t K, int batch, int ks) {
+  const int f = gq_fmt_is_q4k(fmt) ? GQ_FMT_Q4_K : gq_fmt_is_q6k(fmt) ? GQ_FMT_Q6_K : fmt;
+  const int ck = (f == GQ_FMT_Q4_K || f == GQ_FMT_Q6_K) ? 256 : 128;
+  const int C = (int)gq_chunks(f, K);
+  const int nbc = batch == 1 ? 1 : batch == 2 ? 2 : 4;
+  return (size_t)ks * (size_t)xl_layout(ck * ((C + ks - 1) / ks), nbc).wave_bytes;
+}
+constexpr size_t kLdsMax = 160 * 1024;  // LDS per workgroup on gfx950
+
 // Which kernel gq_gemv uses: the fp16 batch kernel from gq_gemv_h_min() on,
-// for Q6_K beyond batch 2 (its int8 MFMA rows hold two batch rows), and where
-// K is too long for the int8 kernel's registers (more than 16 waves x MAXC
-// chunks: K > 16384); the int8 kernel otherwise.
+// for Q6_K beyond batch 2 (its int8 MFMA rows hold two batch rows), where K
+// is too long for the int8 kernel's registers (more than 16 waves x MAXC
+// chunks: K > 16384), and where its activation staging would not fit the LDS
+// (batch 3..4 with K near 16384: Q4_K 4096 x 14336 at batch 4 needs 176 KiB);
+// the int8 kernel otherwise.
 static bool gq_gemv_on_h(int fmt, size_t N, size_t K, int batch) {
   if (batch >= gq_gemv_h_min() || (gq_fmt_is_q6k(fmt) && batch > 2)) return true;
   int R = 1, ks = 2, cpw = 0;
   if (q_plan(fmt, N, K, batch, &R, &ks, &cpw) != GQ_OK) return true;
   const int f = gq_fmt_is_q4k(fmt) ? GQ_FMT_Q4_K : gq_fmt_is_q6k(fmt) ? GQ_FMT_Q6_K : fmt;
   const int maxc = (f == GQ_FMT_Q4_K || f == GQ_FMT_Q6_K) ? 4 : 8;
-  return cpw > maxc / R;
+  if (cpw > maxc / R) return true;
+  return batch <= 4 && q_staging_lds(fmt, K, batch, ks) > kLdsMax;
 }
 
 extern "C" size_t gq_gemv_workspace_bytes(int fmt, size_t K, int batch) {
@@ -882,6 +896,7 @@ int launch_fused_nbc(const GemvFuse &fz, size_t wgs, int ks, const float *x, int
   const int Kp = (int)gq_kpad(FMT, K);
   if ((C + ks - 1) / ks > NCKT) return GQ_ERR_INVALID_ARGS;
   const size_t lds = (size_t)ks * xl_layout(F::CK * ((C + ks - 1) / ks), NBC).wave_bytes;
+  if (lds > kLdsMax) return GQ_ERR_UNSUPPORTED;  // (long K at batch 3..4)
 #define GQ_LAUNCH_F(KS)                                                                                        \
   hipLaunchKernelGGL((k_gemv_q<FMT, NBC, 1, R, NCKT, KS, false, FUSE>), dim3((unsigned)wgs), dim3(64 * KS), \
                      lds, s, fz, x, nullptr, nullptr, K, C, Kp, nb)

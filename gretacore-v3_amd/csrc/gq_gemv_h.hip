@@ -570,7 +570,7 @@ k_gemv_h1(const uint8_t *__restrict__ w, size_t sc_off, const float *__restrict_
 template <int FMT, int CT, int NCK, bool CBF16, int KW = 8, int MT = 4>
 __global__ void __launch_bounds__(64 * KW) k_gemm_sk(const uint8_t *__restrict__ w, size_t sc_off,
                                                      const _Float16 *__restrict__ a16, int lda, void *__restrict__ c,
-                                                     int M, int N, int C) {
+                                                     const float *__restrict__ rs, int M, int N, int C) {
   using F = HFmt<FMT>;
   constexpr int NS = NCK * F::STEPS;  // 64-k steps per wave (static bound)
   __shared__ gq_f4 red[KW][CT * MT][64];
@@ -681,8 +681,9 @@ __global__ void __launch_bounds__(64 * KW) k_gemm_sk(const uint8_t *__restrict__
     for (int v = 0; v < 4; ++v) {
       const int row = m0 + 16 * mt + 4 * g + v;
       if (row >= M) continue;
+      const float o = rs ? sum[v] * rs[row] : sum[v];  // (row scale of the A conversion: a power of two)
       if constexpr (CBF16) {
-        uint32_t u = __float_as_uint(sum[v]);
+        uint32_t u = __float_as_uint(o);
         uint16_t hb;
         if ((u & 0x7F800000u) == 0x7F800000u) {
           hb = (uint16_t)((u >> 16) | ((u & 0xFFFFu) ? 0x40u : 0u));
@@ -692,7 +693,7 @@ __global__ void __launch_bounds__(64 * KW) k_gemm_sk(const uint8_t *__restrict__
         }
         reinterpret_cast<uint16_t *>(c)[(size_t)row * N + col] = hb;
       } else {
-        reinterpret_cast<float *>(c)[(size_t)row * N + col] = sum[v];
+        reinterpret_cast<float *>(c)[(size_t)row * N + col] = o;
       }
     }
   }
@@ -903,8 +904,8 @@ int gq_gemm_skinny_plan(int fmt, size_t M, size_t N, size_t K, int *ct_out, int 
 
 namespace {
 template <int FMT, int CT, bool CBF16>
-int launch_sk(const void *packed, const _Float16 *a16, int lda, void *c, int M, int N, int K, int nck,
-              hipStream_t s) {
+int launch_sk(const void *packed, const _Float16 *a16, int lda, void *c, const float *rs, int M, int N, int K,
+              int nck, hipStream_t s) {
   const int C = (int)gq_chunks(FMT, K);
   const dim3 grid((unsigned)((gq_tiles(N) + CT - 1) / CT), (unsigned)((M + 63) / 64));
   const size_t sc_off = gq_sc_plane_offset(FMT, N, K);
@@ -913,10 +914,10 @@ int launch_sk(const void *packed, const _Float16 *a16, int lda, void *c, int M, 
     if constexpr (CT == 1 && (FMT == GQ_FMT_Q4_0 || FMT == GQ_FMT_Q4_K)) {
       const dim3 g2((unsigned)gq_tiles(N), (unsigned)((M + 31) / 32));
       if (nck == 20)
-        hipLaunchKernelGGL((k_gemm_sk<FMT, 1, 4, CBF16, 16, 2>), g2, dim3(1024), 0, s, w, sc_off, a16, lda, c, M, N,
+        hipLaunchKernelGGL((k_gemm_sk<FMT, 1, 4, CBF16, 16, 2>), g2, dim3(1024), 0, s, w, sc_off, a16, lda, c, rs, M, N,
                            C);
       else if constexpr (FMT == GQ_FMT_Q4_0)
-        hipLaunchKernelGGL((k_gemm_sk<FMT, 1, 8, CBF16, 16, 2>), g2, dim3(1024), 0, s, w, sc_off, a16, lda, c, M, N,
+        hipLaunchKernelGGL((k_gemm_sk<FMT, 1, 8, CBF16, 16, 2>), g2, dim3(1024), 0, s, w, sc_off, a16, lda, c, rs, M, N,
                            C);
       else
         return GQ_ERR_UNSUPPORTED;
@@ -925,37 +926,37 @@ int launch_sk(const void *packed, const _Float16 *a16, int lda, void *c, int M, 
     return GQ_ERR_UNSUPPORTED;
   }
   if (nck <= 1)
-    hipLaunchKernelGGL((k_gemm_sk<FMT, CT, 1, CBF16>), grid, dim3(512), 0, s, w, sc_off, a16, lda, c, M, N, C);
+    hipLaunchKernelGGL((k_gemm_sk<FMT, CT, 1, CBF16>), grid, dim3(512), 0, s, w, sc_off, a16, lda, c, rs, M, N, C);
   else if (nck <= 2)
-    hipLaunchKernelGGL((k_gemm_sk<FMT, CT, 2, CBF16>), grid, dim3(512), 0, s, w, sc_off, a16, lda, c, M, N, C);
+    hipLaunchKernelGGL((k_gemm_sk<FMT, CT, 2, CBF16>), grid, dim3(512), 0, s, w, sc_off, a16, lda, c, rs, M, N, C);
   else if constexpr (FMT != GQ_FMT_Q6_K)
-    hipLaunchKernelGGL((k_gemm_sk<FMT, CT, 4, CBF16>), grid, dim3(512), 0, s, w, sc_off, a16, lda, c, M, N, C);
+    hipLaunchKernelGGL((k_gemm_sk<FMT, CT, 4, CBF16>), grid, dim3(512), 0, s, w, sc_off, a16, lda, c, rs, M, N, C);
   else
     return GQ_ERR_UNSUPPORTED;
   return gq_last_launch();
 }
 template <int FMT, bool CBF16>
-int launch_sk_ct(const void *packed, const _Float16 *a16, int lda, void *c, int M, int N, int K, int ct, int nck,
-                 hipStream_t s) {
-  return ct == 2 ? launch_sk<FMT, 2, CBF16>(packed, a16, lda, c, M, N, K, nck, s)
-                 : launch_sk<FMT, 1, CBF16>(packed, a16, lda, c, M, N, K, nck, s);
+int launch_sk_ct(const void *packed, const _Float16 *a16, int lda, void *c, const float *rs, int M, int N, int K, int ct,
+                 int nck, hipStream_t s) {
+  return ct == 2 ? launch_sk<FMT, 2, CBF16>(packed, a16, lda, c, rs, M, N, K, nck, s)
+                 : launch_sk<FMT, 1, CBF16>(packed, a16, lda, c, rs, M, N, K, nck, s);
 }
 template <int FMT>
-int launch_sk_fmt(const void *packed, const _Float16 *a16, int lda, void *c, int cbf16, int M, int N, int K, int ct,
-                  int nck, hipStream_t s) {
-  return cbf16 ? launch_sk_ct<FMT, true>(packed, a16, lda, c, M, N, K, ct, nck, s)
-               : launch_sk_ct<FMT, false>(packed, a16, lda, c, M, N, K, ct, nck, s);
+int launch_sk_fmt(const void *packed, const _Float16 *a16, int lda, void *c, const float *rs, int cbf16, int M, int N,
+                  int K, int ct, int nck, hipStream_t s) {
+  return cbf16 ? launch_sk_ct<FMT, true>(packed, a16, lda, c, rs, M, N, K, ct, nck, s)
+               : launch_sk_ct<FMT, false>(packed, a16, lda, c, rs, M, N, K, ct, nck, s);
 }
 }  // namespace
 
-int gq_launch_gemm_skinny(int fmt, const void *packed, const _Float16 *a16, int lda, void *c, int cbf16, int M, int N,
-                          int K, hipStream_t s) {
+int gq_launch_gemm_skinny(int fmt, const void *packed, const _Float16 *a16, int lda, void *c, const float *rs,
+                          int cbf16, int M, int N, int K, hipStream_t s) {
   int ct = 1, nck = 1;
   GQ_TRY(gq_gemm_skinny_plan(fmt, (size_t)M, (size_t)N, (size_t)K, &ct, &nck));
-  if (gq_fmt_is_q6k(fmt)) return launch_sk_fmt<GQ_FMT_Q6_K>(packed, a16, lda, c, cbf16, M, N, K, ct, nck, s);
+  if (gq_fmt_is_q6k(fmt)) return launch_sk_fmt<GQ_FMT_Q6_K>(packed, a16, lda, c, rs, cbf16, M, N, K, ct, nck, s);
   switch (gq_fmt_is_q4k(fmt) ? GQ_FMT_Q4_K : fmt) {
-  case GQ_FMT_Q4_0: return launch_sk_fmt<GQ_FMT_Q4_0>(packed, a16, lda, c, cbf16, M, N, K, ct, nck, s);
-  case GQ_FMT_Q8_0: return launch_sk_fmt<GQ_FMT_Q8_0>(packed, a16, lda, c, cbf16, M, N, K, ct, nck, s);
-  default: return launch_sk_fmt<GQ_FMT_Q4_K>(packed, a16, lda, c, cbf16, M, N, K, ct, nck, s);
+  case GQ_FMT_Q4_0: return launch_sk_fmt<GQ_FMT_Q4_0>(packed, a16, lda, c, rs, cbf16, M, N, K, ct, nck, s);
+  case GQ_FMT_Q8_0: return launch_sk_fmt<GQ_FMT_Q8_0>(packed, a16, lda, c, rs, cbf16, M, N, K, ct, nck, s);
+  default: return launch_sk_fmt<GQ_FMT_Q4_K>(packed, a16, lda, c, rs, cbf16, M, N, K, ct, nck, s);
   }
 }

@@ -55,10 +55,11 @@ int gq_gemv_h1_plan(int fmt, size_t N, size_t K, int nb, int *R_out, int *ks_out
 int gq_launch_gemv_h(int fmt, const void *packed, const float *x, float *y, int N, int K, int nb, hipStream_t s);
 
 // skinny GEMM for M <= 256 (gq_gemv_h.hip); A fp16 in the B fragments' order
-// (k_a_to_f16 with the 4-bit permutation for Q4_0 / Q4_K)
+// (k_a_to_f16 with the 4-bit permutation for Q4_0 / Q4_K); rs: per-row
+// factors applied to C (NULL: none)
 int gq_gemm_skinny_plan(int fmt, size_t M, size_t N, size_t K, int *ct_out, int *nck_out);
-int gq_launch_gemm_skinny(int fmt, const void *packed, const _Float16 *a16, int lda, void *c, int cbf16, int M, int N,
-                          int K, hipStream_t s);
+int gq_launch_gemm_skinny(int fmt, const void *packed, const _Float16 *a16, int lda, void *c, const float *rs,
+                          int cbf16, int M, int N, int K, hipStream_t s);
 
 // load-time conversions (gq_loadconv.hip)
 int gq_launch_dequant_q6_k(const void *blocks, size_t n_blocks, float *out, int ggml, hipStream_t s);

@@ -69,6 +69,8 @@ _SIGS = {
     "gq_requant_int4": (ctypes.c_int, [_vp, _c_size, _vp, _vp, _vp]),
     "gq_head_scales": (ctypes.c_int, [_vp, _c_size, ctypes.c_uint32, ctypes.c_uint32, ctypes.c_uint32, _vp, _vp]),
     "gq_split_q8_0": (ctypes.c_int, [_vp, _c_size, _vp, _vp, _vp]),
+    "gq_probe_read": (ctypes.c_int, [_vp, _c_size, ctypes.c_int, ctypes.c_int, _vp, _vp]),
+    "gq_probe_empty": (ctypes.c_int, [ctypes.c_int, ctypes.c_int, _vp]),
     "gq_launch_gemm_mfma_int8_wt_fp32_acc32": (
         ctypes.c_int, [_vp, _vp, _vp, _vp, _vp] + [ctypes.c_uint32] * 7),
     "gq_launch_gemm_mfma_int4_wt_fp32_acc32": (
@@ -344,6 +346,19 @@ def launch_int4_wt(a, b, scales, head_scales, m, n, k, group_size=32, head_dim=0
         _stream(stream), _ptr(a), _ptr(b), _ptr(c), _ptr(scales), _ptr(head_scales), m, n, k, k, n, n, group_size,
         head_dim, int(a.dtype == torch.float16), int(force_gemv)), "gq_launch_gemm_mfma_int4_wt_fp32_acc32")
     return c
+
+
+def probe_read(src, wgs: int, waves_per_wg: int, out, stream=None):
+    """Calibration: stream all of `src` (a uint8 device tensor) with the
+    decode GEMV's grid shape; one word per wave goes to `out`."""
+    _require_device(src, out)
+    check(load().gq_probe_read(_ptr(src), src.numel(), wgs, waves_per_wg, _ptr(out), _stream(stream)),
+          "gq_probe_read")
+
+
+def probe_empty(wgs: int, waves_per_wg: int, stream=None):
+    """Calibration: the same grid with no work."""
+    check(load().gq_probe_empty(wgs, waves_per_wg, _stream(stream)), "gq_probe_empty")
 
 
 def gemv_prep(fmt: int, x, k: int, workspace: Workspace, stream=None):

@@ -34,45 +34,67 @@ void GretaStreamHip::wait_event(GretaEvent *event) {
 }
 void GretaStreamHip::record_event(GretaEvent *event) { event->record(this); }
 
-// ---- Buffer (reference: src/rt/backend/hip/src/buffer.cpp:9-84) ----------
+// ---- Buffer ------------------------------------------------------------------
+// Same contract as the reference's Buffer (src/rt/backend/hip/src/buffer.cpp):
+// owns one allocation (device memory, or pinned host memory for HostVisible),
+// re-allocation releases the old one first, copies are synchronous and
+// bounds-checked.  Every copy goes through one checked helper; the status
+// text names the operation, the byte range and the HIP error.
+namespace {
+
+// [offset, offset + bytes) inside a buffer of `capacity` bytes, without
+// overflow in the sum.
+bool range_inside(size_t offset, size_t bytes, size_t capacity) {
+  return offset <= capacity && bytes <= capacity - offset;
+}
+
+bool report(std::string *err, const std::string &what) {
+  if (err) *err = what;
+  return false;
+}
+
+bool checked_copy(void *dst, const void *src, size_t bytes, hipMemcpyKind kind, const char *op, std::string *err) {
+  if (bytes == 0) return true;
+  const hipError_t e = hipMemcpy(dst, src, bytes, kind);
+  if (e == hipSuccess) return true;
+  return report(err, std::string("Buffer::") + op + ": " + std::to_string(bytes) + "-byte copy: " +
+                         hipGetErrorName(e) + " (" + hipGetErrorString(e) + ")");
+}
+
+}  // namespace
+
 Buffer::~Buffer() { free(); }
 
 bool Buffer::allocate(size_t size, BufferUsage usage, GretaDataType type, std::string *err) {
   free();
+  void *p = nullptr;
+  const hipError_t e = usage == BufferUsage::HostVisible ? hipHostMalloc(&p, size) : hipMalloc(&p, size);
+  if (e != hipSuccess)
+    return report(err, std::string("Buffer::allocate: ") + std::to_string(size) + " bytes of " +
+                           (usage == BufferUsage::HostVisible ? "pinned host" : "device") + " memory: " +
+                           hipGetErrorName(e) + " (" + hipGetErrorString(e) + ")");
+  ptr_ = p;
+  size_ = size;
   usage_ = usage;
   type_ = type;
   qinfo_ = GretaQuantInfo{};
-  hipError_t res = usage == BufferUsage::HostVisible ? hipHostMalloc(&ptr_, size) : hipMalloc(&ptr_, size);
-  if (res != hipSuccess) {
-    if (err) *err = "HIP allocation failed: " + std::string(hipGetErrorString(res));
-    ptr_ = nullptr;
-    size_ = 0;
-    return false;
-  }
-  size_ = size;
   return true;
 }
 
 void Buffer::free() {
-  if (ptr_) {
-    if (usage_ == BufferUsage::HostVisible) (void)hipHostFree(ptr_);
-    else (void)hipFree(ptr_);
-  }
+  void *p = ptr_;
   ptr_ = nullptr;
   size_ = 0;
+  if (!p) return;
+  if (usage_ == BufferUsage::HostVisible) (void)hipHostFree(p);
+  else (void)hipFree(p);
 }
 
 bool Buffer::copy_to_device(const void *host_ptr, size_t size, std::string *err) {
-  if (size > size_) {
-    if (err) *err = "copy_to_device: " + std::to_string(size) + " bytes into a " + std::to_string(size_) + "-byte buffer";
-    return false;
-  }
-  hipError_t res = hipMemcpy(ptr_, host_ptr, size, hipMemcpyHostToDevice);
-  if (res != hipSuccess) {
-    if (err) *err = "hipMemcpy H2D failed: " + std::string(hipGetErrorString(res));
-    return false;
-  }
-  return true;
+  if (!range_inside(0, size, size_))
+    return report(err, "Buffer::copy_to_device: " + std::to_string(size) + " bytes do not fit the " +
+                           std::to_string(size_) + "-byte buffer");
+  return checked_copy(ptr_, host_ptr, size, hipMemcpyHostToDevice, "copy_to_device", err);
 }
 
 bool Buffer::copy_to_host(void *host_ptr, size_t size, std::string *err) const {
@@ -80,18 +102,12 @@ bool Buffer::copy_to_host(void *host_ptr, size_t size, std::string *err) const {
 }
 
 bool Buffer::copy_to_host_offset(void *host_ptr, size_t offset, size_t size, std::string *err) const {
-  if (offset + size > size_) {
-    if (err)
-      *err = "Buffer copy out of bounds: offset=" + std::to_string(offset) + ", size=" + std::to_string(size) +
-             ", total_size=" + std::to_string(size_);
-    return false;
-  }
-  hipError_t res = hipMemcpy(host_ptr, static_cast<char *>(ptr_) + offset, size, hipMemcpyDeviceToHost);
-  if (res != hipSuccess) {
-    if (err) *err = "hipMemcpy D2H failed: " + std::string(hipGetErrorString(res));
-    return false;
-  }
-  return true;
+  if (!range_inside(offset, size, size_))
+    return report(err, "Buffer::copy_to_host: bytes [" + std::to_string(offset) + ", " +
+                           std::to_string(offset) + " + " + std::to_string(size) + ") outside the " +
+                           std::to_string(size_) + "-byte buffer");
+  return checked_copy(host_ptr, static_cast<const char *>(ptr_) + offset, size, hipMemcpyDeviceToHost,
+                      "copy_to_host", err);
 }
 
 }  // namespace gcore::rt::hip

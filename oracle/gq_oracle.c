@@ -435,34 +435,47 @@ void gqo_gqa_transpose(const float *in, uint32_t model_dim, uint32_t kv_dim,
       out[(size_t)r * model_dim + c] = in[(size_t)c * kv_dim + r];
 }
 
-/* gemm_kernels.hip:594-634 (math, rows in the "row" layout). */
+/* Scale of weight (n, k) in the reference's INT8 / INT4 launchers.  The two
+ * routes index the flat per-group scale array differently:
+ *   GEMV kernels (M <= 32 or force_gemv), gemm_kernels.hip:610,615 and
+ *   781,796-797: s_row = scales + (n*K)/gs, then s_row[k/gs];
+ *   MFMA kernels (M > 32), gemm_kernels.hip:717 and 886: scales[(n*K + k)/gs].
+ * They agree whenever K % gs == 0. */
+static size_t scale_index(size_t n, size_t K, size_t k, size_t gs, int gemv_route) {
+  return gemv_route ? (n * K) / gs + k / gs : (n * K + k) / gs;
+}
+
+/* gemm_kernels.hip:594-634 (GEMV route) / 640-740 (MFMA route): the math,
+ * rows in the "row" layout. */
 void gqo_gemm_int8_wt(const float *x, const int8_t *q, const float *s, float *y,
-                      int M, int N, int K, int gs) {
+                      int M, int N, int K, int gs, int gemv_route) {
   for (int m = 0; m < M; ++m)
     for (int n = 0; n < N; ++n) {
       double acc = 0.0;
       for (int k = 0; k < K; ++k) {
         size_t idx = (size_t)n * K + k;
-        volatile float wv = (float)q[idx] * s[idx / gs];
+        volatile float wv = (float)q[idx] * s[scale_index(n, K, k, gs, gemv_route)];
         acc += (double)x[(size_t)m * K + k] * (double)wv;
       }
       y[(size_t)m * N + n] = (float)acc;
     }
 }
 
-/* gemm_kernels.hip:763-817: sign-extended nibbles (even k low), x head scale. */
+/* gemm_kernels.hip:763-817 (GEMV route) / 820-908 (MFMA route): sign-extended
+ * nibbles, row n at byte n*(K/2) (even k in the low nibble), x head scale.
+ * K is even (the reference's loader packs the flat tensor, which matches the
+ * kernels' row addressing only then). */
 void gqo_gemm_int4_wt(const float *x, const uint8_t *packed, const float *s,
                       const float *head_scales, float *y, int M, int N, int K,
-                      int gs, int head_dim) {
+                      int gs, int head_dim, int gemv_route) {
   for (int m = 0; m < M; ++m)
     for (int n = 0; n < N; ++n) {
       double acc = 0.0;
       for (int k = 0; k < K; ++k) {
-        size_t idx = (size_t)n * K + k;
-        uint8_t p = packed[idx / 2];
+        uint8_t p = packed[(size_t)n * (K / 2) + k / 2];
         int v = (k % 2 == 0) ? (p & 0x0F) : (p >> 4);
         if (v & 8) v -= 16;
-        volatile float wv = (float)v * s[idx / gs];
+        volatile float wv = (float)v * s[scale_index(n, K, k, gs, gemv_route)];
         acc += (double)x[(size_t)m * K + k] * (double)wv;
       }
       float h = 1.0f;

@@ -81,12 +81,14 @@ void gqo_gqa_transpose(const float *in, uint32_t model_dim, uint32_t kv_dim,
                        float *out);
 
 /* Reference INT8 / INT4 weight-only GEMV/GEMM math (gemm_kernels.hip:594-634,
- * 763-817): y[m][n] = sum_k x[m][k]*(q[n][k]*s[(n*K+k)/gs]) (x head scale). */
+ * 640-740, 763-817, 820-908): y[m][n] = sum_k x[m][k]*(q[n][k]*s[idx]) (x head
+ * scale), idx = (n*K)/gs + k/gs on the GEMV route (gemv_route != 0: M <= 32
+ * or force_gemv) and (n*K + k)/gs on the MFMA route (M > 32). */
 void gqo_gemm_int8_wt(const float *x, const int8_t *q, const float *s, float *y,
-                      int M, int N, int K, int gs);
+                      int M, int N, int K, int gs, int gemv_route);
 void gqo_gemm_int4_wt(const float *x, const uint8_t *packed, const float *s,
                       const float *head_scales, float *y, int M, int N, int K,
-                      int gs, int head_dim);
+                      int gs, int head_dim, int gemv_route);
 
 /* RMS normalisation of fused_rmsnorm_qkv_gemv_kernel_f16
  * (src/rt/backend/hip/kernels/fused_compute_kernels.hip:36-87), in fp64:

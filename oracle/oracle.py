@@ -62,8 +62,8 @@ def lib():
         L.gqo_requant_int4.argtypes = [vp, sz, vp, vp]
         L.gqo_head_scales.argtypes = [vp, ctypes.c_uint32, ctypes.c_uint32, ctypes.c_uint32, vp]
         L.gqo_gqa_transpose.argtypes = [vp, ctypes.c_uint32, ctypes.c_uint32, vp]
-        L.gqo_gemm_int8_wt.argtypes = [vp, vp, vp, vp, i, i, i, i]
-        L.gqo_gemm_int4_wt.argtypes = [vp, vp, vp, vp, vp, i, i, i, i, i]
+        L.gqo_gemm_int8_wt.argtypes = [vp, vp, vp, vp, i, i, i, i, i]
+        L.gqo_gemm_int4_wt.argtypes = [vp, vp, vp, vp, vp, i, i, i, i, i, i]
         L.gqo_quantize_act_q8.argtypes = [vp, i, i, vp, vp]
         L.gqo_gemm_q8_i8.argtypes = [vp, vp, vp, vp, i, i, i, i]
         _lib = L
@@ -199,22 +199,32 @@ def gqa_transpose(w, model_dim, kv_dim):
     return out
 
 
-def gemm_int8_wt(x, q, s, m, n, k, gs=32):
+def _gemv_route(m, gemv_route):
+    """The reference launchers take the GEMV kernels for M <= 32 (or
+    force_gemv), the MFMA kernels above (gemm_kernels.hip:749, 917)."""
+    return int(m <= 32 if gemv_route is None else gemv_route)
+
+
+def gemm_int8_wt(x, q, s, m, n, k, gs=32, gemv_route=None):
+    """Reference INT8 launcher math; the scale index follows the route the
+    reference takes for m rows unless gemv_route is given."""
     x = np.ascontiguousarray(x, dtype=np.float32)
     q = np.ascontiguousarray(q, dtype=np.int8)
     s = np.ascontiguousarray(s, dtype=np.float32)
     y = np.empty((m, n), dtype=np.float32)
-    lib().gqo_gemm_int8_wt(_p(x), _p(q), _p(s), _p(y), m, n, k, gs)
+    lib().gqo_gemm_int8_wt(_p(x), _p(q), _p(s), _p(y), m, n, k, gs, _gemv_route(m, gemv_route))
     return y
 
 
-def gemm_int4_wt(x, packed, s, hs, m, n, k, gs=32, head_dim=0):
+def gemm_int4_wt(x, packed, s, hs, m, n, k, gs=32, head_dim=0, gemv_route=None):
+    """Reference INT4 launcher math (K even); scale index as gemm_int8_wt."""
+    assert k % 2 == 0
     x = np.ascontiguousarray(x, dtype=np.float32)
     packed = np.ascontiguousarray(packed, dtype=np.uint8)
     s = np.ascontiguousarray(s, dtype=np.float32)
     y = np.empty((m, n), dtype=np.float32)
     hsp = _p(np.ascontiguousarray(hs, dtype=np.float32)) if hs is not None else None
-    lib().gqo_gemm_int4_wt(_p(x), _p(packed), _p(s), hsp, _p(y), m, n, k, gs, head_dim)
+    lib().gqo_gemm_int4_wt(_p(x), _p(packed), _p(s), hsp, _p(y), m, n, k, gs, head_dim, _gemv_route(m, gemv_route))
     return y
 
 

@@ -182,12 +182,41 @@ def test_gemv_plan_in_bounds(fmt, batch, monkeypatch):
             emulate(fmt, n, k, batch)
     if fmt == gq.FMT_Q6_K:
         return
-    # the int8 kernel at every batch (the split prep / prepped form uses it)
+    # the int8 kernel at every batch (the split prep / prepped form uses it);
+    # up to batch 4 gq_gemv stages the activation limbs in LDS, and where that
+    # staging would exceed the 160 KiB of a workgroup the fp16 kernel takes the
+    # shape instead (Q4_K 4096 x 14336 at batch 3..4)
     monkeypatch.setenv("GQ_GEMV_H_MIN", "17")
     for n, k in SHAPES:
         if k % (256 if fmt == gq.FMT_Q4_K else 32):
             continue
+        if batch <= 4 and staging_lds(fmt, n, k, batch) > 160 * 1024:
+            assert gq.gemv_plan(fmt, n, k, batch) != gq.gemv_plan(fmt, n, k, 1)
+            emulate_h(fmt, n, k, batch)
+            continue
         emulate(fmt, n, k, batch)
+
+
+def staging_lds(fmt, n, k, batch):
+    """LDS bytes of the int8 kernel's in-kernel activation staging: per wave,
+    two int8 limb rows per staged batch row of the wave's K slice, a zero row,
+    and a float4 per (batch row, 32-block)."""
+    R, ks, cpw = gq.gemv_plan(fmt, n, k, 1)  # the int8 plan's K split (batch-independent)
+    C = -(-k // CK[fmt])
+    lk = CK[fmt] * -(-C // ks)
+    nb = 1 if batch == 1 else 2 if batch == 2 else 4
+    wave = (2 * nb * lk + lk + nb * (lk // 32) * 16 + 15) & ~15
+    return ks * wave
+
+
+def test_int8_staging_lds_guard():
+    """The known case: Q4_K 4096 x 14336 at batch 4 would stage 176 KiB (16
+    waves of 3.5 KiB-slices: 2 x 4 x 1024 + 1024 + 4 x 32 x 16 bytes each) and
+    runs on the fp16 batch kernel; at batch 2 (112 KiB) it stays on the int8
+    kernel."""
+    assert staging_lds(gq.FMT_Q4_K, 4096, 14336, 4) == 16 * 11264
+    assert staging_lds(gq.FMT_Q4_K, 4096, 14336, 2) <= 160 * 1024
+    assert gq.gemv_plan(gq.FMT_Q4_K, 4096, 14336, 4) != gq.gemv_plan(gq.FMT_Q4_K, 4096, 14336, 2)
 
 
 def test_plan_single_chunk_has_idle_wave():

@@ -297,6 +297,36 @@ def test_reference_int_wt_math():
     assert np.array_equal(O.gemm_int8_wt(x, q, s, m, n, k), (x.astype(np.float64) @ W.T.astype(np.float64)).astype(np.float32))
 
 
+def test_reference_launcher_scale_index_known_answer():
+    """K % group_size != 0: the reference's GEMV kernels pick scale
+    s_row[k/gs] with s_row = scales + (n*K)/gs (gemm_kernels.hip:610,615,
+    781,796-797), its MFMA kernels scales[(n*K + k)/gs] (:717, :886).  Row 1
+    of a K = 48, gs = 32 tensor starts at flat element 48: scale index 1.  For
+    k = 20 the GEMV form gives 1 + 20 // 32 = 1, the flat form (48 + 20) // 32
+    = 2; for k = 40: 1 + 1 = 2 and 88 // 32 = 2; for k = 10: 1 and 1."""
+    n, k, gs = 2, 48, 32
+    s = np.array([1.0, 10.0, 100.0, 1000.0], dtype=np.float32)  # ceil(96 / 32) = 3 used
+    q8 = np.ones((n, k), dtype=np.int8)
+    p4 = np.full(n * k // 2, 0x11, dtype=np.uint8)  # both nibbles = 1
+    for col, gemv_scale, mfma_scale in ((20, 10.0, 100.0), (40, 100.0, 100.0), (10, 10.0, 10.0)):
+        x = np.zeros((1, k), dtype=np.float32)
+        x[0, col] = 1.0
+        for route, want in ((True, gemv_scale), (False, mfma_scale)):
+            y8 = O.gemm_int8_wt(x, q8, s, 1, n, k, gs, gemv_route=route)
+            y4 = O.gemm_int4_wt(x, p4, s, None, 1, n, k, gs, 0, gemv_route=route)
+            assert y8[0, 1] == want and y4[0, 1] == want, (col, route)
+    # row 0 starts at 0: both forms agree
+    x = np.zeros((1, k), dtype=np.float32)
+    x[0, 40] = 1.0
+    assert O.gemm_int8_wt(x, q8, s, 1, n, k, gs, gemv_route=True)[0, 0] == 10.0
+    assert O.gemm_int8_wt(x, q8, s, 1, n, k, gs, gemv_route=False)[0, 0] == 10.0
+    # the default route follows the reference launchers' M <= 32 switch
+    x33 = np.zeros((33, k), dtype=np.float32)
+    x33[:, 20] = 1.0
+    assert O.gemm_int8_wt(x33, q8, s, 33, n, k, gs)[0, 1] == 100.0
+    assert O.gemm_int8_wt(x33[:32], q8, s, 32, n, k, gs)[0, 1] == 10.0
+
+
 def test_act_q8_quant_and_int_gemm():
     rng = np.random.default_rng(7)
     a = rng.standard_normal((4, 64)).astype(np.float32)
