@@ -236,6 +236,18 @@ GQ_DEV void tile_of(int id, int G, int tiles_m, int &mt, int &nt) {
   mt = t % tiles_m;
 }
 
+// Row scales rs[m0 .. m0 + BM) of a tile, four per thread for the first BM / 4
+// threads (1.0 where rs is NULL).  The load is unconditional, from a valid
+// address either way (the scale buffer is padded past M; `any` is any
+// readable 16 bytes), so no branch sits around it.
+template <int BM>
+GQ_DEV gq_f4 ld_row_scales(const float *rs, int m0, int tid, const void *any) {
+  const int t = tid % (BM / 4);
+  const gq_f4 *p = rs ? reinterpret_cast<const gq_f4 *>(rs + m0 + 4 * t) : reinterpret_cast<const gq_f4 *>(any);
+  const gq_f4 v = *p;
+  return rs ? v : gq_f4{1.f, 1.f, 1.f, 1.f};
+}
+
 template <int FMT, int CBF16, int BM, int BN>
 __global__ void __launch_bounds__(NTHR) __attribute__((amdgpu_waves_per_eu(2, 2)))
 k_gemm_t16(const uint8_t *__restrict__ w, uint32_t sc_off, const _Float16 *__restrict__ a16, int lda,
@@ -351,6 +363,10 @@ k_gemm_t16(const uint8_t *__restrict__ w, uint32_t sc_off, const _Float16 *__res
     __syncthreads();
   };
 
+  // the tile's row scales go to LDS with the prologue (read back by the
+  // epilogue, whose global stores would otherwise wait behind their loads)
+  __shared__ __attribute__((aligned(16))) float rs_s[BM];
+  const gq_f4 rs4 = ld_row_scales<BM>(rs, m0, tid, w);
   // prologue: step 0 in buffer 0, step 1 in register stage 1
   load_a_lds<BM>(a16, lda, M, m0, 0, wave, lane, As_0);
   load_w_step(0, 0);
@@ -358,6 +374,7 @@ k_gemm_t16(const uint8_t *__restrict__ w, uint32_t sc_off, const _Float16 *__res
 #pragma unroll
   for (int q = 0; q < KS; ++q) store_w_part(q, 0, 0, B0{});
   __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
+  if (tid < BM / 4) *reinterpret_cast<gq_f4 *>(rs_s + 4 * tid) = rs4;
   __syncthreads();
   // nsteps is even (K is padded to whole 128-k chunks)
   for (int step = 0; step < nsteps; step += 2) {
@@ -367,16 +384,26 @@ k_gemm_t16(const uint8_t *__restrict__ w, uint32_t sc_off, const _Float16 *__res
 
   // D layout (32x32): lane l holds column l%32, rows 8*(v/4) + 4*(l/32) + v%4.
 #pragma unroll
-  for (int i = 0; i < TM; ++i)
+  for (int i = 0; i < TM; ++i) {
+    // the row scales of this lane's 16 rows of MFMA tile row i (from LDS):
+    // four runs of four consecutive rows; exact powers of two
+    const int mb = m0 + (BM / 2) * wm + 32 * i + 4 * (lane >> 5);
+    float rsv[16];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const gq_f4 t = *reinterpret_cast<const gq_f4 *>(rs_s + (mb - m0) + 8 * q);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) rsv[4 * q + e] = t[e];
+    }
 #pragma unroll
     for (int j = 0; j < TN; ++j) {
       const int n = n0 + (BN / 4) * wn + 32 * j + (lane & 31);
       if (n >= N) continue;
 #pragma unroll
       for (int v = 0; v < 16; ++v) {
-        const int m = m0 + (BM / 2) * wm + 32 * i + 8 * (v >> 2) + 4 * (lane >> 5) + (v & 3);
+        const int m = mb + 8 * (v >> 2) + (v & 3);
         if (m < M) {
-          const float o = rs ? acc[i][j][v] * rs[m] : acc[i][j][v];  // (row scale: an exact power of two)
+          const float o = acc[i][j][v] * rsv[v];
           if constexpr (CBF16)
             reinterpret_cast<uint16_t *>(c)[(size_t)m * N + n] = f32_to_bf16_rne(o);
           else
@@ -384,6 +411,7 @@ k_gemm_t16(const uint8_t *__restrict__ w, uint32_t sc_off, const _Float16 *__res
         }
       }
     }
+  }
 }
 
 // ---- register-B kernel: 256 x 256 tiles, 4 waves of 128 x 128 ----------------
@@ -631,11 +659,17 @@ k_gemm_rb(const uint8_t *__restrict__ w, uint32_t sc_off, const _Float16 *__rest
     if constexpr (i < PD - 1) load_a_lds<BM, NW>(a16, lda, M, m0, st, wave, lane, As_of(b));
     load_rstep<FMT, NJ>(w, qo, so, st, wst[i]);
   };
+  // the tile's row scales, requested before the operands (the oldest load,
+  // so the wait below covers it) and kept in LDS for the epilogue, whose
+  // global stores would otherwise wait behind their loads
+  __shared__ __attribute__((aligned(16))) float rs_s[BM];
+  const gq_f4 rs4 = ld_row_scales<BM>(rs, m0, tid, w);
   prime(B0{});
   prime(B1{});
   if constexpr (PD >= 3) prime(B2{});
   if constexpr (PD >= 4) prime(B3{});
   __builtin_amdgcn_s_waitcnt(kWaitPend);
+  if (tid < BM / 4) *reinterpret_cast<gq_f4 *>(rs_s + 4 * tid) = rs4;
   __syncthreads();
   for (int step = 0; step < nsteps; step += PD) {
     run_step(step, B0{});
@@ -647,16 +681,26 @@ k_gemm_rb(const uint8_t *__restrict__ w, uint32_t sc_off, const _Float16 *__rest
   }
 
 #pragma unroll
-  for (int i = 0; i < TM; ++i)
+  for (int i = 0; i < TM; ++i) {
+    // the row scales of this lane's 16 rows of MFMA tile row i (from LDS):
+    // four runs of four consecutive rows; exact powers of two
+    const int mb = m0 + (BM / WM) * wm + 32 * i + 4 * (lane >> 5);
+    float rsv[16];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const gq_f4 t = *reinterpret_cast<const gq_f4 *>(rs_s + (mb - m0) + 8 * q);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) rsv[4 * q + e] = t[e];
+    }
 #pragma unroll
     for (int j = 0; j < NJ; ++j) {
       const int n = n0 + (BN / WN) * wn + 32 * j + (lane & 31);
       if (n >= N) continue;
 #pragma unroll
       for (int v = 0; v < 16; ++v) {
-        const int m = m0 + (BM / WM) * wm + 32 * i + 8 * (v >> 2) + 4 * (lane >> 5) + (v & 3);
+        const int m = mb + 8 * (v >> 2) + (v & 3);
         if (m < M) {
-          const float o = rs ? acc[i][j][v] * rs[m] : acc[i][j][v];  // (row scale: an exact power of two)
+          const float o = acc[i][j][v] * rsv[v];
           if constexpr (CBF16)
             reinterpret_cast<uint16_t *>(c)[(size_t)m * N + n] = f32_to_bf16_rne(o);
           else
@@ -664,6 +708,7 @@ k_gemm_rb(const uint8_t *__restrict__ w, uint32_t sc_off, const _Float16 *__rest
         }
       }
     }
+  }
 }
 
 // Activations -> fp16 [M][ldo] (ldo >= K, columns K..ldo-1 zero), one
@@ -700,24 +745,51 @@ GQ_DEV void load8_f32(const void *a, int a_dtype, size_t off, float (&v)[8]) {
   }
 }
 
-__global__ void __launch_bounds__(256) k_a_to_f16(const void *__restrict__ a, int a_dtype, _Float16 *__restrict__ o,
-                                                  float *__restrict__ rs, int K, int ldo, int q4perm) {
-  __shared__ float wmax[4];
+constexpr int kConvThreads = 512, kConvRuns = 8;  // a row of up to 32768 elements stays in registers
+
+GQ_DEV gq_half8 conv8(const float (&v)[8], float f, int q4perm) {
+  constexpr int perm[8] = {0, 2, 4, 6, 1, 3, 5, 7};
+  gq_half8 h;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    const float x = q4perm ? ((e & 2) ? v[perm[e]] * 0.0625f : v[perm[e]]) : v[e];
+    h[e] = (_Float16)(x * f);
+  }
+  return h;
+}
+
+__global__ void __launch_bounds__(kConvThreads) k_a_to_f16(const void *__restrict__ a, int a_dtype,
+                                                           _Float16 *__restrict__ o, float *__restrict__ rs, int K,
+                                                           int ldo, int q4perm) {
+  __shared__ float wmax[kConvThreads / 64];
   const size_t m = blockIdx.x;
   const int tid = threadIdx.x;
+  constexpr int SPAN = 8 * kConvThreads * kConvRuns;  // elements held in registers
   // K % 8 == 0 (host-checked), so a run of 8 is all inside or all past K
+  float v[kConvRuns][8];
   float amax = 0.f;
-  for (int k0 = 8 * tid; k0 < K; k0 += 2048) {
-    float v[8];
-    load8_f32(a, a_dtype, m * K + k0, v);
 #pragma unroll
-    for (int q = 0; q < 8; ++q) amax = fmaxf(amax, fabsf(v[q]));
+  for (int r = 0; r < kConvRuns; ++r) {
+    const int k0 = 8 * (tid + kConvThreads * r);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) v[r][e] = 0.f;
+    if (k0 < K) load8_f32(a, a_dtype, m * K + k0, v[r]);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) amax = fmaxf(amax, fabsf(v[r][e]));
+  }
+  for (int k0 = SPAN + 8 * tid; k0 < K; k0 += 8 * kConvThreads) {  // (rows longer than SPAN)
+    float u[8];
+    load8_f32(a, a_dtype, m * K + k0, u);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) amax = fmaxf(amax, fabsf(u[e]));
   }
 #pragma unroll
   for (int o2 = 32; o2 > 0; o2 >>= 1) amax = fmaxf(amax, __shfl_xor(amax, o2, 64));
   if ((tid & 63) == 0) wmax[tid >> 6] = amax;
   __syncthreads();
-  amax = fmaxf(fmaxf(wmax[0], wmax[1]), fmaxf(wmax[2], wmax[3]));
+  amax = wmax[0];
+#pragma unroll
+  for (int w = 1; w < kConvThreads / 64; ++w) amax = fmaxf(amax, wmax[w]);
   // s = 14 - floor(log2(amax)) from the exponent field (0 for a zero row,
   // Inf / NaN; clamped so 2^s and 2^-s stay normal floats)
   const uint32_t eb = (__float_as_uint(amax) >> 23) & 0xFFu;
@@ -725,17 +797,15 @@ __global__ void __launch_bounds__(256) k_a_to_f16(const void *__restrict__ a, in
   sh = sh < -100 ? -100 : sh > 100 ? 100 : sh;
   const float f = __uint_as_float((uint32_t)(127 + sh) << 23);
   if (tid == 0) rs[m] = __uint_as_float((uint32_t)(127 - sh) << 23);
-  constexpr int perm[8] = {0, 2, 4, 6, 1, 3, 5, 7};
-  for (int k0 = 8 * tid; k0 < ldo; k0 += 2048) {
-    float v[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-    if (k0 < K) load8_f32(a, a_dtype, m * K + k0, v);
-    gq_half8 h;
 #pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      const float x = q4perm ? ((e & 2) ? v[perm[e]] * 0.0625f : v[perm[e]]) : v[e];
-      h[e] = (_Float16)(x * f);
-    }
-    *reinterpret_cast<gq_half8 *>(o + m * ldo + k0) = h;
+  for (int r = 0; r < kConvRuns; ++r) {
+    const int k0 = 8 * (tid + kConvThreads * r);
+    if (k0 < ldo) *reinterpret_cast<gq_half8 *>(o + m * ldo + k0) = conv8(v[r], f, q4perm);
+  }
+  for (int k0 = SPAN + 8 * tid; k0 < ldo; k0 += 8 * kConvThreads) {
+    float u[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+    if (k0 < K) load8_f32(a, a_dtype, m * K + k0, u);
+    *reinterpret_cast<gq_half8 *>(o + m * ldo + k0) = conv8(u, f, q4perm);
   }
 }
 
@@ -828,9 +898,10 @@ int launch_gemm(const void *packed, const _Float16 *a16, int lda, void *c, const
 extern "C" size_t gq_gemm_workspace_bytes(int fmt, size_t M, size_t K) {
   // activations are first written as fp16 [M][padded K (+ 8 for the skinny
   // kernel)] unless they are fp16 of the padded width already (tiled kernel)
-  // fp16 A, then the M row scales
+  // fp16 A, then the M row scales (padded by one tile: the GEMM epilogues read
+  // them four rows at a time)
   if (!gq_fmt_valid(fmt) || M > GQ_MAX_DIM || K > GQ_MAX_DIM) return 0;
-  return gq_align256(M * (gq_kpad(fmt, K) + 8) * 2) + gq_align256(M * 4);
+  return gq_align256(M * (gq_kpad(fmt, K) + 8) * 2) + gq_align256((M + 256) * 4);
 }
 
 extern "C" int gq_gemm(int fmt, const void *packed, const void *a, int a_dtype, void *c, int c_dtype, size_t M,
@@ -869,7 +940,7 @@ extern "C" int gq_gemm(int fmt, const void *packed, const void *a, int a_dtype, 
     GQ_CHECK(ws_bytes >= need, GQ_ERR_WORKSPACE);
     const int q4 = fmt == GQ_FMT_Q4_0 || gq_fmt_is_q4k(fmt);
     float *rs = (float *)((uint8_t *)ws + gq_align256(M * ldo * 2));
-    hipLaunchKernelGGL(k_a_to_f16, dim3((unsigned)M), dim3(256), 0, s, a, a_dtype, (_Float16 *)ws, rs, (int)K,
+    hipLaunchKernelGGL(k_a_to_f16, dim3((unsigned)M), dim3(kConvThreads), 0, s, a, a_dtype, (_Float16 *)ws, rs, (int)K,
                        (int)ldo, q4);
     GQ_TRY(gq_last_launch());
     return gq_launch_gemm_skinny(fmt, packed, (const _Float16 *)ws, (int)ldo, c, rs, c_dtype == GQ_DT_BF16, (int)M, (int)N,
@@ -887,7 +958,7 @@ extern "C" int gq_gemm(int fmt, const void *packed, const void *a, int a_dtype, 
     }
     GQ_CHECK(ws_bytes >= need, GQ_ERR_WORKSPACE);
     float *rsw = (float *)((uint8_t *)ws + gq_align256(M * Kp * 2));
-    hipLaunchKernelGGL(k_a_to_f16, dim3((unsigned)M), dim3(256), 0, s, a, a_dtype, (_Float16 *)ws, rsw, (int)K,
+    hipLaunchKernelGGL(k_a_to_f16, dim3((unsigned)M), dim3(kConvThreads), 0, s, a, a_dtype, (_Float16 *)ws, rsw, (int)K,
                        (int)Kp, 0);
     GQ_TRY(gq_last_launch());
     a16 = (const _Float16 *)ws;

@@ -677,11 +677,13 @@ __global__ void __launch_bounds__(64 * KW) k_gemm_sk(const uint8_t *__restrict__
     const int t0 = (int)blockIdx.x * CT + ct;
     const int col = t0 * 16 + r;
     if (t0 >= ntiles || col >= N) continue;
+    // row scales of the A conversion (powers of two; the buffer is padded past M)
+    const gq_f4 rsv = rs ? *reinterpret_cast<const gq_f4 *>(rs + m0 + 16 * mt + 4 * g) : gq_f4{1.f, 1.f, 1.f, 1.f};
 #pragma unroll
     for (int v = 0; v < 4; ++v) {
       const int row = m0 + 16 * mt + 4 * g + v;
       if (row >= M) continue;
-      const float o = rs ? sum[v] * rs[row] : sum[v];  // (row scale of the A conversion: a power of two)
+      const float o = sum[v] * rsv[v];
       if constexpr (CBF16) {
         uint32_t u = __float_as_uint(o);
         uint16_t hb;
