@@ -27,6 +27,7 @@
 //    from that XCD's L2.
 #include <stdlib.h>
 
+#include <mutex>
 #include <type_traits>
 
 #include "gq_internal.h"
@@ -970,4 +971,42 @@ extern "C" int gq_gemm(int fmt, const void *packed, const void *a, int a_dtype, 
   case GQ_FMT_Q8_0: return launch_gemm<GQ_FMT_Q8_0>(packed, a16, lda, c, rs, c_dtype, (int)M, (int)N, (int)K, s);
   default: return launch_gemm<GQ_FMT_Q4_K>(packed, a16, lda, c, rs, c_dtype, (int)M, (int)N, (int)K, s);
   }
+}
+
+// ---- allocation-free form of gq_gemm ------------------------------------------
+// The activation conversion (fp16 A and its row scales) lives in a file-scope
+// device array instead of a workspace: one copy per GPU, held until the process
+// ends.  Host code never passes the array's name to a kernel (on the host it is
+// only a stand-in for the symbol): its device address is looked up once per
+// device with hipGetSymbolAddress, with that device current, and kept.
+namespace {
+constexpr size_t kGemmScratchBytes = (size_t)64 << 20;
+constexpr int kMaxDevices = 64;
+__device__ __align__(256) unsigned char scratch[kGemmScratchBytes];
+std::mutex g_scratch_mutex;
+void *g_scratch_ptr[kMaxDevices];
+}  // namespace
+
+extern "C" size_t gq_gemm_static_max_bytes(void) { return kGemmScratchBytes; }
+
+extern "C" int gq_gemm_static(int fmt, const void *packed, const void *a, int a_dtype, void *c, int c_dtype, size_t M,
+                              size_t N, size_t K, void *stream) {
+  GQ_TRY(gq_check_shape(fmt, N, K));
+  GQ_CHECK(M <= GQ_MAX_DIM, GQ_ERR_INVALID_ARGS);
+  const size_t need = gq_gemm_workspace_bytes(fmt, M, K);
+  GQ_CHECK(need <= kGemmScratchBytes, GQ_ERR_WORKSPACE);  // M * (K + 264) * 2 + 4 (M + 256) bytes, rounded
+  int dev = 0;
+  GQ_TRY(gq_hip_status(hipGetDevice(&dev)));
+  GQ_CHECK(dev >= 0 && dev < kMaxDevices, GQ_ERR_NO_DEVICE);
+  void *ptr = nullptr;
+  {
+    std::lock_guard<std::mutex> lock(g_scratch_mutex);
+    if (!g_scratch_ptr[dev]) {
+      void *p = nullptr;
+      GQ_TRY(gq_hip_status(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch))));
+      g_scratch_ptr[dev] = p;
+    }
+    ptr = g_scratch_ptr[dev];
+  }
+  return gq_gemm(fmt, packed, a, a_dtype, c, c_dtype, M, N, K, ptr, kGemmScratchBytes, stream);
 }

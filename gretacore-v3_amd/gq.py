@@ -69,6 +69,9 @@ _SIGS = {
     "gq_requant_int4": (ctypes.c_int, [_vp, _c_size, _vp, _vp, _vp]),
     "gq_head_scales": (ctypes.c_int, [_vp, _c_size, ctypes.c_uint32, ctypes.c_uint32, ctypes.c_uint32, _vp, _vp]),
     "gq_split_q8_0": (ctypes.c_int, [_vp, _c_size, _vp, _vp, _vp]),
+    "gq_gemm_static_max_bytes": (_c_size, []),
+    "gq_gemm_static": (ctypes.c_int, [ctypes.c_int, _vp, _vp, ctypes.c_int, _vp, ctypes.c_int, _c_size, _c_size,
+                                      _c_size, _vp]),
     "gq_probe_read": (ctypes.c_int, [_vp, _c_size, ctypes.c_int, ctypes.c_int, _vp, _vp]),
     "gq_probe_empty": (ctypes.c_int, [ctypes.c_int, ctypes.c_int, _vp]),
     "gq_launch_gemm_mfma_int8_wt_fp32_acc32": (

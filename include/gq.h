@@ -170,6 +170,18 @@ size_t gq_gemm_workspace_bytes(int fmt, size_t M, size_t K);
 int gq_gemm(int fmt, const void *d_packed, const void *d_a, int a_dtype, void *d_c, int c_dtype, size_t M,
             size_t N, size_t K, void *d_workspace, size_t workspace_bytes, void *stream);
 
+/* gq_gemm without a workspace and without any allocation: no counterpart in
+ * the reference; for callers that cannot allocate device memory (code under
+ * HIP graph capture, serving loops, harnesses that forbid hipMalloc).  The
+ * activation conversion uses a library-owned device array of
+ * gq_gemm_static_max_bytes() (64 MiB) per GPU, held until the process ends;
+ * shapes whose conversion needs more (gq_gemm_workspace_bytes(fmt, M, K) >
+ * that) return GQ_ERR_WORKSPACE.  Every call on one GPU shares that array:
+ * calls that overlap on one GPU (other streams, other threads) race. */
+size_t gq_gemm_static_max_bytes(void);
+int gq_gemm_static(int fmt, const void *d_packed, const void *d_a, int a_dtype, void *d_c, int c_dtype, size_t M,
+                   size_t N, size_t K, void *stream);
+
 /* Q8_0 x int8 activations (int8 MFMA): activations quantized per 32-block with
  * the reference's INT8 rule (d = amax/127, q = round(a / d)). */
 int gq_quantize_act_q8(const void *d_a, int a_dtype, size_t M, size_t K, int8_t *d_q, float *d_d,
