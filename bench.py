@@ -182,6 +182,7 @@ def bench_compat(dev, m, n=14336, k=4096):
 def bench_decode_step(dev, steps, warmup):
     """Config 5: 32-layer Llama-3-8B-shaped decode step, Q4_K projections and a
     Q8_0 lm_head: 7 GEMVs per layer + lm_head = 225 single-kernel GEMVs."""
+    import numpy as np
     import torch
 
     import gq
@@ -236,17 +237,54 @@ def bench_decode_step(dev, steps, warmup):
             gq.gemv(Q4K, L["down"], xs[14336], 4096, 14336, y=ys[4096])
         gq.gemv(Q80, lm_packed, xs[4096], 128256, 4096, y=ys[128256])
 
+    # the same projections as one persistent launch per step (gq_gemv_chain):
+    # the real data flow of a decode step (RMSNorm, GQA read of v at one
+    # cached position, residuals, SwiGLU), then the lm_head
+    rng = np.random.default_rng(0)
+    dim, ffd = 4096, 14336
+    hbuf = [torch.from_numpy(O.gen_x(1, dim, seed=3)[0]).to(dev), torch.empty(dim, device=dev)]
+    cb = {"h1": torch.empty(dim, device=dev), "q": torch.empty(dim, device=dev),
+          "k": torch.empty(1024, device=dev), "v": torch.empty(1024, device=dev), "act": torch.empty(ffd, device=dev)}
+    norms = [(torch.from_numpy((0.5 + rng.random(dim)).astype(np.float32)).to(dev),
+              torch.from_numpy((0.5 + rng.random(dim)).astype(np.float32)).to(dev)) for _ in layers]
+    cops = []
+    for l, Lw in enumerate(layers):
+        h_in, h_out = hbuf[l % 2], hbuf[(l + 1) % 2]
+        an, fn = norms[l]
+        prev = [len(cops) - 1] if cops else []
+        i0 = len(cops)
+        for nm, n in (("q", dim), ("k", 1024), ("v", 1024)):
+            cops.append({"w": Lw[nm], "x": h_in, "gamma": an, "y": cb[nm], "N": n, "K": dim, "deps": prev})
+        cops.append({"w": Lw["o"], "x": cb["v"], "x_head_dim": 128, "x_group": 4, "resid": h_in, "y": cb["h1"],
+                     "N": dim, "K": dim, "deps": [i0, i0 + 1, i0 + 2]})
+        cops.append({"w": Lw["gate"], "w_up": Lw["up"], "x": cb["h1"], "gamma": fn, "y": cb["act"], "N": ffd,
+                     "K": dim, "deps": [i0 + 3]})
+        cops.append({"w": Lw["down"], "x": cb["act"], "resid": cb["h1"], "y": h_out, "N": dim, "K": ffd,
+                     "deps": [i0 + 4]})
+    chain = gq.Chain(Q4K, cops, dev)
+    fnorm = torch.from_numpy((0.5 + rng.random(dim)).astype(np.float32)).to(dev)
+
+    def one_step_chain(_i):
+        chain.run()
+        gq.gemv_multi(Q80, [(lm_packed, 128256)], hbuf[len(layers) % 2], 4096, gamma=fnorm, ys=[ys[128256]])
+
     t_eager = time_steps(one_step, 3, 1)
     t_graph = graph_steps(one_step, 4, 1)
     t_grouped = graph_steps(one_step_grouped, 4, 1)
     t_fused = graph_steps(one_step_fused, 4, 1)
+    t_chain = graph_steps(one_step_chain, 4, 1)
+    chain_err = chain.error()
     out = {"weight_bytes": wbytes, "gemv_launches": 225, "eager_ms": t_eager * 1e3, "graph_ms": t_graph * 1e3,
            "graph_GBps": wbytes / t_graph / 1e9, "graph_pct_peak": 100.0 * wbytes / t_graph / 1e9 / HBM_PEAK_GBS,
            "projection_steps_per_s": 1.0 / t_graph,
            "grouped_launches": 129, "grouped_graph_ms": t_grouped * 1e3,
            "grouped_GBps": wbytes / t_grouped / 1e9,
            "grouped_pct_peak": 100.0 * wbytes / t_grouped / 1e9 / HBM_PEAK_GBS,
-           "fused_norm_swiglu_graph_ms": t_fused * 1e3}
+           "fused_norm_swiglu_graph_ms": t_fused * 1e3,
+           "chain_graph_ms": t_chain * 1e3, "chain_launches": 2, "chain_wait_error": chain_err,
+           "chain_note": "one persistent launch for the 32 layers (real data flow: RMSNorm, GQA read, residuals, "
+                         "SwiGLU) + the lm_head; latency-bound on its 128 dependent op boundaries"}
+    del chain
     del layers, lm_packed
     torch.cuda.empty_cache()
     return out

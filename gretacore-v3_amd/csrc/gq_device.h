@@ -46,6 +46,15 @@ GQ_DEV gq_f16v gq_mfma32(const gq_half8 &a, const gq_half8 &b, const gq_f16v &c)
 GQ_DEV gq_u4 gq_ld16(const void *p) { return *reinterpret_cast<const gq_u4 *>(p); }
 // Streaming loads for data read exactly once (weights): non-temporal, so they
 // do not evict reusable lines from L2 / the Infinity Cache.
-GQ_DEV gq_u4 gq_ld16_nt(const void *p) { return __builtin_nontemporal_load(reinterpret_cast<const gq_u4 *>(p)); }
-GQ_DEV uint32_t gq_ld4_nt(const void *p) { return __builtin_nontemporal_load(reinterpret_cast<const uint32_t *>(p)); }
+// Streaming loads of device memory.  The pointer is cast to the global
+// address space: a pointer the compiler cannot trace to a kernel argument
+// (one read from a table in memory) would otherwise become a flat access,
+// which also counts against the LDS counter and defeats load pipelining.
+#define GQ_GLOBAL __attribute__((address_space(1)))
+GQ_DEV gq_u4 gq_ld16_nt(const void *p) {
+  return __builtin_nontemporal_load((const GQ_GLOBAL gq_u4 *)p);
+}
+GQ_DEV uint32_t gq_ld4_nt(const void *p) {
+  return __builtin_nontemporal_load((const GQ_GLOBAL uint32_t *)p);
+}
 GQ_DEV gq_u2 gq_ld8(const void *p) { return *reinterpret_cast<const gq_u2 *>(p); }

@@ -109,6 +109,23 @@ _SIGS_GGUF = {
 }
 _SIGS.update(_SIGS_GGUF)
 
+
+class ChainOp(ctypes.Structure):
+    """gq_chain_op (include/gq_chain.h)."""
+    _fields_ = [("w", _vp), ("w_up", _vp), ("x", _vp), ("gamma", _vp), ("resid", _vp), ("y", _vp),
+                ("N", ctypes.c_uint32), ("K", ctypes.c_uint32), ("k_offset", ctypes.c_uint32),
+                ("k_total", ctypes.c_uint32), ("x_head_dim", ctypes.c_uint32), ("x_group", ctypes.c_uint32),
+                ("dep", ctypes.c_int32 * 3)]
+
+
+# include/gq_chain.h
+_SIGS.update({
+    "gq_gemv_chain_workspace_bytes": (ctypes.c_int, [ctypes.c_int, _vp, ctypes.c_int, ctypes.POINTER(_c_size)]),
+    "gq_gemv_chain_plan": (ctypes.c_int, [ctypes.c_int, _vp, ctypes.c_int, ctypes.c_float, _vp, _c_size]),
+    "gq_gemv_chain_run": (ctypes.c_int, [_vp, _vp]),
+    "gq_gemv_chain_error": (ctypes.c_int, [_vp, ctypes.POINTER(ctypes.c_int)]),
+})
+
 _lib = None
 
 
@@ -362,6 +379,54 @@ def probe_read(src, wgs: int, waves_per_wg: int, out, stream=None):
 def probe_empty(wgs: int, waves_per_wg: int, stream=None):
     """Calibration: the same grid with no work."""
     check(load().gq_probe_empty(wgs, waves_per_wg, _stream(stream)), "gq_probe_empty")
+
+
+def _chain_ops(ops):
+    arr = (ChainOp * len(ops))()
+    for i, o in enumerate(ops):
+        a = arr[i]
+        adr = lambda t: t.data_ptr() if t is not None else None  # noqa: E731
+        a.w, a.w_up = adr(o["w"]), adr(o.get("w_up"))
+        a.x, a.gamma, a.resid, a.y = adr(o["x"]), adr(o.get("gamma")), adr(o.get("resid")), adr(o["y"])
+        a.N, a.K = o["N"], o["K"]
+        a.k_offset, a.k_total = o.get("k_offset", 0), o.get("k_total", 0)
+        a.x_head_dim, a.x_group = o.get("x_head_dim", 0), o.get("x_group", 0)
+        deps = list(o.get("deps", [])) + [-1] * 3
+        for q in range(3):
+            a.dep[q] = deps[q]
+    return arr
+
+
+def chain_workspace_bytes(fmt: int, ops) -> int:
+    """Workspace bytes of a chain plan (host only).  ops: dicts with keys w,
+    x, y, N, K and optionally w_up, gamma, resid, k_offset, k_total,
+    x_head_dim, x_group, deps (see include/gq_chain.h)."""
+    arr = _chain_ops(ops)
+    n = _c_size(0)
+    check(load().gq_gemv_chain_workspace_bytes(fmt, ctypes.cast(arr, _vp), len(ops), ctypes.byref(n)),
+          "gq_gemv_chain_workspace_bytes")
+    return n.value
+
+
+class Chain:
+    """A planned chain of decode GEMVs (gq_gemv_chain_plan); run() launches it."""
+
+    def __init__(self, fmt: int, ops, device, eps: float = 1e-5):
+        import torch
+        self.ops = ops  # (keeps the tensors alive)
+        arr = _chain_ops(ops)
+        nbytes = chain_workspace_bytes(fmt, ops)
+        self.ws = torch.empty(nbytes, dtype=torch.uint8, device=device)
+        check(load().gq_gemv_chain_plan(fmt, ctypes.cast(arr, _vp), len(ops), eps, _ptr(self.ws), nbytes),
+              "gq_gemv_chain_plan")
+
+    def run(self, stream=None):
+        check(load().gq_gemv_chain_run(_ptr(self.ws), _stream(stream)), "gq_gemv_chain_run")
+
+    def error(self) -> int:
+        e = ctypes.c_int(0)
+        check(load().gq_gemv_chain_error(_ptr(self.ws), ctypes.byref(e)), "gq_gemv_chain_error")
+        return e.value
 
 
 def gemv_prep(fmt: int, x, k: int, workspace: Workspace, stream=None):
