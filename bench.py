@@ -159,6 +159,32 @@ def bench_gemm(fmt, m, n, k, steps, warmup, dev, out_dtype="f32"):
             "rel_l2": err}
 
 
+def bench_gemm_q8_i8(m, n, k, steps, dev):
+    """The int8 route for Q8_0: activations quantized per 32-block
+    (gq_quantize_act_q8), then one v_mfma_i32_32x32x32_i8 per block with the
+    two block scales applied in fp32 (gq_gemm_q8_i8).  TOPS of the GEMM
+    kernel's step (the quantization is a separate launch, timed with it)."""
+    import torch
+
+    import gq
+    import oracle as O
+    w = O.gen_weights(O.Q8_0, n, k, seed=1004)
+    packed = gq.repack(O.Q8_0, torch.from_numpy(w).to(dev), n, k)
+    a = torch.randn(m, k, generator=torch.Generator().manual_seed(2004)).to(torch.bfloat16).to(dev)
+    qa, da = gq.quantize_act_q8(a)
+    c = gq.gemm_q8_i8(packed, qa, da, n)
+    rows = list(range(0, m, max(1, m // 16)))
+    err = O.rel_l2(c[rows].cpu().numpy(), O.gemm_q8_i8(w, qa[rows].cpu().numpy(), da[rows].cpu().numpy(), n))
+
+    def run(i):
+        gq.quantize_act_q8(a)
+        gq.gemm_q8_i8(packed, qa, da, n, c=c)
+    t = graph_steps(run, max(4, steps // 8), 2)
+    ops = 2.0 * m * n * k
+    return {"step_us": t * 1e6, "TOPS": ops / t / 1e12, "pct_peak_i8": 100.0 * ops / t / 1e12 / MFMA_I8_PEAK_TOPS,
+            "rel_l2_vs_exact_integer_oracle": err}
+
+
 def bench_compat(dev, m, n=14336, k=4096):
     """The reference's INT4 / INT8 weight-only launchers (requantized weight
     formats of load_tensor_int4/int8, fp32 A): one call per step."""
@@ -519,7 +545,7 @@ def main():
             torch.bitwise_not(src, out=dst)  # reads 64 MiB, writes 64 MiB
         torch.cuda.synchronize()
         del src, dst
-    if args.only and args.only.startswith("gemm_"):
+    if args.only and args.only.startswith("gemm_") and not args.only.startswith("gemm_q8_0_i8_"):
         # gemm_<fmt>_m<M>_<N>x<K>, e.g. gemm_q4_0_m64_4096x4096
         try:
             fname, rest = args.only[5:].rsplit("_m", 1)
@@ -531,6 +557,17 @@ def main():
             print(f"--only: cannot parse {args.only} (gemm_<q4_0|q8_0|q4_k|q6_k>_m<M>_<N>x<K>)", file=sys.stderr)
             sys.exit(2)
         print(json.dumps({args.only: bench_gemm(fmt, m, n, k, steps, warmup, dev)}), flush=True)
+        return
+    if args.only and args.only.startswith("gemm_q8_0_i8_m"):
+        # gemm_q8_0_i8_m<M>_<N>x<K>
+        try:
+            m_s, nk = args.only[len("gemm_q8_0_i8_m"):].split("_", 1)
+            n_s, k_s = nk.split("x")
+            m, n, k = int(m_s), int(n_s), int(k_s)
+        except ValueError:
+            print(f"--only: cannot parse {args.only} (gemm_q8_0_i8_m<M>_<N>x<K>)", file=sys.stderr)
+            sys.exit(2)
+        print(json.dumps({args.only: bench_gemm_q8_i8(m, n, k, steps, dev)}), flush=True)
         return
     if args.only == "read_ceiling":
         print(json.dumps({args.only: bench_read_ceiling(dev, steps, warmup)}), flush=True)
@@ -571,6 +608,9 @@ def main():
                     log(f"[bench] {name}")
                     extra[name] = bench_gemm(fmt, m, n, 4096, steps, warmup, dev)
                     torch.cuda.empty_cache()
+        log("[bench] int8 route for Q8_0 (per-32 activation quantization + int8 MFMA)")
+        extra["gemm_q8_0_i8_m2048_14336x4096"] = bench_gemm_q8_i8(2048, 14336, 4096, steps, dev)
+        torch.cuda.empty_cache()
         for m in (1, 512):
             log(f"[bench] reference INT4/INT8 launchers m={m}")
             extra[f"compat_launchers_14336x4096_m{m}"] = bench_compat(dev, m)
