@@ -844,9 +844,13 @@ int launch_rb(const void *packed, const _Float16 *a16, int lda, void *c, const f
 }
 
 // Kernel and tile shape (measured on MI355X, M = 64 .. 2048 x N = 4096 / 14336):
-//   0: register-B kernel, 256 x 256 (448 workgroups at 2048 x 14336)
-//   3: LDS-B kernel, 256 x 256 (Q4_K at that size: its per-fragment
-//      sub-block decoding costs more than the LDS round trip saves)
+//  12: register-B kernel, 256 x 256 on 8 waves of 256 x 32 (448 workgroups at
+//      2048 x 14336): each wave dequantizes its B fragments for all 256 rows,
+//      so no two waves convert the same weights (twice the activation-fragment
+//      LDS reads of the 2 x 4 wave grid, half its dequantization VALU);
+//      2-8 % faster than 0 (2 x 4 waves) and 3 (LDS-B) for every format
+//   0: register-B kernel, 256 x 256, 2 x 4 waves of 128 x 64
+//   3: LDS-B kernel, 256 x 256
 //   4: register-B, 256 x 128, for >= 192 workgroups
 //   6: register-B, 128 x 128, for >= 192 workgroups (1024 x 4096, 256 x 14336)
 //   9: register-B, 128 x 64 (4 waves), for >= 192 workgroups (512 x 4096:
@@ -854,13 +858,14 @@ int launch_rb(const void *packed, const _Float16 *a16, int lda, void *c, const f
 //  11: register-B, 64 x 64 (4 waves), smaller problems (M <= 256 at N = 4096:
 //      40-43 us vs 49-53)
 // The register-B kernel runs with pipeline depth 4 (1-3 % faster than 2 on
-// the shapes measured), except 256 x 256: depth 2 (at 4 the Q8_0 and Q4_K
-// instances spill registers; Q4_0 gains nothing).  1, 2 (LDS-B 256 x 128, 128 x 128) and 5, 7, 8, 10
-// (other register-B shapes) are kept for tuning through GQ_GEMM_TILE.
+// the shapes measured), except 256 x 256: depth 3 on the 1 x 8 grid, 2 on the
+// 2 x 4 grid (at 4 its Q8_0 and Q4_K instances spill registers).  1, 2 (LDS-B
+// 256 x 128, 128 x 128) and 5, 7, 8, 10 (other register-B shapes) are kept for
+// tuning through GQ_GEMM_TILE.
 int pick_tile(int fmt, int M, int N) {
   auto wgs = [&](int bm, int bn) { return (long)((M + bm - 1) / bm) * ((N + bn - 1) / bn); };
   if (const char *e = getenv("GQ_GEMM_TILE")) return atoi(e);
-  if (wgs(256, 256) >= 384) return fmt == GQ_FMT_Q4_K ? 3 : 0;
+  if (wgs(256, 256) >= 384) return 12;
   if (wgs(256, 128) >= 192) return 4;
   if (wgs(128, 128) >= 192) return 6;
   if (wgs(128, 64) >= 192) return 9;
@@ -880,6 +885,7 @@ int launch_fmt(const void *packed, const _Float16 *a16, int lda, void *c, const 
   case 9: return launch_rb<FMT, CBF16, 128, 64, 2, 2>(packed, a16, lda, c, rs, M, N, K, s);
   case 10: return launch_rb<FMT, CBF16, 64, 128, 2, 4>(packed, a16, lda, c, rs, M, N, K, s);
   case 11: return launch_rb<FMT, CBF16, 64, 64, 2, 2>(packed, a16, lda, c, rs, M, N, K, s);
+  case 12: return launch_rb<FMT, CBF16, 256, 256, 1, 8>(packed, a16, lda, c, rs, M, N, K, s, 3);
   default: return launch_rb<FMT, CBF16, 128, 128, 2, 4>(packed, a16, lda, c, rs, M, N, K, s);
   case 3: return launch_cfg<FMT, CBF16, 256, 256>(packed, a16, lda, c, rs, M, N, K, s);
   case 1: return launch_cfg<FMT, CBF16, 256, 128>(packed, a16, lda, c, rs, M, N, K, s);
