@@ -4,38 +4,53 @@
 // (BlockScheduler: q, k, v, o, gate, up, down per layer,
 // block_scheduler.cpp:1831-1894, 2769-2775, 2967-3003), and so do gq_gemv /
 // gq_gemv_multi / gq_gemv_swiglu: each launch pays the dispatch gap between
-// dependent kernels (~1.8 us on MI355X, as long as streaming 14 MB) plus its
+// dependent kernels (~1.6 us on MI355X, as long as streaming 12 MB) plus its
 // own ramp and tail.  Weight streaming does not depend on the activations, so
 // here one launch runs an ordered list of GEMV "ops" (include/gq_chain.h) and
-// an op's weight loads are issued before its inputs exist.
+// the weights of later ops are in flight while an op waits for its inputs.
 //
 // Design (batch 1, int8 matrix cores as gq_gemv.hip's kernel):
 //  * Persistent grid, one workgroup per CU (all resident at once; the host
-//    checks the occupancy): 8 compute waves that split K, and one control
-//    wave.  The ops are cut into units (NACC 16-row output tiles over the op's
-//    whole K), numbered in op order; workgroup g takes units g, g + G, ...
-//  * A compute wave holds two register sets of weight chunks: while it
-//    computes unit j it already has unit j + G's loads in flight, which so
-//    also cover the wait for that unit's inputs.
-//  * The control wave never has weight loads in flight, so its waits are
-//    short: it polls the dependencies, copies the op's x into LDS (LDS DMA,
-//    with the GQA map applied to the addresses), and finishes every unit: the
-//    K-split reduction, RMS factor, residual or SwiGLU, the stores, a release
-//    fence and the op's counter.  It does this for unit j while the compute
-//    waves already consume unit j + G (the partial sums are double-buffered).
-//  * The activations are split into int8 limbs once per op and wave (every
-//    unit of an op reads the same x), not once per unit.
-//  * Dependencies: a unit whose op names op d waits until d's counter
-//    reaches d's unit count, then acquires (invalidating this CU's caches, so
-//    the other workgroups' outputs are read from memory).  Units are taken in
-//    op order, ops depend only on earlier ops and all workgroups are
-//    resident, so the waits end; each is also bounded: past the spin limit it
-//    sets an error flag and every later wait returns at once, so the kernel
-//    always drains.
+//    checks the occupancy): kCW = 4 compute waves, one per SIMD, that split
+//    K, and one control wave.  An op is cut into units -- one 16-row output
+//    tile over the op's K (SwiGLU: the same tile of gate and of up) --
+//    numbered in op order, and workgroup g takes units g, g + G, ..., so the
+//    units of every op are spread over all CUs.
+//  * A compute wave walks one stream of chunk loads: its K slice of every
+//    unit of its workgroup, in order.  A register ring keeps NSLOT chunks in
+//    flight: when the wave consumes stream position p it requests position
+//    p + NSLOT, whichever unit or op that is.  The ring is indexed by
+//    compile-time slot numbers (the loop body is unrolled NSLOT times) and
+//    every request is unconditional (past the end it re-reads a valid chunk),
+//    so the waits on the loads stay in issue order.
+//  * The control wave never holds weight loads, so its waits are short.  Per
+//    activation stage (ops that read the same input: q, k and v of a layer)
+//    it waits until the ops the stage depends on are complete, copies x into
+//    LDS (LDS DMA, with the GQA map applied to the addresses) and the RMSNorm
+//    weight, computes 1 / rms and posts x * gamma; each compute wave then
+//    splits its K slice per 32-block into the two int8 limbs the matrix
+//    cores take (the GEMV's split).  Per unit it sums the compute waves' partial tiles, applies
+//    1 / rms, the residual or SwiGLU, and stores the rows.
+//  * Compute and control waves meet only through LDS counters: a ring of kRed
+//    partial-tile slots (arrivals / slots freed), the posted stage and the
+//    compute waves' release of the stage's x once they have converted it.  The control
+//    wave's global latencies therefore never stall the weight stream; the
+//    compute waves wait only for a stage's limbs or a free slot.
+//  * Completion of an op: the control wave stores its rows with agent-scope
+//    (write-through) stores and, when its workgroup moves to another op,
+//    waits for them (vmcnt(0)) and sets its flag for the op.  A stage whose
+//    ops name op d waits until every workgroup holding units of d has set its
+//    flag, and reads the outputs of other workgroups with agent-scope loads.  Units are taken in op
+//    order, ops depend only on earlier ops and all workgroups are resident,
+//    so the waits end; each is also bounded: past the spin limit it sets an
+//    error flag and every later wait returns at once, so the kernel always
+//    drains.
 #include <stdlib.h>
 
 #include <map>
 #include <mutex>
+#include <type_traits>
+#include <utility>
 #include <vector>
 
 #include "gq_gemv_i8.h"
@@ -43,25 +58,27 @@
 
 namespace {
 
-constexpr int kCW = 8;   // compute waves (the K split)
-constexpr int kAcc = 4;  // output tiles (accumulators) per unit at most
+constexpr int kCW = 4;              // compute waves (the K split), one per SIMD
+constexpr int kRed = 4;             // partial-tile slots between compute and control waves
+constexpr int kMaxPieceK = 16384;   // longest K of one device op (LDS holds its x and limbs)
+constexpr int kMaxGrid = 256;       // workgroups at most (one per CU); completion flags per op
 
-// chunk slots per compute wave and register set (two sets are held)
+// register ring per format: NSLOT chunks in flight per compute wave, LPC loads
+// per chunk (NSLOT * LPC <= 63, the vmcnt range)
 template <int FMT>
-struct ChainSlots;
+struct Ring;
 template <>
-struct ChainSlots<GQ_FMT_Q4_0> {
-  static constexpr int S = 8;  // 5 VGPRs each
+struct Ring<GQ_FMT_Q4_0> {
+  static constexpr int NSLOT = 20;  // 5 VGPRs per chunk
 };
 template <>
-struct ChainSlots<GQ_FMT_Q8_0> {
-  static constexpr int S = 4;  // 9 VGPRs each
+struct Ring<GQ_FMT_Q8_0> {
+  static constexpr int NSLOT = 12;  // 9 VGPRs
 };
 template <>
-struct ChainSlots<GQ_FMT_Q4_K> {
-  static constexpr int S = 4;  // 12 VGPRs each
+struct Ring<GQ_FMT_Q4_K> {
+  static constexpr int NSLOT = 12;  // 12 VGPRs
 };
-int chain_slots(int f) { return f == GQ_FMT_Q4_0 ? 8 : 4; }
 
 // Device op record (the host builds it from gq_chain_op).
 struct ChainOpD {
@@ -70,328 +87,481 @@ struct ChainOpD {
   float *y;
   uint64_t sc_off;       // scale-plane offset of the tensor (w2: same shape)
   int N, K, C, Crow;     // rows, K of this op, its chunks, chunks per row of the tensor
-  int cbase, nck;        // first chunk of the op in a row, chunks per wave (ceil(C / kCW))
-  int nacc, pair;        // accumulators per unit (SwiGLU: gate, up alternate), SwiGLU flag
-  int unit0, units;      // first unit (global numbering), unit count
+  int cbase, pair;       // first chunk of the op in a row, SwiGLU flag
+  int unit0, units;      // first unit (global numbering), unit count (= row tiles)
   int dep[3];
   int xhd, xgrp;         // GQA read of x (0: none)
-  int pad[3];
+  int stage;             // activation stage (ops of one stage read the same input)
+  int pad[4];
 };
 static_assert(sizeof(ChainOpD) == 128, "op record size");
 
+// LDS words shared by the compute and control waves of a workgroup
+struct ChainSync {
+  unsigned xready;    // activation stages posted by the control wave
+  unsigned released;  // stages whose x the compute waves have converted (kCW per stage)
+  unsigned freed;     // units whose partial-tile slot the control wave has read
+  unsigned lerr;      // a wait of this workgroup gave up
+  unsigned arrive[kRed];  // partial tiles written into each slot (kCW per use)
+};
+
 // the op table's pointers are device memory: global-address-space views of
 // them, so their accesses are global (not flat) memory instructions
+#define GQ_CONST __attribute__((address_space(4)))
 template <typename T>
 GQ_DEV const GQ_GLOBAL T *gmem(const T *p) {
   return (const GQ_GLOBAL T *)p;
 }
-template <typename T>
-GQ_DEV GQ_GLOBAL T *gmem_w(T *p) {
-  return (GQ_GLOBAL T *)p;
-}
 
 // Two ops whose inputs stage identically: same x, RMSNorm weight, GQA map and
-// K slices, and the second depends on nothing the first did not (its inputs
-// were complete when the first staged them).
-GQ_DEV bool same_input(const ChainOpD &a, const ChainOpD &b) {
+// K range, and the same dependencies (its inputs complete when the first's are).
+__host__ __device__ inline bool same_input(const ChainOpD &a, const ChainOpD &b) {
   return a.x == b.x && a.gamma == b.gamma && a.K == b.K && a.C == b.C && a.xhd == b.xhd && a.xgrp == b.xgrp &&
          a.dep[0] == b.dep[0] && a.dep[1] == b.dep[1] && a.dep[2] == b.dep[2];
 }
 
 GQ_DEV unsigned ld_agent(const unsigned *p) { return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); }
+GQ_DEV unsigned lds_ld(const unsigned *p) {
+  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+}
+GQ_DEV void lds_st(unsigned *p, unsigned v) { __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP); }
+GQ_DEV void lds_add(unsigned *p, unsigned v) {
+  __hip_atomic_fetch_add(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+}
+// LDS writes of this wave complete before what follows (no vector-memory
+// wait: the compute waves keep their weight loads in flight)
+GQ_DEV void lds_order() {
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
+  __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0)
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
+}
+
+// Waits (bounded) until the LDS word reaches v; false if it gave up or an
+// earlier wait of the workgroup did.
+GQ_DEV bool lds_wait_ge(const unsigned *p, unsigned v, ChainSync *sy, unsigned spin_limit) {
+  unsigned spins = 0;
+  while (lds_ld(p) < v) {
+    if (lds_ld(&sy->lerr) != 0u) return false;
+    if (++spins > spin_limit) {
+      lds_st(&sy->lerr, 1u);
+      return false;
+    }
+    __builtin_amdgcn_s_sleep(1);
+  }
+  return true;
+}
+
+template <typename F, int... I>
+GQ_DEV void static_for_impl(F &&f, std::integer_sequence<int, I...>) {
+  (f(std::integral_constant<int, I>{}), ...);
+}
+template <int N, typename F>
+GQ_DEV void static_for(F &&f) {
+  static_for_impl(f, std::make_integer_sequence<int, N>{});
+}
+
+// LDS layout (dynamic part): x * gamma as fp32 [kx]; per compute wave its
+// limbs: limb a [sl], limb b [sl], per 32-block float4 (s, S, s / 254, 0)
+// [sl / 32] (sl: the longest K slice of a wave); a zero region [zl]
+struct ChainLds {
+  int kx, sl, zl;
+  int xs, lw, wb, lz, bytes;
+};
+__host__ __device__ inline ChainLds chain_lds_layout(int kx, int sl, int zl) {
+  ChainLds L;
+  L.kx = kx;
+  L.sl = sl;
+  L.zl = zl;
+  L.xs = 0;
+  L.lw = L.xs + 4 * kx;
+  L.wb = 2 * sl + 16 * (sl / 32);
+  L.lz = L.lw + kCW * L.wb;
+  L.bytes = L.lz + zl;
+  return L;
+}
+
+constexpr int kXB = 16;    // float4 loads per lane in one batch of the control wave's x copy
+constexpr int kObuf = 64;  // finished rows (16-row tiles) the control wave holds before storing
 
 template <int FMT>
 __global__ void __launch_bounds__(64 * (kCW + 1), 1)
-k_chain(const ChainOpD *__restrict__ ops, int n_ops, int total, unsigned *__restrict__ done, unsigned *__restrict__ err,
-        float eps, unsigned spin_limit, int xs_bytes) {
+k_chain(const ChainOpD *__restrict__ ops_in, int n_ops, int total, unsigned *__restrict__ done, unsigned *__restrict__ err,
+        float eps, unsigned spin_limit, ChainLds LL) {
   using F = Fmt<FMT>;
-  constexpr int NS = ChainSlots<FMT>::S;
-  constexpr int LKMAX = F::CK * NS;  // a compute wave's K slice at most
-  constexpr int TPR = (LKMAX + 511) / 512;  // 8-element runs per lane
+  constexpr int NSLOT = Ring<FMT>::NSLOT;
+  // the op table does not change during the launch: read it through the
+  // constant address space, so its loads are scalar (SMEM) and never wait on
+  // the weight loads in flight
+  const GQ_CONST ChainOpD *const ops = (const GQ_CONST ChainOpD *)(ops_in);
   constexpr float OFF = (FMT == GQ_FMT_Q4_0) ? 8.f : (FMT == GQ_FMT_Q4_K) ? 1.f : 0.f;
   extern __shared__ __attribute__((aligned(16))) unsigned char gq_dyn_lds[];
-  __shared__ float red[2][kCW][kAcc][16];  // partial sums, double-buffered by unit parity
-  __shared__ float ssred[kCW];              // per-wave sums of squares of the op's x
+  __shared__ float red[kRed][kCW][2][16];  // partial tiles (gate, up) per slot and compute wave
+  __shared__ ChainSync sy;
+  __shared__ float obuf[kObuf][16];  // finished rows of the current op, not yet stored
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const bool ctl = wave == kCW;
   const int g = lane >> 4, r = lane & 15;
   const int G = (int)gridDim.x;
-  float *const xs = reinterpret_cast<float *>(gq_dyn_lds);  // the op's x (fp32)
-  const XlLayout L = xl_layout(LKMAX, 1);
-  unsigned char *const lbase = gq_dyn_lds + xs_bytes + (size_t)(ctl ? 0 : wave) * L.wave_bytes;
-  int8_t *const lm = reinterpret_cast<int8_t *>(lbase);
-  float *const lsc = reinterpret_cast<float *>(lbase + L.scl_off);
-  const int8_t *const lzero = reinterpret_cast<const int8_t *>(lbase + L.zero_off);
-  if (!ctl)
-    for (int o = 16 * lane; o < L.lk; o += 1024)  // the zero A rows, once
-      *reinterpret_cast<gq_u4 *>(lbase + L.zero_off + o) = gq_u4{0u, 0u, 0u, 0u};
-  const uint32_t qlane = 16u * (uint32_t)lane;
-  const uint32_t slane = FMT == GQ_FMT_Q4_K ? 16u * (uint32_t)r : 8u * (uint32_t)r + 4u * (uint32_t)(g >> 1);
+  float *const xs = reinterpret_cast<float *>(gq_dyn_lds + LL.xs);
+  const int8_t *const lz = reinterpret_cast<const int8_t *>(gq_dyn_lds + LL.lz);
 
-  int oi = 0;  // op of the last unit looked up (units ascend: scan forward)
-  auto op_of = [&](int u) {
-    while (oi + 1 < n_ops && u >= ops[oi + 1].unit0) ++oi;
-    return oi;
-  };
-  // Chunk slot s of unit u: accumulator a = s / nck, chunk i = s % nck of
-  // this wave's K slice.  Slots past the unit's accumulators or the slice
-  // re-read a valid chunk: the loads are unconditional.
-  auto issue = [&](int u, Chunk<FMT>(&ch)[NS]) {
-    const ChainOpD &op = ops[op_of(u)];
-    const int j = u - op.unit0;
-    const int ntiles = (int)gq_tiles(op.N);
-    const int c0 = (op.C * wave) / kCW, c1 = (op.C * (wave + 1)) / kCW;
-    const int nw = c1 - c0;
-    const int tpu = op.pair ? op.nacc >> 1 : op.nacc;
+  if (ctl) {
+    for (int o = 16 * lane; o < LL.zl; o += 1024)  // the zero A rows
+      *reinterpret_cast<gq_u4 *>(gq_dyn_lds + LL.lz + o) = gq_u4{0u, 0u, 0u, 0u};
+    if (lane == 0) {
+      sy.xready = sy.released = sy.freed = sy.lerr = 0u;
 #pragma unroll
-    for (int s = 0; s < NS; ++s) {
-      int a = s / op.nck, i = s % op.nck;
-      a = a < op.nacc ? a : op.nacc - 1;
-      i = i < nw ? i : (nw > 0 ? nw - 1 : 0);
-      const uint8_t *wm = (op.pair && (a & 1)) ? op.w2 : op.w;
-      int t = j * tpu + (op.pair ? a >> 1 : a);
-      t = t < ntiles ? t : ntiles - 1;
-      const size_t ci = (size_t)t * op.Crow + op.cbase + c0 + i;
-      load_chunk<FMT>(wm + ci * F::QB, wm + op.sc_off + ci * F::SB, qlane, slane, ch[s]);
+      for (int q = 0; q < kRed; ++q) sy.arrive[q] = 0u;
     }
-  };
+  }
+  __syncthreads();
+  if ((int)blockIdx.x >= total) return;
 
-  int cur_op = -1;
-  auto process = [&](int u, Chunk<FMT>(&cur)[NS], Chunk<FMT>(&nxt)[NS], auto parity) {
-    constexpr int P = decltype(parity)::value;
-    const int o = op_of(u);
-    const ChainOpD &op = ops[o];
-    const int j = u - op.unit0;
-    const int c0 = (op.C * wave) / kCW, c1 = (op.C * (wave + 1)) / kCW;
-    const int nw = ctl ? 0 : c1 - c0;
-    const bool norm = op.gamma != nullptr;
+  if (!ctl) {
+    // ====================== compute waves ======================================
+    const uint32_t qlane = 16u * (uint32_t)lane;
+    const uint32_t slane = FMT == GQ_FMT_Q4_K ? 16u * (uint32_t)r : 8u * (uint32_t)r + 4u * (uint32_t)(g >> 1);
+    // A operand: lane (r, g) is combination c = r >> 2 = (block h, limb l) of
+    // the batch row (r & 3 == 0), with data where its lane group covers block
+    // h of the MFMA pair, zeros otherwise (as gq_gemv.hip's kernel)
+    const int c = r >> 2, h = c >> 1, l = c & 1;
+    const bool act = ((g >> 1) == h) && (r & 3) == 0;
+    const int hp = g >> 1, lp = g & 1;
+    // this wave's limbs (its K slice of the current stage)
+    int8_t *const lw = reinterpret_cast<int8_t *>(gq_dyn_lds + LL.lw + wave * LL.wb);
+    float *const lsw = reinterpret_cast<float *>(gq_dyn_lds + LL.lw + wave * LL.wb + 2 * LL.sl);
+    const int8_t *const abase = act ? lw + (size_t)l * LL.sl + 32 * h + 16 * (g & 1) : lz;
+    const int astep = act ? 1 : 0;  // the zero rows do not move with the chunk
 
-    if (o != cur_op && (cur_op < 0 || !same_input(ops[cur_op], op))) {  // (wave-uniform)
-      // ---- a new op: its inputs, then its x -> LDS, then int8 limbs ---------
-      if (ctl) {
-        if (lane == 0) {
-          for (int q = 0; q < 3; ++q) {
-            const int d = op.dep[q];
-            if (d < 0) continue;
-            const unsigned need = (unsigned)ops[d].units;
-            unsigned spins = 0;
-            while (ld_agent(done + d) < need) {
-              if (ld_agent(err) != 0u) break;  // an earlier wait gave up: drain
-              if (++spins > spin_limit) {
-                __hip_atomic_store(err, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                break;
+    // stream cursor: unit u (>= total: past the end), its op o, entry e of E
+    struct Cur {
+      int u, o, e, E, nw, c0;
+    };
+    auto enter = [&](Cur &cu, int u) {
+      cu.u = u;
+      cu.e = 0;
+      if (u >= total) {
+        cu.E = 1;
+        return;
+      }
+      while (cu.o + 1 < n_ops && u >= ops[cu.o + 1].unit0) ++cu.o;
+      const GQ_CONST ChainOpD &op = ops[cu.o];
+      cu.c0 = (op.C * wave) / kCW;
+      cu.nw = (op.C * (wave + 1)) / kCW - cu.c0;
+      cu.E = (cu.nw > 0 ? cu.nw : 1) * (op.pair ? 2 : 1);
+    };
+    auto advance = [&](Cur &cu) {
+      if (++cu.e >= cu.E && cu.u < total) enter(cu, cu.u + G);
+    };
+    // entry e of a unit: matrix (SwiGLU: gate, up alternate) and chunk of the slice
+    auto entry = [&](const GQ_CONST ChainOpD &op, int e, int &a, int &i) {
+      a = op.pair ? (e & 1) : 0;
+      i = op.pair ? (e >> 1) : e;
+    };
+
+    Chunk<FMT> ring[NSLOT];
+    auto issue = [&](Cur &cu, Chunk<FMT> &slot) {
+      const GQ_CONST ChainOpD &op = ops[cu.o];
+      int t = 0, a = 0, i = 0;
+      if (cu.u < total) {
+        t = cu.u - op.unit0;
+        entry(op, cu.e, a, i);
+        i = i < cu.nw ? i : 0;  // (a wave without chunks re-reads chunk c0 < C)
+      }
+      const uint8_t *wm = a ? op.w2 : op.w;
+      const size_t ci = (size_t)t * (size_t)op.Crow + (size_t)(op.cbase + cu.c0 + i);
+      load_chunk<FMT>(wm + ci * F::QB, wm + op.sc_off + ci * F::SB, qlane, slane, slot);
+      advance(cu);
+    };
+
+    Cur ic, cc;
+    ic.o = cc.o = 0;
+    enter(ic, (int)blockIdx.x);
+    enter(cc, (int)blockIdx.x);
+    int stage = -1;        // stage whose limbs this wave reads
+    unsigned nstage = 0;   // stages posted that this wave has waited for
+    unsigned nunit = 0;    // units of this workgroup finished by this wave
+    float tot[2] = {0.f, 0.f};
+
+    auto consume = [&](Chunk<FMT> &slot) {
+      const GQ_CONST ChainOpD &op = ops[cc.o];
+      if (cc.e == 0) {
+        if (op.stage != stage) {  // (wave-uniform) a new stage: wait for its limbs
+          ++nstage;
+          lds_wait_ge(&sy.xready, nstage, &sy, spin_limit);
+          stage = op.stage;
+          // x * gamma of this wave's K slice -> two int8 limbs per 32-block
+          // (8 elements per lane, a quad of lanes per block); past K: zero
+          const int ls = cc.nw * F::CK, kb0 = cc.c0 * F::CK;
+          for (int kb = 0; kb < ls; kb += 512) {
+            const int kk = kb + 8 * lane, k = kb0 + kk;
+            float v[8];
+            if (kk < ls && k < op.K) {
+              const gq_f4 a0 = *reinterpret_cast<const gq_f4 *>(xs + k);
+              const gq_f4 a1 = *reinterpret_cast<const gq_f4 *>(xs + k + 4);
+#pragma unroll
+              for (int e = 0; e < 4; ++e) {
+                v[e] = a0[e];
+                v[4 + e] = a1[e];
               }
-              __builtin_amdgcn_s_sleep(1);
+            } else {
+#pragma unroll
+              for (int e = 0; e < 8; ++e) v[e] = 0.f;
+            }
+            float amax = 0.f;
+#pragma unroll
+            for (int e = 0; e < 8; ++e) amax = fmaxf(amax, fabsf(v[e]));
+            amax = quad_max(amax);
+            const float rinv = amax > 0.f ? 127.0f * __builtin_amdgcn_rcpf(amax) : 0.f;
+            const float sx = amax * (1.0f / 127.0f);
+            uint32_t pa[2], pb[2];
+            const int t8 = split8(v, rinv, pa, pb);
+            const float sm = (float)quad_sum(t8) * (sx * (1.0f / 254.0f));
+            if (kk < ls) {
+              *reinterpret_cast<gq_u2 *>(lw + kk) = gq_u2{pa[0], pa[1]};
+              *reinterpret_cast<gq_u2 *>(lw + LL.sl + kk) = gq_u2{pb[0], pb[1]};
+              if ((lane & 3) == 0)
+                *reinterpret_cast<gq_f4 *>(lsw + 4 * (kk >> 5)) = gq_f4{sx, sm, sx * (1.0f / 254.0f), 0.f};
             }
           }
+          // x may be replaced by the next stage's once every wave has converted it
+          lds_order();
+          if (lane == 0) lds_add(&sy.released, 1u);
         }
-        // acquire: this CU's L1 and its XCD's L2 drop what other workgroups'
-        // stores made stale, for every wave of the workgroup
-        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
-        // x -> LDS: 16 bytes per lane per instruction (LDS DMA, no registers);
-        // the GQA map keeps runs of 4 together (head_dim % 8 == 0)
-        for (int k0 = 0; k0 < op.K; k0 += 256) {
-          int k = k0 + 4 * lane;
-          k = k < op.K ? k : 0;
-          if (op.xhd > 0) k = (k / (op.xhd * op.xgrp)) * op.xhd + k % op.xhd;
-          __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void *)(op.x + k),
-                                           (__attribute__((address_space(3))) void *)(xs + k0), 16, 0, 0);
-        }
-        __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
+        tot[0] = tot[1] = 0.f;
       }
-      __syncthreads();
-      if (!ctl) {
-        const int k0 = c0 * F::CK, LK = nw * F::CK;
-        float4 gv[TPR][2];
-        if (norm) {
-#pragma unroll
-          for (int i = 0; i < TPR; ++i) {
-            const int e8 = lane + 64 * i;
-            const int k = (8 * e8 < LK && k0 + 8 * e8 < op.K) ? k0 + 8 * e8 : 0;
-            const GQ_GLOBAL gq_f4 *gp = (const GQ_GLOBAL gq_f4 *)gmem(op.gamma + k);
-            const gq_f4 g0 = gp[0], g1 = gp[1];
-            gv[i][0] = float4{g0[0], g0[1], g0[2], g0[3]};
-            gv[i][1] = float4{g1[0], g1[1], g1[2], g1[3]};
-          }
-        }
-        float ss = 0.f;
-#pragma unroll
-        for (int i = 0; i < TPR; ++i) {
-          const int e8 = lane + 64 * i;
-          const bool in = 8 * e8 < LK && k0 + 8 * e8 < op.K;  // (K % 32 == 0: runs are whole)
-          const float4 a0 = *reinterpret_cast<const float4 *>(xs + (in ? k0 + 8 * e8 : 0));
-          const float4 a1 = *reinterpret_cast<const float4 *>(xs + (in ? k0 + 8 * e8 + 4 : 4));
-          float v[8] = {a0.x, a0.y, a0.z, a0.w, a1.x, a1.y, a1.z, a1.w};
-          float amax = 0.f;
-#pragma unroll
-          for (int e = 0; e < 8; ++e) {
-            v[e] = in ? v[e] : 0.f;
-            ss += v[e] * v[e];
-            amax = fmaxf(amax, fabsf(v[e]));
-          }
-          if (norm) {  // x * gamma; the 1 / rms factor is applied after the K reduction
-            const float gg[8] = {gv[i][0].x, gv[i][0].y, gv[i][0].z, gv[i][0].w,
-                                 gv[i][1].x, gv[i][1].y, gv[i][1].z, gv[i][1].w};
-            amax = 0.f;
-#pragma unroll
-            for (int e = 0; e < 8; ++e) {
-              v[e] *= gg[e];
-              amax = fmaxf(amax, fabsf(v[e]));
-            }
-          }
-          amax = quad_max(amax);
-          const float inv = amax > 0.f ? 127.0f * __builtin_amdgcn_rcpf(amax) : 0.f;
-          const float sx = amax * (1.0f / 127.0f);
-          uint32_t la[2], lb[2];
-          const int t8 = split8(v, inv, la, lb);
-          const float sm = (float)quad_sum(t8) * (sx * (1.0f / 254.0f));
-          if (in) {
-            *reinterpret_cast<gq_u2 *>(lm + 8 * e8) = gq_u2{la[0], la[1]};
-            *reinterpret_cast<gq_u2 *>(lm + L.lk + 8 * e8) = gq_u2{lb[0], lb[1]};
-            if ((lane & 3) == 0)
-              *reinterpret_cast<gq_f4 *>(lsc + 4 * (e8 >> 2)) = gq_f4{sx, sm, sx * (1.0f / 254.0f), 0.f};
-          }
-        }
-        ss = wave_sum(ss);
-        if (lane == 0) ssred[wave] = ss;
-        __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
-        __builtin_amdgcn_wave_barrier();
-      }
-    }
-    if (o != cur_op) {
-      // (a new op on the same input keeps the staged limbs; its dependencies
-      // were those of the op that staged them, or later ones already met)
-      cur_op = o;
-    }
-
-    if (!ctl) {
-      // ---- the next unit's weights, then this unit's chunks ---------------------
-      issue(u + G < total ? u + G : u, nxt);  // (the last unit re-reads its own chunks)
-      // A operand: lane (r, g) is combination c = r >> 2 = (block h, limb l)
-      // of the batch row (r & 3 == 0), with data where its lane group covers
-      // block h of the MFMA pair, zeros otherwise (as gq_gemv.hip's kernel)
-      const int c = r >> 2, h = c >> 1, l = c & 1;
-      const bool act = ((g >> 1) == h) && (r & 3) == 0;
-      const int8_t *abase = act ? lm + (size_t)l * L.lk + 32 * h + 16 * (g & 1) : lzero;
-      const int hp = g >> 1, lp = g & 1;
-      float tot[kAcc];
-#pragma unroll
-      for (int q = 0; q < kAcc; ++q) tot[q] = 0.f;
-#pragma unroll
-      for (int s = 0; s < NS; ++s) {
-        const int a = s / op.nck, i = s % op.nck;
-        if (a >= op.nacc || i >= nw) continue;
-        const Chunk<FMT> &cc = cur[s];
+      int a, i;
+      entry(op, cc.e, a, i);
+      if (i < cc.nw) {
+        const int kc = i * F::CK;  // first k of the chunk in this wave's slice
         float acc = 0.f, cor = 0.f;
 #pragma unroll
         for (int m = 0; m < F::STEPS; ++m) {
-          const int koff = i * F::CK + 64 * m;
-          const int blk = i * (F::CK / 32) + 2 * m + hp;
+          const int koff = astep * (kc + 64 * m) + (1 - astep) * (64 * m);
+          const int blk = kc / 32 + 2 * m + hp;
           const gq_i4 av = *reinterpret_cast<const gq_i4 *>(abase + koff);
-          const float2 sv = *reinterpret_cast<const float2 *>(lsc + 4 * blk + 2 * lp);
+          const float2 sv = *reinterpret_cast<const float2 *>(lsw + 4 * blk + 2 * lp);
           gq_i4 bop;
           float ws, wmn = 0.f;
           if constexpr (FMT == GQ_FMT_Q4_0) {
-            bop = codes16(cc.q[2 * m], cc.q[2 * m + 1]);
-            ws = m ? h16hi(cc.d) : h16lo(cc.d);
+            bop = codes16(slot.q[2 * m], slot.q[2 * m + 1]);
+            ws = m ? h16hi(slot.d) : h16lo(slot.d);
             wmn = ws;
           } else if constexpr (FMT == GQ_FMT_Q8_0) {
-            const gq_u4 &qq = m ? cc.q1 : cc.q0;
+            const gq_u4 &qq = m ? slot.q1 : slot.q0;
             bop = gq_i4{(int)qq[0], (int)qq[1], (int)qq[2], (int)qq[3]};
-            ws = m ? h16hi(cc.d) : h16lo(cc.d);
+            ws = m ? h16hi(slot.d) : h16lo(slot.d);
           } else {
-            const uint32_t w0 = (m < 2) ? cc.qa[2 * (m & 1)] : cc.qb[2 * (m & 1)];
-            const uint32_t w1 = (m < 2) ? cc.qa[2 * (m & 1) + 1] : cc.qb[2 * (m & 1) + 1];
+            const uint32_t w0 = (m < 2) ? slot.qa[2 * (m & 1)] : slot.qb[2 * (m & 1)];
+            const uint32_t w1 = (m < 2) ? slot.qa[2 * (m & 1) + 1] : slot.qb[2 * (m & 1) + 1];
             bop = codes16(w0, w1);
-            const uint32_t wsc = hp ? cc.meta[2] : cc.meta[1];
+            const uint32_t wsc = hp ? slot.meta[2] : slot.meta[1];
             const uint32_t byte = (wsc >> (8 * m)) & 0xFFu;
-            const uint32_t b3 = (cc.meta[3] >> (8 * m + 4 * hp)) & 15u;
-            ws = h16lo(cc.meta[0]) * (float)(byte & 63u);
-            wmn = h16hi(cc.meta[0]) * (float)((byte >> 6) | (b3 << 2));
+            const uint32_t b3 = (slot.meta[3] >> (8 * m + 4 * hp)) & 15u;
+            ws = h16lo(slot.meta[0]) * (float)(byte & 63u);
+            wmn = h16hi(slot.meta[0]) * (float)((byte >> 6) | (b3 << 2));
           }
           const gq_i4 D = mfma_i8(av, bop);
           acc += (ws * sv.x) * (float)D[0];
           if constexpr (FMT != GQ_FMT_Q8_0) cor += wmn * sv.y;
         }
         const float val = acc - OFF * cor;
-#pragma unroll
-        for (int q = 0; q < kAcc; ++q) tot[q] += (a == q) ? val : 0.f;
+        if (a) tot[1] += val;
+        else tot[0] += val;
       }
-#pragma unroll
-      for (int q = 0; q < kAcc; ++q) {
-        const float p = sum_lane_groups(tot[q]);
-        if (g == 0) red[P][wave][q][r] = p;
-      }
-    }
-    __syncthreads();
-    if (!ctl) return;
-
-    // ---- control wave: finish the unit ------------------------------------------
-    float inv = 1.f;
-    if (norm) {
-      float t = 0.f;
-#pragma unroll
-      for (int q = 0; q < kCW; ++q) t += ssred[q];
-      inv = 1.0f / sqrtf(t / (float)op.K + eps);
-    }
-    const int tpu = op.pair ? op.nacc >> 1 : op.nacc;
-    if (lane < 16) {
-      float part[kAcc];
-#pragma unroll
-      for (int q = 0; q < kAcc; ++q) {
-        float sum = 0.f;
-#pragma unroll
-        for (int w = 0; w < kCW; ++w) sum += red[P][w][q][r];
-        part[q] = sum * inv;
-      }
-#pragma unroll
-      for (int q = 0; q < kAcc; ++q) {
-        if (q >= tpu) continue;
-        const size_t row = (size_t)(j * tpu + q) * 16 + r;
-        if (row >= (size_t)op.N) continue;
-        float out;
-        if (op.pair) {  // accumulators 2q (gate) and 2q + 1 (up)
-          const float gt = part[(2 * q) % kAcc], up = part[(2 * q + 1) % kAcc];
-          out = gt / (1.0f + expf(-gt)) * up;
-        } else {
-          out = part[q] + (op.resid ? gmem(op.resid)[row] : 0.f);
+      if (cc.e == cc.E - 1) {
+        // ---- the unit's partial tile -> a slot for the control wave ------------
+        const float p0 = sum_lane_groups(tot[0]);
+        const float p1 = op.pair ? sum_lane_groups(tot[1]) : 0.f;
+        const int slot_i = (int)(nunit % kRed);
+        if (nunit >= kRed) lds_wait_ge(&sy.freed, nunit + 1 - kRed, &sy, spin_limit);
+        if (g == 0) {
+          red[slot_i][wave][0][r] = p0;
+          red[slot_i][wave][1][r] = p1;
         }
-        // agent-scope store: written through this XCD's L2 to memory, where
-        // the other XCDs read it
-        __hip_atomic_store(op.y + row, out, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        lds_order();
+        if (lane == 0) lds_add(&sy.arrive[slot_i], 1u);
+        ++nunit;
       }
+      advance(cc);
+    };
+
+    static_for<NSLOT>([&](auto s) { issue(ic, ring[decltype(s)::value]); });
+    while (cc.u < total) {
+      static_for<NSLOT>([&](auto s) {
+        constexpr int S = decltype(s)::value;
+        if (cc.u < total) consume(ring[S]);
+        issue(ic, ring[S]);
+      });
     }
-    // publish: once the stores are complete (vmcnt(0): the control wave has no
-    // other memory operation in flight), the op's counter.  (A release fence
-    // would also write back this XCD's whole L2, which costs microseconds;
-    // the only data published is the write-through stores above.)
-    __atomic_signal_fence(__ATOMIC_SEQ_CST);
-    __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
-    __atomic_signal_fence(__ATOMIC_SEQ_CST);
-    if (lane == 0) __hip_atomic_fetch_add(done + o, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): the surplus loads land before the wave ends
+    if (lds_ld(&sy.lerr) != 0u) __hip_atomic_store(err, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    return;
+  }
+
+  // ====================== control wave ==========================================
+  int o = 0;            // op of the current unit
+  int cnt_op = -1;      // op whose finished units are not yet counted
+  unsigned cnt = 0;     // how many
+  int stage = -1;
+  unsigned nstage = 0;  // stages posted
+  unsigned n = 0;       // units of this workgroup finished
+  float inv = 1.f;      // 1 / rms of the current stage (1 without RMSNorm)
+  bool bad = false;     // a wait gave up: skip the rest of the waits
+
+  int nbuf = 0;          // rows held in obuf (tiles of op cnt_op)
+  int tbuf0 = 0;         // tile of the first of them (the tiles of a workgroup step by G)
+  // stores the held rows (agent scope: written through this XCD's L2 to
+  // memory, where the other XCDs read them)
+  auto flush = [&]() {
+    if (nbuf == 0) return;
+    const GQ_CONST ChainOpD &op = ops[cnt_op];
+    for (int b = 0; b < nbuf; ++b) {
+      const int row = 16 * (tbuf0 + b * G) + r;
+      if (lane < 16 && row < op.N) __hip_atomic_store(op.y + row, obuf[b][r], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    nbuf = 0;
+  };
+  auto publish = [&]() {
+    if (cnt_op >= 0 && cnt > 0) {
+      flush();
+      // the rows' stores complete, then the count
+      __atomic_signal_fence(__ATOMIC_SEQ_CST);
+      __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
+      __atomic_signal_fence(__ATOMIC_SEQ_CST);
+      // (one flag per workgroup and op: 256 atomic adds on one word
+      // serialise at the memory side, ~25 ns each)
+      if (lane == 0) __hip_atomic_store(done + (size_t)cnt_op * kMaxGrid + blockIdx.x, 1u, __ATOMIC_RELAXED,
+                                        __HIP_MEMORY_SCOPE_AGENT);
+    }
+    cnt = 0;
   };
 
-  using P0 = std::integral_constant<int, 0>;
-  using P1 = std::integral_constant<int, 1>;
-  Chunk<FMT> cA[NS], cB[NS];
-  int u = (int)blockIdx.x;
-  if (u >= total) return;
-  if (!ctl) issue(u, cA);
-  while (true) {
-    process(u, cA, cB, P0{});
-    u += G;
-    if (u >= total) break;
-    process(u, cB, cA, P1{});
-    u += G;
-    if (u >= total) break;
+  for (int u = (int)blockIdx.x; u < total; u += G, ++n) {
+    while (o + 1 < n_ops && u >= ops[o + 1].unit0) ++o;
+    const GQ_CONST ChainOpD &op = ops[o];
+    if (o != cnt_op) {
+      publish();
+      cnt_op = o;
+    }
+    if (op.stage != stage) {
+      // ---- a new stage: its inputs complete, x -> LDS, limbs ------------------
+      // the compute waves are done with the previous stage's limbs
+      if (!bad && nstage > 0) bad = !lds_wait_ge(&sy.released, kCW * nstage, &sy, spin_limit);
+      for (int q = 0; q < 3 && !bad; ++q) {
+        const int d = op.dep[q];
+        if (d < 0) continue;
+        // op d is complete when every workgroup that holds units of it has
+        // set its flag (workgroup g holds unit u iff u % G == g)
+        const int d0 = ops[d].unit0, dn = ops[d].units;
+        unsigned spins = 0;
+        while (true) {
+          bool ok = true;
+          for (int g0 = 0; g0 < G; g0 += 64) {
+            const int gg = g0 + lane;
+            const bool holds = gg < G && (dn >= G || ((gg - d0 % G + G) % G) < dn);
+            if (holds && ld_agent(done + (size_t)d * kMaxGrid + gg) == 0u) ok = false;
+          }
+          if (__builtin_amdgcn_ballot_w64(!ok) == 0) break;
+          if (ld_agent(err) != 0u || lds_ld(&sy.lerr) != 0u) {
+            bad = true;
+            break;
+          }
+          if (++spins > spin_limit) {
+            __hip_atomic_store(err, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            bad = true;
+            break;
+          }
+          __builtin_amdgcn_s_sleep(1);
+        }
+      }
+      if (bad) lds_st(&sy.lerr, 1u);
+      // Inputs written by other workgroups are read with agent-scope loads
+      // (sc1: never served from a stale line of this XCD's L2), so no
+      // acquire fence -- which would invalidate the whole L2 -- is needed.
+      // x * gamma -> LDS, in batches of kXB float4 loads per lane (all
+      // requested, then used); the GQA map keeps runs of 4 together
+      // (head_dim % 8 == 0).  Plain loads, not LDS DMA: a DMA in flight would
+      // make every later LDS access of this wave wait on vmcnt, i.e. on the
+      // write-through stores of the finished rows.
+      const bool norm = op.gamma != nullptr;
+      float ss = 0.f;
+      for (int k0 = 0; k0 < op.K; k0 += 256 * kXB) {
+        gq_f4 xv[kXB], gv[kXB];
+#pragma unroll
+        for (int j = 0; j < kXB; ++j) {
+          int k = k0 + 256 * j + 4 * lane;
+          k = k < op.K ? k : 0;
+          const int km = op.xhd > 0 ? (k / (op.xhd * op.xgrp)) * op.xhd + k % op.xhd : k;
+          const unsigned long long *xp = reinterpret_cast<const unsigned long long *>(op.x + km);
+          const unsigned long long v0 = __hip_atomic_load(xp, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+          const unsigned long long v1 = __hip_atomic_load(xp + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+          xv[j] = gq_f4{__uint_as_float((unsigned)v0), __uint_as_float((unsigned)(v0 >> 32)),
+                        __uint_as_float((unsigned)v1), __uint_as_float((unsigned)(v1 >> 32))};
+          if (norm) gv[j] = *reinterpret_cast<const GQ_GLOBAL gq_f4 *>(gmem(op.gamma + k));
+        }
+#pragma unroll
+        for (int j = 0; j < kXB; ++j) {
+          const int k = k0 + 256 * j + 4 * lane;
+          if (k < op.K) {
+            gq_f4 v = xv[j];
+            ss += v[0] * v[0] + v[1] * v[1] + v[2] * v[2] + v[3] * v[3];
+            if (norm) v = v * gv[j];
+            *reinterpret_cast<gq_f4 *>(xs + k) = v;
+          }
+        }
+      }
+      // RMSNorm: 1 / rms scales the finished dot products
+      inv = norm ? 1.0f / sqrtf(wave_sum(ss) / (float)op.K + eps) : 1.f;
+      lds_order();
+      ++nstage;
+      if (lane == 0) lds_st(&sy.xready, nstage);
+      stage = op.stage;
+    }
+
+    // ---- finish unit n: the compute waves' partial tiles -----------------------
+    const int t = u - op.unit0;
+    const int row = 16 * t + r;
+    float res = 0.f;
+    if (lane < 16 && row < op.N && op.resid && !op.pair)  // (requested before the wait)
+      res = __uint_as_float(__hip_atomic_load(reinterpret_cast<const unsigned *>(op.resid) + row, __ATOMIC_RELAXED,
+                                              __HIP_MEMORY_SCOPE_AGENT));
+    const int slot_i = (int)(n % kRed);
+    if (!bad) bad = !lds_wait_ge(&sy.arrive[slot_i], kCW * (n / kRed + 1), &sy, spin_limit);
+    float p0 = 0.f, p1 = 0.f;
+    if (lane < 16) {
+#pragma unroll
+      for (int w = 0; w < kCW; ++w) {
+        p0 += red[slot_i][w][0][r];
+        p1 += red[slot_i][w][1][r];
+      }
+    }
+    lds_order();
+    if (lane == 0) lds_st(&sy.freed, n + 1);
+    if (nbuf == kObuf) flush();
+    if (nbuf == 0) tbuf0 = t;
+    if (lane < 16) {
+      float out;
+      if (op.pair) {
+        const float gt = p0 * inv, up = p1 * inv;
+        out = gt / (1.0f + expf(-gt)) * up;
+      } else {
+        out = p0 * inv + res;
+      }
+      obuf[nbuf][r] = out;
+    }
+    ++nbuf;
+    ++cnt;
   }
-  __builtin_amdgcn_s_waitcnt(0x0F70);  // (the last, redundant prefetch lands before the wave ends)
+  publish();
+  if (bad || lds_ld(&sy.lerr) != 0u) __hip_atomic_store(err, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 // ---- host side ------------------------------------------------------------------
 struct ChainHdr {  // the plan, kept on the host per workspace
-  int fmt, n_ops, total, grid, xs_bytes, lds_bytes;
+  int fmt, n_ops, total, grid;
+  ChainLds lds;
   float eps;
   unsigned spin_limit;
   size_t done_off, err_off, ops_off;
@@ -403,17 +573,17 @@ size_t al256(size_t v) { return (v + 255) & ~(size_t)255; }
 
 int chain_fmt(int fmt) { return gq_fmt_is_q4k(fmt) ? GQ_FMT_Q4_K : fmt; }
 
-// Device ops for the caller's ops: ops whose K needs more chunks per wave
-// than the slots hold are cut into column ranges chained through resid.
-int build_ops(int fmt, const gq_chain_op *ops, int n_ops, std::vector<ChainOpD> &out, int *max_k) {
+// Device ops for the caller's ops: ops whose K exceeds kMaxPieceK are cut
+// into column ranges chained through resid; consecutive ops with the same
+// input share an activation stage.  Also returns the LDS layout.
+int build_ops(int fmt, const gq_chain_op *ops, int n_ops, std::vector<ChainOpD> &out, ChainLds *lds) {
   const int f = chain_fmt(fmt);
   GQ_CHECK(f == GQ_FMT_Q4_0 || f == GQ_FMT_Q8_0 || f == GQ_FMT_Q4_K, GQ_ERR_UNSUPPORTED);
   GQ_CHECK(ops && n_ops >= 1, GQ_ERR_INVALID_ARGS);
-  const int S = chain_slots(f);
   const int ck = (int)gq_chunk_k(f);
+  const int max_c = kMaxPieceK / ck;
   std::vector<int> last(n_ops, -1);  // device index of each caller op's final range
-  int unit0 = 0;
-  *max_k = 0;
+  int unit0 = 0, kx = 0, sl = 0, zl = 0;
   out.clear();
   for (int i = 0; i < n_ops; ++i) {
     const gq_chain_op &p = ops[i];
@@ -425,8 +595,7 @@ int build_ops(int fmt, const gq_chain_op *ops, int n_ops, std::vector<ChainOpD> 
     GQ_CHECK(p.x_head_dim == 0 || (p.x_head_dim % 8 == 0 && p.x_group > 0), GQ_ERR_INVALID_ARGS);
     for (int q = 0; q < 3; ++q) GQ_CHECK(p.dep[q] < i && p.dep[q] >= -1, GQ_ERR_INVALID_ARGS);
     const int C = (int)((p.K + ck - 1) / ck);
-    const int nck_full = (C + kCW - 1) / kCW;
-    const int pieces = (nck_full + S - 1) / S;
+    const int pieces = (C + max_c - 1) / max_c;
     // a cut op must be linear in x: no norm, GQA map or SwiGLU
     GQ_CHECK(pieces == 1 || (!p.gamma && !p.w_up && p.x_head_dim == 0), GQ_ERR_UNSUPPORTED);
     const int cper = (C + pieces - 1) / pieces;
@@ -445,17 +614,8 @@ int build_ops(int fmt, const gq_chain_op *ops, int n_ops, std::vector<ChainOpD> 
       d.C = ce - cb;
       d.Crow = (int)gq_chunks(f, kt);
       d.cbase = (int)(p.k_offset / (uint32_t)ck) + cb;
-      d.nck = (d.C + kCW - 1) / kCW;
-      int nacc = S / d.nck;
-      nacc = nacc < kAcc ? nacc : kAcc;
-      if (p.w_up) {
-        nacc &= ~1;
-        GQ_CHECK(nacc >= 2, GQ_ERR_UNSUPPORTED);  // (K too long for a SwiGLU pair)
-      }
-      d.nacc = nacc;
       d.pair = p.w_up ? 1 : 0;
-      const int tpu = d.pair ? nacc / 2 : nacc;
-      d.units = (int)((gq_tiles(p.N) + tpu - 1) / tpu);
+      d.units = (int)gq_tiles(p.N);
       d.unit0 = unit0;
       unit0 += d.units;
       if (pc == 0) {
@@ -466,29 +626,30 @@ int build_ops(int fmt, const gq_chain_op *ops, int n_ops, std::vector<ChainOpD> 
       }
       d.xhd = (int)p.x_head_dim;
       d.xgrp = (int)p.x_group;
-      *max_k = d.K > *max_k ? d.K : *max_k;
+      d.stage = out.empty() ? 0 : (same_input(out.back(), d) ? out.back().stage : out.back().stage + 1);
+      const int kp = d.C * ck;
+      kx = kp > kx ? kp : kx;
+      const int slice = (d.C + kCW - 1) / kCW * ck;
+      sl = slice > sl ? slice : sl;
+      zl = ck;  // (the zero A rows: one chunk's 64-k steps)
       out.push_back(d);
     }
     last[i] = (int)out.size() - 1;
   }
+  *lds = chain_lds_layout(kx, sl, zl);
   return GQ_OK;
 }
 
 size_t chain_ws_bytes(size_t n_dev_ops) {
-  return 256 /* counters' line */ + al256(n_dev_ops * 4) + 256 /* error flag */ + al256(n_dev_ops * sizeof(ChainOpD));
-}
-
-template <int FMT>
-int chain_lds(int xs_bytes) {
-  using F = Fmt<FMT>;
-  return xs_bytes + kCW * xl_layout(F::CK * ChainSlots<FMT>::S, 1).wave_bytes;
+  return 256 + al256(n_dev_ops * kMaxGrid * 4) /* completion flags */ + 256 /* error flag */ +
+         al256(n_dev_ops * sizeof(ChainOpD));
 }
 
 template <int FMT>
 int chain_launch(const ChainHdr &h, const uint8_t *ws, hipStream_t s) {
-  hipLaunchKernelGGL(k_chain<FMT>, dim3((unsigned)h.grid), dim3(64 * (kCW + 1)), (size_t)h.lds_bytes, s,
+  hipLaunchKernelGGL(k_chain<FMT>, dim3((unsigned)h.grid), dim3(64 * (kCW + 1)), (size_t)h.lds.bytes, s,
                      (const ChainOpD *)(ws + h.ops_off), h.n_ops, h.total, (unsigned *)(ws + h.done_off),
-                     (unsigned *)(ws + h.err_off), h.eps, h.spin_limit, h.xs_bytes);
+                     (unsigned *)(ws + h.err_off), h.eps, h.spin_limit, h.lds);
   return gq_last_launch();
 }
 
@@ -503,8 +664,9 @@ int chain_occupancy(int lds, int *per_cu) {
 extern "C" int gq_gemv_chain_workspace_bytes(int fmt, const gq_chain_op *ops, int n_ops, size_t *bytes) {
   GQ_CHECK(bytes, GQ_ERR_INVALID_ARGS);
   std::vector<ChainOpD> d;
-  int mk = 0;
-  GQ_TRY(build_ops(fmt, ops, n_ops, d, &mk));
+  ChainLds lds;
+  GQ_TRY(build_ops(fmt, ops, n_ops, d, &lds));
+  GQ_CHECK(lds.bytes <= 160 * 1024 - 4096, GQ_ERR_UNSUPPORTED);  // (x too long for the LDS copy)
   *bytes = chain_ws_bytes(d.size());
   return GQ_OK;
 }
@@ -512,32 +674,27 @@ extern "C" int gq_gemv_chain_workspace_bytes(int fmt, const gq_chain_op *ops, in
 extern "C" int gq_gemv_chain_plan(int fmt, const gq_chain_op *ops, int n_ops, float eps, void *ws, size_t ws_bytes) {
   GQ_CHECK(ws, GQ_ERR_INVALID_ARGS);
   std::vector<ChainOpD> d;
-  int max_k = 0;
-  GQ_TRY(build_ops(fmt, ops, n_ops, d, &max_k));
-  GQ_CHECK(ws_bytes >= chain_ws_bytes(d.size()), GQ_ERR_WORKSPACE);
   ChainHdr h{};
+  GQ_TRY(build_ops(fmt, ops, n_ops, d, &h.lds));
+  GQ_CHECK(h.lds.bytes <= 160 * 1024 - 4096, GQ_ERR_UNSUPPORTED);
+  GQ_CHECK(ws_bytes >= chain_ws_bytes(d.size()), GQ_ERR_WORKSPACE);
   h.fmt = chain_fmt(fmt);
   h.n_ops = (int)d.size();
   h.total = d.back().unit0 + d.back().units;
   h.eps = eps;
-  h.xs_bytes = (int)((max_k + 255) / 256 * 256 * 4);  // (the DMA writes whole 256-element runs)
-  h.lds_bytes = h.fmt == GQ_FMT_Q4_0 ? chain_lds<GQ_FMT_Q4_0>(h.xs_bytes)
-                : h.fmt == GQ_FMT_Q8_0 ? chain_lds<GQ_FMT_Q8_0>(h.xs_bytes)
-                                       : chain_lds<GQ_FMT_Q4_K>(h.xs_bytes);
-  GQ_CHECK(h.lds_bytes <= 160 * 1024 - 8192, GQ_ERR_UNSUPPORTED);  // (x too long for the LDS copy)
   int per_cu = 0;
   switch (h.fmt) {
-  case GQ_FMT_Q4_0: GQ_TRY(chain_occupancy<GQ_FMT_Q4_0>(h.lds_bytes, &per_cu)); break;
-  case GQ_FMT_Q8_0: GQ_TRY(chain_occupancy<GQ_FMT_Q8_0>(h.lds_bytes, &per_cu)); break;
-  default: GQ_TRY(chain_occupancy<GQ_FMT_Q4_K>(h.lds_bytes, &per_cu)); break;
+  case GQ_FMT_Q4_0: GQ_TRY(chain_occupancy<GQ_FMT_Q4_0>(h.lds.bytes, &per_cu)); break;
+  case GQ_FMT_Q8_0: GQ_TRY(chain_occupancy<GQ_FMT_Q8_0>(h.lds.bytes, &per_cu)); break;
+  default: GQ_TRY(chain_occupancy<GQ_FMT_Q4_K>(h.lds.bytes, &per_cu)); break;
   }
   const int cus = gq_device_cus();
   GQ_CHECK(per_cu >= 1 && cus > 0, GQ_ERR_UNSUPPORTED);
-  h.grid = cus;  // one workgroup per CU: every workgroup resident at once
+  h.grid = cus < kMaxGrid ? cus : kMaxGrid;  // one workgroup per CU: every workgroup resident at once
   const char *e = getenv("GQ_CHAIN_SPIN");
   h.spin_limit = e ? (unsigned)strtoul(e, nullptr, 0) : (1u << 22);
   h.done_off = 256;
-  h.err_off = h.done_off + al256(d.size() * 4);
+  h.err_off = h.done_off + al256(d.size() * kMaxGrid * 4);
   h.ops_off = h.err_off + 256;
   GQ_TRY(gq_hip_status(hipMemcpy((uint8_t *)ws + h.ops_off, d.data(), d.size() * sizeof(ChainOpD),
                                  hipMemcpyHostToDevice)));

@@ -38,15 +38,17 @@ def layer_ops(base=0):
 def test_chain_plan_sizes_a_decode_step():
     ops = layer_ops()
     n = gq.chain_workspace_bytes(gq.FMT_Q4_K, ops)
-    # counters, error flag and the op table: down (C = 56 chunks) is cut into
-    # two column ranges, so 7 device ops
-    assert n == 256 + 256 + 256 + 256 * ((7 * 128 + 255) // 256)
-    assert gq.chain_workspace_bytes(gq.FMT_Q4_0, ops) > 0
-    # Q8_0 chunks take 9 registers: 4 slots per wave hold a 4096-column SwiGLU
-    # pair's 8 chunks of one wave slice only as two accumulators of 4 -- too many
-    with pytest.raises(gq.GQError):
-        gq.chain_workspace_bytes(gq.FMT_Q8_0, ops)
-    assert gq.chain_workspace_bytes(gq.FMT_Q8_0, [_op(128256, 4096, gamma=_T(1))]) == 256 * 4
+    # completion flags (one word per op and workgroup, 256 workgroups at
+    # most), error flag and the op table: one device op per op (down's 14336
+    # columns are within one op's K range)
+    ws = lambda ops: 256 + 4 * 256 * ops + 256 + 256 * ((ops * 128 + 255) // 256)  # noqa: E731
+    assert n == ws(6)
+    assert gq.chain_workspace_bytes(gq.FMT_Q4_0, ops) == n
+    assert gq.chain_workspace_bytes(gq.FMT_Q8_0, ops) == n
+    assert gq.chain_workspace_bytes(gq.FMT_Q8_0, [_op(128256, 4096, gamma=_T(1))]) == ws(1)
+    # K beyond one op's range (16384) is cut into column ranges chained
+    # through the residual: 40960 columns -> 3 device ops
+    assert gq.chain_workspace_bytes(gq.FMT_Q4_K, [_op(64, 40960)]) == ws(3)
 
 
 @pytest.mark.parametrize("bad", [
@@ -54,7 +56,8 @@ def test_chain_plan_sizes_a_decode_step():
     lambda: [_op(64, 256), _op(64, 256, deps=[2])],                   # on a later op
     lambda: [_op(64, 100)],                                           # K not a multiple of 32
     lambda: [_op(64, 256, w_up=_T(5), resid=_T(6))],                  # SwiGLU with a residual
-    lambda: [_op(64, 16384, gamma=_T(1))],                            # a cut op cannot normalise
+    lambda: [_op(64, 32768, gamma=_T(1))],                            # a cut op cannot normalise
+    lambda: [_op(64, 20480, w_up=_T(5))],                             # nor be a SwiGLU pair
     lambda: [_op(64, 256, x_head_dim=12, x_group=2)],                 # GQA runs of 8
     lambda: [_op(64, 512, k_offset=128, k_total=1024)],               # range not on a chunk (Q4_K: 256)
 ])

@@ -27,7 +27,7 @@ def _w(fmt, n, k, seed, dev):
 
 
 @pytest.mark.parametrize("fmt", [O.Q4_0, O.Q8_0, O.Q4_K])
-@pytest.mark.parametrize("n,k", [(4096, 4096), (1000, 512), (17, 256), (300, 14336), (4096, 2048)])
+@pytest.mark.parametrize("n,k", [(4096, 4096), (1000, 512), (17, 256), (300, 14336), (4096, 2048), (300, 20480)])
 def test_chain_single_gemv(dev, fmt, n, k):
     import torch
 
@@ -106,7 +106,7 @@ def _decode_ref(fmt, L, h, eps, dim=4096, ff=14336, heads=32, kv=8, hd=128):
     return steps
 
 
-@pytest.mark.parametrize("fmt", [O.Q4_K, O.Q4_0])
+@pytest.mark.parametrize("fmt", [O.Q4_K, O.Q4_0, O.Q8_0])
 def test_chain_llama_decode_two_layers(dev, fmt):
     import torch
 
@@ -130,6 +130,33 @@ def test_chain_llama_decode_two_layers(dev, fmt):
         assert O.rel_l2(bufs["v"].cpu().numpy(), v) <= TOL
         assert O.rel_l2(bufs["h1"].cpu().numpy(), h1) <= TOL
         assert O.rel_l2(bufs["act"].cpu().numpy(), act) <= TOL
+
+
+@pytest.mark.parametrize("fmt", [O.Q4_0, O.Q4_K])
+def test_chain_independent_stages(dev, fmt):
+    """Ops that read different inputs and depend on nothing, interleaved with
+    ops that share an input (one activation stage each run of them): every
+    stage reuses the same LDS copy of x once the compute waves release it."""
+    import torch
+
+    import gq
+    print(f"chain independent stages fmt={fmt}", flush=True)
+    specs = [(512, 4096, 0), (256, 4096, 0), (2048, 1024, 1), (64, 14336, 2), (1024, 4096, 3), (1024, 4096, 3)]
+    xs = {j: O.gen_x(1, k, seed=40 + j) for _, k, j in specs}
+    ops, refs, ys = [], [], []
+    for i, (n, k, j) in enumerate(specs):
+        w, p = _w(fmt, n, k, 70 + i, dev)
+        y = torch.full((n,), float("nan"), device=dev)
+        ops.append({"w": p, "x": _dev(xs[j][0], dev), "y": y, "N": n, "K": k})
+        refs.append(O.gemv(fmt, w, xs[j], n, k)[0])
+        ys.append(y)
+    ch = gq.Chain(fmt, ops, dev)
+    for rep in range(2):
+        ch.run()
+        torch.cuda.synchronize()
+        assert ch.error() == 0
+        for i, (y, ref) in enumerate(zip(ys, refs)):
+            assert O.rel_l2(y.cpu().numpy(), ref) <= TOL, (rep, i)
 
 
 def test_chain_in_a_graph(dev):
