@@ -847,7 +847,7 @@ __global__ void __launch_bounds__(256) k_a_to_f16_w(const void *__restrict__ a, 
 
 // A -> fp16 [M][ldo] with per-row scales: k_a_to_f16_w for at least 1024 rows
 // of up to 8192 padded columns (2048 x 4096 bf16: 13.5 -> 11.1 us), else
-// k_a_to_f16 (fewer rows spread over more waves: measured no slower at 512)
+// k_a_to_f16 (one workgroup of 8 waves per row: fewer rows keep more waves busy)
 int launch_a_to_f16(const void *a, int a_dtype, _Float16 *o, float *rs, int M, int K, int ldo, int q4perm,
                     hipStream_t s) {
   const unsigned g4 = (unsigned)((M + 3) / 4);
