@@ -742,9 +742,12 @@ int gq_gemv_h1_plan(int fmt, size_t N, size_t K, int nb, int *R_out, int *ks_out
   const int nckp = nck <= 1 ? 1 : nck <= 2 ? 2 : nck <= 4 ? 4 : nck <= 8 ? 8 : 16;
   if (nckp > maxc) return GQ_ERR_UNSUPPORTED;
   if ((size_t)ks * nckp * CK * 2 * mr > (mr == 8 ? 64 : 128) * 1024) return GQ_ERR_UNSUPPORTED;
-  // 16 rows (one workgroup per CU): measured a win on grids of up to 512 row
-  // tiles only (4096 x 4096: 7.6 vs 8.7 us; 14336 rows: 13.9 vs 13.5 us)
-  if (e != 1 && mr == 16 && tiles > 512) return GQ_ERR_UNSUPPORTED;
+  // a win on grids of up to 512 row tiles only: 4096 x 4096 batch 8 / 16 6.3 / 7.8
+  // vs 6.8 / 9.1 us, 1024 x 4096 batch 8 5.5 vs 6.0 us; on 896 tiles (14336
+  // rows) the windowed kernel's 4-tile workgroups are faster (Q4_K batch 5 / 8
+  // 12.0 / 12.2 vs 12.9-13.3 / 13.4-13.5 us, Q4_0 batch 8 11.9 vs 12.4 us,
+  // measured on two boxes)
+  if (e != 1 && tiles > 512) return GQ_ERR_UNSUPPORTED;
   if (e != 1 && (tiles + tw - 1) / tw > slots) return GQ_ERR_UNSUPPORTED;
   *R_out = tw;
   *ks_out = ks;

@@ -70,7 +70,8 @@ def h1_plan(fmt, n, k, batch):
     """The one-stage fp16 kernel's plan (k_gemv_h1), or None where gq_gemv
     uses the windowed kernel: 4-bit formats, 16 waves as TW tiles x 16 / TW
     parts, MR (8 up to batch 8, else 16) activation rows of all of K in LDS
-    (64 / 128 KiB: 2 / 1 workgroups per CU), one round of workgroups."""
+    (64 / 128 KiB: 2 / 1 workgroups per CU), one round of workgroups, grids
+    of up to 512 row tiles."""
     if fmt not in (gq.FMT_Q4_0, gq.FMT_Q4_K):
         return None
     C = -(-k // CK[fmt])
@@ -87,7 +88,7 @@ def h1_plan(fmt, n, k, batch):
     nckp = 1 if nck <= 1 else 2 if nck <= 2 else 4 if nck <= 4 else 8 if nck <= 8 else 16
     if nckp > (8 if fmt == gq.FMT_Q4_0 else 4) or ks * nckp * CK[fmt] * 2 * mr > (64 if mr == 8 else 128) * 1024:
         return None
-    if mr == 16 and tiles > 512:
+    if tiles > 512:  # larger grids: the windowed kernel's 4-tile workgroups are faster
         return None
     if -(-tiles // tw) > slots:
         return None
