@@ -77,6 +77,22 @@ GQ_DEV void load_chunk(const uint8_t *qp, const uint8_t *sp, uint32_t qo, uint32
   }
 }
 
+// The code words of a chunk only (Q4_0, Q8_0, Q4_K): the scales come from an
+// LDS copy of the wave's scale-plane run (gq_gemv.hip)
+template <int FMT>
+GQ_DEV void load_chunk_codes(const uint8_t *qp, uint32_t qo, Chunk<FMT> &ch) {
+  if constexpr (FMT == GQ_FMT_Q4_0) {
+    ch.q = gq_ld16_nt(qp + qo);
+  } else if constexpr (FMT == GQ_FMT_Q8_0) {
+    ch.q0 = gq_ld16_nt(qp + qo);
+    ch.q1 = gq_ld16_nt(qp + 1024 + qo);
+  } else {
+    static_assert(FMT == GQ_FMT_Q4_K, "Q4_0, Q8_0, Q4_K");
+    ch.qa = gq_ld16_nt(qp + qo);
+    ch.qb = gq_ld16_nt(qp + 1024 + qo);
+  }
+}
+
 // code group (2 words) -> 16 codes as bytes, slot order
 GQ_DEV gq_i4 codes16(uint32_t w0, uint32_t w1) {
   gq_i4 v;
