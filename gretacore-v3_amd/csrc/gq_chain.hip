@@ -666,7 +666,9 @@ extern "C" int gq_gemv_chain_workspace_bytes(int fmt, const gq_chain_op *ops, in
   std::vector<ChainOpD> d;
   ChainLds lds;
   GQ_TRY(build_ops(fmt, ops, n_ops, d, &lds));
-  GQ_CHECK(lds.bytes <= 160 * 1024 - 4096, GQ_ERR_UNSUPPORTED);  // (x too long for the LDS copy)
+  // (x too long for the LDS copy; 8 KiB stay for the static arrays: partial
+  // tiles, counters, held rows)
+  GQ_CHECK(lds.bytes <= 160 * 1024 - 8192, GQ_ERR_UNSUPPORTED);
   *bytes = chain_ws_bytes(d.size());
   return GQ_OK;
 }
@@ -676,7 +678,7 @@ extern "C" int gq_gemv_chain_plan(int fmt, const gq_chain_op *ops, int n_ops, fl
   std::vector<ChainOpD> d;
   ChainHdr h{};
   GQ_TRY(build_ops(fmt, ops, n_ops, d, &h.lds));
-  GQ_CHECK(h.lds.bytes <= 160 * 1024 - 4096, GQ_ERR_UNSUPPORTED);
+  GQ_CHECK(h.lds.bytes <= 160 * 1024 - 8192, GQ_ERR_UNSUPPORTED);
   GQ_CHECK(ws_bytes >= chain_ws_bytes(d.size()), GQ_ERR_WORKSPACE);
   h.fmt = chain_fmt(fmt);
   h.n_ops = (int)d.size();
