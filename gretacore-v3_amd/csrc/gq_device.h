@@ -36,6 +36,29 @@ GQ_DEV float gq_scale_h2f(uint32_t h16) { return gq_h2f(h16); }
 GQ_DEV uint32_t gq_h2_bits(gq_half2 v) { return __builtin_bit_cast(uint32_t, v); }
 GQ_DEV gq_half2 gq_bits_h2(uint32_t v) { return __builtin_bit_cast(gq_half2, v); }
 
+// 4-bit codes straight to fp16: OR-ing a code into the low mantissa bits of
+// 1024.0 (0x6400) gives 1024 + q.  Of a code-group word (slots 0..3 in the
+// low nibbles of bytes 0..3, slots 4..7 in the high nibbles) four and-or ops
+// give the halves (s0, s2), (s4, s6) * 16, (s1, s3), (s5, s7) * 16 -- the high
+// nibbles come out as 1024 + 16 q.  Formats that use this order stage their
+// activations in the same order, with the "* 16" positions divided by 16
+// (exact), so each product is unchanged: element e of a run of 8 holds slot
+// {0, 2, 4, 6, 1, 3, 5, 7}[e], elements 2, 3, 6, 7 scaled by 16.
+// The magic is held in a VGPR (mg): a VOP3 and-or can then take the mask as its
+// one scalar operand and stays a single instruction.
+GQ_DEV uint32_t gq_nib_magic() {
+  uint32_t v;
+  asm volatile("v_mov_b32 %0, 0x64006400" : "=v"(v));
+  return v;
+}
+GQ_DEV void gq_nib_halves(uint32_t w, uint32_t mg, gq_half2 (&p)[4]) {
+  const uint32_t v = w >> 8;
+  p[0] = gq_bits_h2((w & 0x000F000Fu) | mg);
+  p[1] = gq_bits_h2((w & 0x00F000F0u) | mg);
+  p[2] = gq_bits_h2((v & 0x000F000Fu) | mg);
+  p[3] = gq_bits_h2((v & 0x00F000F0u) | mg);
+}
+
 GQ_DEV gq_f4 gq_mfma16(const gq_half8 &a, const gq_half8 &b, const gq_f4 &c) {
   return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
 }

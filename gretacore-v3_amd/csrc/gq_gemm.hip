@@ -445,35 +445,78 @@ struct RStep<GQ_FMT_Q4_K, NJ> {
   gq_u4 meta[NJ];  // d, dmin, W1, W2, W3 of the column's super-block
 };
 
+// Buffer resource over the 4 GiB from p (raw: stride 0, the offset in
+// bytes).  The register-B kernel addresses its operands as a 32-bit per-lane
+// offset fixed for the whole K walk plus a uniform scalar offset per step, so
+// a load costs no vector address arithmetic (the host checks that both the
+// packed weights and the activations lie within 4 GiB).
+GQ_DEV __amdgpu_buffer_rsrc_t gq_rsrc(const void *p) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(p), (short)0, -1, 0x00020000);
+}
+GQ_DEV gq_u2 ld8_b(const void *base, uint32_t vo, uint32_t so) {
+  const auto v = __builtin_amdgcn_raw_buffer_load_b64(gq_rsrc(base), vo, so, 0);
+  return gq_u2{v[0], v[1]};
+}
+GQ_DEV gq_u4 ld16_b(const void *base, uint32_t vo, uint32_t so) {
+  const auto v = __builtin_amdgcn_raw_buffer_load_b128(gq_rsrc(base), vo, so, 0);
+  return gq_u4{v[0], v[1], v[2], v[3]};
+}
+
 template <int FMT, int NJ>
 GQ_DEV void load_rstep(const uint8_t *w, const uint32_t (&qo)[NJ], const uint32_t (&so)[NJ], int step,
                        RStep<FMT, NJ> &st) {
 #pragma unroll
   for (int j = 0; j < NJ; ++j) {
     if constexpr (FMT == GQ_FMT_Q4_0) {
-      const uint8_t *b = w + ((size_t)(step >> 1) << 10) + 8 * (step & 1);
-      st.q[j][0] = gq_ld8(b + qo[j]);
-      st.q[j][1] = gq_ld8(b + qo[j] + 512);
-      st.d[j] = gq_ld8(w + (size_t)(step >> 1) * 128 + so[j]);
+      const uint32_t b = ((uint32_t)(step >> 1) << 10) + 8u * (uint32_t)(step & 1);
+      st.q[j][0] = ld8_b(w, qo[j], b);
+      st.q[j][1] = ld8_b(w, qo[j] + 512u, b);
+      st.d[j] = ld8_b(w, so[j], (uint32_t)(step >> 1) * 128u);
     } else if constexpr (FMT == GQ_FMT_Q8_0) {
-      const uint8_t *b = w + ((size_t)(step >> 1) << 11) + ((step & 1) << 10);
-      st.q[j][0] = gq_ld16(b + qo[j]);
-      st.q[j][1] = gq_ld16(b + qo[j] + 512);
-      st.d[j] = gq_ld8(w + (size_t)(step >> 1) * 128 + so[j]);
+      const uint32_t b = ((uint32_t)(step >> 1) << 11) + ((uint32_t)(step & 1) << 10);
+      st.q[j][0] = ld16_b(w, qo[j], b);
+      st.q[j][1] = ld16_b(w, qo[j] + 512u, b);
+      st.d[j] = ld8_b(w, so[j], (uint32_t)(step >> 1) * 128u);
     } else {
       const int m = step & 3;
-      const uint8_t *b = w + ((size_t)(step >> 2) << 11) + ((m >> 1) << 10) + 8 * (m & 1);
-      st.q[j][0] = gq_ld8(b + qo[j]);
-      st.q[j][1] = gq_ld8(b + qo[j] + 512);
-      st.meta[j] = gq_ld16(w + (size_t)(step >> 2) * 256 + so[j]);
+      const uint32_t b = ((uint32_t)(step >> 2) << 11) + ((uint32_t)(m >> 1) << 10) + 8u * (uint32_t)(m & 1);
+      st.q[j][0] = ld8_b(w, qo[j], b);
+      st.q[j][1] = ld8_b(w, qo[j] + 512u, b);
+      st.meta[j] = ld16_b(w, so[j], (uint32_t)(step >> 2) * 256u);
     }
+  }
+}
+
+// The register-B kernel's activation tile loads (load_a_lds's rows and
+// swizzle): per-lane offsets computed once, the step's columns a scalar offset.
+template <int BM, int NW>
+GQ_DEV void a_offsets(int lda, int M, int m0, int wave, int lane, uint32_t (&ao)[BM / (8 * NW)]) {
+  constexpr int PER_WAVE = BM / (8 * NW);
+#pragma unroll
+  for (int i = 0; i < PER_WAVE; ++i) {
+    const int row0 = 8 * (wave * PER_WAVE + i);
+    const int c = (lane & 7) ^ a_swz(row0 + (lane >> 3));
+    int m = m0 + row0 + (lane >> 3);
+    if (m >= M) m = M - 1;  // clamped; rows >= M are never stored
+    ao[i] = 2u * ((uint32_t)m * (uint32_t)lda + 8u * (uint32_t)c);
+  }
+}
+template <int BM, int NW>
+GQ_DEV void load_a_lds_b(const _Float16 *a, const uint32_t *ao, int step, int wave,
+                         _Float16 *As) {
+  constexpr int PER_WAVE = BM / (8 * NW);
+#pragma unroll
+  for (int i = 0; i < PER_WAVE; ++i) {
+    const int row0 = 8 * (wave * PER_WAVE + i);
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(gq_rsrc(a), (__attribute__((address_space(3))) void *)(As + row0 * BK), 16, ao[i],
+                                             (uint32_t)step * (2u * BK), 0, 0);
   }
 }
 
 // Q4_K: the fp16 factors of the sub-block 2 (step & 3) + h of column block j
 // (sc, -1024 sc, d, -dmin m), decoded once per K step.
 struct QKf {
-  gq_half2 sc2, nsc2, d2, mn2;
+  gq_half2 sc2, nsc2, d2, mn2, mn16;  // mn16 = 16 mn2 (exact): for the 16 x elements
 };
 template <int NJ>
 GQ_DEV void q4k_factors(const RStep<GQ_FMT_Q4_K, NJ> &st, int step, QKf (&f)[NJ][2]) {
@@ -490,7 +533,9 @@ GQ_DEV void q4k_factors(const RStep<GQ_FMT_Q4_K, NJ> &st, int step, QKf (&f)[NJ]
       gq_q4k_meta_codes(mv, 2 * (step & 3) + h, &sc, &mn);
       const _Float16 hsc = (_Float16)(float)sc, hnsc = (_Float16)(-1024.0f * (float)sc);
       const _Float16 hmin = (_Float16)(-(dmin * (float)mn));
-      f[j][h] = QKf{gq_half2{hsc, hsc}, gq_half2{hnsc, hnsc}, gq_half2{hd, hd}, gq_half2{hmin, hmin}};
+      const _Float16 hmin16 = (_Float16)16.0f * hmin;
+      f[j][h] = QKf{gq_half2{hsc, hsc}, gq_half2{hnsc, hnsc}, gq_half2{hd, hd}, gq_half2{hmin, hmin},
+                    gq_half2{hmin16, hmin16}};
     }
   }
 }
@@ -499,7 +544,7 @@ GQ_DEV void q4k_factors(const RStep<GQ_FMT_Q4_K, NJ> &st, int step, QKf (&f)[NJ]
 // (c - bias) * scale (Q4_K: d sc c - dmin m, factors from q4k_factors), each
 // rounded once.
 template <int FMT, int NJ>
-GQ_DEV gq_half8 rfrag(const RStep<FMT, NJ> &st, int j, int ks, int step, const QKf *qk) {
+GQ_DEV gq_half8 rfrag(const RStep<FMT, NJ> &st, int j, int ks, int step, const QKf *qk, uint32_t mg) {
   const int h = ks >> 1;
   gq_half2 p[4];
   if constexpr (FMT == GQ_FMT_Q8_0) {
@@ -513,19 +558,22 @@ GQ_DEV gq_half8 rfrag(const RStep<FMT, NJ> &st, int j, int ks, int step, const Q
 #pragma unroll
     for (int i = 0; i < 4; ++i) p[i] = (p[i] + off) * d2;
   } else {
-    const uint32_t w = st.q[j][h][ks & 1];
-    bytes_to_magic(w & 0x0F0F0F0Fu, p[0], p[1]);
-    bytes_to_magic((w >> 4) & 0x0F0F0F0Fu, p[2], p[3]);
+    // the 4-bit order (gq_nib_halves): pairs 1 and 3 are 1024 + 16 q, their
+    // results 16 x the weight (the activations hold those k divided by 16)
+    gq_nib_halves(st.q[j][h][ks & 1], mg, p);
     if constexpr (FMT == GQ_FMT_Q4_0) {
       const uint32_t db = st.d[j][h];
       const gq_half2 d2 = h2_of_bits16((step & 1) ? (db >> 16) : db);
-      const gq_half2 off = {(_Float16)-1032.0f, (_Float16)-1032.0f};
+      const gq_half2 off1 = {(_Float16)-1032.0f, (_Float16)-1032.0f};
+      const gq_half2 off16 = {(_Float16)-1152.0f, (_Float16)-1152.0f};  // 16 (q - 8), exact
 #pragma unroll
-      for (int i = 0; i < 4; ++i) p[i] = (p[i] + off) * d2;
+      for (int i = 0; i < 4; ++i) p[i] = (p[i] + ((i & 1) ? off16 : off1)) * d2;
     } else {
+      // sc q (or 16 sc q) is exact; then one rounding of d sc q - dmin m
       const QKf &f = qk[h];
 #pragma unroll
-      for (int i = 0; i < 4; ++i) p[i] = __builtin_elementwise_fma(__builtin_elementwise_fma(p[i], f.sc2, f.nsc2), f.d2, f.mn2);
+      for (int i = 0; i < 4; ++i)
+        p[i] = __builtin_elementwise_fma(__builtin_elementwise_fma(p[i], f.sc2, f.nsc2), f.d2, (i & 1) ? f.mn16 : f.mn2);
     }
   }
   gq_half8 o;
@@ -612,6 +660,9 @@ k_gemm_rb(const uint8_t *__restrict__ w, uint32_t sc_off, const _Float16 *__rest
       for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.f;
 
   RStep<FMT, NJ> wst[PD];
+  const uint32_t mg = gq_nib_magic();
+  uint32_t ao[BM / (8 * NW)];
+  a_offsets<BM, NW>(lda, M, m0, wave, lane, ao);
   const int arow = (BM / WM) * wm + (lane & 31);
   const int sw = a_swz(lane & 31);
 
@@ -622,7 +673,7 @@ k_gemm_rb(const uint8_t *__restrict__ w, uint32_t sc_off, const _Float16 *__rest
     using NB = std::integral_constant<int, (BUF + PD - 1) % PD>;  // buffer of step + PD - 1
     const int s1 = step + PD - 1 < nsteps ? step + PD - 1 : nsteps - 1;
     const int s2 = step + PD < nsteps ? step + PD : nsteps - 1;
-    load_a_lds<BM, NW>(a16, lda, M, m0, s1, wave, lane, As_of(NB{}));
+    load_a_lds_b<BM, NW>(a16, ao, s1, wave, As_of(NB{}));
     __builtin_amdgcn_sched_barrier(0);
     const _Float16 *As = As_of(buf_c) + arow * BK;
     RStep<FMT, NJ> &cur = wst[BUF];
@@ -640,7 +691,7 @@ k_gemm_rb(const uint8_t *__restrict__ w, uint32_t sc_off, const _Float16 *__rest
       if (ks + 1 < KS) read_a(ks + 1, (ks + 1) & 1);
 #pragma unroll
       for (int j = 0; j < NJ; ++j) {
-        const gq_half8 bf = rfrag<FMT, NJ>(cur, j, ks, step, qk[j]);
+        const gq_half8 bf = rfrag<FMT, NJ>(cur, j, ks, step, qk[j], mg);
 #pragma unroll
         for (int i = 0; i < TM; ++i) acc[i][j] = gq_mfma32(af[ks & 1][i], bf, acc[i][j]);
       }
@@ -657,7 +708,7 @@ k_gemm_rb(const uint8_t *__restrict__ w, uint32_t sc_off, const _Float16 *__rest
   auto prime = [&](auto b) {
     constexpr int i = decltype(b)::value;
     const int st = i < nsteps ? i : nsteps - 1;
-    if constexpr (i < PD - 1) load_a_lds<BM, NW>(a16, lda, M, m0, st, wave, lane, As_of(b));
+    if constexpr (i < PD - 1) load_a_lds_b<BM, NW>(a16, ao, st, wave, As_of(b));
     load_rstep<FMT, NJ>(w, qo, so, st, wst[i]);
   };
   // the tile's row scales, requested before the operands (the oldest load,
@@ -720,8 +771,8 @@ k_gemm_rb(const uint8_t *__restrict__ w, uint32_t sc_off, const _Float16 *__rest
 // as before, while rows with values beyond 65504 (outliers of the
 // down-projection input, bf16 spikes) or far below 1 keep fp16's full
 // relative precision instead of overflowing to Inf or going subnormal.
-// q4perm: each run of 8 in the order of the 4-bit B fragments of the skinny
-// GEMM (element e holds k slot {0,2,4,6,1,3,5,7}[e], elements 2, 3, 6, 7
+// q4perm: each run of 8 in the order of the 4-bit B fragments (gq_nib_halves) of the
+// skinny and register-B GEMMs (element e holds k slot {0,2,4,6,1,3,5,7}[e], elements 2, 3, 6, 7
 // divided by 16 -- exact, before the one rounding to fp16).
 GQ_DEV void load8_f32(const void *a, int a_dtype, size_t off, float (&v)[8]) {
   if (a_dtype == GQ_DT_BF16) {
@@ -958,7 +1009,7 @@ int launch_gemm(const void *packed, const _Float16 *a16, int lda, void *c, const
 
 extern "C" size_t gq_gemm_workspace_bytes(int fmt, size_t M, size_t K) {
   // activations are first written as fp16 [M][padded K (+ 8 for the skinny
-  // kernel)] unless they are fp16 of the padded width already (tiled kernel)
+  // kernel)] unless they are fp16 of the padded width already and in k order
   // fp16 A, then the M row scales (padded by one tile: the GEMM epilogues read
   // them four rows at a time)
   if (!gq_fmt_valid(fmt) || M > GQ_MAX_DIM || K > GQ_MAX_DIM) return 0;
@@ -1008,8 +1059,15 @@ extern "C" int gq_gemm(int fmt, const void *packed, const void *a, int a_dtype, 
   // Q6_K has no tiled kernel (gq_matmul runs the batch GEMV per 16 rows)
   GQ_CHECK(!gq_fmt_is_q6k(fmt), GQ_ERR_UNSUPPORTED);
   const _Float16 *a16 = (const _Float16 *)a;
-  const float *rs = nullptr;  // (fp16 activations of the padded width are used as they are)
-  if (a_dtype != GQ_DT_F16 || Kp != K) {
+  const float *rs = nullptr;
+  // the register-B kernel takes the 4-bit formats' B fragments in the
+  // gq_nib_halves order, so their activations are staged in that order; fp16
+  // activations of the padded width are used as they are otherwise
+  const int tile = pick_tile(fmt, (int)M, (int)N);
+  const int q4 = (fmt == GQ_FMT_Q4_0 || gq_fmt_is_q4k(fmt)) && tile != 1 && tile != 2 && tile != 3;
+  // (the register-B kernel addresses the activations with 32-bit offsets)
+  GQ_CHECK(tile == 1 || tile == 2 || tile == 3 || M * Kp * 2 < ((size_t)1 << 32), GQ_ERR_INVALID_ARGS);
+  if (a_dtype != GQ_DT_F16 || Kp != K || q4) {
     const size_t need = gq_gemm_workspace_bytes(fmt, M, K);
     if (!ws) {
       GQ_TRY(gq_default_workspace(need, &ws));
@@ -1017,7 +1075,7 @@ extern "C" int gq_gemm(int fmt, const void *packed, const void *a, int a_dtype, 
     }
     GQ_CHECK(ws_bytes >= need, GQ_ERR_WORKSPACE);
     float *rsw = (float *)((uint8_t *)ws + gq_align256(M * Kp * 2));
-    GQ_TRY(launch_a_to_f16(a, a_dtype, (_Float16 *)ws, rsw, (int)M, (int)K, (int)Kp, 0, s));
+    GQ_TRY(launch_a_to_f16(a, a_dtype, (_Float16 *)ws, rsw, (int)M, (int)K, (int)Kp, q4, s));
     a16 = (const _Float16 *)ws;
     rs = rsw;
   }

@@ -95,27 +95,6 @@ GQ_DEV void magic4(uint32_t u, gq_half2 &lo, gq_half2 &hi) {
 
 GQ_DEV gq_half2 splat_h(uint32_t b16) { return gq_bits_h2((b16 & 0xFFFFu) * 0x10001u); }
 
-// 4-bit codes straight to fp16: OR-ing a code into the low mantissa bits of
-// 1024.0 (0x6400) gives 1024 + q.  Of a code-group word (slots 0..3 in the
-// low nibbles of bytes 0..3, slots 4..7 in the high nibbles) four and-or ops
-// give the halves (s0, s2), (s4, s6) * 16, (s1, s3), (s5, s7) * 16 -- the high
-// nibbles come out as 1024 + 16 q.  Formats that use this order stage their
-// activations in the same order, with the "* 16" positions divided by 16
-// (exact), so each product is unchanged (kQ4Perm, kQ4Div16).
-// The magic is held in a VGPR (mg): a VOP3 and-or can then take the mask as its
-// one scalar operand and stays a single instruction.
-GQ_DEV uint32_t magic_h2_vgpr() {
-  uint32_t v;
-  asm volatile("v_mov_b32 %0, 0x64006400" : "=v"(v));
-  return v;
-}
-GQ_DEV void nib_halves(uint32_t w, uint32_t mg, gq_half2 (&p)[4]) {
-  const uint32_t v = w >> 8;
-  p[0] = gq_bits_h2((w & 0x000F000Fu) | mg);
-  p[1] = gq_bits_h2((w & 0x00F000F0u) | mg);
-  p[2] = gq_bits_h2((v & 0x000F000Fu) | mg);
-  p[3] = gq_bits_h2((v & 0x00F000F0u) | mg);
-}
 // B fragment element e of a 4-bit format holds slot kQ4Perm[e]; elements with
 // kQ4Div16 set are 16 x the weight
 constexpr int kQ4Perm[8] = {0, 2, 4, 6, 1, 3, 5, 7};
@@ -126,7 +105,7 @@ constexpr bool kNibOrder = FMT == GQ_FMT_Q4_0 || FMT == GQ_FMT_Q4_K;
 GQ_DEV _Float16 bits_h(uint32_t b16) { return __builtin_bit_cast(_Float16, (uint16_t)(b16 & 0xFFFFu)); }
 
 // The 16 weights a lane holds for MFMA step m -> fp16 B fragments (slots
-// 0..7, 8..15; for the 4-bit formats in nib_halves order).  g is the lane's
+// 0..7, 8..15; for the 4-bit formats in gq_nib_halves order).  g is the lane's
 // 16-lane group: its 16 weights are half g & 1 of 32-block 2 m + (g >> 1) of
 // the chunk (Q6_K: 16-element scale group 4 m + g).
 template <int FMT>
@@ -170,7 +149,7 @@ GQ_DEV void dequant_step(const HChunk<FMT> &c, int m, int g, uint32_t mg, gq_hal
 #pragma unroll
     for (int hw = 0; hw < 2; ++hw) {
       gq_half2 p[4];
-      nib_halves(hw ? w1 : w0, mg, p);
+      gq_nib_halves(hw ? w1 : w0, mg, p);
       gq_half8 &o = hw ? o1 : o0;
 #pragma unroll
       for (int q = 0; q < 4; ++q) {
@@ -333,7 +312,7 @@ k_gemv_h(const uint8_t *__restrict__ w, size_t sc_off, const float *__restrict__
   };
 
   const int nwin = ((c1 - c0) + WC - 1) / WC;  // this wave's windows (<= NI)
-  const uint32_t mg = magic_h2_vgpr();
+  const uint32_t mg = gq_nib_magic();
   HChunk<FMT> w0[WC], w1[WC], w2[WC];
   load_win(0, w0);
   load_win(1, w1);  // (a surplus re-read when NI == 1)
@@ -497,7 +476,7 @@ k_gemv_h1(const uint8_t *__restrict__ w, size_t sc_off, const float *__restrict_
   __syncthreads();
 
   // ---- 3. consume ------------------------------------------------------------------
-  const uint32_t mg = magic_h2_vgpr();
+  const uint32_t mg = gq_nib_magic();
   // this lane's A row: r (MR = 16) or r & 7 (MR = 8)
   const unsigned char *xb = xs + part * PB + (g * MR + (r & (MR - 1))) * 16;
   // two accumulator chains (halves 0 and 1 of each step), summed at the end
@@ -621,7 +600,7 @@ __global__ void __launch_bounds__(64 * KW) k_gemm_sk(const uint8_t *__restrict__
   for (int ct = 0; ct < CT; ++ct)
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt) acc[ct][mt] = gq_f4{0.f, 0.f, 0.f, 0.f};
-  const uint32_t mg = magic_h2_vgpr();
+  const uint32_t mg = gq_nib_magic();
   // A fragments requested AP steps ahead (ring of AP + 1; 2 and 3 measured no
   // faster)
   constexpr int AP = 1;
