@@ -732,6 +732,14 @@ k_gemm_rb(const uint8_t *__restrict__ w, uint32_t sc_off, const _Float16 *__rest
       if (step + 3 < nsteps) run_step(step + 3, B3{});
   }
 
+  // C of this workgroup's rows through a buffer resource starting at row m0
+  // (its range ends at row M) when a tile's offsets fit in 32 bits
+  constexpr uint32_t ES = CBF16 ? 2u : 4u;
+  const bool cfits = (size_t)N * BM * ES < ((size_t)1 << 31);
+  const size_t crange = (size_t)(M - m0) * (size_t)N * ES;
+  const __amdgpu_buffer_rsrc_t cr = __builtin_amdgcn_make_buffer_rsrc(
+      reinterpret_cast<uint8_t *>(c) + (size_t)m0 * N * ES, (short)0,
+      (int)(crange < 0xFFFFFFFFu ? crange : 0xFFFFFFFFu), 0x00020000);
 #pragma unroll
   for (int i = 0; i < TM; ++i) {
     // the row scales of this lane's 16 rows of MFMA tile row i (from LDS):
@@ -748,6 +756,22 @@ k_gemm_rb(const uint8_t *__restrict__ w, uint32_t sc_off, const _Float16 *__rest
     for (int j = 0; j < NJ; ++j) {
       const int n = n0 + (BN / WN) * wn + 32 * j + (lane & 31);
       if (n >= N) continue;
+      if (cfits) {
+        // one per-lane offset per MFMA tile, the row of each value a scalar
+        // offset; rows >= M lie beyond the resource's range, so the hardware
+        // drops their stores
+        const uint32_t vo = ((uint32_t)(mb - m0) * (uint32_t)N + (uint32_t)n) * ES;
+#pragma unroll
+        for (int v = 0; v < 16; ++v) {
+          const uint32_t so = (uint32_t)(8 * (v >> 2) + (v & 3)) * (uint32_t)N * ES;
+          const float o = acc[i][j][v] * rsv[v];
+          if constexpr (CBF16)
+            __builtin_amdgcn_raw_buffer_store_b16(f32_to_bf16_rne(o), cr, vo, so, 0);
+          else
+            __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(o), cr, vo, so, 0);
+        }
+        continue;
+      }
 #pragma unroll
       for (int v = 0; v < 16; ++v) {
         const int m = mb + 8 * (v >> 2) + (v & 3);
