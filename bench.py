@@ -639,12 +639,14 @@ def main():
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "q4_0 weights x int8 2-limb activations, i8 MFMA, f32 accumulate",
+        "dtype": "int8",
         "data": "synthetic (seeded GGUF Q4_0 blocks, x ~ N(0,1))",
         "config": {"workload": "Q4_0 decode GEMV 14336x4096 batch 1 (BASELINE configs[1]); one step = one "
                                "gq_gemv call (a single kernel) on one of the rotated weight copies; K steps "
                                "replayed from one HIP graph",
                    "N": 14336, "K": 4096, "batch": 1, "weight_copies_rotated": h["copies"],
+                   "arithmetic": "Q4_0 codes x two int8 limbs of the activations per 32-block on the int8 "
+                                 "MFMA, int32 products scaled and summed in f32",
                    "alg_bytes_per_step": h["alg_bytes"]},
         "pct_peak": round(h["pct_peak"], 2),
         "rel_l2_vs_oracle": h["rel_l2"],
