@@ -129,22 +129,49 @@ GQ_DEV void dequant_step(const HChunk<FMT> &c, int m, int g, uint32_t mg, gq_hal
       const gq_u4 &q = (m < 2) ? c.qa : c.qb;
       w0 = q[2 * (m & 1)];
       w1 = q[2 * (m & 1) + 1];
-      const uint32_t mv[4] = {c.meta[0], c.meta[1], c.meta[2], c.meta[3]};
-      uint32_t sc, mn;
-      gq_q4k_meta_codes(mv, 2 * m + (g >> 1), &sc, &mn);
+      // The lane's sub-blocks of steps 0..3 are 2 m + h (h = g >> 1): their
+      // 6-bit scales are the low bits of the 4 bytes of meta word 1 + h, the
+      // mins' low 2 bits the top bits of those bytes and their high 4 bits
+      // nibble h of the bytes of meta word 3.  All four steps' factors are
+      // decoded packed, two per instruction (the same values for every step
+      // of a chunk, so the unrolled steps share them).
+      const uint32_t h = (uint32_t)(g >> 1);
+      const uint32_t wh = h ? c.meta[2] : c.meta[1];
+      const uint32_t scb = wh & 0x3F3F3F3Fu;
+      const uint32_t mnb = ((wh >> 6) & 0x03030303u) | (((c.meta[3] >> (4u * h)) & 0x0F0F0F0Fu) << 2);
+      gq_half2 s01, s23, n01, n23;
+      magic4(scb, s01, s23);
+      magic4(mnb, n01, n23);
+      const gq_half2 k1024 = {(_Float16)-1024.0f, (_Float16)-1024.0f};
+      s01 = s01 + k1024;  // sc, exact
+      s23 = s23 + k1024;
+      n01 = n01 + k1024;  // m, exact
+      n23 = n23 + k1024;
+      // -(dmin m): the exact product rounded once, as (half)(-(float)dmin * m)
+      const _Float16 ndmin = -bits_h(c.meta[0] >> 16);
+      const gq_half2 nd2 = {ndmin, ndmin};
+      const gq_half2 hm01 = n01 * nd2, hm23 = n23 * nd2;
+      const gq_half2 k16 = {(_Float16)16.0f, (_Float16)16.0f};
       // (1024 + q) * sc - 1024 sc = q * sc exactly (<= 945; 16 q sc <= 15120,
-      // a multiple of 16: exact too), then one rounding of q sc d - dmin m
-      const _Float16 hsc = (_Float16)(float)sc;
-      const _Float16 dmin = bits_h(mv[0] >> 16);
-      const _Float16 hm = (_Float16)(-((float)dmin * (float)mn));
-      a1 = gq_half2{hsc, hsc};
-      b1 = gq_half2{(_Float16)(-1024.0f * (float)sc), (_Float16)(-1024.0f * (float)sc)};
+      // a multiple of 16: exact too), then one rounding of q sc d - dmin m;
+      // -1024 sc and 16 (-dmin m) are exact
+      const gq_half2 sp = m < 2 ? s01 : s23, mp = m < 2 ? hm01 : hm23;
+      const gq_half2 np = sp * k1024, mp16 = mp * k16;
+      if (m & 1) {
+        a1 = __builtin_shufflevector(sp, sp, 1, 1);
+        b1 = __builtin_shufflevector(np, np, 1, 1);
+        m1 = __builtin_shufflevector(mp, mp, 1, 1);
+        m16 = __builtin_shufflevector(mp16, mp16, 1, 1);
+      } else {
+        a1 = __builtin_shufflevector(sp, sp, 0, 0);
+        b1 = __builtin_shufflevector(np, np, 0, 0);
+        m1 = __builtin_shufflevector(mp, mp, 0, 0);
+        m16 = __builtin_shufflevector(mp16, mp16, 0, 0);
+      }
       a16 = a1;
       b16 = b1;
-      const _Float16 d = bits_h(mv[0]);
+      const _Float16 d = bits_h(c.meta[0]);
       d2 = gq_half2{d, d};
-      m1 = gq_half2{hm, hm};
-      m16 = gq_half2{(_Float16)(16.0f * (float)hm), (_Float16)(16.0f * (float)hm)};
     }
 #pragma unroll
     for (int hw = 0; hw < 2; ++hw) {
@@ -320,13 +347,15 @@ k_gemv_h(const uint8_t *__restrict__ w, size_t sc_off, const float *__restrict__
   store_x(0);
   __syncthreads();
   gq_f4 acc = gq_f4{0.f, 0.f, 0.f, 0.f}, acc2 = acc;  // chains of halves 0 and 1
-  // Window `it` (weights in w0).  PF: the weights of window it + 2 and the
-  // activations of window it + 1 are requested first.  The prefetch choice
-  // is a compile-time constant at every call, so no load sits under a branch
-  // (a branch around a load makes the compiler wait for every load issued
+  // Window `it` (weights in cur).  PF: the weights of window it + 2 (into
+  // nxt, the buffer window it - 1 consumed) and the activations of window
+  // it + 1 are requested first.  The three weight buffers rotate through the
+  // roles by unrolling (no register copies).  The prefetch choices are
+  // compile-time constants at every call, so no load sits under a branch (a
+  // branch around a load makes the compiler wait for every load issued
   // before it).
-  auto window = [&](int it, auto pfw, auto pfx) {
-    if constexpr (decltype(pfw)::value) load_win(it + 2, w2);
+  auto window = [&](int it, HChunk<FMT>(&cur)[WC], HChunk<FMT>(&nxt)[WC], auto pfw, auto pfx) {
+    if constexpr (decltype(pfw)::value) load_win(it + 2, nxt);
     if constexpr (decltype(pfx)::value) load_x(it + 1);
     if (it < nwin) {
       const unsigned char *xb = xs[it & 1][part] + (g * MR + (r & (MR - 1))) * 16;  // this lane's A row
@@ -339,7 +368,7 @@ k_gemv_h(const uint8_t *__restrict__ w, size_t sc_off, const float *__restrict__
             const gq_half8 a0 = *reinterpret_cast<const gq_half8 *>(xb + (ms * 2 + 0) * 4 * MR * 16);
             const gq_half8 a1 = *reinterpret_cast<const gq_half8 *>(xb + (ms * 2 + 1) * 4 * MR * 16);
             gq_half8 b0, b1;
-            dequant_step<FMT>(w0[j], m, g, mg, b0, b1);
+            dequant_step<FMT>(cur[j], m, g, mg, b0, b1);
             acc = mfma16h(a0, b0, acc);
             acc2 = mfma16h(a1, b1, acc2);
           }
@@ -348,18 +377,36 @@ k_gemv_h(const uint8_t *__restrict__ w, size_t sc_off, const float *__restrict__
     }
     if constexpr (decltype(pfx)::value) store_x((it + 1) & 1);
     __syncthreads();
-#pragma unroll
-    for (int j = 0; j < WC; ++j) {
-      w0[j] = w1[j];
-      w1[j] = w2[j];
-    }
   };
   using T_ = std::true_type;
   using F_ = std::false_type;
   int it = 0;
-  for (; it + 2 < NI; ++it) window(it, T_{}, T_{});
-  if (it + 1 < NI) window(it++, F_{}, T_{});
-  window(it, F_{}, F_{});
+  for (; it + 5 <= NI; it += 3) {
+    window(it, w0, w2, T_{}, T_{});
+    window(it + 1, w1, w0, T_{}, T_{});
+    window(it + 2, w2, w1, T_{}, T_{});
+  }
+  // the last 1..4 windows, the buffer roles continuing the rotation
+  switch (NI - it) {
+  case 1:
+    window(it, w0, w2, F_{}, F_{});
+    break;
+  case 2:
+    window(it, w0, w2, F_{}, T_{});
+    window(it + 1, w1, w0, F_{}, F_{});
+    break;
+  case 3:
+    window(it, w0, w2, T_{}, T_{});
+    window(it + 1, w1, w0, F_{}, T_{});
+    window(it + 2, w2, w1, F_{}, F_{});
+    break;
+  default:
+    window(it, w0, w2, T_{}, T_{});
+    window(it + 1, w1, w0, T_{}, T_{});
+    window(it + 2, w2, w1, F_{}, T_{});
+    window(it + 3, w0, w2, F_{}, F_{});
+    break;
+  }
 #pragma unroll
   for (int v = 0; v < 4; ++v) acc[v] += acc2[v];
 
