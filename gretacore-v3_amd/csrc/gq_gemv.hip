@@ -38,6 +38,16 @@
 
 namespace {
 
+constexpr size_t kLdsWg = 160 * 1024;  // LDS per workgroup on gfx950
+
+// Static LDS of a kernel (its __shared__ arrays), looked up once per kernel:
+// the launches check static + dynamic against the workgroup's LDS, so a plan
+// that would not fit fails with an error instead of running past its LDS.
+size_t kernel_static_lds(const void *kern) {
+  hipFuncAttributes a{};
+  return hipFuncGetAttributes(&a, kern) == hipSuccess ? a.sharedSizeBytes : kLdsWg;
+}
+
 // One weight matrix of a launch: T16 data, its scale-plane offset, output
 // y [batch][N], and the end (exclusive) of its workgroup range.
 struct GemvSeg {
@@ -190,7 +200,9 @@ k_gemv_q(const GemvFuse fz, const float *__restrict__ x, const int8_t *__restric
   const int8_t *zero;
   int lds_ld, scl_ld, kbase;  // limb row stride, scale row stride (blocks), slice origin
   if constexpr (!PREP) {
-    const XlLayout L = xl_layout(F::CK * ((C + KSPLIT - 1) / KSPLIT), NBC);
+    // limb rows for the nb batch rows present only (rows nb..NBC-1 of the A
+    // operand never carry data): batch 3 takes three quarters of batch 4's LDS
+    const XlLayout L = xl_layout(F::CK * ((C + KSPLIT - 1) / KSPLIT), nb < NBC ? nb : NBC);
     unsigned char *base = gq_dyn_lds + (size_t)wave * L.wave_bytes;
     int8_t *lm = reinterpret_cast<int8_t *>(base);
     float *sc = reinterpret_cast<float *>(base + L.scl_off);
@@ -260,7 +272,7 @@ k_gemv_q(const GemvFuse fz, const float *__restrict__ x, const int8_t *__restric
       } else {
         s = (float)quad_sum(t8) * (sx * (1.0f / 254.0f));
       }
-      if (8 * e8 < L.lk) {
+      if (b < nb && 8 * e8 < L.lk) {
         *reinterpret_cast<gq_u2 *>(lm + (2 * b) * L.lk + 8 * e8) = gq_u2{la[0], la[1]};
         *reinterpret_cast<gq_u2 *>(lm + (2 * b + 1) * L.lk + 8 * e8) = gq_u2{lb[0], lb[1]};
         if ((lane & 3) == 0)
@@ -531,13 +543,18 @@ int launch_r(const void *packed, const float *x, const void *ws, float *y, int N
   const size_t sc_off = gq_sc_plane_offset(FMT, N, K);
   const int8_t *xl = PREP ? (const int8_t *)ws : nullptr;
   const float *scl = PREP ? (const float *)((const uint8_t *)ws + gq_xl_bytes(FMT, K, nb)) : nullptr;
-  const size_t lds = PREP ? 0 : (size_t)ks * xl_layout(F::CK * ((C + ks - 1) / ks), NBC).wave_bytes;
+  const size_t lds = PREP ? 0 : (size_t)ks * xl_layout(F::CK * ((C + ks - 1) / ks), nb < NBC ? nb : NBC).wave_bytes;
   GemvFuse fz{};
   fz.seg[0] = GemvSeg{(const uint8_t *)packed, sc_off, y, N, (int)wgs};
   fz.nseg = 1;
 #define GQ_LAUNCH_KS(KS)                                                                                         \
-  hipLaunchKernelGGL((k_gemv_q<FMT, NBC, MT, R, NCKT, KS, PREP, 0>), dim3((unsigned)wgs), dim3(64 * KS), lds, s, \
-                     fz, x, xl, scl, K, C, Kp, nb)
+  {                                                                                                              \
+    const void *kern = (const void *)k_gemv_q<FMT, NBC, MT, R, NCKT, KS, PREP, 0>;                              \
+    static const size_t st = kernel_static_lds(kern);                                                           \
+    if (lds + st > kLdsWg) return GQ_ERR_UNSUPPORTED;                                                            \
+    hipLaunchKernelGGL((k_gemv_q<FMT, NBC, MT, R, NCKT, KS, PREP, 0>), dim3((unsigned)wgs), dim3(64 * KS), lds, \
+                       s, fz, x, xl, scl, K, C, Kp, nb);                                                         \
+  }
   switch (ks) {
   case 2: GQ_LAUNCH_KS(2); break;
   case 4: GQ_LAUNCH_KS(4); break;
@@ -554,6 +571,29 @@ int launch_r(const void *packed, const float *x, const void *ws, float *y, int N
 // the activation staging per weight) and KSPLIT waves, so that every wave holds
 // at most MAXC / R chunks and the grid has enough waves to keep HBM busy.
 // Every wave's chunk range [C*w/KSPLIT, C*(w+1)/KSPLIT) lies inside [0, C).
+// LDS bytes of the in-kernel activation staging (batch <= 4) for a plan: one
+// limb region per wave of KSPLIT.
+static size_t q_staging_lds(int fmt, size_t K, int batch, int ks) {
+  const int f = gq_fmt_is_q4k(fmt) ? GQ_FMT_Q4_K : gq_fmt_is_q6k(fmt) ? GQ_FMT_Q6_K : fmt;
+  const int ck = (f == GQ_FMT_Q4_K || f == GQ_FMT_Q6_K) ? 256 : 128;
+  const int C = (int)gq_chunks(f, K);
+  return (size_t)ks * (size_t)xl_layout(ck * ((C + ks - 1) / ks), batch).wave_bytes;
+}
+// The int8 kernel's static LDS beside the staging (k_gemv_q's arrays): the
+// scale-run copies (sdm, where the kernel loads scales by run), the K-split
+// reduction tiles (red) and the norm sums (ssred); batch <= 4 (NBC 1, 2 or 4,
+// MT 1).
+static size_t q_static_lds(int fmt, int batch, int R, int ks, bool fuse) {
+  const int f = gq_fmt_is_q4k(fmt) ? GQ_FMT_Q4_K : gq_fmt_is_q6k(fmt) ? GQ_FMT_Q6_K : fmt;
+  const size_t nbc = batch == 1 ? 1 : batch == 2 ? 2 : 4;
+  const bool sdma = f == GQ_FMT_Q8_0 || (ks == 16 && (f == GQ_FMT_Q4_0 || f == GQ_FMT_Q4_K));
+  const size_t sdm = sdma ? (size_t)ks * R * 1024 : 16;
+  const size_t red = (size_t)ks * R * nbc * 16 * 4;
+  const size_t ssred = (fuse ? (size_t)ks : 1) * nbc * 4;
+  return sdm + red + ssred;
+}
+constexpr size_t kLdsMax = 160 * 1024;  // LDS per workgroup on gfx950
+
 static int q_plan(int fmt, size_t N, size_t K, int batch, int *R_out, int *ksplit_out, int *chunks_per_wave_out) {
   GQ_TRY(gq_check_shape(fmt, N, K));
   GQ_CHECK(batch >= 1 && batch <= GQ_MAX_BATCH, GQ_ERR_UNSUPPORTED);
@@ -592,6 +632,12 @@ static int q_plan(int fmt, size_t N, size_t K, int batch, int *R_out, int *kspli
   int ks = 2;
   while (ks < 16 && (C + ks - 1) / ks > target) ks *= 2;
   while (ks < cap && ((tiles + R - 1) / R) * ks < 1024 && 2 * ks <= C) ks *= 2;
+  // batch <= 4 stages the activation limbs in LDS, about (2 batch + 1) bytes
+  // per k of the padded K: a smaller split pads less (Q4_K 4096 x 14336 at
+  // batch 4: 180 KiB at 16 waves, 154 KiB at 8), where the registers allow
+  while (batch <= 4 && ks > 2 && q_staging_lds(fmt, K, batch, ks) + q_static_lds(fmt, batch, R, ks, false) > kLdsMax &&
+         (C + ks / 2 - 1) / (ks / 2) <= maxc / R)
+    ks /= 2;
   const int e = env_int("GQ_GEMV_KSPLIT");
   if ((e == 2 || e == 4 || e == 8 || e == 16) && (C + e - 1) / e <= maxc / R) ks = e;
   if (R_out) *R_out = R;
@@ -670,16 +716,6 @@ int gq_gemv_h_min(void) {
   return (v >= 1 && v <= GQ_MAX_BATCH + 1) ? v : 5;
 }
 
-// LDS bytes of the in-kernel activation staging (batch <= 4) for a plan: one
-// limb region per wave of KSPLIT.
-static size_t q_staging_lds(int fmt, size_t K, int batch, int ks) {
-  const int f = gq_fmt_is_q4k(fmt) ? GQ_FMT_Q4_K : gq_fmt_is_q6k(fmt) ? GQ_FMT_Q6_K : fmt;
-  const int ck = (f == GQ_FMT_Q4_K || f == GQ_FMT_Q6_K) ? 256 : 128;
-  const int C = (int)gq_chunks(f, K);
-  const int nbc = batch == 1 ? 1 : batch == 2 ? 2 : 4;
-  return (size_t)ks * (size_t)xl_layout(ck * ((C + ks - 1) / ks), nbc).wave_bytes;
-}
-constexpr size_t kLdsMax = 160 * 1024;  // LDS per workgroup on gfx950
 
 // Which kernel gq_gemv uses: the fp16 batch kernel from gq_gemv_h_min() on,
 // for Q6_K beyond batch 2 (its int8 MFMA rows hold two batch rows), where K
@@ -694,7 +730,7 @@ static bool gq_gemv_on_h(int fmt, size_t N, size_t K, int batch) {
   const int f = gq_fmt_is_q4k(fmt) ? GQ_FMT_Q4_K : gq_fmt_is_q6k(fmt) ? GQ_FMT_Q6_K : fmt;
   const int maxc = (f == GQ_FMT_Q4_K || f == GQ_FMT_Q6_K) ? 4 : 8;
   if (cpw > maxc / R) return true;
-  return batch <= 4 && q_staging_lds(fmt, K, batch, ks) > kLdsMax;
+  return batch <= 4 && q_staging_lds(fmt, K, batch, ks) + q_static_lds(fmt, batch, R, ks, false) > kLdsMax;
 }
 
 extern "C" size_t gq_gemv_workspace_bytes(int fmt, size_t K, int batch) {
@@ -770,11 +806,16 @@ int launch_fused_nbc(const GemvFuse &fz, size_t wgs, int ks, const float *x, int
   const int C = (int)gq_chunks(FMT, K);
   const int Kp = (int)gq_kpad(FMT, K);
   if ((C + ks - 1) / ks > NCKT) return GQ_ERR_INVALID_ARGS;
-  const size_t lds = (size_t)ks * xl_layout(F::CK * ((C + ks - 1) / ks), NBC).wave_bytes;
+  const size_t lds = (size_t)ks * xl_layout(F::CK * ((C + ks - 1) / ks), nb < NBC ? nb : NBC).wave_bytes;
   if (lds > kLdsMax) return GQ_ERR_UNSUPPORTED;  // (long K at batch 3..4)
 #define GQ_LAUNCH_F(KS)                                                                                        \
-  hipLaunchKernelGGL((k_gemv_q<FMT, NBC, 1, R, NCKT, KS, false, FUSE>), dim3((unsigned)wgs), dim3(64 * KS), \
-                     lds, s, fz, x, nullptr, nullptr, K, C, Kp, nb)
+  {                                                                                                            \
+    const void *kern = (const void *)k_gemv_q<FMT, NBC, 1, R, NCKT, KS, false, FUSE>;                         \
+    static const size_t st = kernel_static_lds(kern);                                                         \
+    if (lds + st > kLdsWg) return GQ_ERR_UNSUPPORTED;                                                          \
+    hipLaunchKernelGGL((k_gemv_q<FMT, NBC, 1, R, NCKT, KS, false, FUSE>), dim3((unsigned)wgs), dim3(64 * KS), \
+                       lds, s, fz, x, nullptr, nullptr, K, C, Kp, nb);                                         \
+  }
   switch (ks) {
   case 2: GQ_LAUNCH_F(2); break;
   case 4: GQ_LAUNCH_F(4); break;

@@ -185,39 +185,66 @@ def test_gemv_plan_in_bounds(fmt, batch, monkeypatch):
         return
     # the int8 kernel at every batch (the split prep / prepped form uses it);
     # up to batch 4 gq_gemv stages the activation limbs in LDS, and where that
-    # staging would exceed the 160 KiB of a workgroup the fp16 kernel takes the
-    # shape instead (Q4_K 4096 x 14336 at batch 3..4)
+    # staging would exceed the 160 KiB of a workgroup even at a smaller K split
+    # the fp16 kernel takes the shape instead (Q4_K 4096 x 16384 at batch 4)
     monkeypatch.setenv("GQ_GEMV_H_MIN", "17")
     for n, k in SHAPES:
         if k % (256 if fmt == gq.FMT_Q4_K else 32):
             continue
         if batch <= 4 and staging_lds(fmt, n, k, batch) > 160 * 1024:
-            assert gq.gemv_plan(fmt, n, k, batch) != gq.gemv_plan(fmt, n, k, 1)
+            assert gq.gemv_plan(fmt, n, k, batch) != int8_plan(fmt, n, k, batch)
             emulate_h(fmt, n, k, batch)
             continue
+        if batch <= 4:
+            assert gq.gemv_plan(fmt, n, k, batch) == int8_plan(fmt, n, k, batch)
         emulate(fmt, n, k, batch)
 
 
-def staging_lds(fmt, n, k, batch):
-    """LDS bytes of the int8 kernel's in-kernel activation staging: per wave,
-    two int8 limb rows per staged batch row of the wave's K slice, a zero row,
-    and a float4 per (batch row, 32-block)."""
-    R, ks, cpw = gq.gemv_plan(fmt, n, k, 1)  # the int8 plan's K split (batch-independent)
+def staging_lds(fmt, n, k, batch, ks=None, R=None):
+    """LDS bytes of the int8 kernel at batch <= 4: the in-kernel activation
+    staging (per wave, two int8 limb rows per batch row of the wave's K
+    slice, a zero row and a float4 per (batch row, 32-block)) plus the
+    kernel's static arrays (the scale-run copies where scales load by run, the
+    K-split reduction tiles, the norm sums)."""
+    if ks is None or R is None:
+        R, ks, _ = int8_plan(fmt, n, k, batch)
     C = -(-k // CK[fmt])
     lk = CK[fmt] * -(-C // ks)
-    nb = 1 if batch == 1 else 2 if batch == 2 else 4
-    wave = (2 * nb * lk + lk + nb * (lk // 32) * 16 + 15) & ~15
-    return ks * wave
+    wave = (2 * batch * lk + lk + batch * (lk // 32) * 16 + 15) & ~15
+    nbc = 1 if batch == 1 else 2 if batch == 2 else 4
+    sdma = fmt == gq.FMT_Q8_0 or (ks == 16 and fmt in (gq.FMT_Q4_0, gq.FMT_Q4_K, gq.FMT_Q4_K_GGML))
+    static = (ks * R * 1024 if sdma else 16) + ks * R * nbc * 64 + nbc * 4
+    return ks * wave + static
+
+
+def int8_plan(fmt, n, k, batch):
+    """The int8 kernel's plan: the batch-1 plan, its K split halved while its
+    LDS (batch <= 4) exceeds 160 KiB and the halved split's chunks per wave
+    still fit MAXC / R."""
+    R, ks, cpw = gq.gemv_plan(fmt, n, k, 1)
+    C = -(-k // CK[fmt])
+    while (batch <= 4 and ks > 2 and staging_lds(fmt, n, k, batch, ks, R) > 160 * 1024
+           and -(-C // (ks // 2)) <= MAXC[fmt] // R):
+        ks //= 2
+    return R, ks, -(-C // ks)
 
 
 def test_int8_staging_lds_guard():
-    """The known case: Q4_K 4096 x 14336 at batch 4 would stage 176 KiB (16
-    waves of 3.5 KiB-slices: 2 x 4 x 1024 + 1024 + 4 x 32 x 16 bytes each) and
-    runs on the fp16 batch kernel; at batch 2 (112 KiB) it stays on the int8
-    kernel."""
-    assert staging_lds(gq.FMT_Q4_K, 4096, 14336, 4) == 16 * 11264
-    assert staging_lds(gq.FMT_Q4_K, 4096, 14336, 2) <= 160 * 1024
-    assert gq.gemv_plan(gq.FMT_Q4_K, 4096, 14336, 4) != gq.gemv_plan(gq.FMT_Q4_K, 4096, 14336, 2)
+    """Q4_K 4096 x 14336: at batch 4 the 16 waves would need 176 KiB of
+    staging (3.5 KiB slices padded to 1024 k: 2 x 4 x 1024 + 1024 + 4 x 32 x
+    16 bytes each) besides 20 KiB of static arrays, and a smaller split would
+    need 7 chunks per wave (the registers hold 4): the fp16 batch kernel takes
+    it.  Batch 3 stages its three rows only (136 KiB + 20 KiB) and stays on the
+    int8 kernel.  Q4_0 at K = 14336, batch 4: 154 KiB of staging at 16 waves
+    plus the static 20 KiB exceed the LDS, 8 waves would hold 14 chunks (the
+    registers hold 8): the fp16 kernel; batch 3 stays on the int8 kernel."""
+    assert staging_lds(gq.FMT_Q4_K, 4096, 14336, 4, 16, 1) == 16 * 11264 + 16384 + 4096 + 16
+    assert gq.gemv_plan(gq.FMT_Q4_K, 4096, 14336, 4) != int8_plan(gq.FMT_Q4_K, 4096, 14336, 4)
+    assert gq.gemv_plan(gq.FMT_Q4_K, 4096, 14336, 3) == (1, 16, 4) == int8_plan(gq.FMT_Q4_K, 4096, 14336, 3)
+    assert staging_lds(gq.FMT_Q4_K, 4096, 14336, 3) == 16 * 8704 + 16384 + 4096 + 16 <= 160 * 1024
+    assert staging_lds(gq.FMT_Q4_0, 4096, 14336, 4, 16, 1) > 160 * 1024
+    assert gq.gemv_plan(gq.FMT_Q4_0, 4096, 14336, 4) != int8_plan(gq.FMT_Q4_0, 4096, 14336, 4)
+    assert gq.gemv_plan(gq.FMT_Q4_0, 4096, 14336, 3) == (1, 16, 7) == int8_plan(gq.FMT_Q4_0, 4096, 14336, 3)
 
 
 def test_plan_single_chunk_has_idle_wave():

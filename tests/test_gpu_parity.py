@@ -138,6 +138,19 @@ def test_gemv_batch_kernel_plans(dev, fmt, shape, batch):
     assert err <= TOL, err
 
 
+@pytest.mark.parametrize("fmt,n,k,batch", [(O.Q4_K, 4096, 14336, 3), (O.Q4_K, 1000, 16384, 3),
+                                           (O.Q4_0, 4096, 14336, 3), (O.Q8_0, 300, 14336, 3),
+                                           (O.Q4_0, 700, 16384, 3), (O.Q4_0, 4096, 14336, 4),
+                                           (O.Q4_K, 4096, 14336, 4)])
+def test_gemv_long_k_small_batch(dev, fmt, n, k, batch):
+    """Long K at batch 3..4: the int8 kernel stages its activation limbs for
+    the batch rows present only and takes the shape where staging and static
+    arrays fit the 160 KiB of a workgroup (batch 3 here); batch 4 at K =
+    14336 does not fit and runs on the fp16 batch kernel."""
+    err = _gemv_case(dev, fmt, n, k, batch, seed=500 + batch + fmt)
+    assert err <= TOL, err
+
+
 @pytest.mark.parametrize("fmt", [O.Q4_0, O.Q8_0, O.Q4_K, O.Q6_K])
 @pytest.mark.parametrize("batch", [1, 3])
 def test_gemv_long_k_falls_back(dev, fmt, batch):
