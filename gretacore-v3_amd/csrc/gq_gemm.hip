@@ -815,15 +815,20 @@ k_gemm_rb(const uint8_t *__restrict__ w, uint32_t sc_off, const _Float16 *__rest
 // q4perm: each run of 8 in the order of the 4-bit B fragments (gq_nib_halves) of the
 // skinny and register-B GEMMs (element e holds k slot {0,2,4,6,1,3,5,7}[e], elements 2, 3, 6, 7
 // divided by 16 -- exact, before the one rounding to fp16).
-GQ_DEV void load8_f32(const void *a, int a_dtype, size_t off, float (&v)[8]) {
-  if (a_dtype == GQ_DT_BF16) {
+// 8 activations from offset off of a (bf16, fp16 or fp32: DT) as floats.  The
+// conversion kernels issue all their loads unconditionally (addresses clamped into the row), so
+// no load sits under a branch -- a branch around a load makes the compiler
+// wait for every load issued before it, one round trip per load
+template <int DT>
+GQ_DEV void load8_t(const void *a, size_t off, float (&v)[8]) {
+  if constexpr (DT == GQ_DT_BF16) {
     const gq_u4 u = gq_ld16(reinterpret_cast<const uint16_t *>(a) + off);
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
       v[2 * q] = __uint_as_float(u[q] << 16);
       v[2 * q + 1] = __uint_as_float(u[q] & 0xFFFF0000u);
     }
-  } else if (a_dtype == GQ_DT_F16) {
+  } else if constexpr (DT == GQ_DT_F16) {
     const gq_half8 h = *reinterpret_cast<const gq_half8 *>(reinterpret_cast<const _Float16 *>(a) + off);
 #pragma unroll
     for (int q = 0; q < 8; ++q) v[q] = (float)h[q];
@@ -851,9 +856,9 @@ GQ_DEV gq_half8 conv8(const float (&v)[8], float f, int q4perm) {
   return h;
 }
 
-__global__ void __launch_bounds__(kConvThreads) k_a_to_f16(const void *__restrict__ a, int a_dtype,
-                                                           _Float16 *__restrict__ o, float *__restrict__ rs, int K,
-                                                           int ldo, int q4perm) {
+template <int DT, int RUNS>
+__global__ void __launch_bounds__(kConvThreads) k_a_to_f16(const void *__restrict__ a, _Float16 *__restrict__ o,
+                                                           float *__restrict__ rs, int K, int ldo, int q4perm) {
   __shared__ float wmax[kConvThreads / 64];
   const size_t m = blockIdx.x;
   const int tid = threadIdx.x;
@@ -864,15 +869,20 @@ __global__ void __launch_bounds__(kConvThreads) k_a_to_f16(const void *__restric
 #pragma unroll
   for (int r = 0; r < kConvRuns; ++r) {
     const int k0 = 8 * (tid + kConvThreads * r);
+    if (r < RUNS) load8_t<DT>(a, m * K + (k0 < K ? k0 : 0), v[r]);  // (RUNS covers the row up to SPAN)
+  }
 #pragma unroll
-    for (int e = 0; e < 8; ++e) v[r][e] = 0.f;
-    if (k0 < K) load8_f32(a, a_dtype, m * K + k0, v[r]);
+  for (int r = 0; r < kConvRuns; ++r) {
+    const int k0 = 8 * (tid + kConvThreads * r);
 #pragma unroll
-    for (int e = 0; e < 8; ++e) amax = fmaxf(amax, fabsf(v[r][e]));
+    for (int e = 0; e < 8; ++e) {
+      v[r][e] = (r < RUNS && k0 < K) ? v[r][e] : 0.f;
+      amax = fmaxf(amax, fabsf(v[r][e]));
+    }
   }
   for (int k0 = SPAN + 8 * tid; k0 < K; k0 += 8 * kConvThreads) {  // (rows longer than SPAN)
     float u[8];
-    load8_f32(a, a_dtype, m * K + k0, u);
+    load8_t<DT>(a, m * K + k0, u);
 #pragma unroll
     for (int e = 0; e < 8; ++e) amax = fmaxf(amax, fabsf(u[e]));
   }
@@ -897,7 +907,7 @@ __global__ void __launch_bounds__(kConvThreads) k_a_to_f16(const void *__restric
   }
   for (int k0 = SPAN + 8 * tid; k0 < ldo; k0 += 8 * kConvThreads) {
     float u[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-    if (k0 < K) load8_f32(a, a_dtype, m * K + k0, u);
+    if (k0 < K) load8_t<DT>(a, m * K + k0, u);
     *reinterpret_cast<gq_half8 *>(o + m * ldo + k0) = conv8(u, f, q4perm);
   }
 }
@@ -906,8 +916,8 @@ __global__ void __launch_bounds__(kConvThreads) k_a_to_f16(const void *__restric
 // workgroup), the row held in registers (R runs of 8 per lane) and its
 // largest magnitude reduced within the wave -- no LDS, no barrier.  The same
 // scaling and rounding as k_a_to_f16.
-template <int R>
-__global__ void __launch_bounds__(256) k_a_to_f16_w(const void *__restrict__ a, int a_dtype, _Float16 *__restrict__ o,
+template <int R, int DT>
+__global__ void __launch_bounds__(256) k_a_to_f16_w(const void *__restrict__ a, _Float16 *__restrict__ o,
                                                     float *__restrict__ rs, int M, int K, int ldo, int q4perm) {
   const int lane = threadIdx.x & 63;
   const size_t m = (size_t)blockIdx.x * 4 + (threadIdx.x >> 6);
@@ -917,11 +927,16 @@ __global__ void __launch_bounds__(256) k_a_to_f16_w(const void *__restrict__ a, 
 #pragma unroll
   for (int r = 0; r < R; ++r) {
     const int k0 = 8 * (lane + 64 * r);
+    load8_t<DT>(a, m * K + (k0 < K ? k0 : 0), v[r]);
+  }
 #pragma unroll
-    for (int e = 0; e < 8; ++e) v[r][e] = 0.f;
-    if (k0 < K) load8_f32(a, a_dtype, m * K + k0, v[r]);
+  for (int r = 0; r < R; ++r) {
+    const int k0 = 8 * (lane + 64 * r);
 #pragma unroll
-    for (int e = 0; e < 8; ++e) amax = fmaxf(amax, fabsf(v[r][e]));
+    for (int e = 0; e < 8; ++e) {
+      v[r][e] = k0 < K ? v[r][e] : 0.f;
+      amax = fmaxf(amax, fabsf(v[r][e]));
+    }
   }
 #pragma unroll
   for (int o2 = 32; o2 > 0; o2 >>= 1) amax = fmaxf(amax, __shfl_xor(amax, o2, 64));
@@ -938,22 +953,35 @@ __global__ void __launch_bounds__(256) k_a_to_f16_w(const void *__restrict__ a, 
 }
 
 // A -> fp16 [M][ldo] with per-row scales: k_a_to_f16_w for at least 1024 rows
-// of up to 8192 padded columns (2048 x 4096 bf16: 13.5 -> 11.1 us), else
-// k_a_to_f16 (one workgroup of 8 waves per row: fewer rows keep more waves busy)
+// of up to 8192 padded columns (2048 x 4096 bf16: 13.5 -> 11.1 us with loads
+// under branches), else k_a_to_f16 (one workgroup of 8 waves per row: fewer
+// rows keep more waves busy) with the runs per thread the row needs
+template <int DT>
+int launch_a_to_f16_t(const void *a, _Float16 *o, float *rs, int M, int K, int ldo, int q4perm, hipStream_t s) {
+  const unsigned g4 = (unsigned)((M + 3) / 4);
+  if (M >= 1024 && ldo <= 2048)
+    hipLaunchKernelGGL((k_a_to_f16_w<4, DT>), dim3(g4), dim3(256), 0, s, a, o, rs, M, K, ldo, q4perm);
+  else if (M >= 1024 && ldo <= 4096)
+    hipLaunchKernelGGL((k_a_to_f16_w<8, DT>), dim3(g4), dim3(256), 0, s, a, o, rs, M, K, ldo, q4perm);
+  else if (M >= 1024 && ldo <= 8192)
+    hipLaunchKernelGGL((k_a_to_f16_w<16, DT>), dim3(g4), dim3(256), 0, s, a, o, rs, M, K, ldo, q4perm);
+  else if (K <= 8 * kConvThreads)
+    hipLaunchKernelGGL((k_a_to_f16<DT, 1>), dim3((unsigned)M), dim3(kConvThreads), 0, s, a, o, rs, K, ldo, q4perm);
+  else if (K <= 2 * 8 * kConvThreads)
+    hipLaunchKernelGGL((k_a_to_f16<DT, 2>), dim3((unsigned)M), dim3(kConvThreads), 0, s, a, o, rs, K, ldo, q4perm);
+  else if (K <= 4 * 8 * kConvThreads)
+    hipLaunchKernelGGL((k_a_to_f16<DT, 4>), dim3((unsigned)M), dim3(kConvThreads), 0, s, a, o, rs, K, ldo, q4perm);
+  else
+    hipLaunchKernelGGL((k_a_to_f16<DT, kConvRuns>), dim3((unsigned)M), dim3(kConvThreads), 0, s, a, o, rs, K, ldo,
+                       q4perm);
+  return gq_last_launch();
+}
+
 int launch_a_to_f16(const void *a, int a_dtype, _Float16 *o, float *rs, int M, int K, int ldo, int q4perm,
                     hipStream_t s) {
-  const unsigned g4 = (unsigned)((M + 3) / 4);
-  if (M < 1024)
-    hipLaunchKernelGGL(k_a_to_f16, dim3((unsigned)M), dim3(kConvThreads), 0, s, a, a_dtype, o, rs, K, ldo, q4perm);
-  else if (ldo <= 2048)
-    hipLaunchKernelGGL(k_a_to_f16_w<4>, dim3(g4), dim3(256), 0, s, a, a_dtype, o, rs, M, K, ldo, q4perm);
-  else if (ldo <= 4096)
-    hipLaunchKernelGGL(k_a_to_f16_w<8>, dim3(g4), dim3(256), 0, s, a, a_dtype, o, rs, M, K, ldo, q4perm);
-  else if (ldo <= 8192)
-    hipLaunchKernelGGL(k_a_to_f16_w<16>, dim3(g4), dim3(256), 0, s, a, a_dtype, o, rs, M, K, ldo, q4perm);
-  else
-    hipLaunchKernelGGL(k_a_to_f16, dim3((unsigned)M), dim3(kConvThreads), 0, s, a, a_dtype, o, rs, K, ldo, q4perm);
-  return gq_last_launch();
+  if (a_dtype == GQ_DT_BF16) return launch_a_to_f16_t<GQ_DT_BF16>(a, o, rs, M, K, ldo, q4perm, s);
+  if (a_dtype == GQ_DT_F16) return launch_a_to_f16_t<GQ_DT_F16>(a, o, rs, M, K, ldo, q4perm, s);
+  return launch_a_to_f16_t<GQ_DT_F32>(a, o, rs, M, K, ldo, q4perm, s);
 }
 
 template <int FMT, int CBF16, int BM, int BN>
