@@ -347,16 +347,18 @@ k_gemv_h(const uint8_t *__restrict__ w, size_t sc_off, const float *__restrict__
   store_x(0);
   __syncthreads();
   gq_f4 acc = gq_f4{0.f, 0.f, 0.f, 0.f}, acc2 = acc;  // chains of halves 0 and 1
-  // Window `it` (weights in cur).  PF: the weights of window it + 2 (into
-  // nxt, the buffer window it - 1 consumed) and the activations of window
-  // it + 1 are requested first.  The three weight buffers rotate through the
+  // Window `it` (weights in cur).  PF: the activations of window it + 1 and
+  // the weights of window it + 2 (into nxt, the buffer window it - 1
+  // consumed) are requested first.  The three weight buffers rotate through the
   // roles by unrolling (no register copies).  The prefetch choices are
   // compile-time constants at every call, so no load sits under a branch (a
   // branch around a load makes the compiler wait for every load issued
   // before it).
   auto window = [&](int it, HChunk<FMT>(&cur)[WC], HChunk<FMT>(&nxt)[WC], auto pfw, auto pfx) {
-    if constexpr (decltype(pfw)::value) load_win(it + 2, nxt);
+    // (activations first: the wait for them before the staging below then
+    // leaves the weight loads in flight)
     if constexpr (decltype(pfx)::value) load_x(it + 1);
+    if constexpr (decltype(pfw)::value) load_win(it + 2, nxt);
     if (it < nwin) {
       const unsigned char *xb = xs[it & 1][part] + (g * MR + (r & (MR - 1))) * 16;  // this lane's A row
 #pragma unroll
