@@ -631,7 +631,12 @@ static int q_plan(int fmt, size_t N, size_t K, int batch, int *R_out, int *kspli
   if (R == 1 && (C + 15) / 16 <= maxc / 2) target = maxc / 2;
   int ks = 2;
   while (ks < 16 && (C + ks - 1) / ks > target) ks *= 2;
-  while (ks < cap && ((tiles + R - 1) / R) * ks < 1024 && 2 * ks <= C) ks *= 2;
+  // (grown to 512 waves and 8 per workgroup at most: small grids ran faster
+  // so than at 1024 waves / 16 per workgroup -- batch 1 at K = 4096, 4 to 64
+  // workgroups: Q4_0 2.7-2.9 us at 8 waves against 3.2-3.7 at 16, Q4_K 2.9-3.1
+  // against 3.4-3.6, Q8_0 512 rows 3.26 against 4.36; 2048 x 2048 Q4_0 2.65 us
+  // at 4 against 2.85 at 8; the register target above may still ask for 16)
+  while (ks < cap && ks < 8 && ((tiles + R - 1) / R) * ks < 512 && 2 * ks <= C) ks *= 2;
   // batch <= 4 stages the activation limbs in LDS, about (2 batch + 1) bytes
   // per k of the padded K: a smaller split pads less (Q4_K 4096 x 14336 at
   // batch 4: 180 KiB at 16 waves, 154 KiB at 8), where the registers allow
