@@ -23,6 +23,23 @@ namespace {
 GQ_DEV size_t scale_idx(size_t n, size_t K, size_t k, int gs, int srow) {
   return srow ? (n * K) / (size_t)gs + k / (size_t)gs : (n * K + k) / (size_t)gs;
 }
+// The same with the row's part computed once: for row n, q0 = (n K) / gs and
+// r0 = (n K) % gs; a lane's index for k is then q0 + k / gs (srow) or
+// q0 + (r0 + k) / gs, one 32-bit division -- a shift where gs is a power of
+// two (gsh >= 0) -- instead of a 64-bit division per load.
+struct RowScale {
+  size_t q0;
+  uint32_t r0;
+};
+GQ_DEV RowScale row_scale(size_t n, size_t K, int gs) {
+  const size_t nk = n * K;
+  return RowScale{nk / (size_t)gs, (uint32_t)(nk % (size_t)gs)};
+}
+GQ_DEV int gs_shift(int gs) { return (gs & (gs - 1)) == 0 ? __builtin_ctz((unsigned)gs) : -1; }
+GQ_DEV size_t scale_idx_row(RowScale rsc, uint32_t k, int gs, int gsh, int srow) {
+  const uint32_t x = srow ? k : rsc.r0 + k;
+  return rsc.q0 + (gsh >= 0 ? x >> gsh : x / (uint32_t)gs);
+}
 
 GQ_DEV float wave_sum(float v) {
 #pragma unroll
@@ -121,7 +138,7 @@ k_compat_gemv_seg(const TA *__restrict__ a, const uint8_t *__restrict__ b, float
                   const float *__restrict__ scales, const float *__restrict__ head_scales, int M, int N, int K,
                   int lda, int ldc, int gs, int srow, int head_dim) {
   const int lane = threadIdx.x & 63;
-  const int wave = threadIdx.x >> 6;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int n0 = ((int)blockIdx.x * 4 + wave) * RW;
   if (n0 >= N) return;
   const int m_base = (int)blockIdx.y * MB;
@@ -134,6 +151,10 @@ k_compat_gemv_seg(const TA *__restrict__ a, const uint8_t *__restrict__ b, float
   const TA *arow[MB];
 #pragma unroll
   for (int i = 0; i < MB; ++i) arow[i] = a + (size_t)(m_base + (i < mcount ? i : 0)) * lda;
+  const int gsh = gs_shift(gs);
+  RowScale rsc[RW];
+#pragma unroll
+  for (int r = 0; r < RW; ++r) rsc[r] = row_scale((size_t)(n0 + r < N ? n0 + r : N - 1), (size_t)K, gs);
 #pragma unroll 2
   for (int k0 = 16 * lane; k0 < K; k0 += 1024) {
     float xv[MB][16];
@@ -177,7 +198,7 @@ k_compat_gemv_seg(const TA *__restrict__ a, const uint8_t *__restrict__ b, float
 #pragma unroll
         for (int e = 0; e < 16; ++e) wv[e] = (float)(int8_t)((p[e >> 2] >> (8 * (e & 3))) & 0xFFu);
       }
-      const float sc = scales ? scales[scale_idx(n, K, k0, gs, srow)] : 1.0f;
+      const float sc = scales ? scales[scale_idx_row(rsc[r], (uint32_t)k0, gs, gsh, srow)] : 1.0f;
 #pragma unroll
       for (int i = 0; i < MB; ++i) {
         float d = 0.f;
@@ -217,8 +238,9 @@ k_compat_gemv_lds(const TA *__restrict__ a, const uint8_t *__restrict__ b, float
   const int wave = threadIdx.x >> 6;
   const int m_base = (int)blockIdx.y * MB;
   const int mcount = min(MB, M - m_base);
-  const int n0 = ((int)blockIdx.x * 16 + wave) * RW;
+  const int n0 = ((int)blockIdx.x * 16 + __builtin_amdgcn_readfirstlane(wave)) * RW;
   const int nseg = (K + 1023) / 1024;
+  const int gsh = gs_shift(gs);
   // weights and scales of every segment of the wave's RW rows first (clamped,
   // unconditional; a row past N is computed, never stored)
   gq_u4 w8[RW][INT4 ? 1 : NSEG];
@@ -227,6 +249,7 @@ k_compat_gemv_lds(const TA *__restrict__ a, const uint8_t *__restrict__ b, float
 #pragma unroll
   for (int r = 0; r < RW; ++r) {
     const int nr = n0 + r < N ? n0 + r : N - 1;
+    const RowScale rsc = row_scale((size_t)nr, (size_t)K, gs);
 #pragma unroll
     for (int it = 0; it < NSEG; ++it) {
       int k0 = 16 * lane + 1024 * it;
@@ -234,7 +257,7 @@ k_compat_gemv_lds(const TA *__restrict__ a, const uint8_t *__restrict__ b, float
       const size_t idx = (size_t)nr * K + k0;
       if constexpr (INT4) w4[r][it] = gq_ld8(b + idx / 2);
       else w8[r][it] = gq_ld16(b + idx);
-      sc[r][it] = scales ? scales[scale_idx(nr, K, k0, gs, srow)] : 1.0f;
+      sc[r][it] = scales ? scales[scale_idx_row(rsc, (uint32_t)k0, gs, gsh, srow)] : 1.0f;
     }
   }
   // activations -> LDS
