@@ -1023,6 +1023,11 @@ int launch_rb(const void *packed, const _Float16 *a16, int lda, void *c, const f
 }
 
 // Kernel and tile shape (measured on MI355X, M = 64 .. 2048 x N = 4096 / 14336):
+//  13: register-B kernel, 128 x 256 on 8 waves of 128 x 32 (the 1 x 8 grid on
+//      half the rows: each weight dequantized once), depth 4, for >= 192
+//      workgroups: 4-7 % faster than 4 in an interleaved A/B (512 x 14336 x
+//      4096 Q4_0 / Q4_K / Q8_0 66.4 / 73.7 / 69.9 vs 71.3 / 76.7 / 73.5 us,
+//      2048 x 4096 x 4096 Q4_0 76.2 vs 81.8, 1024 x 14336 124.6 vs 133.8)
 //  12: register-B kernel, 256 x 256 on 8 waves of 256 x 32 (448 workgroups at
 //      2048 x 14336): each wave dequantizes its B fragments for all 256 rows,
 //      so no two waves convert the same weights (twice the activation-fragment
@@ -1030,7 +1035,7 @@ int launch_rb(const void *packed, const _Float16 *a16, int lda, void *c, const f
 //      2-8 % faster than 0 (2 x 4 waves) and 3 (LDS-B) for every format
 //   0: register-B kernel, 256 x 256, 2 x 4 waves of 128 x 64
 //   3: LDS-B kernel, 256 x 256
-//   4: register-B, 256 x 128, for >= 192 workgroups
+//   4: register-B, 256 x 128 (2 x 4 waves), the former choice of 13's grids
 //   6: register-B, 128 x 128, for >= 192 workgroups (1024 x 4096, 256 x 14336)
 //   9: register-B, 128 x 64 (4 waves), for >= 192 workgroups (512 x 4096:
 //      50 vs 56 us with 128 x 128; 128 x 14336: 48 vs 54 us)
@@ -1045,7 +1050,7 @@ int pick_tile(int fmt, int M, int N) {
   auto wgs = [&](int bm, int bn) { return (long)((M + bm - 1) / bm) * ((N + bn - 1) / bn); };
   if (const char *e = getenv("GQ_GEMM_TILE")) return atoi(e);
   if (wgs(256, 256) >= 384) return 12;
-  if (wgs(256, 128) >= 192) return 4;
+  if (wgs(128, 256) >= 192) return 13;
   if (wgs(128, 128) >= 192) return 6;
   if (wgs(128, 64) >= 192) return 9;
   return 11;
@@ -1065,6 +1070,7 @@ int launch_fmt(const void *packed, const _Float16 *a16, int lda, void *c, const 
   case 10: return launch_rb<FMT, CBF16, 64, 128, 2, 4>(packed, a16, lda, c, rs, M, N, K, s);
   case 11: return launch_rb<FMT, CBF16, 64, 64, 2, 2>(packed, a16, lda, c, rs, M, N, K, s);
   case 12: return launch_rb<FMT, CBF16, 256, 256, 1, 8>(packed, a16, lda, c, rs, M, N, K, s, 3);
+  case 13: return launch_rb<FMT, CBF16, 128, 256, 1, 8>(packed, a16, lda, c, rs, M, N, K, s);
   default: return launch_rb<FMT, CBF16, 128, 128, 2, 4>(packed, a16, lda, c, rs, M, N, K, s);
   case 3: return launch_cfg<FMT, CBF16, 256, 256>(packed, a16, lda, c, rs, M, N, K, s);
   case 1: return launch_cfg<FMT, CBF16, 256, 128>(packed, a16, lda, c, rs, M, N, K, s);

@@ -123,8 +123,8 @@ def _gemm_check(dev, fmt, m, n, k, a_bf16, seed, nrows=48):
 @pytest.mark.parametrize("m,n,k", [(512, 4096, 4096), (512, 14336, 4096), (2048, 4096, 4096), (2048, 14336, 4096)])
 def test_gemm_benchmark_shapes(dev, fmt, m, n, k):
     """The prefill configurations: 448 workgroups of 256 x 256 at 2048 x 14336
-    (two rounds on 256 CUs, the XCD remap), 256 x 128 / 128 x 128 tiles at
-    M = 512, bf16 A ~ N(0,1), f32 C and bf16 C."""
+    (two rounds on 256 CUs, the XCD remap), 128 x 256 tiles at M = 512 and
+    2048 x 4096, bf16 A ~ N(0,1), f32 C and bf16 C."""
     import torch
     a = torch.randn(m, k, generator=torch.Generator().manual_seed(2004 + m)).to(torch.bfloat16)
     err, bf16_exact = _gemm_check(dev, fmt, m, n, k, a, seed=1004 + fmt)
