@@ -1035,10 +1035,13 @@ int launch_rb(const void *packed, const _Float16 *a16, int lda, void *c, const f
 //      2-8 % faster than 0 (2 x 4 waves) and 3 (LDS-B) for every format
 //   0: register-B kernel, 256 x 256, 2 x 4 waves of 128 x 64
 //   3: LDS-B kernel, 256 x 256
+//  14: register-B, 64 x 128 on 4 waves of 64 x 32 (1 x 4), depth 4, for >= 192
+//      workgroups where 128 x 128 gives fewer: 512 x 4096 x 4096 Q4_0 / Q4_K
+//      37.0 / 38.3 us vs 40.9 / 41.9 for 9, 2048 x 1024 x 4096 40.5 vs 44.9
 //   4: register-B, 256 x 128 (2 x 4 waves), the former choice of 13's grids
 //   6: register-B, 128 x 128, for >= 192 workgroups (1024 x 4096, 256 x 14336)
-//   9: register-B, 128 x 64 (4 waves), for >= 192 workgroups (512 x 4096:
-//      50 vs 56 us with 128 x 128; 128 x 14336: 48 vs 54 us)
+//   9: register-B, 128 x 64 (4 waves), the former choice of 14's grids (512 x
+//      4096: 50 vs 56 us with 128 x 128; 128 x 14336: 48 vs 54 us)
 //  11: register-B, 64 x 64 (4 waves), smaller problems (M <= 256 at N = 4096:
 //      40-43 us vs 49-53)
 // The register-B kernel runs with pipeline depth 4 (1-3 % faster than 2 on
@@ -1052,7 +1055,7 @@ int pick_tile(int fmt, int M, int N) {
   if (wgs(256, 256) >= 384) return 12;
   if (wgs(128, 256) >= 192) return 13;
   if (wgs(128, 128) >= 192) return 6;
-  if (wgs(128, 64) >= 192) return 9;
+  if (wgs(64, 128) >= 192) return 14;
   return 11;
 }
 
@@ -1071,6 +1074,7 @@ int launch_fmt(const void *packed, const _Float16 *a16, int lda, void *c, const 
   case 11: return launch_rb<FMT, CBF16, 64, 64, 2, 2>(packed, a16, lda, c, rs, M, N, K, s);
   case 12: return launch_rb<FMT, CBF16, 256, 256, 1, 8>(packed, a16, lda, c, rs, M, N, K, s, 3);
   case 13: return launch_rb<FMT, CBF16, 128, 256, 1, 8>(packed, a16, lda, c, rs, M, N, K, s);
+  case 14: return launch_rb<FMT, CBF16, 64, 128, 1, 4>(packed, a16, lda, c, rs, M, N, K, s);
   default: return launch_rb<FMT, CBF16, 128, 128, 2, 4>(packed, a16, lda, c, rs, M, N, K, s);
   case 3: return launch_cfg<FMT, CBF16, 256, 256>(packed, a16, lda, c, rs, M, N, K, s);
   case 1: return launch_cfg<FMT, CBF16, 256, 128>(packed, a16, lda, c, rs, M, N, K, s);

@@ -340,7 +340,7 @@ def test_compat_launchers_shapes(dev, m, n, k, gs, hd):
 
 @pytest.mark.parametrize("tile,pd", [(0, 2), (0, 4), (1, 2), (2, 2), (3, 2), (4, 2), (4, 3), (4, 4), (5, 4),
                                      (6, 2), (6, 3), (6, 4), (7, 4), (8, 4), (9, 3), (9, 4), (10, 4), (11, 2),
-                                     (11, 4), (12, 2), (12, 3), (13, 2), (13, 3), (13, 4)])
+                                     (11, 4), (12, 2), (12, 3), (13, 2), (13, 3), (13, 4), (14, 2), (14, 3), (14, 4)])
 @pytest.mark.parametrize("fmt", [O.Q4_0, O.Q8_0, O.Q4_K])
 def test_gemm_every_kernel_shape(dev, fmt, tile, pd, monkeypatch):
     """Each GEMM kernel / tile shape (forced through GQ_GEMM_TILE) and, for the
@@ -367,7 +367,7 @@ def test_gemm_short_k_loops(dev, fmt, k, pd, monkeypatch):
     import gq
     import torch
     monkeypatch.setenv("GQ_GEMM_PD", str(pd))
-    for tile in (4, 6, 11, 12, 13):
+    for tile in (4, 6, 11, 12, 13, 14):
         monkeypatch.setenv("GQ_GEMM_TILE", str(tile))
         m, n = 200, 160
         w = O.gen_weights(fmt, n, k, seed=70 + k)
