@@ -542,17 +542,25 @@ GQ_DEV void q4k_factors(const RStep<GQ_FMT_Q4_K, NJ> &st, int step, QKf (&f)[NJ]
     // the fp16 bits as they are (the reference's NaN-to-Inf conversion would
     // compile to branches here)
     const _Float16 hd = __builtin_bit_cast(_Float16, (uint16_t)(mv[0] & 0xFFFFu));
-    const float dmin = (float)__builtin_bit_cast(_Float16, (uint16_t)(mv[0] >> 16));
-#pragma unroll
-    for (int h = 0; h < 2; ++h) {
-      uint32_t sc, mn;
-      gq_q4k_meta_codes(mv, 2 * (step & 3) + h, &sc, &mn);
-      const _Float16 hsc = (_Float16)(float)sc, hnsc = (_Float16)(-1024.0f * (float)sc);
-      const _Float16 hmin = (_Float16)(-(dmin * (float)mn));
-      const _Float16 hmin16 = (_Float16)16.0f * hmin;
-      f[j][h] = QKf{gq_half2{hsc, hsc}, gq_half2{hnsc, hnsc}, gq_half2{hd, hd}, gq_half2{hmin, hmin},
-                    gq_half2{hmin16, hmin16}};
-    }
+    const _Float16 ndmin = -__builtin_bit_cast(_Float16, (uint16_t)(mv[0] >> 16));
+    // the step's two sub-blocks 2 t and 2 t + 1 (t = step & 3): byte t of meta
+    // words 1 and 2 (6-bit scale, the min's low 2 bits on top) and of word 3
+    // (the mins' high nibbles); both factors of a kind decoded as one fp16
+    // pair: 1024 + code from the mantissa bits, minus 1024 (exact)
+    const uint32_t sh = 8u * (uint32_t)(step & 3);
+    const uint32_t b1 = (mv[1] >> sh) & 0xFFu, b2 = (mv[2] >> sh) & 0xFFu, b3 = (mv[3] >> sh) & 0xFFu;
+    const uint32_t scp = (b1 & 63u) | ((b2 & 63u) << 16);
+    const uint32_t mnp = ((b1 >> 6) | ((b3 & 15u) << 2)) | (((b2 >> 6) | ((b3 >> 4) << 2)) << 16);
+    const gq_half2 k1024 = {(_Float16)-1024.0f, (_Float16)-1024.0f};
+    const gq_half2 sc = gq_bits_h2(scp | 0x64006400u) + k1024;   // sc, exact
+    const gq_half2 mn = gq_bits_h2(mnp | 0x64006400u) + k1024;   // m, exact
+    const gq_half2 nsc = sc * gq_half2{(_Float16)-1024.0f, (_Float16)-1024.0f};  // exact
+    const gq_half2 hm = mn * gq_half2{ndmin, ndmin};  // -(dmin m), the exact product rounded once
+    const gq_half2 hm16 = hm * gq_half2{(_Float16)16.0f, (_Float16)16.0f};  // exact
+    f[j][0] = QKf{__builtin_shufflevector(sc, sc, 0, 0), __builtin_shufflevector(nsc, nsc, 0, 0), gq_half2{hd, hd},
+                  __builtin_shufflevector(hm, hm, 0, 0), __builtin_shufflevector(hm16, hm16, 0, 0)};
+    f[j][1] = QKf{__builtin_shufflevector(sc, sc, 1, 1), __builtin_shufflevector(nsc, nsc, 1, 1), gq_half2{hd, hd},
+                  __builtin_shufflevector(hm, hm, 1, 1), __builtin_shufflevector(hm16, hm16, 1, 1)};
   }
 }
 
