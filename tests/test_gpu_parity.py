@@ -338,6 +338,25 @@ def test_compat_launchers_shapes(dev, m, n, k, gs, hd):
         assert O.rel_l2(y4g.cpu().numpy(), ref4g) <= 1e-5
 
 
+@pytest.mark.parametrize("tile", [12, 14])
+def test_gemm_epilogue_very_wide_n(dev, tile, monkeypatch):
+    """N so wide that a tile's C offsets (N x tile rows x 4 bytes) pass 2 GiB:
+    the register-B kernel's epilogue takes its 64-bit address path instead of
+    the buffer resource; f32 and bf16 C."""
+    import gq
+    import torch
+    monkeypatch.setenv("GQ_GEMM_TILE", str(tile))
+    fmt, m, n, k = O.Q4_0, 5, (1 << 21) + 48, 64
+    w = O.gen_weights(fmt, n, k, seed=77)
+    a = torch.randn(m, k, generator=torch.Generator().manual_seed(77)).to(torch.bfloat16)
+    ref = O.gemv(fmt, w, a.float().numpy(), n, k)
+    packed = _to_dev(gq.repack_host(fmt, w, n, k), dev)
+    c = gq.gemm(fmt, packed, a.to(dev), n, k).cpu().numpy()
+    assert O.rel_l2(c, ref) <= TOL
+    cb = gq.gemm(fmt, packed, a.to(dev), n, k, out_dtype=torch.bfloat16).float().cpu().numpy()
+    assert np.array_equal(cb, _bf16(c))
+
+
 @pytest.mark.parametrize("tile,pd", [(0, 2), (0, 4), (1, 2), (2, 2), (3, 2), (4, 2), (4, 3), (4, 4), (5, 4),
                                      (6, 2), (6, 3), (6, 4), (7, 4), (8, 4), (9, 3), (9, 4), (10, 4), (11, 2),
                                      (11, 4), (12, 2), (12, 3), (13, 2), (13, 3), (13, 4), (14, 2), (14, 3), (14, 4)])
