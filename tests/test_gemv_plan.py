@@ -191,7 +191,7 @@ def test_gemv_plan_in_bounds(fmt, batch, monkeypatch):
     for n, k in SHAPES:
         if k % (256 if fmt == gq.FMT_Q4_K else 32):
             continue
-        if batch <= 4 and staging_lds(fmt, n, k, batch) > 160 * 1024:
+        if batch <= 4 and (staging_lds(fmt, n, k, batch) > 160 * 1024 or q8_spills(fmt, n, k, batch)):
             assert gq.gemv_plan(fmt, n, k, batch) != int8_plan(fmt, n, k, batch)
             emulate_h(fmt, n, k, batch)
             continue
@@ -215,6 +215,13 @@ def staging_lds(fmt, n, k, batch, ks=None, R=None):
     sdma = fmt == gq.FMT_Q8_0 or (ks == 16 and fmt in (gq.FMT_Q4_0, gq.FMT_Q4_K, gq.FMT_Q4_K_GGML))
     static = (ks * R * 1024 if sdma else 16) + ks * R * nbc * 64 + nbc * 4
     return ks * wave + static
+
+
+def q8_spills(fmt, n, k, batch):
+    """Q8_0 at batch 3..4 on 16 waves with more than MAXC / 2 chunks a wave
+    would spill registers (16 waves leave 128 a wave): the fp16 kernel."""
+    R, ks, cpw = int8_plan(fmt, n, k, batch)
+    return fmt == gq.FMT_Q8_0 and 3 <= batch <= 4 and ks == 16 and cpw > MAXC[fmt] // 2
 
 
 def int8_plan(fmt, n, k, batch):
