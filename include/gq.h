@@ -183,7 +183,8 @@ int gq_gemm_static(int fmt, const void *d_packed, const void *d_a, int a_dtype, 
                    size_t N, size_t K, void *stream);
 
 /* Q8_0 x int8 activations (int8 MFMA): activations quantized per 32-block with
- * the reference's INT8 rule (d = amax/127, q = round(a / d)). */
+ * the reference's INT8 rule (d = amax/127, q = round(a / d)).  d_qa int8
+ * [M][K] (16-byte aligned), d_da f32 [M][K/32], d_c f32 [M][N]. */
 int gq_quantize_act_q8(const void *d_a, int a_dtype, size_t M, size_t K, int8_t *d_q, float *d_d,
                        void *stream);
 int gq_gemm_q8_i8(const void *d_packed_q8, const int8_t *d_qa, const float *d_da, float *d_c, size_t M,

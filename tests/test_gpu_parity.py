@@ -225,10 +225,12 @@ def test_gemm_small_m_f32(dev, fmt, m):
     assert O.rel_l2(c, ref) <= TOL
 
 
-def test_q8_i8_path(dev):
+@pytest.mark.parametrize("m,n,k", [(96, 160, 1024), (1, 16, 32), (130, 300, 4192), (257, 48, 224), (128, 256, 4096)])
+def test_q8_i8_path(dev, m, n, k):
+    """Int8 route: partial M / N tiles, a single block, and K % 128 != 0 (a
+    last chunk with padding blocks, whose activation scales are zero)."""
     import gq
     import torch
-    m, n, k = 96, 160, 1024
     w = O.gen_weights(O.Q8_0, n, k, seed=21)
     a = O.gen_x(m, k, seed=22)
     qa, da = gq.quantize_act_q8(_to_dev(a, dev))
