@@ -201,3 +201,28 @@ def test_fused_llama_shapes(dev, fmt, batch, norm):
                        gamma=_dev(gamma, dev) if norm else None, eps=eps).cpu().numpy()
     ref = O.swiglu(O.gemv(fmt, wg, xn, n, k), O.gemv(fmt, wu, xn, n, k))
     assert O.rel_l2(y, ref) <= TOL
+
+
+@pytest.mark.parametrize("m,n,k", [(512, 4096, 4096), (2048, 14336, 4096)])
+def test_gemm_q8_i8_benchmark_shapes(dev, m, n, k):
+    """The int8 route of the prefill configuration (Q8_0, activations quantized
+    per 32-block) at its real size: quantization bit-exact against the
+    oracle's rule on every row, the GEMM against the exact integer block sums
+    (fp64 scale products) on sampled rows, each row on its own too."""
+    import torch
+
+    import gq
+    a = torch.randn(m, k, generator=torch.Generator().manual_seed(7000 + m)).to(torch.bfloat16)
+    w = O.gen_weights(O.Q8_0, n, k, seed=7100 + m)
+    packed = _packed(O.Q8_0, w, n, k, dev)
+    qa, da = gq.quantize_act_q8(a.to(dev))
+    rq, rd = O.quantize_act_q8(a.float().numpy())
+    assert np.array_equal(qa.cpu().numpy(), rq)
+    assert np.array_equal(da.cpu().numpy().view(np.uint32), rd.view(np.uint32))
+    c = gq.gemm_q8_i8(packed, qa, da, n).cpu().numpy()
+    assert np.isfinite(c).all()
+    rows = np.unique(np.concatenate([np.linspace(0, m - 1, 12).astype(int), [127, 128, m - 1]]))
+    ref = O.gemm_q8_i8(w, rq[rows], rd[rows], n)
+    assert O.rel_l2(c[rows], ref) <= 1e-5
+    for i in range(len(rows)):
+        assert O.rel_l2(c[rows[i]], ref[i]) <= 1e-5, rows[i]
