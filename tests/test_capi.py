@@ -119,6 +119,14 @@ def test_argument_validation():
     assert lib.gq_gemv(gq.FMT_Q4_0, buf, buf, buf, 0, 32, 1, None, 0, None) == 0
     assert lib.gq_gemm(gq.FMT_Q4_0, buf, buf, 2, buf, 0, 0, 16, 32, None, 0, None) == 0
     assert lib.gq_launch_gemm_mfma_int8_wt_fp32_acc32(None, buf, buf, buf, None, 0, 4, 4, 4, 4, 4, 32) == 0
+    # int8 Q8_0 route: K a block multiple, activation rows 16-byte aligned
+    base = ctypes.addressof(buf)
+    qa16 = ctypes.c_void_p((base + 15) & ~15)
+    qa_odd = ctypes.c_void_p(((base + 15) & ~15) + 1)
+    assert lib.gq_gemm_q8_i8(buf, qa16, buf, buf, 4, 16, 33, None) == 1   # K not a block multiple
+    assert lib.gq_gemm_q8_i8(buf, qa_odd, buf, buf, 4, 16, 32, None) == 1  # misaligned activations
+    assert lib.gq_gemm_q8_i8(buf, None, buf, buf, 4, 16, 32, None) == 1
+    assert lib.gq_gemm_q8_i8(buf, qa16, buf, buf, 0, 16, 32, None) == 0   # empty: no-op
 
 
 def test_product_path_never_loads_the_oracle():
