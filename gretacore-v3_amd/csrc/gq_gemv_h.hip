@@ -240,6 +240,65 @@ GQ_DEV gq_f4 mfma16h(const gq_half8 &a, const gq_half8 &b, const gq_f4 &c) {
   return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
 }
 
+// Largest (unsigned) value over each 32-lane half of the wave, every lane receiving its
+// half's: quads (DPP lane ^ 1, ^ 2), 8-lane halves (row_half_mirror), 16-lane
+// rows (row_mirror), then the two rows of the half (permlane16 swap returns
+// the pair (own, partner) in some order).
+GQ_DEV uint32_t max_half_wave(uint32_t v) {
+  // (update_dpp with a zero old value and bound_ctrl: 0 is max's identity, so
+  // each move fuses into the max as a DPP operand)
+  v = max(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0xB1, 0xF, 0xF, true));
+  v = max(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x4E, 0xF, 0xF, true));
+  v = max(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x141, 0xF, 0xF, true));
+  v = max(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x140, 0xF, 0xF, true));
+  const auto s = __builtin_amdgcn_permlane16_swap(v, v, false, false);
+  return max(s[0], s[1]);
+}
+
+// Activation range: each batch row's 256-k window (32 runs of 8, one per
+// lane of a 32-lane half) is converted to fp16 after scaling by 2^s, s = 14 -
+// floor(log2(max |x|)) over the window, clamped to [-100, 100] so both 2^s and
+// 2^-s are normal floats: the window's largest entry lands in [2^14, 2^15),
+// so no entry overflows fp16 and entries down to 2^-24 of the largest stay
+// normal (also after the 1/16 of the 4-bit formats' high-nibble slots).  An
+// all-zero window gets 2^100 (zeros stay zeros), one holding Inf or NaN
+// 2^-100 (they stay Inf / NaN).  The window's dot products are multiplied by
+// 2^-s (exact) as they are added to the fp32 accumulator.  `in` false: the
+// run is outside the data (its values do not count).  Returns 2^s; *unscale
+// receives 2^-s.
+GQ_DEV float window_scale(const float (&xv)[8], bool in, float *unscale) {
+  // (magnitudes compared as their bit patterns: monotonic for non-negative
+  // floats, NaN above Inf)
+  float am = 0.f;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) am = fmaxf(am, fabsf(xv[e]));
+  const uint32_t eb = max_half_wave(in ? __float_as_uint(am) : 0u) >> 23;
+  // biased exponent of 2^s: 127 + 14 - (eb - 127), clamped to 127 +- 100
+  const uint32_t fe = (uint32_t)min(max(268 - (int)eb, 27), 227);
+  *unscale = __uint_as_float((254u - fe) << 23);
+  return __uint_as_float(fe << 23);
+}
+
+// 8 activations (one run) -> one fp16 A-fragment half, scaled by f, in the
+// weights' slot order (4-bit formats: kQ4Perm, the kQ4Div16 slots divided by
+// 16); zero when !in
+template <int FMT>
+GQ_DEV gq_u4 stage_run(const float (&xv)[8], float f, bool in) {
+  gq_half8 h;
+  const float f16 = f * 0.0625f;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    if constexpr (kNibOrder<FMT>)
+      h[e] = (_Float16)(xv[kQ4Perm[e]] * (kQ4Div16[e] ? f16 : f));
+    else
+      h[e] = (_Float16)(xv[e] * f);
+  }
+  gq_u4 hv = __builtin_bit_cast(gq_u4, h);
+#pragma unroll
+  for (int e = 0; e < 4; ++e) hv[e] = in ? hv[e] : 0u;
+  return hv;
+}
+
 // Activation staging window: kWin consecutive k of every K part, converted to
 // fp16 A fragments in LDS once per workgroup and shared by its TW row tiles.
 constexpr int kWin = 256;
@@ -267,6 +326,7 @@ k_gemv_h(const uint8_t *__restrict__ w, size_t sc_off, const float *__restrict__
   constexpr int RPT = (KS * MR * (kWin / 8)) / NT;   // x runs of 8 per thread per window
   static_assert(RPT >= 1 && RPT * NT == KS * MR * (kWin / 8), "runs must divide evenly");
   __shared__ __attribute__((aligned(16))) unsigned char xs[2][KS][WB];
+  __shared__ __attribute__((aligned(16))) float xsc[2][KS * MR];  // 2^-s per (part, batch row) of a window
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int tt = wave % TW, part = wave / TW;
@@ -295,10 +355,12 @@ k_gemv_h(const uint8_t *__restrict__ w, size_t sc_off, const float *__restrict__
   const float *xsrc[RPT];
   int xk0[RPT], xk1[RPT];
   uint32_t xdst[RPT];
+  int xsrow[RPT];
 #pragma unroll
   for (int u = 0; u < RPT; ++u) {
     const int run = (int)threadIdx.x + u * NT;
     const int kr = run & 31, b = (run >> 5) % MR, p = run / (32 * MR);
+    xsrow[u] = p * MR + b;
     const int pc0 = (C * p) / KS, pc1 = (C * (p + 1)) / KS;
     xsrc[u] = x + (size_t)(b < nb ? b : 0) * K;
     xk0[u] = pc0 * F::CK + 8 * kr;
@@ -318,23 +380,17 @@ k_gemv_h(const uint8_t *__restrict__ w, size_t sc_off, const float *__restrict__
       xin[u] = in;
     }
   };
+  // (a run's 32-lane half holds one (part, batch row) window: the window's
+  // scale is reduced over it and lane 0 of the half records 2^-s)
   auto store_x = [&](int buf) {
 #pragma unroll
     for (int u = 0; u < RPT; ++u) {
-      gq_half8 h;
       const float xv[8] = {xr[u][0][0], xr[u][0][1], xr[u][0][2], xr[u][0][3],
                            xr[u][1][0], xr[u][1][1], xr[u][1][2], xr[u][1][3]};
-#pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        if constexpr (kNibOrder<FMT>)  // the weights' order, "x 16" positions divided by 16
-          h[e] = kQ4Div16[e] ? (_Float16)(xv[kQ4Perm[e]] * 0.0625f) : (_Float16)xv[kQ4Perm[e]];
-        else
-          h[e] = (_Float16)xv[e];
-      }
-      gq_u4 hv = __builtin_bit_cast(gq_u4, h);
-#pragma unroll
-      for (int e = 0; e < 4; ++e) hv[e] = xin[u] ? hv[e] : 0u;  // k past the part / K, or b >= batch
-      *reinterpret_cast<gq_u4 *>(&xs[buf][0][0] + xdst[u]) = hv;
+      float us;
+      const float f = window_scale(xv, xin[u], &us);  // (xin false: k past the part / K, or b >= batch)
+      *reinterpret_cast<gq_u4 *>(&xs[buf][0][0] + xdst[u]) = stage_run<FMT>(xv, f, xin[u]);
+      if ((lane & 31) == 0) xsc[buf][xsrow[u]] = us;
     }
   };
 
@@ -346,7 +402,9 @@ k_gemv_h(const uint8_t *__restrict__ w, size_t sc_off, const float *__restrict__
   load_x(0);
   store_x(0);
   __syncthreads();
-  gq_f4 acc = gq_f4{0.f, 0.f, 0.f, 0.f}, acc2 = acc;  // chains of halves 0 and 1
+  // acc, acc2: the sums of halves 0 and 1, unscaled (each window's chains
+  // times the window's 2^-s)
+  gq_f4 acc = gq_f4{0.f, 0.f, 0.f, 0.f}, acc2 = acc;
   // Window `it` (weights in cur).  PF: the activations of window it + 1 and
   // the weights of window it + 2 (into nxt, the buffer window it - 1
   // consumed) are requested first.  The three weight buffers rotate through the
@@ -361,6 +419,7 @@ k_gemv_h(const uint8_t *__restrict__ w, size_t sc_off, const float *__restrict__
     if constexpr (decltype(pfw)::value) load_win(it + 2, nxt);
     if (it < nwin) {
       const unsigned char *xb = xs[it & 1][part] + (g * MR + (r & (MR - 1))) * 16;  // this lane's A row
+      gq_f4 wa = gq_f4{0.f, 0.f, 0.f, 0.f}, wb = wa;  // the window's chains of halves 0 and 1
 #pragma unroll
       for (int j = 0; j < WC; ++j) {
         if (c0 + it * WC + j < c1) {
@@ -371,10 +430,17 @@ k_gemv_h(const uint8_t *__restrict__ w, size_t sc_off, const float *__restrict__
             const gq_half8 a1 = *reinterpret_cast<const gq_half8 *>(xb + (ms * 2 + 1) * 4 * MR * 16);
             gq_half8 b0, b1;
             dequant_step<FMT>(cur[j], m, g, mg, b0, b1);
-            acc = mfma16h(a0, b0, acc);
-            acc2 = mfma16h(a1, b1, acc2);
+            wa = mfma16h(a0, b0, wa);
+            wb = mfma16h(a1, b1, wb);
           }
         }
+      }
+      // D rows 4g..4g+3 (MR = 8: A rows 8..15 are rows 0..7 again)
+      const gq_f4 us = *reinterpret_cast<const gq_f4 *>(&xsc[it & 1][part * MR + ((4 * g) & (MR - 1))]);
+#pragma unroll
+      for (int v = 0; v < 4; ++v) {
+        acc[v] = fmaf(wa[v], us[v], acc[v]);
+        acc2[v] = fmaf(wb[v], us[v], acc2[v]);
       }
     }
     if constexpr (decltype(pfx)::value) store_x((it + 1) & 1);
@@ -411,7 +477,6 @@ k_gemv_h(const uint8_t *__restrict__ w, size_t sc_off, const float *__restrict__
   }
 #pragma unroll
   for (int v = 0; v < 4; ++v) acc[v] += acc2[v];
-
   // ---- reduce over the KS parts (LDS reused); D lane (g, r): batch rows 4g..4g+3, column r
   if constexpr (KS > 1) {
     gq_f4 *red = reinterpret_cast<gq_f4 *>(&xs[0][0][0]);  // [KS][TW][64]
@@ -460,9 +525,16 @@ k_gemv_h1(const uint8_t *__restrict__ w, size_t sc_off, const float *__restrict_
   constexpr int NT = 64 * TW * KS;
   constexpr int PK = NCK * F::CK;                // k per part (padded)
   constexpr int PB = PK * 2 * MR;                // LDS bytes per part: [PK/64][2][4][MR][16]
-  constexpr int RUNS = KS * MR * (PK / 8);       // 8-element x runs
+  constexpr int NWIN = (PK + 255) / 256;         // 256-k windows per part (each with its own scale)
+  constexpr int WC = 256 / F::CK;                // chunks per window
+  constexpr int RPR = 32 * NWIN;                 // 8-element runs per (part, batch row), whole windows
+  constexpr int RUNS = KS * MR * RPR;
   constexpr int RPT = (RUNS + NT - 1) / NT;
-  __shared__ __attribute__((aligned(16))) unsigned char xs[KS * PB];
+  constexpr bool kSkip = (RUNS % NT != 0) || (PK % 256 != 0);  // runs with nothing to store exist
+  // (also the partial tiles' reduction [KS][TW][64] x 16 bytes at the end)
+  constexpr int XSB = KS * PB > KS * TW * 64 * 16 ? KS * PB : KS * TW * 64 * 16;
+  __shared__ __attribute__((aligned(16))) unsigned char xs[XSB];
+  __shared__ __attribute__((aligned(16))) float xsc[KS * NWIN * MR];  // 2^-s per (part, window, batch row)
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int tt = wave % TW, part = wave / TW;
@@ -477,13 +549,16 @@ k_gemv_h1(const uint8_t *__restrict__ w, size_t sc_off, const float *__restrict_
                                                                     : 8u * (uint32_t)r + 4u * (uint32_t)(g >> 1);
 
   // ---- 1. activation loads (the workgroup's whole range), then weights -------
+  // run -> (part p, batch row b, run kr of the row's part); the 32 runs of a
+  // window are one 32-lane half (RPR and NT are multiples of 32)
   gq_f4 xr[RPT][2];
   bool xin[RPT];
   uint32_t xdst[RPT];
+  int xsi[RPT];
 #pragma unroll
   for (int u = 0; u < RPT; ++u) {
     const int run = (int)threadIdx.x + u * NT;
-    const int kr = run % (PK / 8), b = (run / (PK / 8)) % MR, p = run / (MR * (PK / 8));
+    const int kr = run % RPR, b = (run / RPR) % MR, p = run / (MR * RPR);
     const int pc0 = (C * p) / KS, pc1 = (C * (p + 1)) / KS;
     const int k = pc0 * F::CK + 8 * kr;
     const bool in = run < RUNS && b < nb && k < pc1 * F::CK && k < K;  // K % 32 == 0: runs are whole
@@ -492,7 +567,8 @@ k_gemv_h1(const uint8_t *__restrict__ w, size_t sc_off, const float *__restrict_
     xr[u][1] = src[1];
     xin[u] = in;
     const int o = 8 * kr, ms = o >> 6, gq = (o & 63) >> 4, j = (o & 15) >> 3;
-    xdst[u] = run < RUNS ? (uint32_t)(p * PB + (((ms * 2 + j) * 4 + gq) * MR + b) * 16) : 0xFFFFFFFFu;
+    xdst[u] = (run < RUNS && o < PK) ? (uint32_t)(p * PB + (((ms * 2 + j) * 4 + gq) * MR + b) * 16) : 0xFFFFFFFFu;
+    xsi[u] = run < RUNS ? (p * NWIN + kr / 32) * MR + b : -1;
   }
   __builtin_amdgcn_sched_barrier(0);
   HChunk<FMT> ch[NCK];
@@ -503,24 +579,16 @@ k_gemv_h1(const uint8_t *__restrict__ w, size_t sc_off, const float *__restrict_
   }
   __builtin_amdgcn_sched_barrier(0);
 
-  // ---- 2. activations -> fp16 A fragments in LDS --------------------------------
+  // ---- 2. activations -> scaled fp16 A fragments in LDS -------------------------
 #pragma unroll
   for (int u = 0; u < RPT; ++u) {
-    if (RUNS % NT != 0 && xdst[u] == 0xFFFFFFFFu) continue;
     const float xv[8] = {xr[u][0][0], xr[u][0][1], xr[u][0][2], xr[u][0][3],
                          xr[u][1][0], xr[u][1][1], xr[u][1][2], xr[u][1][3]};
-    gq_half8 h;
-#pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      if constexpr (kNibOrder<FMT>)
-        h[e] = kQ4Div16[e] ? (_Float16)(xv[kQ4Perm[e]] * 0.0625f) : (_Float16)xv[kQ4Perm[e]];
-      else
-        h[e] = (_Float16)xv[e];
-    }
-    gq_u4 hv = __builtin_bit_cast(gq_u4, h);
-#pragma unroll
-    for (int e = 0; e < 4; ++e) hv[e] = xin[u] ? hv[e] : 0u;
-    *reinterpret_cast<gq_u4 *>(xs + xdst[u]) = hv;
+    float us;
+    const float f = window_scale(xv, xin[u], &us);  // (all lanes: a cross-lane reduction)
+    if ((lane & 31) == 0 && xsi[u] >= 0) xsc[xsi[u]] = us;
+    if (kSkip && xdst[u] == 0xFFFFFFFFu) continue;
+    *reinterpret_cast<gq_u4 *>(xs + xdst[u]) = stage_run<FMT>(xv, f, xin[u]);
   }
   __syncthreads();
 
@@ -528,29 +596,53 @@ k_gemv_h1(const uint8_t *__restrict__ w, size_t sc_off, const float *__restrict_
   const uint32_t mg = gq_nib_magic();
   // this lane's A row: r (MR = 16) or r & 7 (MR = 8)
   const unsigned char *xb = xs + part * PB + (g * MR + (r & (MR - 1))) * 16;
-  // two accumulator chains (halves 0 and 1 of each step), summed at the end
-  gq_f4 acc = gq_f4{0.f, 0.f, 0.f, 0.f}, acc2 = acc;
-  auto consume = [&](int i) {
+  // acc, acc2: the sums of halves 0 and 1, unscaled; pa, pb: the previous
+  // window's chains (window pw), added in times its 2^-s at the start of the
+  // next window, when its MFMAs have finished
+  gq_f4 acc = gq_f4{0.f, 0.f, 0.f, 0.f}, acc2 = acc, pa = acc, pb = acc;
+  int pw = 0;
+  auto fold = [&]() {
+    // D rows 4g..4g+3 (MR = 8: A rows 8..15 are rows 0..7 again)
+    const gq_f4 us = *reinterpret_cast<const gq_f4 *>(&xsc[(part * NWIN + pw) * MR + ((4 * g) & (MR - 1))]);
 #pragma unroll
-    for (int m = 0; m < F::STEPS; ++m) {
-      const int ms = i * F::STEPS + m;
-      const gq_half8 a0 = *reinterpret_cast<const gq_half8 *>(xb + (ms * 2 + 0) * 4 * MR * 16);
-      const gq_half8 a1 = *reinterpret_cast<const gq_half8 *>(xb + (ms * 2 + 1) * 4 * MR * 16);
-      gq_half8 b0, b1;
-      dequant_step<FMT>(ch[i], m, g, mg, b0, b1);
-      acc = mfma16h(a0, b0, acc);
-      acc2 = mfma16h(a1, b1, acc2);
+    for (int v = 0; v < 4; ++v) {
+      acc[v] = fmaf(pa[v], us[v], acc[v]);
+      acc2[v] = fmaf(pb[v], us[v], acc2[v]);
     }
+  };
+  // one window: its chunks on two chains (halves 0 and 1 of each step)
+  auto consume_win = [&](int wv, auto full) {
+    fold();  // (a no-op before the first window: pa, pb are zero)
+    gq_f4 wa = gq_f4{0.f, 0.f, 0.f, 0.f}, wb = wa;
+#pragma unroll
+    for (int jj = 0; jj < WC; ++jj) {
+      const int i = wv * WC + jj;
+      if (i >= NCK) break;
+      if (!decltype(full)::value && i >= nck) break;
+#pragma unroll
+      for (int m = 0; m < F::STEPS; ++m) {
+        const int ms = i * F::STEPS + m;
+        const gq_half8 a0 = *reinterpret_cast<const gq_half8 *>(xb + (ms * 2 + 0) * 4 * MR * 16);
+        const gq_half8 a1 = *reinterpret_cast<const gq_half8 *>(xb + (ms * 2 + 1) * 4 * MR * 16);
+        gq_half8 b0, b1;
+        dequant_step<FMT>(ch[i], m, g, mg, b0, b1);
+        wa = mfma16h(a0, b0, wa);
+        wb = mfma16h(a1, b1, wb);
+      }
+    }
+    pa = wa;
+    pb = wb;
+    pw = wv;
   };
   if (nck == NCK) {
 #pragma unroll
-    for (int i = 0; i < NCK; ++i) consume(i);
+    for (int wv = 0; wv < NWIN; ++wv) consume_win(wv, std::true_type{});
   } else {
 #pragma unroll
-    for (int i = 0; i < NCK; ++i)
-      if (i < nck) consume(i);
+    for (int wv = 0; wv < NWIN; ++wv)
+      if (wv * WC < nck) consume_win(wv, std::false_type{});
   }
-
+  fold();
 #pragma unroll
   for (int v = 0; v < 4; ++v) acc[v] += acc2[v];
 

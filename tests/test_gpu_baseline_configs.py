@@ -91,12 +91,57 @@ def test_gemv_outlier_activations(dev, fmt, n, k, batch):
     """Per-32-block outliers (|x| 300-600) and near-zero entries: the int8
     two-limb split (batch <= 4) scales per 32-block, so its error follows the
     block's largest entry (there the last batch row is ~1e-5 throughout and
-    is checked on its own); the fp16 batch kernel (batch 5..16, and 3..4 at
-    K = 14336) rounds x to fp16 with no row scale, so its inputs stay inside
-    fp16's normal range."""
+    is checked on its own)."""
     x = outlier_x(batch, k, seed=7 + batch, tiny_row=batch <= 2)
     err, y, w, _ = _gemv_err(dev, fmt, n, k, batch, seed=2000 + fmt, x=x)
     assert err <= TOL, err
+    ref = O.gemv(fmt, w, x, n, k)
+    for b in range(batch):
+        assert O.rel_l2(y[b], ref[b]) <= TOL, b
+
+
+@pytest.mark.parametrize("fmt", [O.Q4_0, O.Q8_0, O.Q4_K])
+@pytest.mark.parametrize("n,k", [(14336, 4096), (4096, 14336), (1024, 4096)])
+@pytest.mark.parametrize("batch", [3, 4, 5, 8, 16])
+def test_gemv_wide_range_activations(dev, fmt, n, k, batch):
+    """Activations beyond fp16's range and far below 1 through every batch
+    GEMV kernel: spikes of 1e3..1e5 in every 32-block (beyond fp16's 65504),
+    entries of ~1e-6, and one batch row of ~1e-6 throughout.  The fp16 batch
+    kernels (batch 5..16; 3..4 where the int8 kernel's staging or registers do
+    not fit) scale each batch row's 256-k window by a power of two before the
+    fp16 rounding and restore it on the window's dot products, so outputs stay
+    finite and every row -- the ~1e-6 row too -- is within 1e-3 of the fp64
+    oracle, as the reference's fp32 GEMV band is (gemm_kernels.hip:594-634,
+    763-817).  Shapes: 896 row tiles (the windowed kernel), 4096 x 14336 (long
+    K), 1024 rows (the one-stage kernel)."""
+    import gq
+    spike = (1e3, 1e4, 1e5)[batch % 3]
+    x = outlier_x(batch, k, seed=11 + batch + k, spike=spike)
+    x[batch - 1] = (np.random.default_rng(batch).standard_normal(k) * 1e-6).astype(np.float32)
+    w = O.gen_weights(fmt, n, k, seed=2100 + fmt)
+    y = gq.gemv(fmt, _packed(fmt, w, n, k, dev), _dev(x, dev), n, k).cpu().numpy()
+    assert np.isfinite(y).all()
+    ref = O.gemv(fmt, w, x, n, k)
+    for b in range(batch):
+        assert O.rel_l2(y[b], ref[b]) <= TOL, b
+
+
+@pytest.mark.parametrize("fmt", [O.Q4_0, O.Q8_0, O.Q4_K])
+@pytest.mark.parametrize("batch", [1, 2])
+def test_gemv_int8_limbs_spike_per_block(dev, fmt, batch):
+    """The int8 two-limb GEMV (batch 1..2): N(0,1) rows with one 1e4 spike in
+    every 32-block.  The limb step is the block's max / 32258, so the N(0,1)
+    entries next to a spike carry an absolute error of up to ~0.3; each row
+    must still be within 1e-3 of the fp64 oracle."""
+    import gq
+    n, k = 4096, 4096
+    rng = np.random.default_rng(90 + batch)
+    x = rng.standard_normal((batch, k)).astype(np.float32)
+    pos = rng.integers(0, 32, size=(batch, k // 32)) + 32 * np.arange(k // 32)[None, :]
+    for b in range(batch):
+        x[b, pos[b]] = (rng.choice([-1.0, 1.0], size=k // 32) * 1e4).astype(np.float32)
+    w = O.gen_weights(fmt, n, k, seed=2200 + fmt)
+    y = gq.gemv(fmt, _packed(fmt, w, n, k, dev), _dev(x, dev), n, k).cpu().numpy()
     ref = O.gemv(fmt, w, x, n, k)
     for b in range(batch):
         assert O.rel_l2(y[b], ref[b]) <= TOL, b

@@ -38,13 +38,14 @@ def model(tmp_path_factory):
     return path, spec, d
 
 
-def _run(model, name, kind, M, label="", adt="f32", seed=0, path=None):
+def _run(model, name, kind, M, label="", adt="f32", seed=0, path=None, a=None):
     gguf_path, spec, d = model
     path = path or gguf_path
     sh = spec[name][0]
     K = sh[0]
     N = int(np.prod(sh)) // K
-    a = O.gen_x(M, K, seed)
+    if a is None:
+        a = O.gen_x(M, K, seed)
     ap, cp = str(d / f"a_{name}_{M}.f32"), str(d / f"c_{name}_{M}.f32")
     a.tofile(ap)
     r = subprocess.run([DRIVER, path, name, kind, str(M), ap, cp, label, adt], capture_output=True, text=True,
@@ -75,6 +76,32 @@ def test_gemm_gguf_native(dev, model, name, M, adt):
     sh, fmt, raw = model[1][name]
     ref = O.gemv(fmt, raw, _round_a(a, adt), N, K)
     assert O.rel_l2(c, ref) <= TOL
+
+
+@pytest.mark.parametrize("M", [3, 5, 8, 12, 16])
+@pytest.mark.parametrize("name", ["blk.0.ffn_gate.weight", "blk.0.ffn_down.weight", "blk.0.attn_q.weight",
+                                  "output.weight"])
+def test_gemm_gguf_native_wide_range_f32(dev, model, name, M):
+    """GretaCompute::gemm with fp32 A of M <= 16 rows (the batch GEMV) on
+    activations beyond fp16's range: spikes of 1e5 and a row of ~1e-6.  The
+    reference's launchers keep fp32 activations for these rows
+    (gemm_kernels.hip:594-634, 749-753); here every row must be finite and
+    within 1e-3 of the fp64 oracle."""
+    sh, fmt, raw = model[1][name]
+    K = sh[0]
+    N = int(np.prod(sh)) // K
+    rng = np.random.default_rng(M)
+    a = rng.standard_normal((M, K)).astype(np.float32)
+    pos = rng.integers(0, K, size=(M, 4))
+    for m in range(M):
+        a[m, pos[m]] = (rng.choice([-1.0, 1.0], size=4) * 1e5 * (1 + rng.random(4))).astype(np.float32)
+    a[M - 1] = (rng.standard_normal(K) * 1e-6).astype(np.float32)
+    a, c, route, N, K = _run(model, name, "quant", M, seed=M, a=a)
+    assert route == "GEMV"
+    ref = O.gemv(fmt, raw, a, N, K)
+    assert np.isfinite(c).all()
+    for m in range(M):
+        assert O.rel_l2(c[m], ref[m]) <= TOL, m
 
 
 @pytest.mark.parametrize("M", [1, 40])
