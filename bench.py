@@ -40,6 +40,100 @@ def log(*a):
     print(*a, file=sys.stderr, flush=True)
 
 
+def gpu_sysfs_dir(index=0):
+    """sysfs directory of the GPU torch sees as cuda:<index> (by PCI address)."""
+    import torch
+    try:
+        p = torch.cuda.get_device_properties(index)
+        d = f"/sys/bus/pci/devices/{p.pci_domain_id:04x}:{p.pci_bus_id:02x}:{p.pci_device_id:02x}.0"
+        return d if os.path.isdir(d) else None
+    except (RuntimeError, AttributeError):
+        return None
+
+
+def _read(path):
+    try:
+        with open(path) as f:
+            return f.read()
+    except OSError:
+        return None
+
+
+def _dpm(text):
+    """(levels in MHz, current MHz) of a pp_dpm_* file ('0: 500Mhz *' lines)."""
+    levels, cur = [], None
+    for line in (text or "").splitlines():
+        parts = line.replace(":", " ").split()
+        mhz = [int(t[:-3]) for t in parts if t.lower().endswith("mhz") and t[:-3].isdigit()]
+        if mhz:
+            levels.append(mhz[0])
+            if "*" in line:
+                cur = mhz[0]
+    return levels, cur
+
+
+class ClockSampler:
+    """Samples the GPU's current shader clock (pp_dpm_sclk) and power draw
+    every few ms on a host thread while a benchmark section runs."""
+
+    def __init__(self, sysdir, period_s=0.005):
+        import threading
+        self.sysdir, self.period = sysdir, period_s
+        self.sclk, self.power = [], []
+        self._stop = threading.Event()
+        self._t = threading.Thread(target=self._run, daemon=True)
+
+    def _run(self):
+        import glob
+        hw = glob.glob(os.path.join(self.sysdir, "hwmon", "hwmon*", "power1_average")) + \
+            glob.glob(os.path.join(self.sysdir, "hwmon", "hwmon*", "power1_input"))
+        while not self._stop.is_set():
+            cur = _dpm(_read(os.path.join(self.sysdir, "pp_dpm_sclk")))[1]
+            if cur is not None:
+                self.sclk.append(cur)
+            if hw:
+                v = _read(hw[0])
+                if v and v.strip().isdigit():
+                    self.power.append(int(v) / 1e6)
+            self._stop.wait(self.period)
+
+    def __enter__(self):
+        if self.sysdir:
+            self._t.start()
+        return self
+
+    def __exit__(self, *exc):
+        self._stop.set()
+        if self._t.is_alive():
+            self._t.join()
+
+    def summary(self):
+        def st(v):
+            if not v:
+                return None
+            v = sorted(v)
+            return {"min": v[0], "median": v[len(v) // 2], "max": v[-1], "samples": len(v)}
+        return {"sclk_mhz": st(self.sclk), "power_w": st(self.power)}
+
+
+def box_state():
+    """The GPU's clock levels, current memory clock and power cap from sysfs
+    (null where the box does not expose them), so box-to-box variance is
+    visible on every bench line."""
+    import glob
+    d = gpu_sysfs_dir()
+    if not d:
+        return {"sysfs": None}
+    sl, sc = _dpm(_read(os.path.join(d, "pp_dpm_sclk")))
+    ml, mc = _dpm(_read(os.path.join(d, "pp_dpm_mclk")))
+    out = {"sysfs": d, "sclk_levels_mhz": sl, "mclk_levels_mhz": ml, "mclk_current_mhz": mc}
+    for key, name in (("power_cap_w", "power1_cap"), ("power_cap_max_w", "power1_cap_max")):
+        f = glob.glob(os.path.join(d, "hwmon", "hwmon*", name))
+        v = _read(f[0]) if f else None
+        out[key] = int(v) / 1e6 if v and v.strip().isdigit() else None
+    return out
+
+
 def gemv_bytes(fmt, n, k, batch):
     import gq
     return gq.gguf_bytes(fmt, n, k) + 4 * batch * (n + k)
@@ -473,6 +567,44 @@ def cpu_baseline(target_s=6.0):
             "runs": runs}
 
 
+CALIB_PATH = os.path.join(ROOT, "gretacore-v3_amd", "lib", "libgqcalib.so")
+_calib = None
+
+
+def calib():
+    """ctypes binding of lib/libgqcalib.so (gretacore-v3_amd/calib/gq_probe.h):
+    calibration kernels, built beside the product library."""
+    global _calib
+    if _calib is None:
+        import ctypes
+        import torch  # noqa: F401  (torch's HIP runtime first, as gq.load())
+        if not os.path.exists(CALIB_PATH):
+            raise RuntimeError(f"{CALIB_PATH} not built (run __graft_entry__.build())")
+        lib = ctypes.CDLL(CALIB_PATH)
+        vp = ctypes.c_void_p
+        lib.gq_probe_read.restype = ctypes.c_int
+        lib.gq_probe_read.argtypes = [vp, ctypes.c_size_t, ctypes.c_int, ctypes.c_int, vp, vp]
+        lib.gq_probe_empty.restype = ctypes.c_int
+        lib.gq_probe_empty.argtypes = [ctypes.c_int, ctypes.c_int, vp]
+        _calib = lib
+    return _calib
+
+
+def probe_read(src, wgs, waves, out):
+    import torch
+    s = torch.cuda.current_stream().cuda_stream
+    rc = calib().gq_probe_read(src.data_ptr(), src.numel(), wgs, waves, out.data_ptr(), s)
+    if rc != 0:
+        raise RuntimeError(f"gq_probe_read: status {rc}")
+
+
+def probe_empty(wgs, waves):
+    import torch
+    rc = calib().gq_probe_empty(wgs, waves, torch.cuda.current_stream().cuda_stream)
+    if rc != 0:
+        raise RuntimeError(f"gq_probe_empty: status {rc}")
+
+
 def bench_read_ceiling(dev, steps, warmup):
     """The read ceiling of the headline GEMV: a kernel of the GEMV's grid (its
     workgroups and waves, every wave issuing all its loads up front) that only
@@ -490,8 +622,8 @@ def bench_read_ceiling(dev, steps, warmup):
     ncopies = max(8, -(-CACHE_DEFEAT_BYTES // nbytes))
     copies = [torch.randint(0, 256, (nbytes,), dtype=torch.uint8, device=dev) for _ in range(ncopies)]
     out = torch.empty(wgs * ks, dtype=torch.int32, device=dev)
-    t_read = graph_steps(lambda i: gq.probe_read(copies[i % ncopies], wgs, ks, out), steps, warmup)
-    t_empty = graph_steps(lambda i: gq.probe_empty(wgs, ks), steps, warmup)
+    t_read = graph_steps(lambda i: probe_read(copies[i % ncopies], wgs, ks, out), steps, warmup)
+    t_empty = graph_steps(lambda i: probe_empty(wgs, ks), steps, warmup)
     del copies
     return {"read_us": round(t_read * 1e6, 3), "read_GBps": round(nbytes / t_read / 1e9, 1),
             "read_pct_peak": round(100.0 * nbytes / t_read / 1e9 / HBM_PEAK_GBS, 2),
@@ -589,7 +721,9 @@ def main():
         return
     log("[bench] headline: Q4_0 GEMV 14336x4096 batch 1")
     head = GemvCase(O.Q4_0, 14336, 4096, 1, wseed=1002, xseed=2002, dev=dev)
-    h = bench_gemv(head, steps, warmup)
+    sysdir = gpu_sysfs_dir()
+    with ClockSampler(sysdir) as clk_head:
+        h = bench_gemv(head, steps, warmup)
     log(f"[bench] headline {h}")
     extra = {}
     log("[bench] read ceiling of the headline grid")
@@ -608,7 +742,10 @@ def main():
                 for n in (4096, 14336):
                     name = f"gemm_{fname}_m{m}_{n}x4096"
                     log(f"[bench] {name}")
-                    extra[name] = bench_gemm(fmt, m, n, 4096, steps, warmup, dev)
+                    with ClockSampler(sysdir) as clk:
+                        extra[name] = bench_gemm(fmt, m, n, 4096, steps, warmup, dev)
+                    if m == 2048 and n == 14336:
+                        extra[name]["clock_during"] = clk.summary()
                     torch.cuda.empty_cache()
         log("[bench] int8 route for Q8_0 (per-32 activation quantization + int8 MFMA)")
         extra["gemm_q8_0_i8_m2048_14336x4096"] = bench_gemm_q8_i8(2048, 14336, 4096, steps, dev)
@@ -647,7 +784,8 @@ def main():
                    "N": 14336, "K": 4096, "batch": 1, "weight_copies_rotated": h["copies"],
                    "arithmetic": "Q4_0 codes x two int8 limbs of the activations per 32-block on the int8 "
                                  "MFMA, int32 products scaled and summed in f32",
-                   "alg_bytes_per_step": h["alg_bytes"]},
+                   "alg_bytes_per_step": h["alg_bytes"],
+                   "box": dict(box_state(), clock_during_headline=clk_head.summary())},
         "pct_peak": round(h["pct_peak"], 2),
         "rel_l2_vs_oracle": h["rel_l2"],
         "roofline": {"bound": "hbm", "achieved": round(h["GBps"], 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",

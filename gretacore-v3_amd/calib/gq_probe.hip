@@ -1,4 +1,6 @@
-// gq_probe.hip -- calibration kernels for the benchmark's roofline figures.
+// gq_probe.hip -- calibration kernels for the benchmark's roofline figures
+// (built into lib/libgqcalib.so, apart from the product library; bench.py
+// loads it; no counterpart in the reference).
 //
 // k_probe_read streams a buffer the way the decode GEMV streams its weights
 // (the same grid of workgroups and waves, each wave issuing all of its
@@ -7,9 +9,15 @@
 // can move those bytes, i.e. the read ceiling the GEMV's time is compared
 // with.  k_probe_empty is the same grid with no work: the fixed cost of a
 // launch.
-#include "gq_internal.h"
+#include "gq_probe.h"
+
+#include "../../include/gq.h"
+#include "gq_device.h"
 
 namespace {
+
+// the launch's status (this library stands alone: no libgq symbols)
+int last_launch() { return hipGetLastError() == hipSuccess ? GQ_OK : GQ_ERR_HIP; }
 
 // NL loads of 1 KiB per wave (16 bytes per lane), all issued before any is
 // used; a wave past the end of the buffer does nothing.  The data is folded
@@ -46,7 +54,7 @@ int launch_probe(const void *src, size_t bytes, int wgs, int waves, uint32_t *ou
     if ((size_t)NL * 1024 * per < bytes) return launch_probe<NL + 1>(src, bytes, wgs, waves, out, s);
     hipLaunchKernelGGL(k_probe_read<NL>, dim3((unsigned)wgs), dim3(64 * waves), 0, s, (const uint8_t *)src, bytes,
                        0x9E3779B9u, out);
-    return gq_last_launch();
+    return last_launch();
   }
 }
 
@@ -54,14 +62,14 @@ int launch_probe(const void *src, size_t bytes, int wgs, int waves, uint32_t *ou
 
 extern "C" int gq_probe_read(const void *src, size_t bytes, int wgs, int waves_per_wg, uint32_t *out,
                              void *stream) {
-  GQ_CHECK(src && out && bytes >= 16 && bytes % 16 == 0, GQ_ERR_INVALID_ARGS);
-  GQ_CHECK(wgs > 0 && waves_per_wg >= 1 && waves_per_wg <= 16, GQ_ERR_INVALID_ARGS);
+  if (!(src && out && bytes >= 16 && bytes % 16 == 0)) return GQ_ERR_INVALID_ARGS;
+  if (!(wgs > 0 && waves_per_wg >= 1 && waves_per_wg <= 16)) return GQ_ERR_INVALID_ARGS;
   // the fewest 1 KiB loads per wave that cover the buffer (at most 16)
   return launch_probe<1>(src, bytes, wgs, waves_per_wg, out, (hipStream_t)stream);
 }
 
 extern "C" int gq_probe_empty(int wgs, int waves_per_wg, void *stream) {
-  GQ_CHECK(wgs > 0 && waves_per_wg >= 1 && waves_per_wg <= 16, GQ_ERR_INVALID_ARGS);
+  if (!(wgs > 0 && waves_per_wg >= 1 && waves_per_wg <= 16)) return GQ_ERR_INVALID_ARGS;
   hipLaunchKernelGGL(k_probe_empty, dim3((unsigned)wgs), dim3(64 * waves_per_wg), 0, (hipStream_t)stream);
-  return gq_last_launch();
+  return last_launch();
 }

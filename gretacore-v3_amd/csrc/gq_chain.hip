@@ -573,6 +573,50 @@ size_t al256(size_t v) { return (v + 255) & ~(size_t)255; }
 
 int chain_fmt(int fmt) { return gq_fmt_is_q4k(fmt) ? GQ_FMT_Q4_K : fmt; }
 
+// Write hazards between ops: the kernel orders an op after the ops it
+// depends on (transitively) and after nothing else, so an op whose y overlaps
+// a buffer an earlier op reads (x, gamma, resid) or writes (y) must reach
+// that op through its dependencies; otherwise the two may run at the same
+// time inside the one launch.  Returns GQ_ERR_INVALID_ARGS for such a pair.
+int check_hazards(const gq_chain_op *ops, int n_ops) {
+  struct Range {
+    uintptr_t a, b;
+  };
+  auto rng = [](const void *p, size_t n_floats) {
+    return Range{(uintptr_t)p, (uintptr_t)p + 4 * n_floats};
+  };
+  auto meets = [](Range u, Range v) { return u.a < v.b && v.a < u.b; };
+  // anc[i][j]: op j precedes op i through dependencies
+  std::vector<std::vector<char>> anc(n_ops, std::vector<char>(n_ops, 0));
+  for (int i = 0; i < n_ops; ++i) {
+    for (int q = 0; q < 3; ++q) {
+      const int d = ops[i].dep[q];
+      if (d < 0 || d >= i) continue;  // (bad indices are rejected with the op)
+      anc[i][d] = 1;
+      for (int j = 0; j < d; ++j) anc[i][j] |= anc[d][j];
+    }
+  }
+  auto xlen = [](const gq_chain_op &o) {
+    return o.x_head_dim && o.x_group ? (size_t)o.x_head_dim * (o.K / ((size_t)o.x_head_dim * o.x_group))
+                                     : (size_t)o.K;
+  };
+  for (int i = 0; i < n_ops; ++i) {
+    const gq_chain_op &p = ops[i];
+    const Range yi = rng(p.y, p.N);
+    // (an op's own y must not alias its inputs)
+    GQ_CHECK(!meets(yi, rng(p.x, xlen(p))) && !(p.gamma && meets(yi, rng(p.gamma, p.K))) &&
+                 !(p.resid && meets(yi, rng(p.resid, p.N))),
+             GQ_ERR_INVALID_ARGS);
+    for (int j = 0; j < i; ++j) {
+      const gq_chain_op &o = ops[j];
+      const bool hit = meets(yi, rng(o.y, o.N)) || meets(yi, rng(o.x, xlen(o))) ||
+                       (o.gamma && meets(yi, rng(o.gamma, o.K))) || (o.resid && meets(yi, rng(o.resid, o.N)));
+      GQ_CHECK(!hit || anc[i][j], GQ_ERR_INVALID_ARGS);
+    }
+  }
+  return GQ_OK;
+}
+
 // Device ops for the caller's ops: ops whose K exceeds kMaxPieceK are cut
 // into column ranges chained through resid; consecutive ops with the same
 // input share an activation stage.  Also returns the LDS layout.
@@ -585,9 +629,13 @@ int build_ops(int fmt, const gq_chain_op *ops, int n_ops, std::vector<ChainOpD> 
   std::vector<int> last(n_ops, -1);  // device index of each caller op's final range
   int unit0 = 0, kx = 0, sl = 0, zl = 0;
   out.clear();
+  GQ_TRY(check_hazards(ops, n_ops));
   for (int i = 0; i < n_ops; ++i) {
     const gq_chain_op &p = ops[i];
     GQ_CHECK(p.w && p.x && p.y && p.N > 0 && p.K > 0, GQ_ERR_INVALID_ARGS);
+    // the kernel reads x with 8-byte and gamma with 16-byte vector loads
+    GQ_CHECK((uintptr_t)p.x % 16 == 0 && (uintptr_t)p.gamma % 16 == 0, GQ_ERR_INVALID_ARGS);
+    GQ_CHECK((uintptr_t)p.y % 4 == 0 && (uintptr_t)p.resid % 4 == 0, GQ_ERR_INVALID_ARGS);
     const size_t kt = p.k_total ? p.k_total : (size_t)p.K + p.k_offset;
     GQ_TRY(gq_check_shape(f, p.N, kt));
     GQ_CHECK(p.k_offset % (uint32_t)ck == 0 && p.K % 32 == 0 && p.k_offset + (size_t)p.K <= kt, GQ_ERR_INVALID_ARGS);

@@ -1108,6 +1108,17 @@ extern "C" size_t gq_gemm_workspace_bytes(int fmt, size_t M, size_t K) {
   return gq_align256(M * (gq_kpad(fmt, K) + 8) * 2) + gq_align256((M + 256) * 4);
 }
 
+// Whether gq_gemm converts A (into the workspace) for this call: always on
+// the skinny route; on the tiled route unless A is fp16 of the padded width
+// and the kernel takes it in k order (not the 4-bit register-B kernels).
+static bool gemm_converts_a(int fmt, size_t M, size_t N, size_t K, int a_dtype) {
+  int ct = 0, nck = 0;
+  if (gq_gemm_skinny_plan(fmt, M, N, K, &ct, &nck) == GQ_OK) return true;
+  const int tile = pick_tile(fmt, (int)M, (int)N);
+  const bool q4 = (fmt == GQ_FMT_Q4_0 || gq_fmt_is_q4k(fmt)) && tile != 1 && tile != 2 && tile != 3;
+  return a_dtype != GQ_DT_F16 || gq_kpad(fmt, K) != K || q4;
+}
+
 extern "C" int gq_gemm(int fmt, const void *packed, const void *a, int a_dtype, void *c, int c_dtype, size_t M,
                        size_t N, size_t K, void *ws, size_t ws_bytes, void *stream) {
   GQ_TRY(gq_check_shape(fmt, N, K));
@@ -1159,7 +1170,7 @@ extern "C" int gq_gemm(int fmt, const void *packed, const void *a, int a_dtype, 
   const int q4 = (fmt == GQ_FMT_Q4_0 || gq_fmt_is_q4k(fmt)) && tile != 1 && tile != 2 && tile != 3;
   // (the register-B kernel addresses the activations with 32-bit offsets)
   GQ_CHECK(tile == 1 || tile == 2 || tile == 3 || M * Kp * 2 < ((size_t)1 << 32), GQ_ERR_INVALID_ARGS);
-  if (a_dtype != GQ_DT_F16 || Kp != K || q4) {
+  if (gemm_converts_a(fmt, M, N, K, a_dtype)) {
     const size_t need = gq_gemm_workspace_bytes(fmt, M, K);
     if (!ws) {
       GQ_TRY(gq_default_workspace(need, &ws));
@@ -1199,8 +1210,11 @@ extern "C" int gq_gemm_static(int fmt, const void *packed, const void *a, int a_
                               size_t N, size_t K, void *stream) {
   GQ_TRY(gq_check_shape(fmt, N, K));
   GQ_CHECK(M <= GQ_MAX_DIM, GQ_ERR_INVALID_ARGS);
-  const size_t need = gq_gemm_workspace_bytes(fmt, M, K);
-  GQ_CHECK(need <= kGemmScratchBytes, GQ_ERR_WORKSPACE);  // M * (K + 264) * 2 + 4 (M + 256) bytes, rounded
+  // the scratch holds the A conversion, when the call makes one:
+  // gq_gemm_workspace_bytes = M * (padded K + 8) * 2 + (M + 256) * 4 bytes,
+  // each term rounded up to 256
+  if (gq_fmt_valid(fmt) && K > 0 && gemm_converts_a(fmt, M, N, K, a_dtype))
+    GQ_CHECK(gq_gemm_workspace_bytes(fmt, M, K) <= kGemmScratchBytes, GQ_ERR_WORKSPACE);
   int dev = 0;
   GQ_TRY(gq_hip_status(hipGetDevice(&dev)));
   GQ_CHECK(dev >= 0 && dev < kMaxDevices, GQ_ERR_NO_DEVICE);

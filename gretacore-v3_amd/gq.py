@@ -72,8 +72,6 @@ _SIGS = {
     "gq_gemm_static_max_bytes": (_c_size, []),
     "gq_gemm_static": (ctypes.c_int, [ctypes.c_int, _vp, _vp, ctypes.c_int, _vp, ctypes.c_int, _c_size, _c_size,
                                       _c_size, _vp]),
-    "gq_probe_read": (ctypes.c_int, [_vp, _c_size, ctypes.c_int, ctypes.c_int, _vp, _vp]),
-    "gq_probe_empty": (ctypes.c_int, [ctypes.c_int, ctypes.c_int, _vp]),
     "gq_launch_gemm_mfma_int8_wt_fp32_acc32": (
         ctypes.c_int, [_vp, _vp, _vp, _vp, _vp] + [ctypes.c_uint32] * 7),
     "gq_launch_gemm_mfma_int4_wt_fp32_acc32": (
@@ -366,19 +364,6 @@ def launch_int4_wt(a, b, scales, head_scales, m, n, k, group_size=32, head_dim=0
         _stream(stream), _ptr(a), _ptr(b), _ptr(c), _ptr(scales), _ptr(head_scales), m, n, k, k, n, n, group_size,
         head_dim, int(a.dtype == torch.float16), int(force_gemv)), "gq_launch_gemm_mfma_int4_wt_fp32_acc32")
     return c
-
-
-def probe_read(src, wgs: int, waves_per_wg: int, out, stream=None):
-    """Calibration: stream all of `src` (a uint8 device tensor) with the
-    decode GEMV's grid shape; one word per wave goes to `out`."""
-    _require_device(src, out)
-    check(load().gq_probe_read(_ptr(src), src.numel(), wgs, waves_per_wg, _ptr(out), _stream(stream)),
-          "gq_probe_read")
-
-
-def probe_empty(wgs: int, waves_per_wg: int, stream=None):
-    """Calibration: the same grid with no work."""
-    check(load().gq_probe_empty(wgs, waves_per_wg, _stream(stream)), "gq_probe_empty")
 
 
 def _chain_ops(ops):

@@ -438,8 +438,9 @@ bool GGUFLoader::plan(const std::string &name, LoadKind kind, LoadPlan *p, std::
     if (t.shape[0] == dm && t.shape[1] == kv) r.transpose = true;
     else if (t.shape[0] == kv && t.shape[1] == dm) {
     } else
-      return set_err(err, std::string("GQA KV ") + what + "load failed for " + name + ": unsupported shape [" +
-                              std::to_string(t.shape[0]) + "," + std::to_string(t.shape[1]) + "]"),
+      return set_err(err, std::string("GQA KV ") + what + "load failed for " + name + ": shape " +
+                              std::to_string(t.shape[0]) + " x " + std::to_string(t.shape[1]) +
+                              " matches neither dim x kv nor kv x dim"),
              false;
     return true;
   };
@@ -462,7 +463,7 @@ bool GGUFLoader::plan(const std::string &name, LoadKind kind, LoadPlan *p, std::
     break;
   case LoadKind::INT8:
     if (!dequantizable())
-      return set_err(err, "Unsupported INT8 conversion for type " + t.dtype), false;
+      return set_err(err, "no INT8 requantization from tensor type " + t.dtype), false;
     // Q8_0 blocks are split as stored (no transpose), other types requantized
     if (type != T_Q8_0 && !gqa("INT8 ")) return false;
     r.bytes = r.n_elem;
@@ -471,7 +472,7 @@ bool GGUFLoader::plan(const std::string &name, LoadKind kind, LoadPlan *p, std::
     break;
   case LoadKind::INT4: {
     if (!dequantizable())
-      return set_err(err, "Unsupported INT4 conversion for type " + t.dtype), false;
+      return set_err(err, "no INT4 requantization from tensor type " + t.dtype), false;
     if (!gqa("INT4 ")) return false;
     r.bytes = (r.n_elem + 1) / 2;
     r.scale_bytes = ((r.n_elem + 31) / 32) * 4;
@@ -524,7 +525,7 @@ bool GGUFLoader::load_into(const std::string &name, LoadKind kind, const LoadPla
   const size_t n = p.n_elem;
   const size_t kv = (size_t)cfg.num_heads_kv * cfg.head_dim, dm = cfg.dim;
   auto note_transpose = [&]() {
-    std::cout << "[GRETA_LOAD] Transposed " << name << " from [D, KV] to [KV, D]" << std::endl;
+    std::cout << "[gq-load] " << name << ": K/V rows reordered, dim x kv -> kv x dim" << std::endl;
   };
 
   if (kind == LoadKind::QUANT) {
@@ -678,7 +679,7 @@ std::unique_ptr<WeightLoader> create_weight_loader(const std::string &path, std:
     if (!l->open(path, err)) return nullptr;
     return l;
   }
-  set_err(err, "Unsupported format");
+  set_err(err, "not a .gguf or .greta path: " + path);
   return nullptr;
 }
 

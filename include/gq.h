@@ -208,16 +208,6 @@ int gq_launch_gemm_mfma_int4_wt_fp32_acc32(void *stream, const void *a, const in
                                             uint32_t group_size, uint32_t head_dim, int is_fp16_a,
                                             int force_gemv);
 
-/* ---- calibration (no counterpart in the reference) ------------------------
- * Kernels the benchmark times beside the GEMV to state its read ceiling.
- * gq_probe_read: wgs workgroups of waves_per_wg waves stream `bytes` (a
- * multiple of 16) of src as the decode GEMV streams its weights (each wave a
- * contiguous share of whole KiB, at most 16 KiB, all loads issued up front);
- * out (wgs * waves_per_wg words) is never written in practice, it keeps the
- * loads live.  gq_probe_empty: the same grid doing nothing. */
-int gq_probe_read(const void *d_src, size_t bytes, int wgs, int waves_per_wg, uint32_t *d_out, void *stream);
-int gq_probe_empty(int wgs, int waves_per_wg, void *stream);
-
 #ifdef __cplusplus
 }
 #endif

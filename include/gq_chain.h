@@ -19,6 +19,14 @@
  * columns [k_offset, k_offset + K) of an N x k_total tensor; x then holds
  * those K values.  The library splits ops whose K exceeds its per-launch
  * limit into such ranges itself (chained through resid).
+ *
+ * Ordering: inside the one launch an op runs after the ops it depends on
+ * (transitively) and is unordered with every other op.  So an op whose y
+ * overlaps a buffer that an earlier op reads (x, gamma, resid) or writes (y)
+ * must depend on that op, directly or through other ops; the plan refuses
+ * such a pair otherwise (GQ_ERR_INVALID_ARGS), as it refuses a y that
+ * aliases the op's own inputs.  Alignment: x and gamma 16 bytes (vector
+ * loads), resid and y 4 bytes.
  */
 #ifndef GQ_CHAIN_H
 #define GQ_CHAIN_H

@@ -135,3 +135,16 @@ def test_product_path_never_loads_the_oracle():
     assert "gqoracle" not in deps and "gqref" not in deps
     src = open(os.path.join(ROOT, "gretacore-v3_amd", "gq.py")).read()
     assert "oracle" not in src.replace("no CPU fallback", "")
+
+
+def test_calibration_library_is_separate():
+    """The benchmark's calibration kernels (read probe, empty kernel) live in
+    lib/libgqcalib.so, which exports them and needs nothing from libgq.so;
+    the product library does not carry them."""
+    calib = os.path.join(os.path.dirname(gq.LIB_PATH), "libgqcalib.so")
+    defined = subprocess.run(["nm", "-D", "--defined-only", calib], capture_output=True, text=True,
+                             check=True).stdout
+    assert "gq_probe_read" in defined and "gq_probe_empty" in defined
+    undef = subprocess.run(["nm", "-D", "-u", calib], capture_output=True, text=True, check=True).stdout
+    assert "gq_" not in undef
+    assert not any("probe" in s for s in exported_symbols())

@@ -2,7 +2,7 @@
 through the C ABI: two calls in a row on one GPU, the second with a smaller
 input, each bit-identical to gq_gemm with a caller workspace (the same
 kernels on the same data); a shape whose conversion exceeds the fixed scratch
-is refused."""
+is refused, and the same size with no conversion to make is accepted."""
 import ctypes
 
 import numpy as np
@@ -54,3 +54,15 @@ def test_gemm_static_matches_gemm(dev):
     packed = torch.zeros(gq.packed_size(O.Q4_0, 16, k), dtype=torch.uint8, device=dev)
     st, _ = _run_static(lib, O.Q4_0, packed, a, 16, k, torch.float32)
     assert st == 4  # GQ_ERR_WORKSPACE
+    # the same size needs no scratch when A is used as it is (fp16 of the
+    # padded width, Q8_0's k order): accepted, bit-identical to gq_gemm
+    n = 512
+    w = O.gen_weights(O.Q8_0, n, k, seed=510)
+    packed = gq.repack(O.Q8_0, torch.from_numpy(w).to(dev), n, k)
+    a = torch.randn(m, k, generator=torch.Generator().manual_seed(610)).to(torch.float16).to(dev)
+    assert gq.gemm_workspace_bytes(O.Q8_0, m, k) > lib.gq_gemm_static_max_bytes()
+    ref = gq.gemm(O.Q8_0, packed, a, n, k, out_dtype=torch.float32)
+    st, c = _run_static(lib, O.Q8_0, packed, a, n, k, torch.float32)
+    assert st == 0, gq.load().gq_status_string(st)
+    torch.cuda.synchronize()
+    assert torch.equal(c, ref)
