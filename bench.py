@@ -33,7 +33,7 @@ CACHE_DEFEAT_BYTES = 512 << 20  # > 256 MB Infinity Cache
 # FETCH_SIZE + WRITE_SIZE and calibrated against a 64 MiB bitwise_not in the
 # same runs (profiles/k_gemv_q_q4_0_14336x4096.md); valid for the launch plan
 # it was measured with.
-PROFILED_TRAFFIC = {("q4_0", 14336, 4096, 1, 2, 8): 33_280_000}
+PROFILED_TRAFFIC = {("q4_0", 14336, 4096, 1, 2, 8): 33_291_776}
 
 
 def log(*a):
@@ -113,7 +113,7 @@ class ClockSampler:
                 return None
             v = sorted(v)
             return {"min": v[0], "median": v[len(v) // 2], "max": v[-1], "samples": len(v)}
-        return {"sclk_mhz": st(self.sclk), "power_w": st(self.power)}
+        return {"dpm_level_sclk_mhz": st(self.sclk), "power_average_w": st(self.power)}
 
 
 def box_state():
@@ -586,6 +586,8 @@ def calib():
         lib.gq_probe_read.argtypes = [vp, ctypes.c_size_t, ctypes.c_int, ctypes.c_int, vp, vp]
         lib.gq_probe_empty.restype = ctypes.c_int
         lib.gq_probe_empty.argtypes = [ctypes.c_int, ctypes.c_int, vp]
+        lib.gq_probe_clock.restype = ctypes.c_int
+        lib.gq_probe_clock.argtypes = [vp, ctypes.c_int, ctypes.c_int, vp]
         _calib = lib
     return _calib
 
@@ -603,6 +605,20 @@ def probe_empty(wgs, waves):
     rc = calib().gq_probe_empty(wgs, waves, torch.cuda.current_stream().cuda_stream)
     if rc != 0:
         raise RuntimeError(f"gq_probe_empty: status {rc}")
+
+
+def probe_clock_mhz(dev, iters=50000):
+    """Effective shader clock (MHz) while every SIMD runs MFMA chains on
+    changing operands (~20 ms): s_memtime ticks over s_memrealtime's 100 MHz
+    ticks in one wave (the sysfs level is the DPM state, not the clock held
+    under load)."""
+    import torch
+    out = torch.zeros(8, dtype=torch.int64, device=dev)
+    rc = calib().gq_probe_clock(out.data_ptr(), 1024, iters, torch.cuda.current_stream().cuda_stream)
+    if rc != 0:
+        raise RuntimeError(f"gq_probe_clock: status {rc}")
+    t0, t1, r0, r1 = (int(v) for v in out[:4].cpu())
+    return round((t1 - t0) / max(1, r1 - r0) * 100.0, 1)
 
 
 def bench_read_ceiling(dev, steps, warmup):
@@ -719,6 +735,7 @@ def main():
         c = GemvCase(fmt, n, k, b, wseed=seed, xseed=seed + 1000, dev=dev)
         print(json.dumps({name: bench_gemv(c, steps, warmup)}), flush=True)
         return
+    clock_mhz = {"before_headline": probe_clock_mhz(dev)}
     log("[bench] headline: Q4_0 GEMV 14336x4096 batch 1")
     head = GemvCase(O.Q4_0, 14336, 4096, 1, wseed=1002, xseed=2002, dev=dev)
     sysdir = gpu_sysfs_dir()
@@ -747,6 +764,7 @@ def main():
                     if m == 2048 and n == 14336:
                         extra[name]["clock_during"] = clk.summary()
                     torch.cuda.empty_cache()
+        clock_mhz["after_gemms"] = probe_clock_mhz(dev)
         log("[bench] int8 route for Q8_0 (per-32 activation quantization + int8 MFMA)")
         extra["gemm_q8_0_i8_m2048_14336x4096"] = bench_gemm_q8_i8(2048, 14336, 4096, steps, dev)
         torch.cuda.empty_cache()
@@ -785,7 +803,8 @@ def main():
                    "arithmetic": "Q4_0 codes x two int8 limbs of the activations per 32-block on the int8 "
                                  "MFMA, int32 products scaled and summed in f32",
                    "alg_bytes_per_step": h["alg_bytes"],
-                   "box": dict(box_state(), clock_during_headline=clk_head.summary())},
+                   "box": dict(box_state(), clock_during_headline=clk_head.summary(),
+                               sclk_under_mfma_load_mhz=clock_mhz)},
         "pct_peak": round(h["pct_peak"], 2),
         "rel_l2_vs_oracle": h["rel_l2"],
         "roofline": {"bound": "hbm", "achieved": round(h["GBps"], 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",

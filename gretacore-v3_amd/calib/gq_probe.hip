@@ -73,3 +73,51 @@ extern "C" int gq_probe_empty(int wgs, int waves_per_wg, void *stream) {
   hipLaunchKernelGGL(k_probe_empty, dim3((unsigned)wgs), dim3(64 * waves_per_wg), 0, (hipStream_t)stream);
   return last_launch();
 }
+
+// ---- effective shader clock under matrix-core load --------------------------
+// Every SIMD runs chains of v_mfma_f32_32x32x16_f16 on operands that change
+// every iteration (so the data toggles as a real GEMM's do); wave 0 of
+// workgroup 0 reads the shader-clock counter (s_memtime) and the constant
+// 100 MHz counter (s_memrealtime) before and after its loop.  The ratio of
+// the two differences is the clock the box holds under MFMA load.
+namespace {
+__global__ void __launch_bounds__(256) k_probe_clock(unsigned long long *out, int iters, uint32_t never) {
+  const int lane = threadIdx.x & 63;
+  uint32_t h = 0x9E3779B9u * (uint32_t)(threadIdx.x + 1) ^ (uint32_t)blockIdx.x * 0x85EBCA6Bu;
+  gq_u4 ua, ub;
+  for (int e = 0; e < 4; ++e) {
+    h = h * 1664525u + 1013904223u;
+    ua[e] = (h & 0x3BFF3BFFu);  // fp16 values below 1 in magnitude, random mantissas
+    h = h * 1664525u + 1013904223u;
+    ub[e] = (h & 0x3BFF3BFFu);
+  }
+  gq_f16v acc0 = {}, acc1 = {}, acc2 = {}, acc3 = {};
+  const unsigned long long t0 = __builtin_amdgcn_s_memtime(), r0 = __builtin_amdgcn_s_memrealtime();
+  for (int i = 0; i < iters; ++i) {
+    const gq_half8 a = __builtin_bit_cast(gq_half8, ua), b = __builtin_bit_cast(gq_half8, ub);
+    acc0 = gq_mfma32(a, b, acc0);
+    acc1 = gq_mfma32(b, a, acc1);
+    acc2 = gq_mfma32(a, a, acc2);
+    acc3 = gq_mfma32(b, b, acc3);
+    ua ^= gq_u4{0x01230123u, 0x02460246u, 0x00FF00FFu, 0x01010101u};
+    ub ^= gq_u4{0x00110011u, 0x03000300u, 0x000F000Fu, 0x02020202u};
+  }
+  const unsigned long long t1 = __builtin_amdgcn_s_memtime(), r1 = __builtin_amdgcn_s_memrealtime();
+  float s = 0.f;
+  for (int v = 0; v < 16; ++v) s += acc0[v] + acc1[v] + acc2[v] + acc3[v];
+  if (__float_as_uint(s) == never) out[4] = (unsigned long long)lane;
+  if (blockIdx.x == 0 && threadIdx.x == 0) {
+    out[0] = t0;
+    out[1] = t1;
+    out[2] = r0;
+    out[3] = r1;
+  }
+}
+}  // namespace
+
+extern "C" int gq_probe_clock(unsigned long long *d_out, int wgs, int iters, void *stream) {
+  if (!d_out || wgs <= 0 || iters <= 0) return GQ_ERR_INVALID_ARGS;
+  hipLaunchKernelGGL(k_probe_clock, dim3((unsigned)wgs), dim3(256), 0, (hipStream_t)stream, d_out, iters,
+                     0x7FC12345u);
+  return last_launch();
+}
