@@ -230,6 +230,32 @@ def bench_gemv(case, steps, warmup):
     }
 
 
+def bench_f16w(n, k, batch, steps, warmup, dev):
+    """The FP16-weight route (gq_gemm_f16w; the reference's FP16 GretaCompute::gemm
+    path, e.g. a Q6_K lm_head dequantized to fp16 at load): one call per step
+    over a weight matrix larger than the Infinity Cache (no rotation needed);
+    parity on 1024 sampled rows against an fp64 product."""
+    import numpy as np
+    import torch
+
+    import gq
+    import oracle as O
+    g = torch.Generator(device="cpu").manual_seed(1007)
+    w = (torch.randn(n, k, generator=g) * 0.05).to(torch.float16)
+    x = torch.randn(batch, k, generator=g)
+    wd, xd = w.to(dev), x.to(dev)
+    y = torch.empty((batch, n), dtype=torch.float32, device=dev)
+    gq.gemm_f16w(wd, xd, n, k, c=y)
+    rows = np.linspace(0, n - 1, 1024).astype(int)
+    ref = x.double().numpy() @ w[rows].double().numpy().T
+    err = O.rel_l2(y[:, rows].cpu().numpy(), ref)
+    byts = n * k * 2 + 4 * batch * (n + k)
+    t = graph_steps(lambda i: gq.gemm_f16w(wd, xd, n, k, c=y), steps, warmup)
+    del wd
+    return {"step_us": t * 1e6, "GBps": byts / t / 1e9, "pct_peak": 100.0 * byts / t / 1e9 / HBM_PEAK_GBS,
+            "alg_bytes": byts, "rel_l2": err}
+
+
 def bench_gemm(fmt, m, n, k, steps, warmup, dev, out_dtype="f32"):
     import torch
 
@@ -754,6 +780,9 @@ def main():
             extra[name] = bench_gemv(c, max(20, steps // 2), warmup)
             del c
             torch.cuda.empty_cache()
+        log("[bench] fp16-weight lm_head (the reference's FP16 route)")
+        extra["f16_lm_head_128256x4096_b1"] = bench_f16w(128256, 4096, 1, 20, 3, dev)
+        torch.cuda.empty_cache()
         for fmt, fname in ((O.Q4_0, "q4_0"), (O.Q8_0, "q8_0"), (O.Q4_K, "q4_k")):
             for m in (64, 512, 2048):
                 for n in (4096, 14336):

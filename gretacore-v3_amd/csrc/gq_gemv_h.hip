@@ -40,8 +40,19 @@ struct HFmt<GQ_FMT_Q6_K> {
   static constexpr int CK = 256, QB = 3072, SB = 288, STEPS = 4;
 };
 
+// fp16 weights, row-major N x K (the reference's FP16 route, no T16 layout):
+// a "chunk" is 128 k of one row tile, read straight from the 16 rows
+template <>
+struct HFmt<GQ_FMT_F16> {
+  static constexpr int CK = 128, QB = 0, SB = 0, STEPS = 2;
+};
+
 template <int FMT>
 struct HChunk;
+template <>
+struct HChunk<GQ_FMT_F16> {
+  gq_u4 q[4];  // step m: q[2m], q[2m + 1] = the lane's 16 fp16 weights (halves 0, 1)
+};
 template <>
 struct HChunk<GQ_FMT_Q4_0> {
   gq_u4 q;  // steps 0, 1: 8-byte code groups
@@ -87,6 +98,58 @@ GQ_DEV void load_hchunk(const uint8_t *qp, const uint8_t *sp, uint32_t qo, uint3
   }
 }
 
+// Where a wave's chunks of one row tile come from: T16 records (chunk ci of
+// the tile at q + ci * QB, its scales at s + ci * SB, this lane's offsets
+// qo / so), or, for row-major fp16 weights, this lane's row (row tile rows
+// past N read row N - 1, never stored) with the lane's k offset qo (bytes)
+// and the row length K.
+template <int FMT>
+struct HSrc {
+  const uint8_t *q, *s;
+  uint32_t qo, so;
+  int K;
+};
+template <int FMT>
+GQ_DEV HSrc<FMT> hsrc(const uint8_t *w, size_t sc_off, size_t tile, int C, int N, int K, int lane) {
+  const int g = lane >> 4, r = lane & 15;
+  if constexpr (FMT == GQ_FMT_F16) {
+    size_t n = tile * 16 + (size_t)r;
+    n = n < (size_t)N ? n : (size_t)N - 1;
+    return HSrc<FMT>{w + n * (size_t)K * 2, nullptr, 32u * (uint32_t)g, 0u, K};
+  } else {
+    using F = HFmt<FMT>;
+    const uint32_t slane = (FMT == GQ_FMT_Q4_K || FMT == GQ_FMT_Q6_K) ? 16u * (uint32_t)r
+                                                                      : 8u * (uint32_t)r + 4u * (uint32_t)(g >> 1);
+    return HSrc<FMT>{w + tile * (size_t)C * F::QB, w + sc_off + tile * (size_t)C * F::SB, 16u * (uint32_t)lane,
+                     slane, K};
+  }
+}
+
+template <int FMT>
+GQ_DEV void load_src(const HSrc<FMT> &src, int ci, HChunk<FMT> &ch) {
+  if constexpr (FMT == GQ_FMT_F16) {
+    // step m: k = 128 ci + 64 m + 16 g .. + 15 (K % 32 == 0: wholly in or out
+    // of the row); a run past K reads the row's start and is zeroed
+#pragma unroll
+    for (int m = 0; m < 2; ++m) {
+      const uint32_t kb = 2u * (uint32_t)(128 * ci + 64 * m) + src.qo;  // byte offset in the row
+      const bool in = kb < 2u * (uint32_t)src.K;
+      const uint8_t *p = src.q + (in ? kb : 0u);
+      gq_u4 a = gq_ld16_nt(p), b = gq_ld16_nt(p + 16);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        a[e] = in ? a[e] : 0u;
+        b[e] = in ? b[e] : 0u;
+      }
+      ch.q[2 * m] = a;
+      ch.q[2 * m + 1] = b;
+    }
+  } else {
+    using F = HFmt<FMT>;
+    load_hchunk<FMT>(src.q + (size_t)ci * F::QB, src.s + (size_t)ci * F::SB, src.qo, src.so, ch);
+  }
+}
+
 // 4 byte values u (0..255) -> 2 fp16 pairs holding (1024 + u)
 GQ_DEV void magic4(uint32_t u, gq_half2 &lo, gq_half2 &hi) {
   lo = gq_bits_h2(__builtin_amdgcn_perm(0x64646464u, u, 0x04010400u));
@@ -110,7 +173,11 @@ GQ_DEV _Float16 bits_h(uint32_t b16) { return __builtin_bit_cast(_Float16, (uint
 // the chunk (Q6_K: 16-element scale group 4 m + g).
 template <int FMT>
 GQ_DEV void dequant_step(const HChunk<FMT> &c, int m, int g, uint32_t mg, gq_half8 &o0, gq_half8 &o1) {
-  if constexpr (FMT == GQ_FMT_Q4_0 || FMT == GQ_FMT_Q4_K) {
+  if constexpr (FMT == GQ_FMT_F16) {
+    o0 = __builtin_bit_cast(gq_half8, c.q[2 * m]);
+    o1 = __builtin_bit_cast(gq_half8, c.q[2 * m + 1]);
+    return;
+  } else if constexpr (FMT == GQ_FMT_Q4_0 || FMT == GQ_FMT_Q4_K) {
     uint32_t w0, w1;
     gq_half2 a1, b1, a16, b16;  // (h * a + b) per pair; then * d2 + m2 (Q4_K)
     gq_half2 d2, m1, m16;
@@ -333,11 +400,8 @@ k_gemv_h(const uint8_t *__restrict__ w, size_t sc_off, const float *__restrict__
   const int g = lane >> 4, r = lane & 15;
   const int ntiles = (int)gq_tiles(N);
   const size_t tile = (size_t)blockIdx.x * TW + tt;
-  const size_t tb = (tile < (size_t)ntiles ? tile : (size_t)ntiles - 1) * (size_t)C;
+  const HSrc<FMT> src = hsrc<FMT>(w, sc_off, tile < (size_t)ntiles ? tile : (size_t)ntiles - 1, C, N, K, lane);
   const int c0 = (C * part) / KS, c1 = (C * (part + 1)) / KS;  // this wave's chunks (c0 < c1: KS <= C)
-  const uint32_t qlane = 16u * (uint32_t)lane;
-  const uint32_t slane = (FMT == GQ_FMT_Q4_K || FMT == GQ_FMT_Q6_K) ? 16u * (uint32_t)r
-                                                                    : 8u * (uint32_t)r + 4u * (uint32_t)(g >> 1);
 
   // weights of window `it` (chunks past the part re-read its last chunk)
   auto load_win = [&](int it, HChunk<FMT> (&ch)[WC]) {
@@ -345,7 +409,7 @@ k_gemv_h(const uint8_t *__restrict__ w, size_t sc_off, const float *__restrict__
     for (int j = 0; j < WC; ++j) {
       int ci = c0 + it * WC + j;
       ci = ci < c1 ? ci : c1 - 1;
-      load_hchunk<FMT>(w + (tb + ci) * F::QB, w + sc_off + (tb + ci) * F::SB, qlane, slane, ch[j]);
+      load_src<FMT>(src, ci, ch[j]);
     }
   };
   // activations: run u of this thread = (part p, batch row b, 8-run kr); its
@@ -541,12 +605,9 @@ k_gemv_h1(const uint8_t *__restrict__ w, size_t sc_off, const float *__restrict_
   const int g = lane >> 4, r = lane & 15;
   const int ntiles = (int)gq_tiles(N);
   const size_t tile = (size_t)blockIdx.x * TW + tt;
-  const size_t tb = (tile < (size_t)ntiles ? tile : (size_t)ntiles - 1) * (size_t)C;
+  const HSrc<FMT> src = hsrc<FMT>(w, sc_off, tile < (size_t)ntiles ? tile : (size_t)ntiles - 1, C, N, K, lane);
   const int c0 = (C * part) / KS, c1 = (C * (part + 1)) / KS;  // c0 < c1 (KS <= C)
   const int nck = c1 - c0;                                     // <= NCK (host-checked)
-  const uint32_t qlane = 16u * (uint32_t)lane;
-  const uint32_t slane = (FMT == GQ_FMT_Q4_K || FMT == GQ_FMT_Q6_K) ? 16u * (uint32_t)r
-                                                                    : 8u * (uint32_t)r + 4u * (uint32_t)(g >> 1);
 
   // ---- 1. activation loads (the workgroup's whole range), then weights -------
   // run -> (part p, batch row b, run kr of the row's part); the 32 runs of a
@@ -575,7 +636,7 @@ k_gemv_h1(const uint8_t *__restrict__ w, size_t sc_off, const float *__restrict_
 #pragma unroll
   for (int i = 0; i < NCK; ++i) {
     const int ci = c0 + i < c1 ? c0 + i : c1 - 1;  // surplus loads re-read the last chunk
-    load_hchunk<FMT>(w + (tb + ci) * F::QB, w + sc_off + (tb + ci) * F::SB, qlane, slane, ch[i]);
+    load_src<FMT>(src, ci, ch[i]);
   }
   __builtin_amdgcn_sched_barrier(0);
 
@@ -690,7 +751,7 @@ k_gemv_h1(const uint8_t *__restrict__ w, size_t sc_off, const float *__restrict_
 template <int FMT, int CT, int NCK, bool CBF16, int KW = 8, int MT = 4>
 __global__ void __launch_bounds__(64 * KW) k_gemm_sk(const uint8_t *__restrict__ w, size_t sc_off,
                                                      const _Float16 *__restrict__ a16, int lda, void *__restrict__ c,
-                                                     const float *__restrict__ rs, int M, int N, int C) {
+                                                     const float *__restrict__ rs, int M, int N, int C, int K) {
   using F = HFmt<FMT>;
   constexpr int NS = NCK * F::STEPS;  // 64-k steps per wave (static bound)
   __shared__ gq_f4 red[KW][CT * MT][64];
@@ -702,20 +763,17 @@ __global__ void __launch_bounds__(64 * KW) k_gemm_sk(const uint8_t *__restrict__
   const int c0 = (C * wave) / KW, c1 = (C * (wave + 1)) / KW;
   const int nck = c1 - c0;  // <= NCK (host-checked); 0 when C < KW
   const int clast = nck > 0 ? c1 - 1 : c0;  // last chunk a load may name (c0 < C always)
-  const uint32_t qlane = 16u * (uint32_t)lane;
-  const uint32_t slane = (FMT == GQ_FMT_Q4_K || FMT == GQ_FMT_Q6_K) ? 16u * (uint32_t)r
-                                                                    : 8u * (uint32_t)r + 4u * (uint32_t)(g >> 1);
   // weights: every chunk of the wave, tile by tile (surplus loads re-read the
   // last chunk)
   HChunk<FMT> ch[CT][NCK];
 #pragma unroll
   for (int ct = 0; ct < CT; ++ct) {
     const int t0 = (int)blockIdx.x * CT + ct;
-    const size_t tb = (size_t)(t0 < ntiles ? t0 : ntiles - 1) * (size_t)C;
+    const HSrc<FMT> src = hsrc<FMT>(w, sc_off, (size_t)(t0 < ntiles ? t0 : ntiles - 1), C, N, K, lane);
 #pragma unroll
     for (int i = 0; i < NCK; ++i) {
       const int ci = c0 + i <= clast ? c0 + i : clast;
-      load_hchunk<FMT>(w + (tb + ci) * F::QB, w + sc_off + (tb + ci) * F::SB, qlane, slane, ch[ct][i]);
+      load_src<FMT>(src, ci, ch[ct][i]);
     }
   }
   // this lane's A rows: 16 mt + r of the block, k offset 16 g
@@ -848,6 +906,7 @@ int gq_gemv_h1_plan(int fmt, size_t N, size_t K, int nb, int *R_out, int *ks_out
   const int e = env_int("GQ_GEMV_H1");
   if (e == 0 && getenv("GQ_GEMV_H1")) return GQ_ERR_UNSUPPORTED;
   if (e != 1 && (f == GQ_FMT_Q8_0 || f == GQ_FMT_Q6_K)) return GQ_ERR_UNSUPPORTED;
+  if (f == GQ_FMT_F16) return GQ_ERR_UNSUPPORTED;  // (its chunks spill the 16-wave workgroups)
   const int C = (int)gq_chunks(f, K);
   const int CK = f == GQ_FMT_Q4_K || f == GQ_FMT_Q6_K ? 256 : 128;
   const int maxc = f == GQ_FMT_Q4_0 || f == GQ_FMT_Q8_0 ? 8 : 4;
@@ -883,11 +942,15 @@ int gq_gemv_h_plan(int fmt, size_t N, size_t K, int nb, int *R_out, int *ks_out,
   const int er = env_int("GQ_GEMV_H_R");
   if (er == 1 || er == 2 || er == 4) tw = er;
   (void)nb;  // batch-independent (a 16-way split of 8-row windows measured slower than 8)
+  // fp16 weights: 64 registers of weights per window and wave; at most 8
+  // waves per workgroup, so the register budget holds them without spilling
+  const int maxw = f == GQ_FMT_F16 ? 8 : 16;
+  if (tw > maxw) tw = maxw;
   int ks = 1;
-  while (ks < 8 && tiles * ks < 3584 && 2 * ks <= C && tw * ks < 16) ks *= 2;
+  while (ks < 8 && tiles * ks < 3584 && 2 * ks <= C && tw * ks < maxw) ks *= 2;
   const int e = env_int("GQ_GEMV_H_KSPLIT");
   if ((e == 1 || e == 2 || e == 4 || e == 8) && e <= C) ks = e;
-  if (tw * ks > 16) tw = 16 / ks;
+  if (tw * ks > maxw) tw = maxw / ks > 0 ? maxw / ks : 1;
   *R_out = tw;
   *ks_out = ks;
   *cpw_out = (C + ks - 1) / ks;
@@ -905,7 +968,7 @@ int launch_h_tw(const void *packed, const float *x, float *y, int N, int K, int 
   const int NI = ((C + ks - 1) / ks + WC - 1) / WC;
   // x runs must spread evenly over the threads (TW <= MR / 2)
 #define GQ_LAUNCH_H(KS)                                                                                               \
-  if constexpr (2 * TW <= MR) {                                                                                       \
+  if constexpr (2 * TW <= MR && !(FMT == GQ_FMT_F16 && TW * KS > 8)) {                                               \
     hipLaunchKernelGGL((k_gemv_h<FMT, TW, KS, MR>), dim3((unsigned)wgs), dim3(64 * TW * KS), 0, s, w, sc_off, x, y, \
                        N, K, C, nb, NI);                                                                              \
   } else {                                                                                                            \
@@ -986,6 +1049,49 @@ int gq_launch_gemv_h(int fmt, const void *packed, const float *x, float *y, int 
   }
 }
 
+// ---- fp16 weights (row-major N x K): the reference's FP16 route ---------------
+// C[M][N] = A[M][K] W^T with fp32 A, fp16 W and fp32 accumulation, batch
+// GEMVs of up to 16 rows of A at a time on the fp16 batch kernels (the
+// weights need no dequantization; A is rounded to fp16 after the per-window
+// power-of-two scaling, as every batch GEMV here does).  Rows of A beyond 16
+// take further launches (each re-reads W).
+extern "C" int gq_gemm_f16w(const void *w, const float *a, float *c, size_t M, size_t N, size_t K, void *stream) {
+  GQ_CHECK(M <= GQ_MAX_DIM && N <= GQ_MAX_DIM && K <= GQ_MAX_DIM, GQ_ERR_INVALID_ARGS);
+  GQ_CHECK(w && a && c, GQ_ERR_INVALID_ARGS);
+  // 16-element lane runs must not straddle rows, and rows start 16-byte aligned
+  GQ_CHECK(K % 32 == 0 && (uintptr_t)w % 16 == 0 && (uintptr_t)a % 16 == 0, GQ_ERR_UNSUPPORTED);
+  hipStream_t s = (hipStream_t)stream;
+  if (M == 0 || N == 0) return GQ_OK;
+  if (K == 0) return gq_fill_zero(c, M * N, s);
+  for (size_t m0 = 0; m0 < M; m0 += GQ_MAX_BATCH) {
+    const int nb = (int)(M - m0 < (size_t)GQ_MAX_BATCH ? M - m0 : (size_t)GQ_MAX_BATCH);
+    GQ_TRY(launch_h<GQ_FMT_F16>(w, a + m0 * K, c + m0 * N, (int)N, (int)K, nb, s));
+  }
+  return GQ_OK;
+}
+
+// The reference's two FP16-weight launchers under their argument lists
+// (gemm_kernels.hpp:30-44): W is N x K (row stride K whatever ldb says, as the
+// reference's kernels read b[n * K + k]); A rows at stride lda, C rows at
+// stride ldc, both as GretaCompute::gemm passes them (K and N; other strides
+// are refused).  The VALU launcher writes zeros for K == 0; the MFMA one
+// returns at once when any dimension is zero (gemm_kernels.hip:347-358,
+// 509-514).
+extern "C" int gq_launch_gemm_mixed_f16f32(void *stream, const float *a, const void *b, float *c, uint32_t M,
+                                           uint32_t N, uint32_t K, uint32_t lda, uint32_t ldb, uint32_t ldc) {
+  (void)ldb;
+  if (M == 0 || N == 0) return GQ_OK;
+  GQ_CHECK(lda == K && ldc == N, GQ_ERR_UNSUPPORTED);
+  return gq_gemm_f16w(b, a, c, M, N, K, stream);
+}
+extern "C" int gq_launch_gemm_mfma_mixed_f16f32(void *stream, const float *a, const void *b, float *c, uint32_t M,
+                                                uint32_t N, uint32_t K, uint32_t lda, uint32_t ldb, uint32_t ldc) {
+  (void)ldb;
+  if (M == 0 || N == 0 || K == 0) return GQ_OK;
+  GQ_CHECK(lda == K && ldc == N, GQ_ERR_UNSUPPORTED);
+  return gq_gemm_f16w(b, a, c, M, N, K, stream);
+}
+
 // Skinny GEMM plan: M <= 256 (Q6_K: any M), a chunk list of at most 4 per wave
 // of 8 (K <= 4096 for Q4_0 / Q8_0, 8192 for Q4_K; Q6_K 2, K <= 4096) or, for
 // Q4_0 / Q4_K, 8 per wave of 16 (K <= 16384 / 32768; *nck_out = 16 + chunks), CT = 2 row tiles per workgroup where that
@@ -1040,10 +1146,10 @@ int launch_sk(const void *packed, const _Float16 *a16, int lda, void *c, const f
       const dim3 g2((unsigned)gq_tiles(N), (unsigned)((M + 31) / 32));
       if (nck == 20)
         hipLaunchKernelGGL((k_gemm_sk<FMT, 1, 4, CBF16, 16, 2>), g2, dim3(1024), 0, s, w, sc_off, a16, lda, c, rs, M, N,
-                           C);
+                           C, K);
       else if constexpr (FMT == GQ_FMT_Q4_0)
         hipLaunchKernelGGL((k_gemm_sk<FMT, 1, 8, CBF16, 16, 2>), g2, dim3(1024), 0, s, w, sc_off, a16, lda, c, rs, M, N,
-                           C);
+                           C, K);
       else
         return GQ_ERR_UNSUPPORTED;
       return gq_last_launch();
@@ -1051,11 +1157,11 @@ int launch_sk(const void *packed, const _Float16 *a16, int lda, void *c, const f
     return GQ_ERR_UNSUPPORTED;
   }
   if (nck <= 1)
-    hipLaunchKernelGGL((k_gemm_sk<FMT, CT, 1, CBF16>), grid, dim3(512), 0, s, w, sc_off, a16, lda, c, rs, M, N, C);
+    hipLaunchKernelGGL((k_gemm_sk<FMT, CT, 1, CBF16>), grid, dim3(512), 0, s, w, sc_off, a16, lda, c, rs, M, N, C, K);
   else if (nck <= 2)
-    hipLaunchKernelGGL((k_gemm_sk<FMT, CT, 2, CBF16>), grid, dim3(512), 0, s, w, sc_off, a16, lda, c, rs, M, N, C);
+    hipLaunchKernelGGL((k_gemm_sk<FMT, CT, 2, CBF16>), grid, dim3(512), 0, s, w, sc_off, a16, lda, c, rs, M, N, C, K);
   else if constexpr (FMT != GQ_FMT_Q6_K)
-    hipLaunchKernelGGL((k_gemm_sk<FMT, CT, 4, CBF16>), grid, dim3(512), 0, s, w, sc_off, a16, lda, c, rs, M, N, C);
+    hipLaunchKernelGGL((k_gemm_sk<FMT, CT, 4, CBF16>), grid, dim3(512), 0, s, w, sc_off, a16, lda, c, rs, M, N, C, K);
   else
     return GQ_ERR_UNSUPPORTED;
   return gq_last_launch();

@@ -72,6 +72,9 @@ _SIGS = {
     "gq_gemm_static_max_bytes": (_c_size, []),
     "gq_gemm_static": (ctypes.c_int, [ctypes.c_int, _vp, _vp, ctypes.c_int, _vp, ctypes.c_int, _c_size, _c_size,
                                       _c_size, _vp]),
+    "gq_gemm_f16w": (ctypes.c_int, [_vp, _vp, _vp, _c_size, _c_size, _c_size, _vp]),
+    "gq_launch_gemm_mixed_f16f32": (ctypes.c_int, [_vp, _vp, _vp, _vp] + [ctypes.c_uint32] * 6),
+    "gq_launch_gemm_mfma_mixed_f16f32": (ctypes.c_int, [_vp, _vp, _vp, _vp] + [ctypes.c_uint32] * 6),
     "gq_launch_gemm_mfma_int8_wt_fp32_acc32": (
         ctypes.c_int, [_vp, _vp, _vp, _vp, _vp] + [ctypes.c_uint32] * 7),
     "gq_launch_gemm_mfma_int4_wt_fp32_acc32": (
@@ -340,6 +343,28 @@ def matmul(fmt: int, d_packed, a, n: int, k: int, c=None, stream=None):
     if c is None:
         c = torch.empty((m, n), dtype=torch.float32, device=a.device)
     check(load().gq_matmul(fmt, _ptr(d_packed), _ptr(a), _ptr(c), m, n, k, _stream(stream)), "gq_matmul")
+    return c
+
+
+def gemm_f16w(w, a, n: int, k: int, c=None, stream=None):
+    """C[m][n] = sum_k A[m][k] * W[n][k]: fp16 weights W [n][k] (row-major,
+    as GGUF F16 tensors), A float32 [m][k], C float32 (gq_gemm_f16w)."""
+    import torch
+    _require_device(w, a)
+    m = 1 if a.dim() == 1 else a.shape[0]
+    if c is None:
+        c = torch.empty((m, n), dtype=torch.float32, device=a.device)
+    check(load().gq_gemm_f16w(_ptr(w), _ptr(a), _ptr(c), m, n, k, _stream(stream)), "gq_gemm_f16w")
+    return c
+
+
+def launch_mixed_f16f32(a, w, m, n, k, mfma=False, c=None, stream=None):
+    """The reference's FP16-weight launchers (gemm_kernels.hpp:30-44)."""
+    import torch
+    if c is None:
+        c = torch.empty((m, n), dtype=torch.float32, device=a.device)
+    f = load().gq_launch_gemm_mfma_mixed_f16f32 if mfma else load().gq_launch_gemm_mixed_f16f32
+    check(f(_stream(stream), _ptr(a), _ptr(w), _ptr(c), m, n, k, k, n, n), "gq_launch_gemm_mixed_f16f32")
     return c
 
 

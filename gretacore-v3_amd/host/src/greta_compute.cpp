@@ -167,8 +167,33 @@ GretaResult GretaCompute::gemm(GretaStream *stream, GretaMemory *A, GretaMemory 
     }
     break;
   }
+  case GretaDataType::FP16: {
+    // the reference's FP16 route (greta_compute_hip.cpp:361-371): W is N x K
+    // fp16, A fp32 (the reference reads A as float whatever its type); VALU
+    // launcher for M <= 32 or an lm_head label, MFMA launcher above -- both
+    // run gq_gemm_f16w here
+    if (A->data_type() != GretaDataType::FP32) return GretaResult::ERROR_INVALID_ARGS;
+    if (B->size() < (size_t)N * K * 2) return GretaResult::ERROR_INVALID_ARGS;
+    // (the lm_head labels of greta_compute_hip.cpp:73-76 take the VALU route
+    // unless GRETA_LMHEAD_FORCE_ROUTE asks otherwise; GRETA_GEMM_FORCE=MFMA|VALU
+    // forces either, :174-184)
+    bool valu = M <= 32;
+    const bool lm = label == "lm_head" || label == "lm_head_prefill" || label == "lm_head_decode";
+    const char *ff = std::getenv("GRETA_GEMM_FORCE");
+    if (ff && std::string(ff) == "MFMA") valu = false;
+    if (ff && std::string(ff) == "VALU") valu = true;
+    const char *lf = std::getenv("GRETA_LMHEAD_FORCE_ROUTE");
+    if (lm) valu = !(lf && (std::string(lf) == "mfma" || std::string(lf) == "MFMA"));
+    audit.quant_mode = "FP16";
+    audit.route = valu ? "VALU" : "MFMA";
+    st = valu ? gq_launch_gemm_mixed_f16f32(s, static_cast<const float *>(A->data()), B->data(),
+                                            static_cast<float *>(C->data()), M, N, K, K, N, N)
+              : gq_launch_gemm_mfma_mixed_f16f32(s, static_cast<const float *>(A->data()), B->data(),
+                                                 static_cast<float *>(C->data()), M, N, K, K, N, N);
+    break;
+  }
   default:
-    return GretaResult::ERROR_NOT_IMPLEMENTED;  // FP16 / FP32 weights are outside this path
+    return GretaResult::ERROR_NOT_IMPLEMENTED;  // FP32 weights: the reference reads them as fp16 (a bug)
   }
   if (st == GQ_ERR_INVALID_ARGS || st == GQ_ERR_UNSUPPORTED) return GretaResult::ERROR_INVALID_ARGS;
   return st == GQ_OK ? GretaResult::SUCCESS : GretaResult::ERROR_KERNEL_LAUNCH;

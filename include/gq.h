@@ -208,6 +208,24 @@ int gq_launch_gemm_mfma_int4_wt_fp32_acc32(void *stream, const void *a, const in
                                             uint32_t group_size, uint32_t head_dim, int is_fp16_a,
                                             int force_gemv);
 
+/* ---- FP16 weights --------------------------------------------------------
+ * The reference's FP16 route: GretaCompute::gemm with FP16 B
+ * (greta_compute_hip.cpp:361-371) -> launch_gemm_mixed_f16f32 /
+ * launch_gemm_mfma_mixed_f16f32 (gemm_kernels.hpp:30-44, gemm_kernels.hip:
+ * 294-358, 387-523): C[M][N] = A[M][K] W^T, A fp32, W fp16 row-major N x K
+ * (GGUF F16 tensors, e.g. a dequantized lm_head), C fp32.  Here on the fp16
+ * matrix cores in batches of up to 16 rows of A (fp32 accumulation; A rounded
+ * to fp16 after a per-window power-of-two scaling).  K % 32 == 0, d_w and d_a
+ * 16-byte aligned (GQ_ERR_UNSUPPORTED otherwise).  Rows of A beyond 16 take
+ * further launches, each streaming W again. */
+int gq_gemm_f16w(const void *d_w, const float *d_a, float *d_c, size_t M, size_t N, size_t K, void *stream);
+/* The two reference launchers under their argument lists; lda must be K and
+ * ldc N (what GretaCompute::gemm passes), ldb is ignored as in the reference. */
+int gq_launch_gemm_mixed_f16f32(void *stream, const float *a, const void *b, float *c, uint32_t M, uint32_t N,
+                                uint32_t K, uint32_t lda, uint32_t ldb, uint32_t ldc);
+int gq_launch_gemm_mfma_mixed_f16f32(void *stream, const float *a, const void *b, float *c, uint32_t M, uint32_t N,
+                                     uint32_t K, uint32_t lda, uint32_t ldb, uint32_t ldc);
+
 #ifdef __cplusplus
 }
 #endif

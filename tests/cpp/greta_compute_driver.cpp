@@ -5,10 +5,10 @@
 // GretaStreamHip.  Test infrastructure: tests/test_host_mirror.py runs it and
 // checks the result file against the oracle.
 //
-// usage: greta_compute_driver <file.gguf|file.greta> <tensor> <quant|int8|int4> <M>
+// usage: greta_compute_driver <file.gguf|file.greta> <tensor> <quant|int8|int4|fp16> <M>
 //                             <a.f32> <c.f32> [op_label] [a_dtype f32|f16|bf16]
 // A is read as M x K float32 (converted to the requested A dtype on the host),
-// C written as M x N float32.  Prints "route=<GEMV|GEMM> quant=<mode>".
+// C written as M x N float32.  Prints "route=<GEMV|GEMM|VALU|MFMA> quant=<mode>".
 #include <cmath>
 #include <cstdio>
 #include <cstring>
@@ -64,6 +64,7 @@ int main(int argc, char **argv) {
   bool ok = kind == "quant"  ? (gg ? gg->load_tensor_quant(name, B, &err) : gr->load_tensor_quant(name, B, &err))
             : kind == "int8" ? wl->load_tensor_int8(name, B, scales, &err)
             : kind == "int4" ? wl->load_tensor_int4(name, B, scales, head_scales, &err)
+            : kind == "fp16" ? wl->load_tensor_fp16(name, B, &err)
                              : (err = "unknown kind " + kind, false);
   if (!ok) return fail("load: " + err);
 

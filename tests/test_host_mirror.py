@@ -104,6 +104,25 @@ def test_gemm_gguf_native_wide_range_f32(dev, model, name, M):
         assert O.rel_l2(c[m], ref[m]) <= TOL, m
 
 
+@pytest.mark.parametrize("M", [1, 8, 40])
+@pytest.mark.parametrize("name", ["blk.0.ffn_gate.weight", "blk.0.attn_k.weight", "output.weight"])
+def test_gemm_fp16_weights(dev, model, name, M):
+    """load_tensor_fp16 (GGUF blocks dequantized, then rounded to fp16 with the
+    reference's truncating conversion; K/V tensors GQA-reordered) and
+    GretaCompute::gemm on the FP16 B it returns: the reference's FP16 route
+    (greta_compute_hip.cpp:361-371), VALU launcher up to 32 rows, MFMA
+    launcher above, against the fp64 product of the same fp16 weights."""
+    a, c, route, N, K = _run(model, name, "fp16", M, seed=90 + M)
+    assert route == ("VALU" if M <= 32 else "MFMA")
+    sh, fmt, raw = model[1][name]
+    w = O.dequant(fmt, raw)
+    if "attn_k" in name:
+        w = O.gqa_transpose(w, DIM, KV)
+    w16 = O.fp16_to_fp32(O.fp32_to_fp16_trunc(np.ascontiguousarray(w, dtype=np.float32).ravel()))
+    ref = a.astype(np.float64) @ w16.reshape(N, K).astype(np.float64).T
+    assert O.rel_l2(c, ref) <= TOL
+
+
 @pytest.mark.parametrize("M", [1, 40])
 def test_gemm_q6k_output(dev, model, M):
     """Q6_K output.weight through GretaCompute::gemm: GEMV up to 16 rows, the
