@@ -309,10 +309,8 @@ k_chain(const ChainOpD *__restrict__ ops_in, int n_ops, int total, unsigned *__r
 #pragma unroll
               for (int e = 0; e < 8; ++e) v[e] = 0.f;
             }
-            float amax = 0.f;
-#pragma unroll
-            for (int e = 0; e < 8; ++e) amax = fmaxf(amax, fabsf(v[e]));
-            amax = quad_max(amax);
+            // a NaN or Inf in the block: zero limbs, sx NaN or Inf, NaN outputs
+            const float amax = quad_max(abs_max_bits8(v));
             const float rinv = amax > 0.f ? 127.0f * __builtin_amdgcn_rcpf(amax) : 0.f;
             const float sx = amax * (1.0f / 127.0f);
             uint32_t pa[2], pb[2];

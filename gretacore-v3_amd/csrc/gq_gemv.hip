@@ -247,15 +247,13 @@ k_gemv_q(const GemvFuse fz, const float *__restrict__ x, const int8_t *__restric
           for (int e = 0; e < 8; ++e) v[e] = v[e] * gg[e];
         }
       }
-      float amax = 0.f;
 #pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        v[e] = xin[i] ? v[e] : 0.f;
-        amax = fmaxf(amax, fabsf(v[e]));
-      }
-      amax = quad_max(amax);
+      for (int e = 0; e < 8; ++e) v[e] = xin[i] ? v[e] : 0.f;
+      const float amax = quad_max(abs_max_bits8(v));
       // 127 / amax to one ulp: a (represented) limb split needs no correctly
-      // rounded quotient, the scale sx below is what the products use
+      // rounded quotient, the scale sx below is what the products use.  A
+      // block holding a NaN or Inf gets inv = 0 (zero limbs) and sx = NaN or
+      // Inf, so every output that reads the block comes out NaN.
       const float inv = amax > 0.f ? 127.0f * __builtin_amdgcn_rcpf(amax) : 0.f;
       const float sx = amax * (1.0f / 127.0f);
       uint32_t la[2], lb[2];

@@ -161,10 +161,22 @@ GQ_DEV int split8(const float (&v)[8], float inv, uint32_t (&la)[2], uint32_t (&
   return 254 * sa + sb;
 }
 
-// Quad-wide (lanes 4j .. 4j+3) max / integer sum through DPP quad permutes.
-GQ_DEV float quad_max(float v) {
-  v = fmaxf(v, __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0xB1, 0xF, 0xF, false)));  // lane ^ 1
-  return fmaxf(v, __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x4E, 0xF, 0xF, false)));  // lane ^ 2
+// Largest |v| of 8 elements as a bit pattern: the sign cleared, the patterns
+// compare as unsigned integers in the order of the magnitudes, and a NaN
+// (exponent all ones, mantissa nonzero) ranks above Inf, so a NaN or Inf in
+// the block comes out as the block's maximum instead of being skipped the way
+// fmaxf skips a NaN.
+GQ_DEV uint32_t abs_max_bits8(const float (&v)[8]) {
+  uint32_t m = 0u;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) m = max(m, __float_as_uint(v[e]) & 0x7FFFFFFFu);
+  return m;
+}
+// Quad-wide (lanes 4j .. 4j+3) max of such patterns / integer sum through DPP
+// quad permutes.  The quad max returns the float the pattern encodes.
+GQ_DEV float quad_max(uint32_t v) {
+  v = max(v, (uint32_t)__builtin_amdgcn_mov_dpp((int)v, 0xB1, 0xF, 0xF, false));  // lane ^ 1
+  return __uint_as_float(max(v, (uint32_t)__builtin_amdgcn_mov_dpp((int)v, 0x4E, 0xF, 0xF, false)));  // lane ^ 2
 }
 GQ_DEV int quad_sum(int v) {
   v += __builtin_amdgcn_mov_dpp(v, 0xB1, 0xF, 0xF, false);
