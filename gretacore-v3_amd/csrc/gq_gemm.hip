@@ -617,25 +617,36 @@ GQ_DEV gq_half8 rfrag(const RStep<FMT, NJ> &st, int j, int ks, int step, const Q
 // step waits on loads issued PD - 1 steps earlier: depth 2 for large tiles,
 // 3 or 4 for grids whose short steps would otherwise wait out each load's
 // latency.
-template <int FMT, int CBF16, int BM, int BN, int WM, int WN, int PD = 2>
-__global__ void __launch_bounds__(64 * WM * WN) __attribute__((amdgpu_waves_per_eu(WM * WN / 4, WM * WN / 4)))
+// KG: K groups.  KG groups of WM x WN waves share the workgroup's tile, group
+// g taking the K steps g, g + KG, g + 2 KG, ... with its own activation
+// buffers; the groups' accumulators are added through LDS at the end (group
+// 0 stores).  Grids with one workgroup per CU (M = 512) otherwise run one
+// wave per SIMD, each waiting out its loads' latency; KG groups put KG waves
+// on every SIMD with no partial sums leaving the CU.  nsteps % KG == 0.
+template <int FMT, int CBF16, int BM, int BN, int WM, int WN, int PD = 2, int KG = 1>
+__global__ void __launch_bounds__(64 * WM * WN * KG)
+__attribute__((amdgpu_waves_per_eu(WM * WN * KG / 4, WM * WN * KG / 4)))
 k_gemm_rb(const uint8_t *__restrict__ w, uint32_t sc_off, const _Float16 *__restrict__ a16, int lda,
           void *__restrict__ c, const float *__restrict__ rs, int M, int N, int C, int nsteps, int tiles_m,
           int gm) {
   constexpr int KS = BK / 16;
-  constexpr int NW = WM * WN, TM = BM / WM / 32, NJ = BN / WN / 32;  // waves, MFMA tiles per wave
+  constexpr int NW = WM * WN, TM = BM / WM / 32, NJ = BN / WN / 32;  // waves per group, MFMA tiles per wave
   static_assert(TM >= 1 && NJ >= 1 && BM % (8 * NW) == 0, "tile shape");
   static_assert(PD >= 2 && PD <= 4, "pipeline depth");
+  static_assert(KG == 1 || KG == 2 || KG == 4, "K groups");
   // one array per buffer: the buffer index is a compile-time constant
   // everywhere, so no wait for an in-flight DMA into another buffer is needed
-  __shared__ __attribute__((aligned(16))) _Float16 As_0[BM * BK];
-  __shared__ __attribute__((aligned(16))) _Float16 As_1[BM * BK];
-  __shared__ __attribute__((aligned(16))) _Float16 As_2[PD >= 3 ? BM * BK : 8];
-  __shared__ __attribute__((aligned(16))) _Float16 As_3[PD >= 4 ? BM * BK : 8];
+  // (each K group uses its own BM x BK part of every buffer)
+  __shared__ __attribute__((aligned(16))) _Float16 As_0[KG * BM * BK];
+  __shared__ __attribute__((aligned(16))) _Float16 As_1[KG * BM * BK];
+  __shared__ __attribute__((aligned(16))) _Float16 As_2[PD >= 3 ? KG * BM * BK : 8];
+  __shared__ __attribute__((aligned(16))) _Float16 As_3[PD >= 4 ? KG * BM * BK : 8];
+  const int kg = KG == 1 ? 0 : __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6) / NW);
   auto As_of = [&](auto b) -> _Float16 * {
     constexpr int v = decltype(b)::value;
-    return v == 0 ? As_0 : v == 1 ? As_1 : v == 2 ? As_2 : As_3;
+    return (v == 0 ? As_0 : v == 1 ? As_1 : v == 2 ? As_2 : As_3) + kg * (BM * BK);
   };
+  const int nl = nsteps / KG;  // this group's steps
   using B0 = std::integral_constant<int, 0>;
   using B1 = std::integral_constant<int, 1>;
   using B2 = std::integral_constant<int, 2>;
@@ -647,7 +658,7 @@ k_gemm_rb(const uint8_t *__restrict__ w, uint32_t sc_off, const _Float16 *__rest
   static_assert(pend <= 63, "vmcnt immediate");
   constexpr int kWaitPend = 0x0F70 | (pend & 15) | ((pend >> 4) << 14);
   const int tid = threadIdx.x, lane = tid & 63;
-  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wave = __builtin_amdgcn_readfirstlane((tid >> 6) % NW);  // within the K group
   const int wm = wave / WN, wn = wave % WN;
   int mt, nt;
   tile_of_g(blockIdx.x, gridDim.x, tiles_m, (N + BN - 1) / BN, gm, mt, nt);
@@ -691,13 +702,16 @@ k_gemm_rb(const uint8_t *__restrict__ w, uint32_t sc_off, const _Float16 *__rest
   const int arow = (BM / WM) * wm + (lane & 31);
   const int sw = a_swz(lane & 31);
 
-  // step `step` (buffer and register stage step % PD); steps past the end
-  // are skipped by every wave alike
-  auto run_step = [&](int step, auto buf_c) {
+  // the group's l-th step of K
+  auto gstep = [&](int l) { return l * KG + kg; };
+  // the group's step l (buffer and register stage l % PD; `step` the K step);
+  // steps past the end are skipped by every wave alike
+  auto run_step = [&](int l, auto buf_c) {
     constexpr int BUF = decltype(buf_c)::value;
-    using NB = std::integral_constant<int, (BUF + PD - 1) % PD>;  // buffer of step + PD - 1
-    const int s1 = step + PD - 1 < nsteps ? step + PD - 1 : nsteps - 1;
-    const int s2 = step + PD < nsteps ? step + PD : nsteps - 1;
+    using NB = std::integral_constant<int, (BUF + PD - 1) % PD>;  // buffer of l + PD - 1
+    const int step = gstep(l);
+    const int s1 = gstep(l + PD - 1 < nl ? l + PD - 1 : nl - 1);
+    const int s2 = gstep(l + PD < nl ? l + PD : nl - 1);
     load_a_lds_b<BM, NW>(a16, ao, s1, wave, As_of(NB{}));
     __builtin_amdgcn_sched_barrier(0);
     const _Float16 *As = As_of(buf_c) + arow * BK;
@@ -732,7 +746,7 @@ k_gemm_rb(const uint8_t *__restrict__ w, uint32_t sc_off, const _Float16 *__rest
   // must land
   auto prime = [&](auto b) {
     constexpr int i = decltype(b)::value;
-    const int st = i < nsteps ? i : nsteps - 1;
+    const int st = gstep(i < nl ? i : nl - 1);
     if constexpr (i < PD - 1) load_a_lds_b<BM, NW>(a16, ao, st, wave, As_of(b));
     load_rstep<FMT, NJ>(w, qo, so, st, wst[i]);
   };
@@ -748,13 +762,42 @@ k_gemm_rb(const uint8_t *__restrict__ w, uint32_t sc_off, const _Float16 *__rest
   __builtin_amdgcn_s_waitcnt(kWaitPend);
   if (tid < BM / 4) *reinterpret_cast<gq_f4 *>(rs_s + 4 * tid) = rs4;
   __syncthreads();
-  for (int step = 0; step < nsteps; step += PD) {
-    run_step(step, B0{});
-    if (step + 1 < nsteps) run_step(step + 1, B1{});
+  for (int l = 0; l < nl; l += PD) {
+    run_step(l, B0{});
+    if (l + 1 < nl) run_step(l + 1, B1{});
     if constexpr (PD >= 3)
-      if (step + 2 < nsteps) run_step(step + 2, B2{});
+      if (l + 2 < nl) run_step(l + 2, B2{});
     if constexpr (PD >= 4)
-      if (step + 3 < nsteps) run_step(step + 3, B3{});
+      if (l + 3 < nl) run_step(l + 3, B3{});
+  }
+  if constexpr (KG > 1) {
+    // the groups' sums, one MFMA tile at a time: groups 1 .. KG - 1 write
+    // theirs (lane-contiguous float4s), group 0 adds them in group order
+    __shared__ __attribute__((aligned(16))) gq_f4 xs[(KG - 1) * NW * 4 * 64];
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
+#pragma unroll
+      for (int j = 0; j < NJ; ++j) {
+        if (kg > 0) {
+#pragma unroll
+          for (int q = 0; q < 4; ++q)
+            xs[(((kg - 1) * NW + wave) * 4 + q) * 64 + lane] =
+                gq_f4{acc[i][j][4 * q], acc[i][j][4 * q + 1], acc[i][j][4 * q + 2], acc[i][j][4 * q + 3]};
+        }
+        __syncthreads();
+        if (kg == 0) {
+#pragma unroll
+          for (int g = 0; g < KG - 1; ++g)
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+              const gq_f4 t = xs[((g * NW + wave) * 4 + q) * 64 + lane];
+#pragma unroll
+              for (int e = 0; e < 4; ++e) acc[i][j][4 * q + e] += t[e];
+            }
+        }
+        __syncthreads();
+      }
+    if (kg > 0) return;
   }
 
   // C of this workgroup's rows through a buffer resource starting at row m0
@@ -1006,7 +1049,7 @@ int launch_cfg(const void *packed, const _Float16 *a16, int lda, void *c, const 
 
 // pd_default: the pipeline depth of the shape (GQ_GEMM_PD=2|3|4 overrides it,
 // for tuning)
-template <int FMT, int CBF16, int BM, int BN, int WM, int WN>
+template <int FMT, int CBF16, int BM, int BN, int WM, int WN, int KG = 1>
 int launch_rb(const void *packed, const _Float16 *a16, int lda, void *c, const float *rs, int M, int N, int K,
               hipStream_t s, int pd_default = 4) {
   const int C = (int)gq_chunks(FMT, K);
@@ -1020,12 +1063,27 @@ int launch_rb(const void *packed, const _Float16 *a16, int lda, void *c, const f
   const char *eg = getenv("GQ_GEMM_GM");
   const int gm = eg ? atoi(eg) : 4;
 #define GQ_LAUNCH_RB(PD)                                                                                        \
-  hipLaunchKernelGGL((k_gemm_rb<FMT, CBF16, BM, BN, WM, WN, PD>), dim3((unsigned)(tiles_m * tiles_n)),          \
-                     dim3(64 * WM * WN), 0, s, (const uint8_t *)packed, (uint32_t)gq_sc_plane_offset(FMT, N, K), \
+  hipLaunchKernelGGL((k_gemm_rb<FMT, CBF16, BM, BN, WM, WN, PD, KG>), dim3((unsigned)(tiles_m * tiles_n)),      \
+                     dim3(64 * WM * WN * KG), 0, s, (const uint8_t *)packed, (uint32_t)gq_sc_plane_offset(FMT, N, K), \
                      a16, lda, c, rs, M, N, C, nsteps, tiles_m, gm)
-  if (pd == 4) GQ_LAUNCH_RB(4);
-  else if (pd == 3) GQ_LAUNCH_RB(3);
-  else GQ_LAUNCH_RB(2);
+  // the depths whose LDS fits (activation buffers, the K groups' exchange,
+  // the row scales); a deeper request falls back to the deepest that fits
+  constexpr auto lds = [](int d) { return d * KG * BM * BK * 2 + (KG - 1) * WM * WN * 4096 + BM * 4; };
+  constexpr int kLds = 160 * 1024;
+  if (KG > 1 && nsteps % KG) return GQ_ERR_INVALID_ARGS;
+  if constexpr (lds(4) <= kLds) {
+    if (pd == 4) {
+      GQ_LAUNCH_RB(4);
+      return gq_last_launch();
+    }
+  }
+  if constexpr (lds(3) <= kLds) {
+    if (pd >= 3) {
+      GQ_LAUNCH_RB(3);
+      return gq_last_launch();
+    }
+  }
+  GQ_LAUNCH_RB(2);
 #undef GQ_LAUNCH_RB
   return gq_last_launch();
 }
@@ -1052,17 +1110,34 @@ int launch_rb(const void *packed, const _Float16 *a16, int lda, void *c, const f
 //      4096: 50 vs 56 us with 128 x 128; 128 x 14336: 48 vs 54 us)
 //  11: register-B, 64 x 64 (4 waves), smaller problems (M <= 256 at N = 4096:
 //      40-43 us vs 49-53)
+//  17: 128 x 128 on 1 x 4 waves in 2 K groups (8 waves), depth 4, where 6
+//      was chosen: 1024 x 4096 x 4096 Q4_0 / Q4_K / Q8_0 49 / 53-56 / 53 us
+//      against 57 / 64-65 / 57-58 for 6; 768 x 4096 42-45 vs 48; 256 x
+//      14336 44-45 vs 47-50 (conversion included, graph replays)
+//  15: 64 x 128 on 1 x 4 waves in 4 K groups (16 waves), depth 3, for every
+//      smaller grid: 512 x 4096 x 4096 30-34 us against 36-39 (14); 256 x
+//      4096 24-26 vs 32-36 (11 / skinny); 64 x 14336 22-24 vs 30-34
+//      (skinny).  2 K groups (18) ran the same at 512 rows and 1-5 % slower
+//      below; 2 K groups on 128 x 256 (16) no faster than 13.
 // The register-B kernel runs with pipeline depth 4 (1-3 % faster than 2 on
 // the shapes measured), except 256 x 256: depth 3 on the 1 x 8 grid, 2 on the
 // 2 x 4 grid (at 4 its Q8_0 and Q4_K instances spill registers).  1, 2 (LDS-B
 // 256 x 128, 128 x 128) and 5, 7, 8, 10 (other register-B shapes) are kept for
 // tuning through GQ_GEMM_TILE.
-int pick_tile(int fmt, int M, int N) {
+int pick_tile(int fmt, int M, int N, int K) {
   auto wgs = [&](int bm, int bn) { return (long)((M + bm - 1) / bm) * ((N + bn - 1) / bn); };
-  if (const char *e = getenv("GQ_GEMM_TILE")) return atoi(e);
+  const int nsteps = (int)(gq_kpad(fmt, K) / BK);
+  if (const char *e = getenv("GQ_GEMM_TILE")) {
+    const int t = atoi(e);
+    // K-group shapes need the K steps to divide among the groups
+    if (t == 15 && nsteps % 4) return 14;
+    if ((t == 16 || t == 17 || t == 18) && nsteps % 2) return t == 16 ? 13 : t == 17 ? 6 : 14;
+    return t;
+  }
   if (wgs(256, 256) >= 384) return 12;
   if (wgs(128, 256) >= 192) return 13;
-  if (wgs(128, 128) >= 192) return 6;
+  if (wgs(128, 128) >= 192) return nsteps % 2 ? 6 : 17;
+  if (nsteps % 4 == 0) return 15;
   if (wgs(64, 128) >= 192) return 14;
   return 11;
 }
@@ -1070,7 +1145,7 @@ int pick_tile(int fmt, int M, int N) {
 template <int FMT, int CBF16>
 int launch_fmt(const void *packed, const _Float16 *a16, int lda, void *c, const float *rs, int M, int N, int K,
                hipStream_t s) {
-  switch (pick_tile(FMT, M, N)) {
+  switch (pick_tile(FMT, M, N, K)) {
   case 0: return launch_rb<FMT, CBF16, 256, 256, 2, 4>(packed, a16, lda, c, rs, M, N, K, s, 2);
   case 4: return launch_rb<FMT, CBF16, 256, 128, 2, 4>(packed, a16, lda, c, rs, M, N, K, s);
   case 5: return launch_rb<FMT, CBF16, 128, 256, 2, 4>(packed, a16, lda, c, rs, M, N, K, s);
@@ -1083,6 +1158,10 @@ int launch_fmt(const void *packed, const _Float16 *a16, int lda, void *c, const 
   case 12: return launch_rb<FMT, CBF16, 256, 256, 1, 8>(packed, a16, lda, c, rs, M, N, K, s, 3);
   case 13: return launch_rb<FMT, CBF16, 128, 256, 1, 8>(packed, a16, lda, c, rs, M, N, K, s);
   case 14: return launch_rb<FMT, CBF16, 64, 128, 1, 4>(packed, a16, lda, c, rs, M, N, K, s);
+  case 15: return launch_rb<FMT, CBF16, 64, 128, 1, 4, 4>(packed, a16, lda, c, rs, M, N, K, s);
+  case 16: return launch_rb<FMT, CBF16, 128, 256, 1, 8, 2>(packed, a16, lda, c, rs, M, N, K, s, 3);
+  case 17: return launch_rb<FMT, CBF16, 128, 128, 1, 4, 2>(packed, a16, lda, c, rs, M, N, K, s);
+  case 18: return launch_rb<FMT, CBF16, 64, 128, 1, 4, 2>(packed, a16, lda, c, rs, M, N, K, s);
   default: return launch_rb<FMT, CBF16, 128, 128, 2, 4>(packed, a16, lda, c, rs, M, N, K, s);
   case 3: return launch_cfg<FMT, CBF16, 256, 256>(packed, a16, lda, c, rs, M, N, K, s);
   case 1: return launch_cfg<FMT, CBF16, 256, 128>(packed, a16, lda, c, rs, M, N, K, s);
@@ -1114,7 +1193,7 @@ extern "C" size_t gq_gemm_workspace_bytes(int fmt, size_t M, size_t K) {
 static bool gemm_converts_a(int fmt, size_t M, size_t N, size_t K, int a_dtype) {
   int ct = 0, nck = 0;
   if (gq_gemm_skinny_plan(fmt, M, N, K, &ct, &nck) == GQ_OK) return true;
-  const int tile = pick_tile(fmt, (int)M, (int)N);
+  const int tile = pick_tile(fmt, (int)M, (int)N, (int)K);
   const bool q4 = (fmt == GQ_FMT_Q4_0 || gq_fmt_is_q4k(fmt)) && tile != 1 && tile != 2 && tile != 3;
   return a_dtype != GQ_DT_F16 || gq_kpad(fmt, K) != K || q4;
 }
@@ -1166,7 +1245,7 @@ extern "C" int gq_gemm(int fmt, const void *packed, const void *a, int a_dtype, 
   // the register-B kernel takes the 4-bit formats' B fragments in the
   // gq_nib_halves order, so their activations are staged in that order; fp16
   // activations of the padded width are used as they are otherwise
-  const int tile = pick_tile(fmt, (int)M, (int)N);
+  const int tile = pick_tile(fmt, (int)M, (int)N, (int)K);
   const int q4 = (fmt == GQ_FMT_Q4_0 || gq_fmt_is_q4k(fmt)) && tile != 1 && tile != 2 && tile != 3;
   // (the register-B kernel addresses the activations with 32-bit offsets)
   GQ_CHECK(tile == 1 || tile == 2 || tile == 3 || M * Kp * 2 < ((size_t)1 << 32), GQ_ERR_INVALID_ARGS);

@@ -1127,7 +1127,13 @@ int gq_gemm_skinny_plan(int fmt, size_t M, size_t N, size_t K, int *ct_out, int 
     ct = 1;
     wgs = tiles * ((M + 31) / 32);
   }
-  if (!q6 && wgs > 2 * cus) return GQ_ERR_UNSUPPORTED;
+  // (short K) more workgroups than CUs: the tiled GEMM's K-group shapes are
+  // faster (4096 x 4096: 22-25 vs 29-36 us at 192 / 256 rows; 14336 x 4096:
+  // 22-29 vs 30-35 us at 64 / 128 rows); up to one per CU the skinny kernel
+  // is (4096 x 4096 at 64 / 128 rows: 15.6 / 17.5 vs 20-23 us)
+  // (GQ_GEMM_SKINNY=2: up to two per CU, for tuning)
+  const size_t lim = (nckp >= 16 || (e && e[0] == '2')) ? 2 * cus : cus;
+  if (!q6 && wgs > lim) return GQ_ERR_UNSUPPORTED;
   *ct_out = ct;
   *nck_out = nckp;
   return GQ_OK;

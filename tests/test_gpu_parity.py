@@ -361,12 +361,16 @@ def test_gemm_epilogue_very_wide_n(dev, tile, monkeypatch):
 
 @pytest.mark.parametrize("tile,pd", [(0, 2), (0, 4), (1, 2), (2, 2), (3, 2), (4, 2), (4, 3), (4, 4), (5, 4),
                                      (6, 2), (6, 3), (6, 4), (7, 4), (8, 4), (9, 3), (9, 4), (10, 4), (11, 2),
-                                     (11, 4), (12, 2), (12, 3), (13, 2), (13, 3), (13, 4), (14, 2), (14, 3), (14, 4)])
+                                     (11, 4), (12, 2), (12, 3), (13, 2), (13, 3), (13, 4), (14, 2), (14, 3), (14, 4),
+                                     (15, 2), (15, 3), (15, 4), (16, 2), (16, 3), (17, 2), (17, 3), (17, 4),
+                                     (18, 2), (18, 4)])
 @pytest.mark.parametrize("fmt", [O.Q4_0, O.Q8_0, O.Q4_K])
 def test_gemm_every_kernel_shape(dev, fmt, tile, pd, monkeypatch):
     """Each GEMM kernel / tile shape (forced through GQ_GEMM_TILE) and, for the
     register-B kernel, pipeline depths (GQ_GEMM_PD), on a shape with partial
-    tiles in M and N."""
+    tiles in M and N.  15-18 split K among 2 or 4 wave groups of one
+    workgroup (the groups' sums added through LDS); a depth whose LDS does not
+    fit falls back to the deepest that does."""
     import gq
     import torch
     monkeypatch.setenv("GQ_GEMM_TILE", str(tile))
@@ -384,11 +388,13 @@ def test_gemm_every_kernel_shape(dev, fmt, tile, pd, monkeypatch):
 @pytest.mark.parametrize("pd", [2, 3, 4])
 def test_gemm_short_k_loops(dev, fmt, k, pd, monkeypatch):
     """K step counts of 2..24 (fewer steps than the pipeline is deep, and the
-    unrolled step loops' guarded tails) for each pipeline depth."""
+    unrolled step loops' guarded tails) for each pipeline depth; the K-group
+    shapes also with one step per group, and with a step count the groups do
+    not divide (the plan then takes the same tile without K groups)."""
     import gq
     import torch
     monkeypatch.setenv("GQ_GEMM_PD", str(pd))
-    for tile in (4, 6, 11, 12, 13, 14):
+    for tile in (4, 6, 11, 12, 13, 14, 15, 16, 17, 18):
         monkeypatch.setenv("GQ_GEMM_TILE", str(tile))
         m, n = 200, 160
         w = O.gen_weights(fmt, n, k, seed=70 + k)
