@@ -164,8 +164,10 @@ int gq_gemv_swiglu_plan(int fmt, size_t N, size_t K, int batch, int *ksplit, int
 /* A is [M][K] of a_dtype (GQ_DT_BF16 / F16 / F32), C is [M][N] of c_dtype
  * (GQ_DT_F32 or GQ_DT_BF16).  Computes on f16 MFMA (v_mfma_f32_32x32x16_f16)
  * with fp32 accumulation, weights dequantized into fp16 fragments.  Few rows
- * (M <= 256 where the grid stays within two workgroups per CU) run on a
- * skinny kernel that splits K over the waves of a workgroup. */
+ * (M <= 256 where the grid stays within one workgroup per CU, or two for K
+ * beyond 4096) run on a skinny kernel that splits K over the waves of a
+ * workgroup; small tiled grids split K over 2 or 4 wave groups of a
+ * workgroup. */
 size_t gq_gemm_workspace_bytes(int fmt, size_t M, size_t K);
 int gq_gemm(int fmt, const void *d_packed, const void *d_a, int a_dtype, void *d_c, int c_dtype, size_t M,
             size_t N, size_t K, void *d_workspace, size_t workspace_bytes, void *stream);
