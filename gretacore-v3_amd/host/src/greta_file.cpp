@@ -249,6 +249,7 @@ struct GretaLoader::Impl {
   }
   Uploader &uploader() {
     if (!up) up = std::make_unique<Uploader>();
+    up->bind_file(fd, map, size);  // slices of the mapping are read with pread
     return *up;
   }
   const GretaRecord *find(const std::string &name) const {

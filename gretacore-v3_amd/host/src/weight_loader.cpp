@@ -199,6 +199,7 @@ struct GGUFLoader::Impl {
 
   Uploader &uploader() {
     if (!up) up = std::make_unique<Uploader>();
+    up->bind_file(fd, map, map_size);  // slices of the mapping are read with pread
     return *up;
   }
   bool upload(void *dst, const uint8_t *src, size_t bytes, std::string *err) {
