@@ -44,7 +44,8 @@ struct HFmt<GQ_FMT_Q6_K> {
 // a "chunk" is 128 k of one row tile, read straight from the 16 rows
 template <>
 struct HFmt<GQ_FMT_F16> {
-  static constexpr int CK = 128, QB = 0, SB = 0, STEPS = 2;
+  static constexpr int CK = 128, STEPS = 2;
+  [[maybe_unused]] static constexpr int QB = 0, SB = 0;  // (no T16 records or scale plane)
 };
 
 template <int FMT>
