@@ -443,7 +443,10 @@ def bench_load(dev, layers=8):
     shaped file of `layers` Q4_K layers (~1 GB) in the page cache, every matrix
     loaded with gq_gguf_load(QUANT) (pinned sliced upload + on-GPU T16 repack),
     against the reference's way of loading: read into pageable memory, a
-    synchronous pageable copy, then the repack.  GB/s of GGUF bytes."""
+    synchronous pageable copy, then the repack; many_GBps is the same tensors
+    through gq_gguf_load_quant_many (one pipelined pass; the bytes it leaves
+    are the ones compared with the reference-style load).  GB/s of GGUF
+    bytes."""
     import shutil
     import tempfile
 
@@ -498,10 +501,17 @@ def bench_load(dev, layers=8):
                     torch.cuda.synchronize()
             return res
 
+        def ours_many():
+            g.load_quant_many(names, [outs[nm] for nm in names])
+            torch.cuda.synchronize()
+
         ours()  # staging buffers allocated here
         t0 = time.perf_counter()
         ours()
         t_ours = time.perf_counter() - t0
+        t0 = time.perf_counter()
+        ours_many()
+        t_many = time.perf_counter() - t0
         t0 = time.perf_counter()
         ref = reference_style()
         t_ref = time.perf_counter() - t0
@@ -533,6 +543,7 @@ def bench_load(dev, layers=8):
         same = same and all(torch.equal(outs[nm], gouts[nm]) for nm in names)
         h.close()
         return {"GBps": round(total / t_ours / 1e9, 2), "ms": round(t_ours * 1e3, 1), "bytes": total,
+                "many_GBps": round(total / t_many / 1e9, 2),
                 "reference_style_GBps": round(total / t_ref / 1e9, 2),
                 "greta_cache_GBps": round(total / t_cache / 1e9, 2), "greta_write_s": round(t_write, 2),
                 "same_bytes": same, "layers": layers, "format": "Q4_K",

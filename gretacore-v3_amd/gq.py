@@ -96,6 +96,7 @@ _SIGS_GGUF = {
     "gq_gguf_read_raw": (ctypes.c_int, [_vp, ctypes.c_char_p, _vp, _c_size]),
     "gq_gguf_plan_load": (ctypes.c_int, [_vp, ctypes.c_char_p, ctypes.c_int, _vp]),
     "gq_gguf_load": (ctypes.c_int, [_vp, ctypes.c_char_p, ctypes.c_int, _vp, _c_size, _vp, _c_size, _vp, _c_size]),
+    "gq_gguf_load_quant_many": (ctypes.c_int, [_vp, _c_size, _vp, _vp, _vp]),
     # include/gq_greta.h
     "gq_greta_write": (ctypes.c_int, [_vp, ctypes.c_char_p, ctypes.c_int, ctypes.POINTER(_c_size)]),
     "gq_greta_open": (ctypes.c_int, [ctypes.c_char_p, ctypes.POINTER(_vp)]),
@@ -653,6 +654,20 @@ class GGUF:
         p = _Plan()
         self._check(load().gq_gguf_plan_load(self._h, name.encode(), kind, ctypes.byref(p)), "gq_gguf_plan_load")
         return {f: getattr(p, f) for f, _ in _Plan._fields_}
+
+    def load_quant_many(self, names, outs):
+        """GQ_LOAD_QUANT of every name into the matching device tensor of `outs`
+        (uint8, at least the planned bytes) in one pipelined pass."""
+        n = len(names)
+        if n != len(outs):
+            raise ValueError("names and outs differ in length")
+        _require_device(*outs)
+        enc = [nm.encode() for nm in names]
+        N = (ctypes.c_char_p * n)(*enc)
+        P = (_vp * n)(*[t.data_ptr() for t in outs])
+        B = (_c_size * n)(*[t.numel() * t.element_size() for t in outs])
+        self._check(load().gq_gguf_load_quant_many(self._h, n, ctypes.cast(N, _vp), ctypes.cast(P, _vp),
+                                                   ctypes.cast(B, _vp)), "gq_gguf_load_quant_many")
 
     def load(self, name: str, kind: int, device="cuda"):
         """Returns (data, scales, head_scales, plan) as device tensors (None where absent)."""

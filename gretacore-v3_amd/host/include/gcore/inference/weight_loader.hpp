@@ -94,6 +94,14 @@ public:
   bool plan(const std::string &name, LoadKind kind, LoadPlan *plan, std::string *err) const;
   bool load_into(const std::string &name, LoadKind kind, const LoadPlan &plan, void *out, void *scales,
                  void *head_scales, std::string *err) const;
+  // LoadKind::QUANT of several tensors in one pipelined pass (no counterpart
+  // in the reference, which loads tensor by tensor): outs[i] holds at least
+  // out_bytes[i] >= plan(names[i], QUANT).bytes.  Every name is planned and
+  // checked before any data moves; returns when all tensors are on the
+  // device.  After a failure during the transfer, tensors before the failing
+  // one may be loaded and the rest not.
+  bool load_quant_many(const std::string *names, void *const *outs, const size_t *out_bytes, size_t n,
+                       std::string *err) const;
 
 private:
   struct Impl;

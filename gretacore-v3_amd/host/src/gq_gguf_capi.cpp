@@ -1,6 +1,7 @@
 // C ABI over gcore::inference::GGUFLoader (declared in gq_gguf.h).
 #include <cstring>
 #include <string>
+#include <vector>
 
 #include "gcore/inference/greta_file.hpp"
 #include "gcore/inference/weight_loader.hpp"
@@ -171,6 +172,29 @@ int gq_gguf_load(const gq_gguf *g, const char *name, int kind, void *d_out, size
     return GQ_ERR_INVALID_ARGS;
   }
   if (!g->loader.load_into(name, k, p, d_out, d_scales, d_head_scales, &g->err)) return GQ_ERR_HIP;
+  return GQ_OK;
+}
+
+int gq_gguf_load_quant_many(const gq_gguf *g, size_t n, const char *const *names, void *const *d_outs,
+                            const size_t *out_bytes) {
+  if (!g) return GQ_ERR_INVALID_ARGS;
+  if (n == 0) return GQ_OK;
+  if (!names || !d_outs || !out_bytes) return GQ_ERR_INVALID_ARGS;
+  std::vector<std::string> nm(n);
+  for (size_t i = 0; i < n; ++i) {
+    if (!names[i]) return GQ_ERR_INVALID_ARGS;
+    nm[i] = names[i];
+  }
+  // the checks (names, types, sizes) before any transfer
+  for (size_t i = 0; i < n; ++i) {
+    GGUFLoader::LoadPlan p;
+    if (!g->loader.plan(nm[i], GGUFLoader::LoadKind::QUANT, &p, &g->err)) return GQ_ERR_INVALID_ARGS;
+    if (!d_outs[i] || out_bytes[i] < p.bytes) {
+      g->err = "gq_gguf_load_quant_many: destination missing or smaller than planned: " + nm[i];
+      return GQ_ERR_INVALID_ARGS;
+    }
+  }
+  if (!g->loader.load_quant_many(nm.data(), d_outs, out_bytes, n, &g->err)) return GQ_ERR_HIP;
   return GQ_OK;
 }
 

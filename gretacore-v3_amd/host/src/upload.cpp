@@ -227,6 +227,20 @@ bool Uploader::repack(int fmt, const uint8_t *src, size_t N, size_t K, size_t ro
   return hip_ok(hipStreamSynchronize(stream_), "repack", err);
 }
 
+bool Uploader::repack_many(const RepackJob *jobs, size_t n, std::string *err) {
+  if (n == 0) return true;
+  if (!jobs) return fail(err, "upload: null pointer");
+  for (size_t i = 0; i < n; ++i)
+    if (jobs[i].N && jobs[i].K && (!jobs[i].src || !jobs[i].packed)) return fail(err, "upload: null pointer");
+  if (!init(err)) return false;
+  for (size_t i = 0; i < n; ++i) {
+    const RepackJob &j = jobs[i];
+    if (j.N == 0 || j.K == 0) continue;
+    if (!repack_slices(j.fmt, j.src, j.N, j.K, j.row_bytes, j.packed, err)) return drain_after_error();
+  }
+  return hip_ok(hipStreamSynchronize(stream_), "repack", err);
+}
+
 bool Uploader::repack_slices(int fmt, const uint8_t *src, size_t N, size_t K, size_t row_bytes, void *packed,
                              std::string *err) {
   advise_willneed(src, N * row_bytes);

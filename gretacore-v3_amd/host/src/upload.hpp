@@ -56,6 +56,18 @@ public:
   // Returns when the repack has finished.
   bool repack(int fmt, const uint8_t *src, size_t N, size_t K, size_t row_bytes, void *packed, std::string *err);
 
+  // Several tensors through the ring without waiting in between: the slices
+  // of tensor i + 1 are read while those of tensor i are still in flight, so
+  // the ring stays full across tensors.  Returns when every tensor has been
+  // repacked; after a failure, when the work already queued has finished.
+  struct RepackJob {
+    int fmt;
+    const uint8_t *src;
+    size_t N, K, row_bytes;
+    void *packed;
+  };
+  bool repack_many(const RepackJob *jobs, size_t n, std::string *err);
+
   // Slice size (bytes) and ring depth; GQ_LOAD_SLICE_MB, GQ_LOAD_SLOTS and
   // GQ_LOAD_THREADS override the defaults (16 MiB, 4, min(16, cores)).
   size_t slice_bytes() const { return slice_; }

@@ -653,6 +653,26 @@ bool GGUFLoader::load_tensor_int4(const std::string &name, gcore::rt::hip::Buffe
   return true;
 }
 
+bool GGUFLoader::load_quant_many(const std::string *names, void *const *outs, const size_t *out_bytes, size_t n,
+                                 std::string *err) const {
+  if (n == 0) return true;
+  if (!names || !outs || !out_bytes) return set_err(err, "load_quant_many: null argument"), false;
+  std::vector<Uploader::RepackJob> jobs(n);
+  for (size_t i = 0; i < n; ++i) {
+    LoadPlan p;
+    if (!plan(names[i], LoadKind::QUANT, &p, err)) return false;
+    if (!outs[i] || out_bytes[i] < p.bytes)
+      return set_err(err, "load_quant_many: destination missing or smaller than planned: " + names[i]), false;
+    int idx = -1;
+    const uint8_t *data = nullptr;
+    if (!impl_->locate(names[i], idx, data, err)) return false;
+    const size_t rb = impl_->tensors[idx].size_bytes;
+    if (p.N == 0 || rb % p.N) return set_err(err, "load_quant_many: ragged rows in " + names[i]), false;
+    jobs[i] = Uploader::RepackJob{p.fmt, data, p.N, p.K, rb / p.N, outs[i]};
+  }
+  return impl_->uploader().repack_many(jobs.data(), n, err);
+}
+
 bool GGUFLoader::load_tensor_quant(const std::string &name, gcore::rt::hip::Buffer &packed, std::string *err) {
   LoadPlan p;
   if (!plan(name, LoadKind::QUANT, &p, err) || !alloc_buffer(packed, p.bytes, p.type, err)) return false;

@@ -92,6 +92,17 @@ int gq_gguf_plan_load(const gq_gguf *g, const char *name, int kind, gq_gguf_plan
 int gq_gguf_load(const gq_gguf *g, const char *name, int kind, void *d_out, size_t out_bytes, void *d_scales,
                  size_t scale_bytes, void *d_head_scales, size_t head_scale_bytes);
 
+/* GQ_LOAD_QUANT of n tensors in one pass: no counterpart in the reference
+ * (whose loader, and gq_gguf_load, take one tensor per call and return when
+ * it is on the device).  Here the pinned staging ring stays full across the
+ * tensors, so a layer's many small tensors load at the large-tensor rate.
+ * d_outs[i] holds out_bytes[i] >= the planned bytes of names[i].  Every name
+ * is planned and checked before any data moves (GQ_ERR_INVALID_ARGS, nothing
+ * loaded); returns when all tensors are on the device.  A transfer error
+ * (GQ_ERR_HIP) may leave the tensors before the failing one loaded. */
+int gq_gguf_load_quant_many(const gq_gguf *g, size_t n, const char *const *names, void *const *d_outs,
+                            const size_t *out_bytes);
+
 #ifdef __cplusplus
 }
 #endif

@@ -345,3 +345,43 @@ def test_sliced_upload_with_many_slices(dev, tmp_path, monkeypatch):
         blk = np.frombuffer(tensors[2][3], dtype=np.uint8).reshape(-1, 34)  # Q8_0 split as stored
         assert _bits_equal(q8.cpu().numpy(), blk[:, 2:].copy())
         assert _bits_equal(s8.cpu().numpy(), O.fp16_to_fp32(blk[:, :2].copy().view(np.uint16).ravel()))
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("slice_mb", ["1", "16"])
+def test_load_quant_many_matches_single_loads(dev, tmp_path, monkeypatch, slice_mb):
+    """gq_gguf_load_quant_many: several tensors of every quantized format,
+    small and several slices long, ragged row counts, in one pipelined pass
+    through a ring of 2 slots -- bit-identical to the host repack; the
+    destinations of the failing calls (a missing name, a short destination,
+    a non-quantized tensor) are checked before anything moves."""
+    import torch
+
+    import gq
+    monkeypatch.setenv("GQ_LOAD_SLICE_MB", slice_mb)
+    monkeypatch.setenv("GQ_LOAD_SLOTS", "2")
+    specs = [("a.weight", [4096, 1000], W.GGML_Q4_0, O.Q4_0), ("b.weight", [2048, 333], W.GGML_Q6_K, O.Q6_K),
+             ("c.weight", [1024, 900], W.GGML_Q8_0, O.Q8_0), ("d.weight", [512, 17], W.GGML_Q4_K, O.Q4_K),
+             ("e.weight", [4096, 2000], W.GGML_Q4_K, O.Q4_K), ("f.weight", [64, 30], W.GGML_F32, None)]
+    tensors = [(nm, sh, gt, _tensor_data(nm, sh, gt, f, 40 + i)) for i, (nm, sh, gt, f) in enumerate(specs)]
+    path = _write(tmp_path, "many.gguf", W.llama_kv(dim=DIM, heads=HEADS, heads_kv=HEADS_KV, layers=1, ff=512,
+                                                    ctx=2048, vocab=VOCAB, rope=1e4, eps=1e-5), tensors)
+    quant = [(s, t) for s, t in zip(specs, tensors) if s[3] is not None]
+    with _ours(path) as g:
+        names = [s[0] for s, _ in quant] * 2  # each tensor twice: the ring wraps across tensors
+        outs = [torch.full((g.plan(nm, gq.LOAD_QUANT)["bytes"],), 0xAB, dtype=torch.uint8, device=dev)
+                for nm in names]
+        g.load_quant_many(names, outs)
+        for nm, o in zip(names, outs):
+            (_, sh, _, f), (_, _, _, data) = next((s, t) for s, t in quant if s[0] == nm)
+            k, n = sh[0], int(np.prod(sh)) // sh[0]
+            assert _bits_equal(o.cpu().numpy(), gq.repack_host(f, np.frombuffer(data, dtype=np.uint8), n, k)), nm
+        g.load_quant_many([], [])
+        for bad_names, bad_outs in ((["a.weight", "nope.weight"], outs[:2]),
+                                    (["a.weight", "c.weight"], [outs[0], outs[2][:-1]]),
+                                    (["f.weight"], [torch.empty(64 * 30 * 4, dtype=torch.uint8, device=dev)])):
+            before = [o.clone() for o in bad_outs]
+            with pytest.raises(gq.GQError):
+                g.load_quant_many(bad_names, bad_outs)
+            for o, b in zip(bad_outs, before):
+                assert torch.equal(o, b)
