@@ -17,7 +17,9 @@
 // on the MI355X boxes' hosts), where pread copies from the page cache with no
 // user-space faults (58-80 GB/s on 4-16 threads, above the ~57 GB/s of the
 // pinned H2D link).  Other sources are copied with memcpy.  The copy threads
-// are a pool owned by the uploader.
+// are a pool owned by the uploader.  One uploader serves one host thread at a
+// time (its ring, stream and copy job are shared state), as the loaders that
+// own one are used.
 // A slot is reused only after the event recorded behind its last use has
 // completed.  For GGUF-native tensors the DMA lands in a device slot and
 // gq_repack_rows writes the slice's T16 tiles straight into the destination,
