@@ -1042,6 +1042,7 @@ int launch_cfg(const void *packed, const _Float16 *a16, int lda, void *c, const 
   const int C = (int)gq_chunks(FMT, K);
   const int nsteps = (int)(gq_kpad(FMT, K) / BK);
   const int tiles_m = (M + BM - 1) / BM, tiles_n = (N + BN - 1) / BN;
+  if ((size_t)tiles_m * (size_t)tiles_n > 0x7FFFFFFFu) return GQ_ERR_INVALID_ARGS;  // (one grid dimension)
   hipLaunchKernelGGL(kern, dim3((unsigned)(tiles_m * tiles_n)), dim3(NTHR), 0, s, (const uint8_t *)packed,
                      (uint32_t)gq_sc_plane_offset(FMT, N, K), a16, lda, c, rs, M, N, C, nsteps, tiles_m);
   return gq_last_launch();
@@ -1055,6 +1056,7 @@ int launch_rb(const void *packed, const _Float16 *a16, int lda, void *c, const f
   const int C = (int)gq_chunks(FMT, K);
   const int nsteps = (int)(gq_kpad(FMT, K) / BK);
   const int tiles_m = (M + BM - 1) / BM, tiles_n = (N + BN - 1) / BN;
+  if ((size_t)tiles_m * (size_t)tiles_n > 0x7FFFFFFFu) return GQ_ERR_INVALID_ARGS;  // (one grid dimension)
   const char *e = getenv("GQ_GEMM_PD");
   const int pd = e ? atoi(e) : pd_default;
   // tile order in groups of 4 M tiles (GQ_GEMM_GM=n overrides, 0: plain
