@@ -429,9 +429,9 @@ def bench_decode_step(dev, steps, warmup):
            "fused_norm_swiglu_graph_ms": t_fused * 1e3,
            "chain_graph_ms": t_chain * 1e3, "chain_launches": 2, "chain_wait_error": chain_err,
            "chain_note": "one persistent launch for the 32 layers (real data flow: RMSNorm, GQA read, residuals, "
-                         "SwiGLU) + the lm_head; each of its 128 dependent stage boundaries costs ~8 us of "
-                         "cross-CU signalling (flags, coherent loads, the stage's first tiles), more than a "
-                         "kernel boundary in a graph (~3 us), so the grouped launches stay the faster decode path"}
+                         "SwiGLU) + the lm_head; its compute waves idle ~48 % of the step waiting for each "
+                         "stage's input (flag latency ~2.5 us, x staging 2-6 us, the stage's last units) and "
+                         "stream at ~3.7 TB/s otherwise, so the grouped launches stay the faster decode path"}
     del chain
     del layers, lm_packed
     torch.cuda.empty_cache()
