@@ -43,9 +43,13 @@ constexpr size_t kLdsWg = 160 * 1024;  // LDS per workgroup on gfx950
 // Static LDS of a kernel (its __shared__ arrays), looked up once per kernel:
 // the launches check static + dynamic against the workgroup's LDS, so a plan
 // that would not fit fails with an error instead of running past its LDS.
-size_t kernel_static_lds(const void *kern) {
+// Without a device (host-only plan queries) the attributes are unavailable:
+// `otherwise` is returned (kLdsWg: nothing fits; a plan passes its estimate).
+size_t kernel_static_lds(const void *kern, size_t otherwise = kLdsWg) {
   hipFuncAttributes a{};
-  return hipFuncGetAttributes(&a, kern) == hipSuccess ? a.sharedSizeBytes : kLdsWg;
+  if (hipFuncGetAttributes(&a, kern) == hipSuccess) return a.sharedSizeBytes;
+  (void)hipGetLastError();
+  return otherwise;
 }
 
 // One weight matrix of a launch: T16 data, its scale-plane offset, output
@@ -806,8 +810,10 @@ int ks_for(int fmt, size_t wgs, int C, int R) {
 
 // HALF: register room for MAXC / R / 2 chunks per wave where the plan needs no
 // more (fewer surplus loads, fewer registers)
+// dry: only the checks (the staging fits the LDS), no launch
 template <int FMT, int NBC, int R, int FUSE, bool HALF>
-int launch_fused_nbc(const GemvFuse &fz, size_t wgs, int ks, const float *x, int K, int nb, hipStream_t s) {
+int launch_fused_nbc(const GemvFuse &fz, size_t wgs, int ks, const float *x, int K, int nb, hipStream_t s,
+                     bool dry) {
   using F = Fmt<FMT>;
   constexpr int NCKT = F::MAXC / R / (HALF ? 2 : 1);
   const int C = (int)gq_chunks(FMT, K);
@@ -818,8 +824,9 @@ int launch_fused_nbc(const GemvFuse &fz, size_t wgs, int ks, const float *x, int
 #define GQ_LAUNCH_F(KS)                                                                                        \
   {                                                                                                            \
     const void *kern = (const void *)k_gemv_q<FMT, NBC, 1, R, NCKT, KS, false, FUSE>;                         \
-    static const size_t st = kernel_static_lds(kern);                                                         \
+    static const size_t st = kernel_static_lds(kern, q_static_lds(FMT, nb, R, KS, FUSE > 0));                  \
     if (lds + st > kLdsWg) return GQ_ERR_UNSUPPORTED;                                                          \
+    if (dry) return GQ_OK;                                                                                     \
     hipLaunchKernelGGL((k_gemv_q<FMT, NBC, 1, R, NCKT, KS, false, FUSE>), dim3((unsigned)wgs), dim3(64 * KS), \
                        lds, s, fz, x, nullptr, nullptr, K, C, Kp, nb);                                         \
   }
@@ -834,29 +841,87 @@ int launch_fused_nbc(const GemvFuse &fz, size_t wgs, int ks, const float *x, int
 }
 
 template <int FMT, int R, int FUSE, bool HALF>
-int launch_fused_h(const GemvFuse &fz, size_t wgs, int ks, const float *x, int K, int nb, hipStream_t s) {
-  if (nb == 1) return launch_fused_nbc<FMT, 1, R, FUSE, HALF>(fz, wgs, ks, x, K, nb, s);
-  if (nb == 2) return launch_fused_nbc<FMT, 2, R, FUSE, HALF>(fz, wgs, ks, x, K, nb, s);
-  return launch_fused_nbc<FMT, 4, R, FUSE, HALF>(fz, wgs, ks, x, K, nb, s);
+int launch_fused_h(const GemvFuse &fz, size_t wgs, int ks, const float *x, int K, int nb, hipStream_t s, bool dry) {
+  if (nb == 1) return launch_fused_nbc<FMT, 1, R, FUSE, HALF>(fz, wgs, ks, x, K, nb, s, dry);
+  if (nb == 2) return launch_fused_nbc<FMT, 2, R, FUSE, HALF>(fz, wgs, ks, x, K, nb, s, dry);
+  return launch_fused_nbc<FMT, 4, R, FUSE, HALF>(fz, wgs, ks, x, K, nb, s, dry);
 }
 
 template <int FMT, int R, int FUSE>
-int launch_fused(const GemvFuse &fz, size_t wgs, int ks, const float *x, int K, int nb, hipStream_t s) {
+int launch_fused(const GemvFuse &fz, size_t wgs, int ks, const float *x, int K, int nb, hipStream_t s, bool dry) {
   const int C = (int)gq_chunks(FMT, K);
   if constexpr (R == 1) {  // (one-tile workgroups: a half list still stages whole 512-k slices)
-    if ((C + ks - 1) / ks <= Fmt<FMT>::MAXC / 2) return launch_fused_h<FMT, 1, FUSE, true>(fz, wgs, ks, x, K, nb, s);
+    if ((C + ks - 1) / ks <= Fmt<FMT>::MAXC / 2)
+      return launch_fused_h<FMT, 1, FUSE, true>(fz, wgs, ks, x, K, nb, s, dry);
   }
-  return launch_fused_h<FMT, R, FUSE, false>(fz, wgs, ks, x, K, nb, s);
+  return launch_fused_h<FMT, R, FUSE, false>(fz, wgs, ks, x, K, nb, s, dry);
 }
 
 template <int R, int FUSE>
 int launch_fused_fmt(int fmt, const GemvFuse &fz, size_t wgs, int ks, const float *x, int K, int nb,
-                     hipStream_t s) {
+                     hipStream_t s, bool dry = false) {
   switch (gq_fmt_is_q4k(fmt) ? GQ_FMT_Q4_K : fmt) {
-  case GQ_FMT_Q4_0: return launch_fused<GQ_FMT_Q4_0, R, FUSE>(fz, wgs, ks, x, K, nb, s);
-  case GQ_FMT_Q8_0: return launch_fused<GQ_FMT_Q8_0, R, FUSE>(fz, wgs, ks, x, K, nb, s);
-  default: return launch_fused<GQ_FMT_Q4_K, R, FUSE>(fz, wgs, ks, x, K, nb, s);
+  case GQ_FMT_Q4_0: return launch_fused<GQ_FMT_Q4_0, R, FUSE>(fz, wgs, ks, x, K, nb, s, dry);
+  case GQ_FMT_Q8_0: return launch_fused<GQ_FMT_Q8_0, R, FUSE>(fz, wgs, ks, x, K, nb, s, dry);
+  default: return launch_fused<GQ_FMT_Q4_K, R, FUSE>(fz, wgs, ks, x, K, nb, s, dry);
   }
+}
+
+// ---- the fused forms' fallback ------------------------------------------------
+// Batch 3..4 with long K (about 15000 and more for Q4_0 / Q4_K) cannot stage
+// the activation limbs of a fused launch in LDS.  Those shapes run as: x
+// RMS-normalised into a workspace row (when gamma is given), one gq_gemv per
+// matrix (which takes them to the fp16 batch kernel), and for SwiGLU an
+// elementwise silu(gate) * up.  Same results within the GEMV's bound; the
+// normalisation is applied to x before the products instead of to the dot
+// products after them.
+__global__ void __launch_bounds__(256) k_rmsnorm_rows(const float *__restrict__ x, const float *__restrict__ gamma,
+                                                      float *__restrict__ xn, int K, float eps) {
+  const size_t b = blockIdx.x;
+  const float *xr = x + b * (size_t)K;
+  float *o = xn + b * (size_t)K;
+  float ss = 0.f;
+  for (int k = (int)threadIdx.x; k < K; k += 256) ss += xr[k] * xr[k];
+  __shared__ float part[4];
+  ss = wave_sum(ss);
+  if ((threadIdx.x & 63) == 0) part[threadIdx.x >> 6] = ss;
+  __syncthreads();
+  const float inv = 1.0f / sqrtf((part[0] + part[1] + part[2] + part[3]) / (float)K + eps);
+  for (int k = (int)threadIdx.x; k < K; k += 256) o[k] = xr[k] * inv * gamma[k];
+}
+
+__global__ void __launch_bounds__(256) k_silu_mul(const float *__restrict__ g, const float *__restrict__ u,
+                                                  float *__restrict__ y, size_t n) {
+  const size_t i = (size_t)blockIdx.x * 256 + threadIdx.x;
+  if (i < n) {
+    const float gt = g[i];
+    y[i] = gt / (1.0f + expf(-gt)) * u[i];
+  }
+}
+
+// mats: n_mats matrices (SwiGLU: gate, up; y[0] the output)
+int fused_fallback(int fmt, int n_mats, const void *const *packed, const size_t *N, size_t K, const float *x,
+                   float *const *y, int batch, const float *gamma, float eps, bool swiglu, hipStream_t s) {
+  const size_t xb = gamma ? gq_align256((size_t)batch * K * 4) : 0;
+  const size_t tb = swiglu ? gq_align256((size_t)batch * N[0] * 4) : 0;
+  void *ws = nullptr;
+  if (xb + 2 * tb) GQ_TRY(gq_default_workspace(xb + 2 * tb, &ws));
+  const float *xin = x;
+  if (gamma) {
+    hipLaunchKernelGGL(k_rmsnorm_rows, dim3((unsigned)batch), dim3(256), 0, s, x, gamma, (float *)ws, (int)K, eps);
+    GQ_TRY(gq_last_launch());
+    xin = (const float *)ws;
+  }
+  if (!swiglu) {
+    for (int i = 0; i < n_mats; ++i) GQ_TRY(gq_gemv(fmt, packed[i], xin, y[i], N[i], K, batch, nullptr, 0, s));
+    return GQ_OK;
+  }
+  float *tg = (float *)((uint8_t *)ws + xb), *tu = (float *)((uint8_t *)ws + xb + tb);
+  GQ_TRY(gq_gemv(fmt, packed[0], xin, tg, N[0], K, batch, nullptr, 0, s));
+  GQ_TRY(gq_gemv(fmt, packed[1], xin, tu, N[0], K, batch, nullptr, 0, s));
+  const size_t n = (size_t)batch * N[0];
+  hipLaunchKernelGGL(k_silu_mul, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, tg, tu, y[0], n);
+  return gq_last_launch();
 }
 
 }  // namespace
@@ -872,6 +937,12 @@ extern "C" int gq_gemv_multi_plan(int fmt, int n_mats, const size_t *N, size_t K
   }
   int R = 1, ks = 2, cpw = 0;
   GQ_TRY(q_plan(fmt, tiles * 16, K, batch, &R, &ks, &cpw));
+  // (0, 0, 0): the staging does not fit, the call runs the fallback
+  const int st = K == 0 ? GQ_OK
+                        : R == 2 ? launch_fused_fmt<2, 1>(fmt, GemvFuse{}, 1, ks, nullptr, (int)K, batch, nullptr, true)
+                                 : launch_fused_fmt<1, 1>(fmt, GemvFuse{}, 1, ks, nullptr, (int)K, batch, nullptr, true);
+  // (the fused kernel's chunk list or its LDS staging does not fit)
+  if (st == GQ_ERR_UNSUPPORTED || st == GQ_ERR_INVALID_ARGS) R = ks = cpw = 0;
   if (R_out) *R_out = R;
   if (ksplit_out) *ksplit_out = ks;
   if (chunks_per_wave_out) *chunks_per_wave_out = cpw;
@@ -884,6 +955,10 @@ extern "C" int gq_gemv_multi(int fmt, int n_mats, const void *const *packed, con
   GQ_CHECK(packed && y && x && N, GQ_ERR_INVALID_ARGS);
   int R = 1, ks = 2, cpw = 0;
   GQ_TRY(gq_gemv_multi_plan(fmt, n_mats, N, K, batch, &R, &ks, &cpw));
+  if (R == 0) {
+    for (int i = 0; i < n_mats; ++i) GQ_CHECK(packed[i] && y[i], GQ_ERR_INVALID_ARGS);
+    return fused_fallback(fmt, n_mats, packed, N, K, x, y, batch, gamma, eps, false, (hipStream_t)stream);
+  }
   GemvFuse fz{};
   size_t wgs = 0;
   for (int i = 0; i < n_mats; ++i) {
@@ -906,10 +981,16 @@ extern "C" int gq_gemv_swiglu_plan(int fmt, size_t N, size_t K, int batch, int *
   GQ_TRY(gq_check_shape(fmt, N, K));
   GQ_CHECK(batch >= 1 && batch <= 4 && !gq_fmt_is_q6k(fmt), GQ_ERR_UNSUPPORTED);
   const int C = (int)gq_chunks(fmt, K);
-  const int ks = ks_for(fmt, gq_tiles(N), C, 2);
-  GQ_CHECK(ks > 0, GQ_ERR_UNSUPPORTED);
+  int ks = ks_for(fmt, gq_tiles(N), C, 2);
+  int cpw = ks > 0 ? (C + ks - 1) / ks : 0;
+  // (0, 0): K too long for a wave's chunk list, or the staging does not fit
+  // the LDS: the call runs the fallback
+  const int st = (K == 0 || ks <= 0) ? GQ_OK
+                                      : launch_fused_fmt<2, 2>(fmt, GemvFuse{}, 1, ks, nullptr, (int)K, batch, nullptr,
+                                                               true);
+  if (ks <= 0 || st == GQ_ERR_UNSUPPORTED || st == GQ_ERR_INVALID_ARGS) ks = cpw = 0;
   if (ksplit_out) *ksplit_out = ks;
-  if (chunks_per_wave_out) *chunks_per_wave_out = (C + ks - 1) / ks;
+  if (chunks_per_wave_out) *chunks_per_wave_out = cpw;
   return GQ_OK;
 }
 
@@ -920,6 +1001,12 @@ extern "C" int gq_gemv_swiglu(int fmt, const void *gate, const void *up, size_t 
   GQ_TRY(gq_gemv_swiglu_plan(fmt, N, K, batch, &ks, &cpw));
   if (N == 0) return GQ_OK;
   GQ_CHECK(K > 0, GQ_ERR_INVALID_ARGS);
+  if (ks == 0) {
+    const void *pk[2] = {gate, up};
+    const size_t nn[2] = {N, N};
+    float *yy[1] = {y};
+    return fused_fallback(fmt, 2, pk, nn, K, x, yy, batch, gamma, eps, true, (hipStream_t)stream);
+  }
   GemvFuse fz{};
   const size_t sc = gq_sc_plane_offset(fmt, N, K);
   const size_t wgs = gq_tiles(N);

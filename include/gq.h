@@ -151,13 +151,20 @@ int gq_gemv_prepped(int fmt, const void *d_packed, const void *d_workspace, floa
  * format sharing K and x (e.g. q, k, v with GQA shapes). */
 int gq_gemv_multi(int fmt, int n_mats, const void *const *d_packed, const size_t *N, size_t K, const float *d_x,
                   float *const *d_y, int batch, const float *d_gamma, float eps, void *stream);
-/* Launch plan of gq_gemv_multi (row tiles per workgroup, waves, chunks per wave). */
+/* Shapes whose activation staging does not fit one fused launch (batch 3..4
+ * with K beyond about 14000, or K too long for a wave's chunk list) run as a
+ * fallback: x RMS-normalised into the library's workspace (when gamma is
+ * given), one gq_gemv per matrix, and for gq_gemv_swiglu an elementwise
+ * silu(gate) * up -- the same results within the GEMV bound, in 2-4 launches.
+ * Launch plan of gq_gemv_multi (row tiles per workgroup, waves, chunks per
+ * wave); (0, 0, 0) when the call takes the fallback. */
 int gq_gemv_multi_plan(int fmt, int n_mats, const size_t *N, size_t K, int batch, int *row_tiles_per_wg,
                        int *ksplit, int *chunks_per_wave);
 /* gq_gemv_swiglu: y [batch][N] = silu(W_gate xn) * (W_up xn), silu(g) = g / (1 + e^-g)
  * (the FFN front of launch_fused_ffn_front_f16). */
 int gq_gemv_swiglu(int fmt, const void *d_gate, const void *d_up, size_t N, size_t K, const float *d_x, float *d_y,
                    int batch, const float *d_gamma, float eps, void *stream);
+/* Launch plan of gq_gemv_swiglu (waves, chunks per wave); (0, 0) for the fallback. */
 int gq_gemv_swiglu_plan(int fmt, size_t N, size_t K, int batch, int *ksplit, int *chunks_per_wave);
 
 /* ---- prefill GEMM: C[m][n] = sum_k A[m][k] * W[n][k] ------------------------ */

@@ -289,6 +289,9 @@ def test_fused_plans_in_bounds(fmt, batch):
         if k % (256 if fmt == gq.FMT_Q4_K else 32):
             continue
         R, ks, cpw = gq.gemv_multi_plan(fmt, list(ns), k, batch)
+        if R == 0:  # the activation staging of a fused launch does not fit: gq_gemv_multi's fallback
+            assert (R, ks, cpw) == (0, 0, 0) and batch >= 3 and k > 8192
+            continue
         assert ks in (2, 4, 8, 16) and R in (1, 2)
         for n in ns:
             _emulate_int8_segment(fmt, n, k, R, ks)

@@ -88,3 +88,36 @@ def test_fused_reject_bad_args(dev):
         gq.gemv_multi(O.Q4_0, [(p, 64)], x, 256)  # batch 5 is not supported by the fused path
     with pytest.raises(gq.GQError):
         gq.gemv_swiglu(O.Q4_0, p, p, x, 64, 256)
+
+
+@pytest.mark.parametrize("fmt", [O.Q4_0, O.Q8_0, O.Q4_K])
+@pytest.mark.parametrize("norm", [False, True])
+def test_fused_fallback_long_k(dev, fmt, norm):
+    """Shapes one fused launch cannot stage: batch 4 with K = 16384 (gq_gemv_multi
+    and gq_gemv_swiglu) and K = 14336 at batch 1 for gq_gemv_swiglu (its
+    gate/up chunk lists exceed a wave's registers).  The plans report the
+    fallback (zeros) and the calls give the fused forms' results: RMSNorm,
+    one GEMV per matrix, silu(gate) * up."""
+    import gq
+    eps = 1e-5
+    for k, batch, multi in ((16384, 4, True), (16384, 4, False), (14336, 1, False)):
+        print(f"fused fallback fmt={fmt} k={k} batch={batch} multi={multi} norm={norm}", flush=True)
+        x = O.gen_x(batch, k, 21) * 3.0
+        gamma = (np.random.default_rng(22).standard_normal(k) * 0.5 + 1.0).astype(np.float32)
+        xin = O.rmsnorm(x, gamma, eps).astype(np.float32) if norm else x
+        g = _dev(gamma, dev) if norm else None
+        if multi:
+            ns = [300, 64, 1000]
+            assert gq.gemv_multi_plan(fmt, ns, k, batch) == (0, 0, 0)
+            pw = [_packed(fmt, n, k, 80 + i, dev) for i, n in enumerate(ns)]
+            ys = gq.gemv_multi(fmt, [(p, n) for (_, p), n in zip(pw, ns)], _dev(x, dev), k, gamma=g, eps=eps)
+            for (w, _), n, y in zip(pw, ns, ys):
+                assert O.rel_l2(y.cpu().numpy(), O.gemv(fmt, w, xin, n, k)) <= TOL
+        else:
+            n = 200
+            assert gq.gemv_swiglu_plan(fmt, n, k, batch) == (0, 0)
+            wg, pg = _packed(fmt, n, k, 90, dev)
+            wu, pu = _packed(fmt, n, k, 91, dev)
+            y = gq.gemv_swiglu(fmt, pg, pu, _dev(x, dev), n, k, gamma=g, eps=eps).cpu().numpy()
+            ref = O.swiglu(O.gemv(fmt, wg, xin, n, k), O.gemv(fmt, wu, xin, n, k))
+            assert O.rel_l2(y, ref) <= TOL
