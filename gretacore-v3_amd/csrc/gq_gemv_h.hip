@@ -1056,14 +1056,41 @@ int gq_launch_gemv_h(int fmt, const void *packed, const float *x, float *y, int 
 // weights need no dequantization; A is rounded to fp16 after the per-window
 // power-of-two scaling, as every batch GEMV here does).  Rows of A beyond 16
 // take further launches (each re-reads W).
+namespace {
+// fp16 weights of any K or alignment (the matrix-core kernel needs K % 32 == 0
+// and 16-byte rows): one workgroup of 4 waves per output column n, each wave
+// one row of A, fp32 products of the fp32 activation and the fp16 weight
+// summed over K (the reference's VALU route's arithmetic); rows of A beyond
+// the grid's 4 * gridDim.y are taken in further strides
+__global__ void __launch_bounds__(256) k_f16w_any(const _Float16 *__restrict__ w, const float *__restrict__ a,
+                                                  float *__restrict__ c, int M, int N, int K) {
+  const int n = blockIdx.x, lane = threadIdx.x & 63;
+  const _Float16 *wr = w + (size_t)n * K;
+  for (int m = blockIdx.y * 4 + (threadIdx.x >> 6); m < M; m += gridDim.y * 4) {
+    const float *ar = a + (size_t)m * K;
+    float sum = 0.f;
+    for (int k = lane; k < K; k += 64) sum = fmaf(ar[k], (float)wr[k], sum);
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) sum += __shfl_xor(sum, o, 64);
+    if (lane == 0) c[(size_t)m * N + n] = sum;
+  }
+}
+}  // namespace
+
 extern "C" int gq_gemm_f16w(const void *w, const float *a, float *c, size_t M, size_t N, size_t K, void *stream) {
   GQ_CHECK(M <= GQ_MAX_DIM && N <= GQ_MAX_DIM && K <= GQ_MAX_DIM, GQ_ERR_INVALID_ARGS);
   GQ_CHECK(w && a && c, GQ_ERR_INVALID_ARGS);
-  // 16-element lane runs must not straddle rows, and rows start 16-byte aligned
-  GQ_CHECK(K % 32 == 0 && (uintptr_t)w % 16 == 0 && (uintptr_t)a % 16 == 0, GQ_ERR_UNSUPPORTED);
   hipStream_t s = (hipStream_t)stream;
   if (M == 0 || N == 0) return GQ_OK;
   if (K == 0) return gq_fill_zero(c, M * N, s);
+  // the matrix-core kernel's 16-element lane runs must not straddle rows, and
+  // rows start 16-byte aligned; other shapes take the plain kernel
+  if (K % 32 != 0 || (uintptr_t)w % 16 != 0 || (uintptr_t)a % 16 != 0) {
+    const unsigned gy = (unsigned)((M + 3) / 4 < 65535 ? (M + 3) / 4 : 65535);
+    hipLaunchKernelGGL(k_f16w_any, dim3((unsigned)N, gy), dim3(256), 0, s, (const _Float16 *)w, a, c, (int)M, (int)N,
+                       (int)K);
+    return gq_last_launch();
+  }
   for (size_t m0 = 0; m0 < M; m0 += GQ_MAX_BATCH) {
     const int nb = (int)(M - m0 < (size_t)GQ_MAX_BATCH ? M - m0 : (size_t)GQ_MAX_BATCH);
     GQ_TRY(launch_h<GQ_FMT_F16>(w, a + m0 * K, c + m0 * N, (int)N, (int)K, nb, s));

@@ -224,9 +224,10 @@ int gq_launch_gemm_mfma_int4_wt_fp32_acc32(void *stream, const void *a, const in
  * 294-358, 387-523): C[M][N] = A[M][K] W^T, A fp32, W fp16 row-major N x K
  * (GGUF F16 tensors, e.g. a dequantized lm_head), C fp32.  Here on the fp16
  * matrix cores in batches of up to 16 rows of A (fp32 accumulation; A rounded
- * to fp16 after a per-window power-of-two scaling).  K % 32 == 0, d_w and d_a
- * 16-byte aligned (GQ_ERR_UNSUPPORTED otherwise).  Rows of A beyond 16 take
- * further launches, each streaming W again. */
+ * to fp16 after a per-window power-of-two scaling) when K % 32 == 0 and d_w and
+ * d_a are 16-byte aligned; any other K or alignment runs a plain fp32-accumulating
+ * kernel (fp32 A times the fp16 weight, as the reference's VALU route).  Rows of
+ * A beyond 16 take further launches, each streaming W again. */
 int gq_gemm_f16w(const void *d_w, const float *d_a, float *d_c, size_t M, size_t N, size_t K, void *stream);
 /* The two reference launchers under their argument lists; lda must be K and
  * ldc N (what GretaCompute::gemm passes), ldb is ignored as in the reference. */

@@ -114,3 +114,33 @@ def test_reference_f16_launchers(dev):
     lib = gq.load()
     st = lib.gq_launch_gemm_mixed_f16f32(gq._stream(None), gq._ptr(a), gq._ptr(w), gq._ptr(c), 4, n, 32, 64, n, n)
     assert st == 2  # GQ_ERR_UNSUPPORTED
+
+
+@pytest.mark.parametrize("n,k,m", [(300, 40, 3), (1000, 100, 17), (77, 8, 1), (513, 4104, 5)])
+def test_f16w_any_k_and_alignment(dev, n, k, m):
+    """K not a multiple of 32 (the reference's FP16 launchers take any K) and
+    operands not 16-byte aligned run the plain fp32-accumulating kernel:
+    rel-L2 <= 1e-5 against the fp64 product of the same fp16 weights (fp32
+    activations, fp32 sums), through gq_gemm_f16w and both reference launchers."""
+    import torch
+
+    import gq
+    w16 = _w(n, k, seed=n + k)
+    a = np.random.default_rng(k).standard_normal((m, k)).astype(np.float32)
+    ref = _ref(w16, a)
+    y = _run(dev, w16, a)
+    assert _rel(y, ref) <= 1e-5
+    for mfma in (False, True):
+        c = gq.launch_mixed_f16f32(torch.from_numpy(a).to(dev), torch.from_numpy(w16).to(dev), m, n, k, mfma=mfma)
+        assert _rel(c.cpu().numpy(), ref) <= 1e-5
+    # K % 32 == 0 but the operands start 4 bytes into their buffers
+    k2 = 64
+    w2 = _w(n, k2, seed=7)
+    a2 = np.random.default_rng(8).standard_normal((m, k2)).astype(np.float32)
+    wb = torch.zeros(n * k2 + 8, dtype=torch.float16, device=dev)
+    ab = torch.zeros(m * k2 + 4, dtype=torch.float32, device=dev)
+    wv, av = wb[2:2 + n * k2].view(n, k2), ab[1:1 + m * k2].view(m, k2)
+    wv.copy_(torch.from_numpy(w2))
+    av.copy_(torch.from_numpy(a2))
+    c2 = gq.gemm_f16w(wv, av, n, k2).cpu().numpy()
+    assert _rel(c2, _ref(w2, a2)) <= 1e-5
