@@ -385,3 +385,84 @@ def test_load_quant_many_matches_single_loads(dev, tmp_path, monkeypatch, slice_
                 g.load_quant_many(bad_names, bad_outs)
             for o, b in zip(bad_outs, before):
                 assert torch.equal(o, b)
+
+
+def _random_gguf(rng, path):
+    """A GGUF file inside what the reference parser reads correctly: llama.*
+    keys as integer / f32 scalars (not type 7, which it reads as a double),
+    other keys of every scalar type, strings and flat arrays, a token list with
+    over-long entries, and 1..10 tensors of every loader type."""
+    u32_keys = ["llama.embedding_length", "llama.feed_forward_length", "llama.block_count",
+                "llama.attention.head_count", "llama.attention.head_count_kv", "llama.context_length"]
+    f32_keys = ["llama.rope.freq_base", "llama.norm_eps"]
+    kv = []
+    for key in u32_keys:
+        if rng.random() < 0.85:
+            t = int(rng.choice([W.U32, W.I32, W.U16, W.I16]))
+            hi = {W.U32: 1 << 20, W.I32: 1 << 20, W.U16: 60000, W.I16: 30000}[t]
+            kv.append((key, t, int(rng.integers(1, hi))))
+    for key in f32_keys:
+        if rng.random() < 0.85:
+            kv.append((key, W.F32, float(np.float32(rng.uniform(1e-7, 1e6)))))
+    scal = {W.U8: (0, 255), W.I8: (-128, 127), W.U16: (0, 65535), W.I16: (-32768, 32767), W.U32: (0, 1 << 31),
+            W.I32: (-(1 << 31), 1 << 31), W.U64: (0, 1 << 62), W.I64: (-(1 << 62), 1 << 62)}
+    for j in range(int(rng.integers(0, 8))):
+        c = int(rng.integers(0, 5))
+        key = f"general.extra_{j}"
+        if c == 0:
+            t = int(rng.choice(list(scal)))
+            kv.append((key, t, int(rng.integers(*scal[t]))))
+        elif c == 1:
+            kv.append((key, int(rng.choice([W.F32, W.F64])), float(rng.standard_normal())))
+        elif c == 2:
+            kv.append((key, W.STR, "x" * int(rng.integers(0, 300))))
+        elif c == 3:
+            t = int(rng.choice(list(scal)))
+            kv.append((key, W.ARR, (t, [int(v) for v in rng.integers(*scal[t], size=int(rng.integers(0, 40)))])))
+        else:
+            kv.append((key, W.ARR, (W.STR, ["s" * int(rng.integers(0, 20)) for _ in range(int(rng.integers(0, 30)))])))
+    vocab = None
+    if rng.random() < 0.7:
+        vocab = ["t%d" % i if rng.random() < 0.95 else "L" * int(rng.integers(1025, 1500))
+                 for i in range(int(rng.integers(1, 200)))]
+        kv.append(("tokenizer.ggml.tokens", W.ARR, (W.STR, vocab)))
+    order = rng.permutation(len(kv))
+    kv = [kv[i] for i in order]
+    types = [W.GGML_F32, W.GGML_F16, W.GGML_Q4_0, W.GGML_Q8_0, W.GGML_Q4_K, W.GGML_Q6_K]
+    tensors = []
+    for j in range(int(rng.integers(1, 11))):
+        gt = int(rng.choice(types))
+        be = W._BLOCK[gt][0]
+        ne0 = be * int(rng.integers(1, 9)) if be > 1 else int(rng.integers(1, 600))
+        shape = [ne0] + [int(rng.integers(1, 40)) for _ in range(int(rng.integers(0, 3)))]
+        nb = W.tensor_bytes(gt, shape)
+        tensors.append((f"blk.{j}.w{int(rng.integers(0, 1000))}.weight", shape, gt,
+                        rng.integers(0, 256, nb, dtype=np.uint8).tobytes()))
+    W.write_gguf(path, kv, tensors)
+    return tensors, vocab
+
+
+@pytest.mark.skipif(not O.ref_available(), reason="oracle/_ref not built")
+def test_parse_random_files_match_reference(tmp_path):
+    """40 seeded random GGUF files: tensor tables, the config and the token
+    list as the reference parser reads them (its Q8_0 dtype string is
+    "UNKNOWN"), and every tensor's bytes where the file says they are."""
+    rng = np.random.default_rng(20261205)
+    for i in range(40):
+        path = str(tmp_path / f"r{i}.gguf")
+        tensors, vocab = _random_gguf(rng, path)
+        rts, rcfg, err = O.ref_gguf_parse(path)
+        assert rts is not None, (i, err)
+        with _ours(path) as g:
+            ts = g.tensors()
+            assert len(ts) == len(rts) == len(tensors), i
+            for a, b, (name, shape, gt, data) in zip(ts, rts, tensors):
+                assert a["name"] == b["name"] == name and a["shape"] == b["shape"] == shape, i
+                assert a["offset"] == b["offset"] and a["size_bytes"] == b["size_bytes"] == len(data), i
+                assert ("UNKNOWN" if a["dtype"] == "Q8_0" else a["dtype"]) == b["dtype"], i
+                assert g.read_raw(name).tobytes() == data, i
+            c = g.config()
+            for k, v in rcfg.items():
+                assert c[k] == v, (i, k)
+            if vocab is not None:
+                assert g.vocab() == [b"<too_long>" if len(v) > 1024 else v.encode() for v in vocab], i
