@@ -78,6 +78,13 @@ def ref():
     """The reference's own CPU functions (oracle/_ref), or None if not built."""
     global _ref
     if _ref is None and ref_available():
+        # the reference's loader is HIP code: PyTorch's HIP runtime (same
+        # soname) must be loaded first, or the two runtimes disagree and the
+        # reference's allocations report no device once torch holds the GPU
+        try:
+            import torch  # noqa: F401
+        except ImportError:
+            pass
         R = ctypes.CDLL(REF_SO)
         vp, sz, i = ctypes.c_void_p, ctypes.c_size_t, ctypes.c_int
         R.gqref_fp16_to_fp32.restype = ctypes.c_float

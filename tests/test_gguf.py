@@ -466,3 +466,43 @@ def test_parse_random_files_match_reference(tmp_path):
                 assert c[k] == v, (i, k)
             if vocab is not None:
                 assert g.vocab() == [b"<too_long>" if len(v) > 1024 else v.encode() for v in vocab], i
+
+
+@pytest.mark.gpu
+@pytest.mark.skipif(not O.ref_available(), reason="oracle/_ref not built")
+def test_load_random_tensors_match_reference_loader(dev, tmp_path):
+    """Random tensors of the types the reference loader converts (F32, F16,
+    Q4_K, Q6_K; random ragged shapes, element counts a whole number of
+    32-blocks) through every load kind (F32, F16, INT8, INT4), bit-identical to
+    the reference GGUFLoader run on the same file.  Cases the reference
+    refuses are skipped (none is expected)."""
+    rng = np.random.default_rng(20261206)
+    kinds_done = 0
+    for f in range(6):
+        tensors = []
+        for j in range(6):
+            gt = int(rng.choice([W.GGML_F32, W.GGML_F16, W.GGML_Q4_K, W.GGML_Q6_K]))
+            be = W._BLOCK[gt][0]
+            ne0 = be * int(rng.integers(1, 5)) if be > 1 else 32 * int(rng.integers(1, 40))
+            shape = [ne0, int(rng.integers(1, 70))]
+            tensors.append((f"blk.{j}.ffn_x{j}.weight", shape, gt,
+                            _tensor_data(f"t{f}_{j}", shape, gt, O.Q4_K if gt == W.GGML_Q4_K else
+                                         O.Q6_K if gt == W.GGML_Q6_K else None, 100 * f + j)))
+        path = _write(tmp_path, f"rl{f}.gguf", W.llama_kv(dim=DIM, heads=HEADS, heads_kv=HEADS_KV, layers=1,
+                                                          ff=512, ctx=2048, vocab=VOCAB, rope=1e4, eps=1e-5),
+                      tensors)
+        with _ours(path) as g:
+            for name, shape, gt, _ in tensors:
+                for kind in (0, 1, 2, 3):
+                    print(f"random load file {f} {name} shape={shape} type={gt} kind={kind}", flush=True)
+                    try:
+                        rq, rs, rh = O.ref_gguf_load(path, name, kind, max_bytes=4 << 20)
+                    except RuntimeError as e:
+                        print("reference refused:", e, flush=True)
+                        continue
+                    data, sc, hs, _ = g.load(name, kind, device=dev)
+                    assert _bits_equal(data.cpu().numpy(), rq), (name, kind)
+                    if kind >= 2:
+                        assert _bits_equal(sc.cpu().numpy(), rs), (name, kind)
+                    kinds_done += 1
+    assert kinds_done >= 100
