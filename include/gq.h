@@ -156,8 +156,11 @@ int gq_gemv_multi(int fmt, int n_mats, const void *const *d_packed, const size_t
  * fallback: x RMS-normalised into the library's workspace (when gamma is
  * given), one gq_gemv per matrix, and for gq_gemv_swiglu an elementwise
  * silu(gate) * up -- the same results within the GEMV bound, in 2-4 launches.
- * Launch plan of gq_gemv_multi (row tiles per workgroup, waves, chunks per
- * wave); (0, 0, 0) when the call takes the fallback. */
+ * The fallback's normalised x and gate / up rows live in the library's default
+ * workspace, which is allocated (after a device synchronisation) when a call
+ * first needs more of it: under HIP graph capture, run such a shape once
+ * before capturing.  Launch plan of gq_gemv_multi (row tiles per workgroup,
+ * waves, chunks per wave); (0, 0, 0) when the call takes the fallback. */
 int gq_gemv_multi_plan(int fmt, int n_mats, const size_t *N, size_t K, int batch, int *row_tiles_per_wg,
                        int *ksplit, int *chunks_per_wave);
 /* gq_gemv_swiglu: y [batch][N] = silu(W_gate xn) * (W_up xn), silu(g) = g / (1 + e^-g)
