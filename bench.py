@@ -720,6 +720,10 @@ def main():
     gemv_cfgs = [("q8_0_4096x4096_b1", O.Q8_0, 4096, 4096, 1, 1001),
                  ("q8_0_lm_head_128256x4096_b1", O.Q8_0, 128256, 4096, 1, 1005),
                  ("q6_k_lm_head_128256x4096_b1", O.Q6_K, 128256, 4096, 1, 1006),
+                 # the Q4 GEMV on a launch large enough that the launch ramp and
+                 # tail stop mattering (the lm_head's shape): the rate it sustains
+                 ("q4_0_128256x4096_b1", O.Q4_0, 128256, 4096, 1, 1007),
+                 ("q4_k_128256x4096_b1", O.Q4_K, 128256, 4096, 1, 1008),
                  ("q4_0_4096x4096_b1", O.Q4_0, 4096, 4096, 1, 1002),
                  ("q4_0_4096x14336_b1", O.Q4_0, 4096, 14336, 1, 1002)]
     gemv_cfgs += [(f"q4_k_14336x4096_b{b}", O.Q4_K, 14336, 4096, b, 1003) for b in (1, 4, 8, 16)]
