@@ -1123,9 +1123,9 @@ extern "C" int gq_launch_gemm_mfma_mixed_f16f32(void *stream, const float *a, co
 // Skinny GEMM plan: M <= 256 (Q6_K: any M), a chunk list of at most 4 per wave
 // of 8 (K <= 4096 for Q4_0 / Q8_0, 8192 for Q4_K; Q6_K 2, K <= 4096) or, for
 // Q4_0 / Q4_K, 8 per wave of 16 (K <= 16384 / 32768; *nck_out = 16 + chunks), CT = 2 row tiles per workgroup where that
-// still gives every CU a workgroup, and at most two workgroups per CU in all
-// (each reads its 64 rows of A whole: measured slower than the tiled GEMM
-// beyond that, e.g. 128 x 14336: 54 vs 45 us).  GQ_ERR_UNSUPPORTED otherwise
+// still gives every CU a workgroup, and at most one workgroup per CU in all
+// (two for the long-K form; each reads its 64 rows of A whole: measured slower
+// than the tiled GEMM's K-group tiles beyond that).  GQ_ERR_UNSUPPORTED otherwise
 // (the tiled GEMM takes the shape).  GQ_GEMM_SKINNY=0, or a tiled shape forced
 // through GQ_GEMM_TILE, turns the kernel off.
 int gq_gemm_skinny_plan(int fmt, size_t M, size_t N, size_t K, int *ct_out, int *nck_out) {
