@@ -929,11 +929,17 @@ int fused_fallback(int fmt, int n_mats, const void *const *packed, const size_t 
 extern "C" int gq_gemv_multi_plan(int fmt, int n_mats, const size_t *N, size_t K, int batch, int *R_out,
                                   int *ksplit_out, int *chunks_per_wave_out) {
   GQ_CHECK(n_mats >= 1 && n_mats <= 4 && N, GQ_ERR_INVALID_ARGS);
-  GQ_CHECK(batch >= 1 && batch <= 4 && !gq_fmt_is_q6k(fmt), GQ_ERR_UNSUPPORTED);
+  GQ_CHECK(batch >= 1 && batch <= 4, GQ_ERR_UNSUPPORTED);
   size_t tiles = 0;
   for (int i = 0; i < n_mats; ++i) {
     GQ_TRY(gq_check_shape(fmt, N[i], K));
     tiles += gq_tiles(N[i]);
+  }
+  if (gq_fmt_is_q6k(fmt)) {  // no fused Q6_K kernel: the fallback
+    if (R_out) *R_out = 0;
+    if (ksplit_out) *ksplit_out = 0;
+    if (chunks_per_wave_out) *chunks_per_wave_out = 0;
+    return GQ_OK;
   }
   int R = 1, ks = 2, cpw = 0;
   GQ_TRY(q_plan(fmt, tiles * 16, K, batch, &R, &ks, &cpw));
@@ -979,7 +985,12 @@ extern "C" int gq_gemv_multi(int fmt, int n_mats, const void *const *packed, con
 extern "C" int gq_gemv_swiglu_plan(int fmt, size_t N, size_t K, int batch, int *ksplit_out,
                                    int *chunks_per_wave_out) {
   GQ_TRY(gq_check_shape(fmt, N, K));
-  GQ_CHECK(batch >= 1 && batch <= 4 && !gq_fmt_is_q6k(fmt), GQ_ERR_UNSUPPORTED);
+  GQ_CHECK(batch >= 1 && batch <= 4, GQ_ERR_UNSUPPORTED);
+  if (gq_fmt_is_q6k(fmt)) {  // no fused Q6_K kernel: the fallback
+    if (ksplit_out) *ksplit_out = 0;
+    if (chunks_per_wave_out) *chunks_per_wave_out = 0;
+    return GQ_OK;
+  }
   const int C = (int)gq_chunks(fmt, K);
   int ks = ks_for(fmt, gq_tiles(N), C, 2);
   int cpw = ks > 0 ? (C + ks - 1) / ks : 0;

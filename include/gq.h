@@ -48,9 +48,9 @@ extern "C" {
 #define GQ_FMT_F16 1         /* one "block" = one fp16 value (weight_loader.cpp:91-110) */
 /* Q6_K (both layouts): T16 repack, dequant, gq_gemv (int8 matrix-core
    kernel at batch 1..2, fp16 above) and gq_gemm for K <= 4096 (skinny kernel,
-   any M); gq_gemm with longer K, gq_gemv_prep / prepped, gq_gemv_multi and
-   gq_gemv_swiglu return GQ_ERR_UNSUPPORTED for it (gq_matmul then runs 16-row
-   GEMV batches). */
+   any M); gq_gemv_multi / gq_gemv_swiglu run their fallback for it (RMSNorm,
+   one gq_gemv per matrix); gq_gemm with longer K and gq_gemv_prep / prepped
+   return GQ_ERR_UNSUPPORTED for it (gq_matmul then runs 16-row GEMV batches). */
 
 /* activation / output dtypes */
 #define GQ_DT_F32 0
@@ -151,8 +151,8 @@ int gq_gemv_prepped(int fmt, const void *d_packed, const void *d_workspace, floa
  * format sharing K and x (e.g. q, k, v with GQA shapes). */
 int gq_gemv_multi(int fmt, int n_mats, const void *const *d_packed, const size_t *N, size_t K, const float *d_x,
                   float *const *d_y, int batch, const float *d_gamma, float eps, void *stream);
-/* Shapes whose activation staging does not fit one fused launch (batch 3..4
- * with K beyond about 14000, or K too long for a wave's chunk list) run as a
+/* Q6_K, and shapes whose activation staging does not fit one fused launch
+ * (batch 3..4 with K beyond about 14000, or K too long for a wave's chunk list), run as a
  * fallback: x RMS-normalised into the library's workspace (when gamma is
  * given), one gq_gemv per matrix, and for gq_gemv_swiglu an elementwise
  * silu(gate) * up -- the same results within the GEMV bound, in 2-4 launches.

@@ -121,3 +121,26 @@ def test_fused_fallback_long_k(dev, fmt, norm):
             y = gq.gemv_swiglu(fmt, pg, pu, _dev(x, dev), n, k, gamma=g, eps=eps).cpu().numpy()
             ref = O.swiglu(O.gemv(fmt, wg, xin, n, k), O.gemv(fmt, wu, xin, n, k))
             assert O.rel_l2(y, ref) <= TOL
+
+
+@pytest.mark.parametrize("fmt", [O.Q6_K, O.Q6_K_GGML])
+@pytest.mark.parametrize("batch", [1, 3])
+def test_fused_q6k(dev, fmt, batch):
+    """Q6_K (Q4_K_M files keep some projections in it): the fused entry points
+    take the fallback (plans report zeros) and match the oracle, with RMSNorm."""
+    import gq
+    k, eps = 1024, 1e-5
+    ns = [256, 64]
+    pw = [_packed(fmt, n, k, 95 + i, dev) for i, n in enumerate(ns)]
+    x = O.gen_x(batch, k, 23)
+    gamma = (np.random.default_rng(24).standard_normal(k) * 0.5 + 1.0).astype(np.float32)
+    xin = O.rmsnorm(x, gamma, eps).astype(np.float32)
+    assert gq.gemv_multi_plan(fmt, ns, k, batch) == (0, 0, 0)
+    ys = gq.gemv_multi(fmt, [(p, n) for (_, p), n in zip(pw, ns)], _dev(x, dev), k, gamma=_dev(gamma, dev), eps=eps)
+    for (w, _), n, y in zip(pw, ns, ys):
+        assert O.rel_l2(y.cpu().numpy(), O.gemv(fmt, w, xin, n, k)) <= TOL
+    assert gq.gemv_swiglu_plan(fmt, ns[0], k, batch) == (0, 0)
+    wu, pu = _packed(fmt, ns[0], k, 99, dev)
+    y = gq.gemv_swiglu(fmt, pw[0][1], pu, _dev(x, dev), ns[0], k, gamma=_dev(gamma, dev), eps=eps).cpu().numpy()
+    ref = O.swiglu(O.gemv(fmt, pw[0][0], xin, ns[0], k), O.gemv(fmt, wu, xin, ns[0], k))
+    assert O.rel_l2(y, ref) <= TOL
